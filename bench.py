@@ -1,0 +1,269 @@
+"""Benchmark of the quantized DiT hot path on one MI355X (gfx950).
+
+Metric: INT8 TOPS + % MFMA peak, W8A8 GEMM & Sage attention at
+Wan-14B shapes, 1 GPU.
+
+One step = the Wan-14B block's hot path on synthetic inputs already resident
+in HBM:
+  * the four ConvRot W8A8 linears of config 4 (M=32760 tokens; qkv K5120 N15360,
+    out K5120 N5120, ffn-up K5120 N13824, ffn-down K13824 N5120), each = ConvRot
+    quantize (G=128) + INT8 GEMM with the per-token x per-channel epilogue;
+  * Sage attention of config 3 (B1 H40 L32760 D128): K mean, Q/K per-128-token
+    INT8 quantization, INT8 QK^T + online softmax + bf16 PV.
+value = (sum of 2MNK over the linears + 4 B H L^2 D) / step time, in TOPS.
+
+Per-kernel average durations come from HIP events recorded on the launch
+stream inside the timed region.  The roofline entry is for the kernel with the
+largest total time.  cpu_baseline times the CPU oracle (oracle/, a plain-C
+restatement of the reference arithmetic) on a bounded sample of the same
+workload on this host's cores.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "comfyui-turing-utils_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+PEAK_INT8_TOPS = 5000.0     # MI355X published dense INT8 MFMA, 5.0 POP/s
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E, 8 TB/s
+M_TOKENS = 32760
+LINEARS = (("qkv", 5120, 15360), ("out", 5120, 5120), ("ffn_up", 5120, 13824), ("ffn_down", 13824, 5120))
+ATTN = dict(b=1, h=40, l=32760, d=128)
+GROUP = 128
+BLK = 128
+
+
+def parse_args():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=10)
+    p.add_argument("--warmup", type=int, default=2)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-seconds", type=float, default=15.0, help="approximate CPU baseline budget")
+    return p.parse_args()
+
+
+class KernelTimer:
+    """Pairs of HIP events around launches on the current stream, per kernel name."""
+
+    def __init__(self, torch):
+        self.torch = torch
+        self.pending = []
+        self.enabled = False
+
+    def __call__(self, name, fn, *args, **kwargs):
+        if not self.enabled:
+            return fn(*args, **kwargs)
+        start = self.torch.cuda.Event(enable_timing=True)
+        end = self.torch.cuda.Event(enable_timing=True)
+        start.record()
+        out = fn(*args, **kwargs)
+        end.record()
+        self.pending.append((name, start, end))
+        return out
+
+    def summary(self, steps):
+        totals = {}
+        counts = {}
+        for name, s, e in self.pending:
+            totals[name] = totals.get(name, 0.0) + s.elapsed_time(e)
+            counts[name] = counts.get(name, 0) + 1
+        return {n: {"ms_avg": totals[n] / counts[n], "ms_per_step": totals[n] / steps, "launches": counts[n]}
+                for n in totals}
+
+
+def main():
+    args = parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(the hot path shards by tokens/heads with no exchange; see DESIGN.md). "
+              "Run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    import comfyui_turing_utils_kernel  # noqa: F401  (registers torch.ops.turing_utils.*)
+    from comfyui_turing_utils_kernel import _lib
+    from comfyui_turing_utils_kernel.turing_sage import quant as sage_quant
+    from comfyui_turing_utils_kernel.turing_sage.core import sageattn_prequantized
+    from tests import inputs
+
+    dev = torch.device("cuda", 0)
+    if not _lib.device_supported(dev):
+        raise SystemExit(f"bench.py needs a gfx950 GPU, got {torch.cuda.get_device_name(0)}")
+    torch.cuda.set_device(dev)
+
+    # ---- synthetic inputs, generated on the CPU with fixed seeds, then moved to HBM
+    lin = []
+    for idx, (name, k, n) in enumerate(LINEARS):
+        x = inputs.activation(M_TOKENS, k, 3 + idx).to(dev)
+        w, ws, _ = inputs.weights(n, k, 3 + idx, with_bias=False)
+        lin.append((name, k, n, x, w.to(dev), ws.to(dev)))
+    q, k_, v = (t.to(dev) for t in inputs.attention(ATTN["b"], ATTN["h"], ATTN["l"], ATTN["d"], 2))
+    torch.cuda.synchronize()
+
+    timer = KernelTimer(torch)
+    ops = torch.ops.turing_utils
+    sm_scale = ATTN["d"] ** -0.5
+
+    def step():
+        for name, _, _, x, w, ws in lin:
+            qa, sa = timer(f"convrot_quant_k{x.shape[1]}", ops.bf16_int8_convrot_quantize, x, GROUP)
+            timer(f"int8_gemm_{name}", ops.int8_linear, qa, w, sa, ws, None)
+        mean = timer("sage_kmean", sage_quant.key_channel_mean, k_, "HND")
+        q8, qs = timer("sage_quant_q", sage_quant.quantize_per_block, q, BLK, "HND")
+        k8, ks = timer("sage_quant_k", sage_quant.quantize_per_block, k_, BLK, "HND", mean)
+        return timer("sage_attn", sageattn_prequantized, q8, qs, k8, ks, v, tensor_layout="HND",
+                     sm_scale=sm_scale, blkq=BLK, blkk=BLK)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    timer.enabled = True
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ms_per_step = (t1 - t0) * 1e3 / args.steps
+    kernels = timer.summary(args.steps)
+
+    lin_ops = sum(2.0 * M_TOKENS * n * k for _, k, n, *_ in lin)
+    attn_ops = 4.0 * ATTN["b"] * ATTN["h"] * ATTN["l"] ** 2 * ATTN["d"]
+    total_ops = lin_ops + attn_ops
+    value = total_ops / (ms_per_step * 1e-3) / 1e12
+
+    # Per-kernel algorithmic work: GEMM 2MNK ops; attention 4BHL^2D ops;
+    # ConvRot quantize 2 B/elem read + 1 B/elem write + 4 B/row; Sage quantize
+    # 2 B read + 1 B write per element (K also reads its mean: negligible);
+    # K mean 2 B/elem read.
+    work = {}
+    for name, k, n, *_ in lin:
+        work[f"int8_gemm_{name}"] = ("mfma", 2.0 * M_TOKENS * n * k)
+        work[f"convrot_quant_k{k}"] = ("hbm", 3.0 * M_TOKENS * k + 4.0 * M_TOKENS)
+    elems = ATTN["b"] * ATTN["h"] * ATTN["l"] * ATTN["d"]
+    work["sage_attn"] = ("mfma", attn_ops)
+    work["sage_quant_q"] = ("hbm", 3.0 * elems)
+    work["sage_quant_k"] = ("hbm", 3.0 * elems)
+    work["sage_kmean"] = ("hbm", 2.0 * elems)
+    for name, rec in kernels.items():
+        bound, amount = work[name]
+        sec = rec["ms_avg"] * 1e-3
+        if bound == "mfma":
+            rec["tops"] = amount / sec / 1e12
+            rec["frac_int8_peak"] = rec["tops"] / PEAK_INT8_TOPS
+        else:
+            rec["gbs"] = amount / sec / 1e9
+            rec["frac_hbm_peak"] = rec["gbs"] / PEAK_HBM_GBS
+    dominant = max(kernels, key=lambda n: kernels[n]["ms_per_step"])
+    bound, amount = work[dominant]
+    achieved = kernels[dominant]["tops"] if bound == "mfma" else kernels[dominant]["gbs"]
+    peak = PEAK_INT8_TOPS if bound == "mfma" else PEAK_HBM_GBS
+    roofline = {
+        "kernel": dominant,
+        "bound": bound,
+        "achieved": achieved,
+        "peak": peak,
+        "unit": "TFLOP/s" if bound == "mfma" else "GB/s",
+        "frac": achieved / peak,
+        "traffic": None,
+    }
+
+    cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds)
+
+    record = {
+        "metric": "INT8 TOPS + % MFMA peak: W8A8 GEMM & Sage attn at Wan-14B shapes, 1 GPU",
+        "value": value,
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded Wan-14B shapes: 0.1% x20 outlier channels; int8 weights; "
+                "K per-head channel bias), inputs resident in HBM",
+        "config": {
+            "workload": "wan14b_block_hot_path: 4x ConvRot W8A8 linear (config 4, M=32760, G=128) "
+                        "+ Sage INT8 attention (config 3, B1 H40 L32760 D128, BLKQ=BLKK=128, K-smoothing)",
+            "linears": [{"name": n, "M": M_TOKENS, "K": k, "N": nn} for n, k, nn, *_ in lin],
+            "attention": ATTN,
+            "ops_per_step": total_ops,
+        },
+        "kernels": kernels,
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(record))
+    return 0
+
+
+def cpu_baseline(budget_s: float):
+    """CPU oracle (port) on a bounded sample of the same workload.
+
+    Sample: ffn-up linear on S rows (ConvRot quantize G=128 + exact int GEMM +
+    epilogue, K=5120, N=13824) and the Sage attention oracle on R query rows of
+    config 3 (full 32760-key softmax per row).  Both are expressed as TOPS of
+    the same op count the GPU figure uses, and combined with the GPU step's
+    op mix (linears vs attention) into one step-equivalent rate.
+    """
+    import numpy as np
+
+    from oracle import oracle
+    from tests import inputs
+
+    threads = os.cpu_count() or 1
+    k, n = 5120, 13824
+    rows = 64
+    x = inputs.activation(rows, k, 5)
+    w, ws, _ = inputs.weights(n, k, 5, with_bias=False)
+    xb, wn, wsn = inputs.bits(x), w.numpy(), ws.numpy()
+    t0 = time.perf_counter()
+    qa, sa = oracle.convrot_quant(xb, GROUP)
+    acc = oracle.int8_gemm_i32(qa, wn)
+    oracle.epilogue_bf16(acc, sa, wsn)
+    t_lin = time.perf_counter() - t0
+    lin_tops = 2.0 * rows * n * k / t_lin / 1e12
+
+    l, d = ATTN["l"], ATTN["d"]
+    g = np.random.default_rng(0)
+    q8 = g.integers(-127, 128, (1, 1, 256, d), dtype=np.int8)
+    k8 = g.integers(-127, 128, (1, 1, l, d), dtype=np.int8)
+    vb = inputs.bits(inputs.attention(1, 1, l, d, 2)[2])
+    qs = np.full((1, 1, 2), 1e-3, np.float32)
+    ks = np.full((1, 1, (l + 127) // 128), 1e-3, np.float32)
+    rows_a = max(threads, 16)
+    sel = np.stack([np.zeros(rows_a, np.int64), np.zeros(rows_a, np.int64), np.arange(rows_a) % 256], 1)
+    t0 = time.perf_counter()
+    oracle.sage_attn_rows(q8, qs, 128, k8, ks, 128, vb, d ** -0.5, sel)
+    t_att = time.perf_counter() - t0
+    att_tops = 4.0 * rows_a * l * d / t_att / 1e12
+
+    lin_ops = sum(2.0 * M_TOKENS * nn * kk for _, kk, nn in LINEARS)
+    attn_ops = 4.0 * ATTN["b"] * ATTN["h"] * ATTN["l"] ** 2 * d
+    step_s = lin_ops / (lin_tops * 1e12) + attn_ops / (att_tops * 1e12)
+    return {
+        "value": (lin_ops + attn_ops) / step_s / 1e12,
+        "unit": "TOPS",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"oracle ffn-up linear on {rows} rows ({t_lin:.2f} s, {lin_tops:.4f} TOPS) and Sage "
+                  f"attention oracle on {rows_a} query rows x 32760 keys ({t_att:.2f} s, {att_tops:.4f} TOPS), "
+                  f"combined with the step's op mix; projected step {step_s:.0f} s",
+    }
+
+
+if __name__ == "__main__":
+    sys.exit(main())

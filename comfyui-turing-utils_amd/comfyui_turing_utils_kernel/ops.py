@@ -1,0 +1,202 @@
+"""torch.library ops of the ConvRot W8A8 linear path, backed by libtu_hip.so.
+
+Names, signatures, fake (meta) implementations and error types follow the
+reference package's ``kernel/comfyui_turing_utils_kernel/ops.py`` so callers
+that dispatch through ``torch.ops.turing_utils.*`` or the package attributes
+(``comfyui_turing_utils/quantization/dispatch.py:63-67``) run unchanged.
+
+Differences from the reference, by design of this MI355X build:
+  * the device predicate is gfx950 instead of sm75;
+  * ``bf16_int8_convrot_quantize`` accepts ``group_size`` 128 (this build's
+    block-Hadamard extension) as well as 256 (the reference's only size);
+  * ``int8_gemm_i32`` is an extra op exposing the raw INT32 accumulator of
+    the same GEMM kernel, used for bit-exact parity checks.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+
+def _require_device(t: torch.Tensor, what: str) -> None:
+    if t.device.type != "cuda":
+        raise RuntimeError(f"{what} requires CUDA (HIP) tensors")
+    if not _lib.device_supported(t.device):
+        raise RuntimeError(f"{what} requires a gfx950 (MI355X-class) GPU")
+
+
+# ---------------------------------------------------------------------------
+# INT8 linear (reference ops.py:96-126, bindings.cpp:371-421)
+# ---------------------------------------------------------------------------
+@torch.library.custom_op("turing_utils::int8_linear", mutates_args=())
+def turing_int8_linear(
+    activation: torch.Tensor,
+    weight: torch.Tensor,
+    activation_scale: torch.Tensor,
+    weight_scale: torch.Tensor,
+    bias: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """W8A8 contraction with the fused per-token x per-channel scale + bias epilogue."""
+    _require_device(activation, "INT8 linear")
+    activation = activation.contiguous()
+    weight = weight.contiguous()
+    activation_scale = activation_scale.reshape(-1).to(torch.float32).contiguous()
+    weight_scale = weight_scale.reshape(-1).to(torch.float32).contiguous()
+    if bias is not None:
+        bias = bias.reshape(-1).to(torch.float32).contiguous()
+    if activation.dim() != 2 or weight.dim() != 2:
+        raise ValueError("INT8 linear activation and weight must be 2D")
+    if activation.dtype != torch.int8 or weight.dtype != torch.int8:
+        raise TypeError("INT8 linear activation and weight must be int8")
+    devices = {activation.device, weight.device, activation_scale.device, weight_scale.device}
+    if bias is not None:
+        devices.add(bias.device)
+    if len(devices) != 1:
+        raise ValueError("INT8 linear tensors must use the same CUDA device")
+    m, k = activation.shape
+    n = weight.shape[0]
+    if weight.shape[1] != k:
+        raise ValueError("INT8 linear K dimensions must match")
+    if k % 16 != 0 or n % 8 != 0:
+        raise ValueError("INT8 linear requires K%16=0 and N%8=0")
+    if activation_scale.numel() != m:
+        raise ValueError("activation_scale must contain one value per row")
+    if weight_scale.numel() != n:
+        raise ValueError("weight_scale must contain one value per output channel")
+    if bias is not None and bias.numel() != n:
+        raise ValueError("bias must contain one value per output channel")
+    out = torch.empty((m, n), dtype=torch.bfloat16, device=activation.device)
+    if m == 0:
+        return out
+    with torch.cuda.device(activation.device):
+        _lib.call(
+            "tu_int8_gemm_bf16",
+            activation.data_ptr(), weight.data_ptr(), activation_scale.data_ptr(), weight_scale.data_ptr(),
+            _lib.ptr(bias), out.data_ptr(), m, n, k, _lib.stream_of(activation.device),
+        )
+    return out
+
+
+@turing_int8_linear.register_fake
+def _turing_int8_linear_fake(activation, weight, activation_scale, weight_scale, bias=None):
+    return torch.empty((activation.size(0), weight.size(0)), dtype=torch.bfloat16, device=activation.device)
+
+
+@torch.library.custom_op("turing_utils::int8_gemm_i32", mutates_args=())
+def turing_int8_gemm_i32(activation: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """INT32 accumulator ``activation @ weight.T`` of the same MFMA GEMM kernel."""
+    _require_device(activation, "INT8 GEMM")
+    activation = activation.contiguous()
+    weight = weight.contiguous()
+    if activation.dtype != torch.int8 or weight.dtype != torch.int8:
+        raise TypeError("INT8 GEMM operands must be int8")
+    if activation.dim() != 2 or weight.dim() != 2 or weight.shape[1] != activation.shape[1]:
+        raise ValueError("INT8 GEMM operands must be [M, K] and [N, K]")
+    if activation.device != weight.device:
+        raise ValueError("INT8 GEMM operands must share one device")
+    m, k = activation.shape
+    n = weight.shape[0]
+    if k % 16 != 0 or n % 8 != 0:
+        raise ValueError("INT8 GEMM requires K%16=0 and N%8=0")
+    out = torch.empty((m, n), dtype=torch.int32, device=activation.device)
+    if m == 0:
+        return out
+    with torch.cuda.device(activation.device):
+        _lib.call("tu_int8_gemm_i32", activation.data_ptr(), weight.data_ptr(), out.data_ptr(), m, n, k,
+                  _lib.stream_of(activation.device))
+    return out
+
+
+@turing_int8_gemm_i32.register_fake
+def _turing_int8_gemm_i32_fake(activation, weight):
+    return torch.empty((activation.size(0), weight.size(0)), dtype=torch.int32, device=activation.device)
+
+
+# ---------------------------------------------------------------------------
+# INT32 -> BF16 epilogue (reference ops.py:129-160, bindings.cpp:423-472)
+# ---------------------------------------------------------------------------
+@torch.library.custom_op("turing_utils::dequantize_int8_bf16", mutates_args=())
+def turing_dequantize_int8_bf16(
+    accumulator: torch.Tensor,
+    activation_scale: torch.Tensor,
+    weight_scale: torch.Tensor,
+    output_columns: int = -1,
+) -> torch.Tensor:
+    """Dequantize an INT32 GEMM workspace directly into packed BF16 stores."""
+    _require_device(accumulator, "BF16 epilogue")
+    if accumulator.dtype != torch.int32 or accumulator.ndim != 2:
+        raise TypeError("accumulator must be a 2D int32 tensor")
+    accumulator = accumulator.contiguous()
+    activation_scale = activation_scale.reshape(-1).to(torch.float32).contiguous()
+    weight_scale = weight_scale.reshape(-1).to(torch.float32).contiguous()
+    if accumulator.device != activation_scale.device or accumulator.device != weight_scale.device:
+        raise ValueError("accumulator and scales must use the same CUDA device")
+    rows, acc_cols = accumulator.shape
+    cols = acc_cols if output_columns < 0 else output_columns
+    if rows <= 0 or acc_cols <= 0:
+        raise ValueError("INT8 BF16 epilogue dimensions must be positive")
+    if not 0 < cols <= acc_cols:
+        raise ValueError("output_columns must be positive and no larger than the accumulator width")
+    if activation_scale.numel() != rows:
+        raise ValueError("activation_scale must contain one value per accumulator row")
+    if weight_scale.numel() not in (1, cols):
+        raise ValueError("weight_scale must be scalar or contain one value per output column")
+    out = torch.empty((rows, cols), dtype=torch.bfloat16, device=accumulator.device)
+    with torch.cuda.device(accumulator.device):
+        _lib.call(
+            "tu_dequant_i32_bf16", accumulator.data_ptr(), acc_cols, activation_scale.data_ptr(),
+            weight_scale.data_ptr(), int(weight_scale.numel() == 1), out.data_ptr(), rows, cols,
+            _lib.stream_of(accumulator.device),
+        )
+    return out
+
+
+@turing_dequantize_int8_bf16.register_fake
+def _turing_dequantize_int8_bf16_fake(accumulator, activation_scale, weight_scale, output_columns=-1):
+    columns = accumulator.size(1) if output_columns < 0 else output_columns
+    return torch.empty((accumulator.size(0), columns), dtype=torch.bfloat16, device=accumulator.device)
+
+
+# ---------------------------------------------------------------------------
+# ConvRot INT8 activation quantizer (reference ops.py:257-282)
+# ---------------------------------------------------------------------------
+SUPPORTED_GROUP_SIZES = (128, 256)
+
+
+@torch.library.custom_op("turing_utils::bf16_int8_convrot_quantize", mutates_args=())
+def turing_bf16_int8_convrot_quantize(
+    x: torch.Tensor,
+    group_size: int = 256,
+    *,
+    swiglu: bool = False,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Whole-row BF16 ConvRot rotation + per-token symmetric INT8 quantization."""
+    _require_device(x, "BF16 row-buffer ConvRot")
+    if x.dtype != torch.bfloat16:
+        raise TypeError("BF16 row-buffer ConvRot input must be bfloat16")
+    if x.ndim != 2:
+        raise ValueError("BF16 row-buffer ConvRot input must be 2D")
+    if swiglu:
+        raise RuntimeError("SwiGLU folding is not available in the gfx950 ConvRot quantizer")
+    if group_size not in SUPPORTED_GROUP_SIZES:
+        raise ValueError(f"BF16 row-buffer ConvRot supports group_size {SUPPORTED_GROUP_SIZES}, got {group_size}")
+    x = x.contiguous()
+    rows, hidden = x.shape
+    if rows <= 0 or hidden <= 0 or hidden % group_size:
+        raise ValueError(f"BF16 row-buffer ConvRot width must be positive and divisible by {group_size}")
+    q = torch.empty((rows, hidden), dtype=torch.int8, device=x.device)
+    scales = torch.empty((rows, 1), dtype=torch.float32, device=x.device)
+    with torch.cuda.device(x.device):
+        _lib.call("tu_convrot_quant_i8", x.data_ptr(), q.data_ptr(), scales.data_ptr(), rows, hidden,
+                  group_size, 0, _lib.stream_of(x.device))
+    return q, scales
+
+
+@turing_bf16_int8_convrot_quantize.register_fake
+def _turing_bf16_int8_convrot_quantize_fake(x, group_size=256, *, swiglu=False):
+    hidden = x.size(1) // 2 if swiglu else x.size(1)
+    return (
+        torch.empty((x.size(0), hidden), dtype=torch.int8, device=x.device),
+        torch.empty((x.size(0), 1), dtype=torch.float32, device=x.device),
+    )

@@ -1,0 +1,216 @@
+"""Sage INT8 attention facade on gfx950.
+
+Follows the reference's ``turing_sage/core.py``: validation and head-dim
+padding (``prequantize_sageattn``, :409-474), the split prequantize / execute
+API (``PrequantizedSageAttention``, ``sageattn_from_prequantized``,
+``sageattn_prequantized``, :477-653) and the one-call ``sageattn`` (:543-570).
+
+MI355X build choices (each a parameter with the Wan default):
+  * Q and K are quantized per 128-token block (``BLKQ``, ``BLKK``); the
+    reference used Q per 16 tokens and K per 64 tokens for its 64-row Turing
+    CTA.
+  * K is mean-smoothed by default (``smooth_k=True``); the reference's
+    production Turing path raises on smoothing (core.py:421-422).
+  * PV runs in bf16 on MFMA; the reference converted V to fp16 for Turing.
+  * The kernel is used for every sequence length (no SDPA short-sequence
+    detour): tails are masked inside the kernel.
+  * head_dim <= 128 is zero-padded to 128, which leaves Q.K and P.V exact.
+"""
+from __future__ import annotations
+
+import dataclasses
+import math
+from typing import Optional
+
+import torch
+
+from .. import _lib
+from .quant import SUPPORTED_BLOCKS, _layout_dims, per_block_int8
+
+KERNEL_HEAD_DIM = 128
+
+
+@dataclasses.dataclass(frozen=True)
+class PrequantizedSageAttention:
+    """Quantized Q/K plus V, ready for ``sageattn_from_prequantized``."""
+
+    query_int8: torch.Tensor
+    query_scale: torch.Tensor
+    key_int8: torch.Tensor
+    key_scale: torch.Tensor
+    value: torch.Tensor
+    tensor_layout: str
+    original_head_dim: int
+    is_causal: bool
+    sm_scale: float
+    blkq: int
+    blkk: int
+    output_dtype: torch.dtype
+
+
+def _validate(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, tensor_layout: str) -> None:
+    if tensor_layout not in ("HND", "NHD"):
+        raise ValueError(f"Unsupported tensor_layout: {tensor_layout}")
+    if not q.is_cuda:
+        raise ValueError("Input tensors must be on CUDA")
+    if q.dtype not in (torch.float16, torch.bfloat16):
+        raise TypeError("Sage Q/K/V must be float16 or bfloat16")
+    if q.device != k.device or q.device != v.device:
+        raise ValueError("Q/K/V must be on the same device")
+    if q.dtype != k.dtype or q.dtype != v.dtype:
+        raise TypeError("Q/K/V must have matching dtypes")
+    if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
+        raise ValueError("Sage Q/K/V must be four-dimensional")
+    if k.shape != v.shape:
+        raise ValueError("K and V must have the same shape")
+    qh, ql, *_ = _layout_dims(q, tensor_layout)
+    kh, kl, *_ = _layout_dims(k, tensor_layout)
+    if q.size(0) != k.size(0) or q.size(-1) != k.size(-1):
+        raise ValueError("Q and K must agree in batch and head_dim")
+    if kh <= 0 or qh % kh != 0:
+        raise ValueError("Q heads must be divisible by KV heads")
+    if ql <= 0 or kl <= 0:
+        raise ValueError("Sage attention requires non-empty Q/K sequences")
+    if q.size(-1) > KERNEL_HEAD_DIM:
+        raise ValueError(f"Unsupported head_dim: {q.size(-1)}")
+
+
+def _prepare(x: torch.Tensor) -> torch.Tensor:
+    """bf16, channels padded to the kernel head_dim, last dim contiguous."""
+    if x.dtype != torch.bfloat16:
+        x = x.to(torch.bfloat16)
+    pad = KERNEL_HEAD_DIM - x.size(-1)
+    if pad:
+        x = torch.nn.functional.pad(x, (0, pad))
+    if x.stride(-1) != 1 or x.data_ptr() % 16 != 0 or any(s % 8 for s in x.stride()[:-1]):
+        x = x.contiguous()
+    return x
+
+
+def prequantize_sageattn(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    tensor_layout: str = "HND",
+    is_causal: bool = False,
+    sm_scale: Optional[float] = None,
+    smooth_k: bool = True,
+    BLKQ: int = 128,
+    BLKK: int = 128,
+) -> PrequantizedSageAttention:
+    """Quantize Q/K (K smoothed) and keep V, before the output is allocated."""
+    _validate(q, k, v, tensor_layout)
+    if BLKQ not in SUPPORTED_BLOCKS or BLKK not in SUPPORTED_BLOCKS or BLKK % 64:
+        raise ValueError(f"BLKQ must be in {SUPPORTED_BLOCKS} and BLKK in (64, 128)")
+    head_dim = q.size(-1)
+    scale = float(sm_scale) if sm_scale is not None else head_dim ** -0.5
+    if not (scale > 0.0 and math.isfinite(scale)):
+        raise ValueError("sm_scale must be a positive finite number")
+    output_dtype = q.dtype
+    qp, kp, vp = _prepare(q), _prepare(k), _prepare(v)
+    with torch.cuda.device(q.device):
+        q_int8, q_scale, k_int8, k_scale, _ = per_block_int8(
+            qp, kp, BLKQ=BLKQ, BLKK=BLKK, tensor_layout=tensor_layout, smooth_k=smooth_k
+        )
+    return PrequantizedSageAttention(
+        query_int8=q_int8, query_scale=q_scale, key_int8=k_int8, key_scale=k_scale, value=vp,
+        tensor_layout=tensor_layout, original_head_dim=head_dim, is_causal=bool(is_causal),
+        sm_scale=scale, blkq=BLKQ, blkk=BLKK, output_dtype=output_dtype,
+    )
+
+
+def sageattn_prequantized(
+    q_int8: torch.Tensor,
+    q_scale: torch.Tensor,
+    k_int8: torch.Tensor,
+    k_scale: torch.Tensor,
+    v: torch.Tensor,
+    *,
+    tensor_layout: str = "HND",
+    is_causal: bool = False,
+    sm_scale: Optional[float] = None,
+    blkq: int = 128,
+    blkk: int = 128,
+    output: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Attention on already-quantized Q/K and bf16 V (all head_dim 128)."""
+    if tensor_layout not in ("HND", "NHD"):
+        raise ValueError(f"Unsupported tensor_layout: {tensor_layout}")
+    if q_int8.dtype != torch.int8 or k_int8.dtype != torch.int8:
+        raise TypeError("prequantized Sage Q/K must be int8")
+    if v.dtype != torch.bfloat16:
+        raise TypeError("prequantized Sage V must be bfloat16")
+    if q_scale.dtype != torch.float32 or k_scale.dtype != torch.float32:
+        raise TypeError("prequantized Sage scales must be float32")
+    if q_int8.ndim != 4 or k_int8.ndim != 4 or v.ndim != 4:
+        raise ValueError("prequantized Sage Q/K/V must be four-dimensional")
+    devices = {q_int8.device, k_int8.device, v.device, q_scale.device, k_scale.device}
+    if len(devices) != 1:
+        raise ValueError("prequantized Sage tensors must share one device")
+    if q_int8.size(-1) != KERNEL_HEAD_DIM or k_int8.size(-1) != KERNEL_HEAD_DIM or v.size(-1) != KERNEL_HEAD_DIM:
+        raise ValueError("prequantized Sage requires head_dim 128")
+    hq, lq, qsb, qsh, qsl = _layout_dims(q_int8, tensor_layout)
+    hkv, lk, ksb, ksh, ksl = _layout_dims(k_int8, tensor_layout)
+    vh, vl, vsb, vsh, vsl = _layout_dims(v, tensor_layout)
+    batch = q_int8.size(0)
+    if k_int8.size(0) != batch or v.size(0) != batch or vh != hkv or vl != lk:
+        raise ValueError("prequantized Sage Q/K/V shapes are incompatible")
+    if hkv <= 0 or hq % hkv != 0:
+        raise ValueError("prequantized Sage Q heads must be divisible by KV heads")
+    if blkk % 64 or blkq <= 0:
+        raise ValueError("prequantized Sage needs blkq > 0 and blkk % 64 == 0")
+    if q_scale.shape != (batch, hq, (lq + blkq - 1) // blkq):
+        raise ValueError("prequantized Sage Q scale shape is incompatible")
+    if k_scale.shape != (batch, hkv, (lk + blkk - 1) // blkk):
+        raise ValueError("prequantized Sage K scale shape is incompatible")
+    if any(t.stride(-1) != 1 for t in (q_int8, k_int8, v)):
+        raise ValueError("the last Q/K/V dimension must be contiguous")
+    scale = float(sm_scale) if sm_scale is not None else KERNEL_HEAD_DIM ** -0.5
+    if output is None:
+        output = torch.empty(q_int8.shape, dtype=torch.bfloat16, device=v.device)
+    elif output.shape != q_int8.shape or output.dtype != torch.bfloat16 or output.device != v.device or output.stride(-1) != 1:
+        raise ValueError("prequantized Sage output is incompatible")
+    _, _, osb, osh, osl = _layout_dims(output, tensor_layout)
+    q_scale = q_scale.contiguous()
+    k_scale = k_scale.contiguous()
+    with torch.cuda.device(v.device):
+        _lib.call(
+            "tu_sage_attn_fwd",
+            q_int8.data_ptr(), q_scale.data_ptr(), blkq, k_int8.data_ptr(), k_scale.data_ptr(), blkk,
+            v.data_ptr(), output.data_ptr(), batch, hq, hkv, lq, lk, KERNEL_HEAD_DIM,
+            qsb, qsh, qsl, ksb, ksh, ksl, vsb, vsh, vsl, osb, osh, osl,
+            scale, int(bool(is_causal)), _lib.stream_of(v.device),
+        )
+    return output
+
+
+def sageattn_from_prequantized(quantized: PrequantizedSageAttention) -> torch.Tensor:
+    out = sageattn_prequantized(
+        quantized.query_int8, quantized.query_scale, quantized.key_int8, quantized.key_scale, quantized.value,
+        tensor_layout=quantized.tensor_layout, is_causal=quantized.is_causal, sm_scale=quantized.sm_scale,
+        blkq=quantized.blkq, blkk=quantized.blkk,
+    )
+    out = out[..., : quantized.original_head_dim]
+    if quantized.output_dtype != torch.bfloat16:
+        out = out.to(quantized.output_dtype)
+    return out
+
+
+def sageattn(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    tensor_layout: str = "HND",
+    is_causal: bool = False,
+    sm_scale: Optional[float] = None,
+    smooth_k: bool = True,
+    BLKQ: int = 128,
+    BLKK: int = 128,
+) -> torch.Tensor:
+    """One-call Sage attention: K mean-smoothing, per-block INT8 Q/K, INT8 QK^T,
+    online softmax, bf16 PV.  Output has q's shape and dtype."""
+    quantized = prequantize_sageattn(
+        q, k, v, tensor_layout=tensor_layout, is_causal=is_causal, sm_scale=sm_scale,
+        smooth_k=smooth_k, BLKQ=BLKQ, BLKK=BLKK,
+    )
+    return sageattn_from_prequantized(quantized)

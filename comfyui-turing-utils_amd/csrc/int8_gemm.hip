@@ -1,0 +1,285 @@
+// INT8 x INT8 -> INT32 GEMM with the W8A8 epilogue, for gfx950.
+//
+// Contract (reference: turing_utils::int8_linear, kernel/csrc/turing/w4a8.cu
+// :1185-1219 with the CUTLASS EVT epilogue of :480-525):
+//   acc[m][n] = sum_k a[m][k] * w[n][k]            (exact int32)
+//   out[m][n] = bf16_rn(((float(acc) * as[m]) * ws[n]) + bias[n])
+// a and w are both K-contiguous ("TN"), so every MFMA operand is a 16-byte
+// contiguous load along K.
+//
+// MI355X mapping
+//   * Workgroup tile 256 (n) x 256 (m) x 64 (k), 4 wave64 in a 2 x 2 grid, each
+//     wave owning a 128 x 128 output tile = 8 x 8 v_mfma_i32_16x16x64_i8 per
+//     K step (256 accumulator registers, AGPR-resident).
+//   * The W tile is the MFMA A operand and the activation tile the B operand,
+//     so each lane ends with 4 consecutive output columns of one row: the
+//     epilogue issues one 8-byte store per 16 x 16 sub-tile.
+//   * LDS double buffer (2 x 32 KiB).  Rows are 64 B; the 16-byte chunk index
+//     is XOR-swizzled with row bits 2..3 so the 16 lanes that read one chunk
+//     column of 16 consecutive rows hit distinct banks.  Global loads for
+//     step k+1 are issued before the MFMAs of step k.
+//   * Tiles are renumbered so each XCD (workgroup id mod 8) owns a contiguous
+//     range, walked in groups of 8 m-tiles for L2 reuse of the A and W panels.
+#include "tu_common.h"
+
+namespace tu {
+namespace {
+
+constexpr int kBM = 256;  // activation rows per workgroup
+constexpr int kBN = 256;  // weight rows (output columns) per workgroup
+constexpr int kBK = 64;   // bytes of K per step
+constexpr int kThreads = 256;
+constexpr int kGroupM = 8;
+
+__device__ __forceinline__ int swz(int row, int chunk) { return row * kBK + ((chunk ^ ((row >> 2) & 3)) << 4); }
+
+struct TileLoad {
+    i32x4 a[4];
+    i32x4 w[4];
+};
+
+// Loads the 256 x 64 B activation and weight panels of step k0 into registers.
+// Rows past the end are clamped (their results are never stored); columns past
+// K are zero.
+__device__ __forceinline__ void load_tiles(TileLoad &t, const int8_t *__restrict__ a,
+                                           const int8_t *__restrict__ w, int64_t m0, int64_t n0,
+                                           int64_t m, int64_t n, int64_t k, int64_t k0, int tid) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int id = tid + kThreads * i;
+        const int row = id >> 2;
+        const int chunk = id & 3;
+        const int64_t kk = k0 + chunk * 16;
+        const int64_t ra = min(m0 + row, m - 1);
+        const int64_t rw = min(n0 + row, n - 1);
+        if (kk < k) {
+            t.a[i] = *reinterpret_cast<const i32x4 *>(a + ra * k + kk);
+            t.w[i] = *reinterpret_cast<const i32x4 *>(w + rw * k + kk);
+        } else {
+            t.a[i] = i32x4{0, 0, 0, 0};
+            t.w[i] = i32x4{0, 0, 0, 0};
+        }
+    }
+}
+
+__device__ __forceinline__ void store_tiles(const TileLoad &t, int8_t *lds_a, int8_t *lds_w, int tid) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int id = tid + kThreads * i;
+        const int row = id >> 2;
+        const int chunk = id & 3;
+        *reinterpret_cast<i32x4 *>(lds_a + swz(row, chunk)) = t.a[i];
+        *reinterpret_cast<i32x4 *>(lds_w + swz(row, chunk)) = t.w[i];
+    }
+}
+
+// Maps the linear workgroup id to (m-tile, n-tile): XCD-contiguous ranges,
+// grouped m-major inside each range.
+__device__ __forceinline__ void tile_coords(int bid, int tiles_m, int tiles_n, int &tm, int &tn) {
+    const int total = tiles_m * tiles_n;
+    const int q = total / 8, r = total % 8;
+    const int xcd = bid % 8, idx = bid / 8;
+    const int t = xcd < r ? xcd * (q + 1) + idx : r * (q + 1) + (xcd - r) * q + idx;
+    const int per_group = kGroupM * tiles_n;
+    const int group = t / per_group;
+    const int first_m = group * kGroupM;
+    const int gsm = min(tiles_m - first_m, kGroupM);
+    const int in_group = t % per_group;
+    tm = first_m + in_group % gsm;
+    tn = in_group / gsm;
+}
+
+template <bool kI32Out>
+__global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(
+    const int8_t *__restrict__ a, const int8_t *__restrict__ w, const float *__restrict__ as,
+    const float *__restrict__ ws, const float *__restrict__ bias, void *__restrict__ out,
+    int64_t m, int64_t n, int64_t k, int tiles_m, int tiles_n) {
+    __shared__ __align__(16) int8_t lds[2][2][kBM * kBK];  // [buffer][a|w][rows*64]
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wn = wave >> 1;  // which 128-row half of the W tile
+    const int wm = wave & 1;   // which 128-row half of the activation tile
+
+    int tm, tn;
+    tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+    const int64_t m0 = static_cast<int64_t>(tm) * kBM;
+    const int64_t n0 = static_cast<int64_t>(tn) * kBN;
+
+    i32x4 acc[8][8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[i][j] = i32x4{0, 0, 0, 0};
+
+    const int steps = static_cast<int>((k + kBK - 1) / kBK);
+    TileLoad t;
+    load_tiles(t, a, w, m0, n0, m, n, k, 0, tid);
+    store_tiles(t, lds[0][0], lds[0][1], tid);
+    __syncthreads();
+
+    const int frag_row = lane & 15;
+    const int frag_chunk = lane >> 4;
+
+    for (int s = 0; s < steps; ++s) {
+        const int cur = s & 1;
+        if (s + 1 < steps) load_tiles(t, a, w, m0, n0, m, n, k, static_cast<int64_t>(s + 1) * kBK, tid);
+
+        const int8_t *la = lds[cur][0];
+        const int8_t *lw = lds[cur][1];
+        i32x4 bfrag[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            bfrag[j] = *reinterpret_cast<const i32x4 *>(la + swz(wm * 128 + j * 16 + frag_row, frag_chunk));
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const i32x4 afrag =
+                *reinterpret_cast<const i32x4 *>(lw + swz(wn * 128 + i * 16 + frag_row, frag_chunk));
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(afrag, bfrag[j], acc[i][j], 0, 0, 0);
+        }
+
+        if (s + 1 < steps) store_tiles(t, lds[cur ^ 1][0], lds[cur ^ 1][1], tid);
+        __syncthreads();
+    }
+
+    // acc[i][j][r] = C[m = m0 + wm*128 + 16j + (lane & 15)]
+    //                  [n = n0 + wn*128 + 16i + 4*(lane >> 4) + r]
+    const int g = lane >> 4;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int64_t row = m0 + wm * 128 + j * 16 + (lane & 15);
+        if (row >= m) continue;
+        float arow = 0.0f;
+        if constexpr (!kI32Out) arow = as[row];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int64_t col = n0 + wn * 128 + i * 16 + 4 * g;
+            if (col >= n) continue;  // n % 8 == 0, so a group of 4 is all in or all out
+            if constexpr (kI32Out) {
+                *reinterpret_cast<i32x4 *>(static_cast<int32_t *>(out) + row * n + col) = acc[i][j];
+            } else {
+                const f32x4 wsv = *reinterpret_cast<const f32x4 *>(ws + col);
+                f32x4 bv = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                if (bias) bv = *reinterpret_cast<const f32x4 *>(bias + col);
+                float v[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    float x = static_cast<float>(acc[i][j][r]);
+                    x = x * arow;
+                    x = x * wsv[r];
+                    if (bias) x = x + bv[r];
+                    v[r] = x;
+                }
+                u32x2 packed;
+                packed.x = pack_bf16x2(v[0], v[1]);
+                packed.y = pack_bf16x2(v[2], v[3]);
+                *reinterpret_cast<u32x2 *>(static_cast<uint16_t *>(out) + row * n + col) = packed;
+            }
+        }
+    }
+}
+
+// out[m][c] = bf16_rn((float(acc[m*ld + c]) * as[m]) * ws[c or 0]),
+// bf16_epilogue.cu:46-143.  Each thread converts 4 consecutive columns when
+// the row width allows, else one.
+template <bool kScalarWs, bool kVec4>
+__global__ __launch_bounds__(256) void dequant_kernel(const int32_t *__restrict__ acc, int64_t ld,
+                                                      const float *__restrict__ as,
+                                                      const float *__restrict__ ws,
+                                                      uint16_t *__restrict__ out, int64_t m,
+                                                      int64_t cols) {
+    const int64_t per_row = kVec4 ? cols / 4 : cols;
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (idx >= m * per_row) return;
+    const int64_t row = idx / per_row;
+    const int64_t c = (idx - row * per_row) * (kVec4 ? 4 : 1);
+    const float xs = as[row];
+    if constexpr (kVec4) {
+        const i32x4 v = *reinterpret_cast<const i32x4 *>(acc + row * ld + c);
+        float r[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) r[e] = (static_cast<float>(v[e]) * xs) * ws[kScalarWs ? 0 : c + e];
+        u32x2 p;
+        p.x = pack_bf16x2(r[0], r[1]);
+        p.y = pack_bf16x2(r[2], r[3]);
+        *reinterpret_cast<u32x2 *>(out + row * cols + c) = p;
+    } else {
+        const float r = (static_cast<float>(acc[row * ld + c]) * xs) * ws[kScalarWs ? 0 : c];
+        out[row * cols + c] = static_cast<uint16_t>(bf16_rne_bits(r));
+    }
+}
+
+int32_t check_gemm_args(const int8_t *a, const int8_t *w, const void *out, int64_t m, int64_t n,
+                        int64_t k) {
+    TU_REQUIRE(m >= 0 && n > 0 && k > 0, "INT8 GEMM dimensions must be positive (m=%lld n=%lld k=%lld)",
+               static_cast<long long>(m), static_cast<long long>(n), static_cast<long long>(k));
+    TU_REQUIRE(k % 16 == 0 && n % 8 == 0, "INT8 GEMM requires K%%16==0 and N%%8==0 (K=%lld N=%lld)",
+               static_cast<long long>(k), static_cast<long long>(n));
+    TU_REQUIRE(k < 131072, "INT8 GEMM K=%lld would overflow the int32 accumulator", static_cast<long long>(k));
+    TU_REQUIRE((m + kBM - 1) / kBM * ((n + kBN - 1) / kBN) < 0x7fffffff, "INT8 GEMM grid too large");
+    TU_REQUIRE(a && w && out, "INT8 GEMM pointers must be non-null");
+    TU_REQUIRE((reinterpret_cast<uintptr_t>(a) & 15) == 0 && (reinterpret_cast<uintptr_t>(w) & 15) == 0,
+               "INT8 GEMM operands must be 16-byte aligned");
+    TU_REQUIRE((reinterpret_cast<uintptr_t>(out) & 15) == 0, "INT8 GEMM output must be 16-byte aligned");
+    return require_gfx950();
+}
+
+template <bool kI32Out>
+int32_t launch_gemm(const int8_t *a, const int8_t *w, const float *as, const float *ws, const float *bias,
+                    void *out, int64_t m, int64_t n, int64_t k, void *stream) {
+    if (m == 0) return 0;
+    const int tiles_m = static_cast<int>((m + kBM - 1) / kBM);
+    const int tiles_n = static_cast<int>((n + kBN - 1) / kBN);
+    int8_gemm_kernel<kI32Out><<<dim3(tiles_m * tiles_n), kThreads, 0, static_cast<hipStream_t>(stream)>>>(
+        a, w, as, ws, bias, out, m, n, k, tiles_m, tiles_n);
+    return check_launch(kI32Out ? "tu_int8_gemm_i32" : "tu_int8_gemm_bf16");
+}
+
+}  // namespace
+}  // namespace tu
+
+extern "C" int32_t tu_int8_gemm_bf16(const int8_t *a, const int8_t *w, const float *a_scale,
+                                     const float *w_scale, const float *bias, void *out_bf16, int64_t m,
+                                     int64_t n, int64_t k, void *stream) {
+    using namespace tu;
+    if (check_gemm_args(a, w, out_bf16, m, n, k)) return -1;
+    TU_REQUIRE(a_scale && w_scale, "INT8 GEMM scales must be non-null");
+    TU_REQUIRE((reinterpret_cast<uintptr_t>(w_scale) & 15) == 0 && (reinterpret_cast<uintptr_t>(bias) & 15) == 0,
+               "INT8 GEMM weight scale and bias must be 16-byte aligned");
+    return launch_gemm<false>(a, w, a_scale, w_scale, bias, out_bf16, m, n, k, stream);
+}
+
+extern "C" int32_t tu_int8_gemm_i32(const int8_t *a, const int8_t *w, int32_t *acc, int64_t m, int64_t n,
+                                    int64_t k, void *stream) {
+    using namespace tu;
+    if (check_gemm_args(a, w, acc, m, n, k)) return -1;
+    return launch_gemm<true>(a, w, nullptr, nullptr, nullptr, acc, m, n, k, stream);
+}
+
+extern "C" int32_t tu_dequant_i32_bf16(const int32_t *acc, int64_t acc_ld, const float *a_scale,
+                                       const float *w_scale, int32_t ws_scalar, void *out_bf16, int64_t m,
+                                       int64_t cols, void *stream) {
+    using namespace tu;
+    TU_REQUIRE(m >= 0 && cols > 0 && acc_ld >= cols, "dequantize: need rows >= 0 and 0 < cols <= acc_ld");
+    TU_REQUIRE(acc && a_scale && w_scale && out_bf16, "dequantize pointers must be non-null");
+    if (require_gfx950()) return -1;
+    if (m == 0) return 0;
+    const bool vec4 = cols % 4 == 0 && acc_ld % 4 == 0 && (reinterpret_cast<uintptr_t>(acc) & 15) == 0 &&
+                      (reinterpret_cast<uintptr_t>(out_bf16) & 7) == 0;
+    const int64_t work = m * (vec4 ? cols / 4 : cols);
+    TU_REQUIRE((work + 255) / 256 < 0x7fffffff, "dequantize grid too large");
+    const dim3 grid(static_cast<unsigned>((work + 255) / 256));
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    auto *o = static_cast<uint16_t *>(out_bf16);
+    if (ws_scalar) {
+        if (vec4) dequant_kernel<true, true><<<grid, 256, 0, s>>>(acc, acc_ld, a_scale, w_scale, o, m, cols);
+        else dequant_kernel<true, false><<<grid, 256, 0, s>>>(acc, acc_ld, a_scale, w_scale, o, m, cols);
+    } else {
+        if (vec4) dequant_kernel<false, true><<<grid, 256, 0, s>>>(acc, acc_ld, a_scale, w_scale, o, m, cols);
+        else dequant_kernel<false, false><<<grid, 256, 0, s>>>(acc, acc_ld, a_scale, w_scale, o, m, cols);
+    }
+    return check_launch("tu_dequant_i32_bf16");
+}

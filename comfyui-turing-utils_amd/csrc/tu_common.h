@@ -1,0 +1,62 @@
+// Shared device/host helpers for the gfx950 kernels of libtu_hip.so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "../../include/tu_hip.h"
+
+namespace tu {
+
+// ---------------------------------------------------------------------------
+// Host-side error reporting: every C entry point returns 0 or sets a message
+// retrievable through tu_last_error() on the calling thread.
+// ---------------------------------------------------------------------------
+void set_error(const std::string &msg);
+int32_t fail(const char *fmt, ...) __attribute__((format(printf, 1, 2)));
+int32_t check_launch(const char *what);
+// Returns 0 if the current device is gfx950, otherwise sets an error.
+int32_t require_gfx950();
+
+#define TU_REQUIRE(cond, ...)          \
+    do {                               \
+        if (!(cond)) return tu::fail(__VA_ARGS__); \
+    } while (0)
+
+// ---------------------------------------------------------------------------
+// Vector types for MFMA operands.
+// ---------------------------------------------------------------------------
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------------------
+// bf16 <-> fp32.  Round-to-nearest-even with a canonical NaN (0x7fff), the
+// conversion of kernel/csrc/turing/convrot_quant.cu:293-305.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t bf16_rne_bits(float v) {
+    const uint32_t bits = __float_as_uint(v);
+    if ((bits & 0x7fffffffu) > 0x7f800000u) return 0x7fffu;
+    // bits + 0x7fff + lsb, then truncate: RNE for finite values (no overflow
+    // past inf: the largest finite fp32 rounds to bf16 inf as RNE requires).
+    const uint32_t lsb = (bits >> 16) & 1u;
+    return (bits + 0x7fffu + lsb) >> 16;
+}
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
+
+__device__ __forceinline__ float bf16_round(float v) { return bf16_bits_to_f32(bf16_rne_bits(v)); }
+
+// Packs two floats to two bf16 (low = a) with the same rounding.
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+    return bf16_rne_bits(a) | (bf16_rne_bits(b) << 16);
+}
+
+}  // namespace tu

@@ -1,0 +1,142 @@
+/*
+ * tu_hip.h -- C ABI of the MI355X (gfx950) kernels for the quantized DiT hot
+ * path of comfyui-turing-utils: ConvRot W8A8 linear and Sage INT8 attention.
+ *
+ * Library: libtu_hip.so (comfyui-turing-utils_amd/comfyui_turing_utils_kernel/).
+ *
+ * Conventions
+ *   - Every pointer is a device pointer on the current HIP device, except
+ *     where noted.  bf16 tensors are passed as `const void *` holding IEEE
+ *     bfloat16 bit patterns.
+ *   - `stream` is a hipStream_t (NULL = the legacy default stream).  Work is
+ *     enqueued asynchronously; nothing synchronises.
+ *   - The return value is 0 on success.  A non-zero value means nothing was
+ *     launched (argument or device check failed) or the launch failed; the
+ *     message is available from tu_last_error() on the same host thread.
+ *   - Strides are in elements.  The innermost (channel) dimension must be
+ *     contiguous.
+ *   - No entry point allocates device memory: outputs and scratch are
+ *     provided by the caller.
+ *
+ * Each entry point names the reference interface it replaces.  Paths are
+ * relative to the reference tree.
+ */
+#ifndef TU_HIP_H_
+#define TU_HIP_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status / introspection ------------------------------------------------- */
+
+/* Message of the last failed call on this host thread ("" if none). */
+const char *tu_last_error(void);
+
+/* ABI version of this library (bumped on any signature change). */
+int32_t tu_abi_version(void);
+
+/* 1 if `device` is a gfx950 (MI355X-class) GPU this library was built for,
+ * 0 otherwise; negative on a HIP error.  Replaces the sm75 predicate
+ * comfyui_turing_utils/hardware.py:24-32. */
+int32_t tu_device_supported(int32_t device);
+
+/* ConvRot INT8 activation quantizer -------------------------------------- */
+
+/* Rotates each row of x by the block-Hadamard ConvRot transform (group 128
+ * or 256), then quantizes per row to symmetric INT8:
+ *   scale[r] = max(min(absmax_r, 3.38953139e38) / 127, 1e-30)
+ *   q[r][c]  = clamp(rne(bf16(bf16(y[r][c]) / bf16(scale[r]))), -128, 127)
+ * x: bf16 [rows, cols] (act 0) or [rows, 2*cols] (act 2, SwiGLU over the
+ * [gate | up] halves), row-major contiguous.  q: int8 [rows, cols];
+ * scale: fp32 [rows].  cols % group == 0.
+ * act: 0 none, 2 SwiGLU.  (1, tanh-GELU, is reserved and rejected.)
+ * Replaces turing_utils::bf16_int8_convrot_quantize
+ * (kernel/comfyui_turing_utils_kernel/ops.py:257-282 ->
+ *  kernel/csrc/bindings.cpp:603-646 -> kernel/csrc/turing/convrot_quant.cu:566-589). */
+int32_t tu_convrot_quant_i8(const void *x_bf16, int8_t *q, float *scale, int64_t rows,
+                            int64_t cols, int32_t group, int32_t act, void *stream);
+
+/* INT8 GEMM ---------------------------------------------------------------- */
+
+/* out[m][n] = bf16_rn(((float(acc) * a_scale[m]) * w_scale[n]) + bias[n]),
+ * acc[m][n] = sum_k a[m][k] * w[n][k] (exact int32).
+ * a: int8 [m, k] row-major; w: int8 [n, k] row-major; a_scale: fp32 [m];
+ * w_scale: fp32 [n]; bias: fp32 [n] or NULL; out: bf16 [m, n] row-major.
+ * Requires k % 16 == 0 and n % 8 == 0 (the reference's constraint).
+ * Replaces turing_utils::int8_linear (ops.py:96-126 -> bindings.cpp:371-421
+ * -> kernel/csrc/turing/w4a8.cu:1185-1219). */
+int32_t tu_int8_gemm_bf16(const int8_t *a, const int8_t *w, const float *a_scale,
+                          const float *w_scale, const float *bias, void *out_bf16, int64_t m,
+                          int64_t n, int64_t k, void *stream);
+
+/* acc[m][n] = sum_k a[m][k] * w[n][k] as int32, row-major [m, n].  Same
+ * kernel as tu_int8_gemm_bf16 with the epilogue replaced by an int32 store;
+ * the accumulator half of the reference's cuBLAS INT8 + epilogue split
+ * (comfyui_turing_utils/quantization/dispatch.py:481-535). */
+int32_t tu_int8_gemm_i32(const int8_t *a, const int8_t *w, int32_t *acc, int64_t m, int64_t n,
+                         int64_t k, void *stream);
+
+/* out[m][n] = bf16_rn((float(acc[m*acc_ld + n]) * a_scale[m]) * w_scale[ws_scalar ? 0 : n])
+ * for n < cols.  Replaces turing_utils::dequantize_int8_bf16 (ops.py:129-160
+ * -> bindings.cpp:423-472 -> kernel/csrc/turing/bf16_epilogue.cu:147-218). */
+int32_t tu_dequant_i32_bf16(const int32_t *acc, int64_t acc_ld, const float *a_scale,
+                            const float *w_scale, int32_t ws_scalar, void *out_bf16, int64_t m,
+                            int64_t cols, void *stream);
+
+/* Sage attention: Q/K quantization ---------------------------------------- */
+
+/* Per-(batch, head) channel mean of K over the sequence, rounded to bf16,
+ * with a fixed fp32 summation order (128-token chunks; see the oracle
+ * or_sage_kmean).  k: bf16, element strides (s_b, s_h, s_l), channels
+ * contiguous; dim in {64, 128}.  chunk_sums: fp32 scratch of
+ * batch*heads*ceil(len/128)*dim elements.  mean: bf16 [batch, heads, dim].
+ * Smoothing is the `sub_mean` path of QuantInt8Kernel
+ * (kernel/csrc/turing/sage/fused.cu:93-128); the reference does not ship a
+ * mean kernel (its production path disables smoothing, turing_sage/core.py:421). */
+int32_t tu_sage_kmean(const void *k_bf16, int64_t batch, int64_t heads, int64_t len,
+                      int64_t dim, int64_t s_b, int64_t s_h, int64_t s_l, float *chunk_sums,
+                      void *mean_bf16, void *stream);
+
+/* Per-block symmetric INT8 quantization of Q or K, optionally after
+ * subtracting a per-(batch, head) channel mean (K smoothing):
+ *   amax = max(1e-7, max |x - mean| over blk tokens x dim channels)
+ *   scale[b][h][t / blk] = amax / 127;  q = sat_rne_s8((x - mean) * (127 / amax))
+ * x: bf16 strides (s_b, s_h, s_l); q: int8 strides (q_b, q_h, q_l);
+ * scale: fp32 [batch, heads, ceil(len / blk)]; mean: bf16 [batch, heads, dim]
+ * or NULL.  blk in {16, 32, 64, 128}; dim in {64, 128}.
+ * Replaces quant_per_block_int8_cuda / quant_per_warp_int8_cuda
+ * (kernel/csrc/turing/sage/fused.cu:899-1068, QuantInt8Kernel :66-200). */
+int32_t tu_sage_quant(const void *x_bf16, const void *mean_bf16, int64_t batch, int64_t heads,
+                      int64_t len, int64_t dim, int64_t s_b, int64_t s_h, int64_t s_l,
+                      int64_t blk, int8_t *q, int64_t q_b, int64_t q_h, int64_t q_l,
+                      float *scale, void *stream);
+
+/* Sage attention: forward --------------------------------------------------- */
+
+/* O = softmax(Q K^T * sm_scale) V on INT8 Q/K and bf16 V:
+ *   s = float(q8 . k8) * q_scale[row / blkq] * k_scale[key / blkk] * sm_scale
+ *   online softmax in base 2, P rounded to bf16, O accumulated in fp32 by
+ *   bf16 MFMA, O / rowsum(P) stored as bf16.
+ * q8: int8 [batch, hq, lq, dim] addressed by strides (q_sb, q_sh, q_sl);
+ * k8: int8, v: bf16, o: bf16 likewise (kv heads hkv, hq % hkv == 0, GQA).
+ * q_scale: fp32 [batch, hq, ceil(lq/blkq)]; k_scale: fp32 [batch, hkv, ceil(lk/blkk)].
+ * dim == 128; blkq >= 1; blkk % 64 == 0.  causal: top-left aligned.
+ * Replaces qk_int8_sv_f16_accum_f32_attn
+ * (kernel/csrc/turing/sage/qk_int_sv_f16_cuda_sm75.cu:984-1123), the kernel
+ * behind turing_utils::sage_attention (turing_sage/custom_ops.py:137-168). */
+int32_t tu_sage_attn_fwd(const int8_t *q8, const float *q_scale, int64_t blkq, const int8_t *k8,
+                         const float *k_scale, int64_t blkk, const void *v_bf16, void *o_bf16,
+                         int64_t batch, int64_t hq, int64_t hkv, int64_t lq, int64_t lk,
+                         int64_t dim, int64_t q_sb, int64_t q_sh, int64_t q_sl, int64_t k_sb,
+                         int64_t k_sh, int64_t k_sl, int64_t v_sb, int64_t v_sh, int64_t v_sl,
+                         int64_t o_sb, int64_t o_sh, int64_t o_sl, float sm_scale, int32_t causal,
+                         void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TU_HIP_H_ */

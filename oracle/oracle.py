@@ -1,0 +1,208 @@
+"""numpy/ctypes front end of the C oracle (oracle/tu_oracle.c).
+
+TEST INFRASTRUCTURE ONLY: a CPU restatement of the reference's arithmetic used
+to check the HIP kernels.  Only tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg may import it.  See tu_oracle.c for the reference citations
+and for how each function is pinned.
+
+bf16 tensors cross this interface as numpy uint16 bit patterns.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+import threading
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+_lock = threading.Lock()
+_lib = None
+
+_p = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int
+
+
+def build() -> str:
+    """Compiles liboracle.so with the committed Makefile (gcc)."""
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+    return LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                build()
+            L = ctypes.CDLL(LIB_PATH)
+            L.or_f32_to_bf16_rne.restype = ctypes.c_uint16
+            L.or_f32_to_bf16_rne.argtypes = [ctypes.c_float]
+            L.or_bf16_to_f32.restype = ctypes.c_float
+            L.or_bf16_to_f32.argtypes = [ctypes.c_uint16]
+            L.or_f32_to_bf16_n.restype = None
+            L.or_f32_to_bf16_n.argtypes = [_p, _p, _i64]
+            L.or_convrot_rotate_group.restype = _i32
+            L.or_convrot_rotate_group.argtypes = [_p, _p, _i32]
+            L.or_convrot_quant_i8.restype = _i32
+            L.or_convrot_quant_i8.argtypes = [_p, _i64, _i64, _i32, _i32, _i32, _p, _p]
+            L.or_div_markstein_f32.restype = ctypes.c_float
+            L.or_div_markstein_f32.argtypes = [ctypes.c_float, ctypes.c_float]
+            L.or_check_markstein_quant.restype = _i64
+            L.or_check_markstein_quant.argtypes = [_p, _p]
+            L.or_int8_gemm_i32.restype = _i32
+            L.or_int8_gemm_i32.argtypes = [_p, _p, _i64, _i64, _i64, _p]
+            L.or_int8_epilogue_bf16.restype = _i32
+            L.or_int8_epilogue_bf16.argtypes = [_p, _i64, _p, _p, _i32, _p, _i64, _i64, _p]
+            L.or_sage_kmean.restype = _i32
+            L.or_sage_kmean.argtypes = [_p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p]
+            L.or_sage_quant.restype = _i32
+            L.or_sage_quant.argtypes = [_p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                                        _p, _i64, _i64, _i64, _p]
+            L.or_sage_attn_rows.restype = _i32
+            L.or_sage_attn_rows.argtypes = [_p, _i64, _i64, _i64, _p, _i64,
+                                            _p, _i64, _i64, _i64, _p, _i64,
+                                            _p, _i64, _i64, _i64,
+                                            _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _i32, _i32,
+                                            _p, _i64, _p]
+            _lib = L
+    return _lib
+
+
+def _ptr(a: np.ndarray) -> int:
+    return a.ctypes.data
+
+
+def _check(status: int, what: str) -> None:
+    if status != 0:
+        raise ValueError(f"oracle {what} rejected its arguments (status {status})")
+
+
+# --- bf16 ------------------------------------------------------------------
+
+def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.uint16)
+    lib().or_f32_to_bf16_n(_ptr(x), _ptr(out), x.size)
+    return out
+
+
+def bf16_bits_to_f32(b: np.ndarray) -> np.ndarray:
+    return (np.ascontiguousarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+# --- ConvRot ---------------------------------------------------------------
+
+def rotate_group(x: np.ndarray, group: int) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    assert x.shape == (group,)
+    y = np.empty(group, dtype=np.float32)
+    _check(lib().or_convrot_rotate_group(_ptr(x), _ptr(y), group), "rotate_group")
+    return y
+
+
+def convrot_quant(x_bits: np.ndarray, group: int, staged: bool = False) -> tuple[np.ndarray, np.ndarray]:
+    """(int8 codes [M, K], fp32 scales [M]) of the row-buffer quantizer."""
+    x_bits = np.ascontiguousarray(x_bits, dtype=np.uint16)
+    m, k = x_bits.shape
+    q = np.empty((m, k), dtype=np.int8)
+    s = np.empty(m, dtype=np.float32)
+    _check(lib().or_convrot_quant_i8(_ptr(x_bits), m, k, group, 0, int(staged), _ptr(q), _ptr(s)), "convrot_quant")
+    return q, s
+
+
+def div_markstein(a: float, b: float) -> float:
+    return lib().or_div_markstein_f32(a, b)
+
+
+def check_markstein_quant() -> tuple[int, int, int]:
+    """(code mismatches, pairs checked, fp32 quotient mismatches)."""
+    pairs = ctypes.c_int64(0)
+    fp32 = ctypes.c_int64(0)
+    bad = lib().or_check_markstein_quant(ctypes.byref(pairs), ctypes.byref(fp32))
+    return int(bad), int(pairs.value), int(fp32.value)
+
+
+# --- GEMM ------------------------------------------------------------------
+
+def int8_gemm_i32(a: np.ndarray, w: np.ndarray) -> np.ndarray:
+    a = np.ascontiguousarray(a, dtype=np.int8)
+    w = np.ascontiguousarray(w, dtype=np.int8)
+    m, k = a.shape
+    n = w.shape[0]
+    assert w.shape[1] == k
+    acc = np.empty((m, n), dtype=np.int32)
+    _check(lib().or_int8_gemm_i32(_ptr(a), _ptr(w), m, n, k, _ptr(acc)), "int8_gemm_i32")
+    return acc
+
+
+def epilogue_bf16(acc: np.ndarray, a_scale: np.ndarray, w_scale: np.ndarray,
+                  bias: np.ndarray | None = None, cols: int | None = None) -> np.ndarray:
+    """bf16 bits [M, cols] of bf16_rn(((acc * as) * ws) + bias)."""
+    acc = np.ascontiguousarray(acc, dtype=np.int32)
+    m, ld = acc.shape
+    cols = ld if cols is None else cols
+    a_scale = np.ascontiguousarray(a_scale, dtype=np.float32).reshape(-1)
+    w_scale = np.ascontiguousarray(w_scale, dtype=np.float32).reshape(-1)
+    scalar = int(w_scale.size == 1)
+    b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32).reshape(-1)
+    out = np.empty((m, cols), dtype=np.uint16)
+    _check(lib().or_int8_epilogue_bf16(_ptr(acc), ld, _ptr(a_scale), _ptr(w_scale), scalar,
+                                       None if b is None else _ptr(b), m, cols, _ptr(out)), "epilogue")
+    return out
+
+
+# --- Sage --------------------------------------------------------------------
+
+def _hnd(x: np.ndarray) -> tuple[int, int, int, int, int, int, int]:
+    b, h, l, d = x.shape
+    return b, h, l, d, h * l * d, l * d, d
+
+
+def sage_kmean(k_bits: np.ndarray) -> np.ndarray:
+    """bf16 bits [B, H, D] of the K channel mean; k is HND [B, H, L, D]."""
+    k_bits = np.ascontiguousarray(k_bits, dtype=np.uint16)
+    b, h, l, d, sb, sh, sl = _hnd(k_bits)
+    mean = np.empty((b, h, d), dtype=np.uint16)
+    _check(lib().or_sage_kmean(_ptr(k_bits), b, h, l, d, sb, sh, sl, _ptr(mean)), "sage_kmean")
+    return mean
+
+
+def sage_quant(x_bits: np.ndarray, blk: int, mean_bits: np.ndarray | None = None) -> tuple[np.ndarray, np.ndarray]:
+    """(int8 codes HND, fp32 scales [B, H, ceil(L/blk)]) for HND x."""
+    x_bits = np.ascontiguousarray(x_bits, dtype=np.uint16)
+    b, h, l, d, sb, sh, sl = _hnd(x_bits)
+    q = np.empty(x_bits.shape, dtype=np.int8)
+    s = np.empty((b, h, (l + blk - 1) // blk), dtype=np.float32)
+    mean = None if mean_bits is None else np.ascontiguousarray(mean_bits, dtype=np.uint16)
+    _check(lib().or_sage_quant(_ptr(x_bits), None if mean is None else _ptr(mean), b, h, l, d, sb, sh, sl, blk,
+                               _ptr(q), sb, sh, sl, _ptr(s)), "sage_quant")
+    return q, s
+
+
+def sage_attn_rows(q8: np.ndarray, qs: np.ndarray, blkq: int, k8: np.ndarray, ks: np.ndarray, blkk: int,
+                   v_bits: np.ndarray, sm_scale: float, rows: np.ndarray, causal: bool = False,
+                   p_bf16: bool = True) -> np.ndarray:
+    """fp32 [len(rows), D] attention outputs for (b, h, i) rows; HND inputs."""
+    q8 = np.ascontiguousarray(q8, dtype=np.int8)
+    k8 = np.ascontiguousarray(k8, dtype=np.int8)
+    v_bits = np.ascontiguousarray(v_bits, dtype=np.uint16)
+    qs = np.ascontiguousarray(qs, dtype=np.float32)
+    ks = np.ascontiguousarray(ks, dtype=np.float32)
+    rows = np.ascontiguousarray(rows, dtype=np.int64).reshape(-1, 3)
+    b, hq, lq, d, qsb, qsh, qsl = _hnd(q8)
+    _, hkv, lk, _, ksb, ksh, ksl = _hnd(k8)
+    _, _, _, _, vsb, vsh, vsl = _hnd(v_bits)
+    out = np.empty((rows.shape[0], d), dtype=np.float32)
+    _check(lib().or_sage_attn_rows(_ptr(q8), qsb, qsh, qsl, _ptr(qs), blkq,
+                                   _ptr(k8), ksb, ksh, ksl, _ptr(ks), blkk,
+                                   _ptr(v_bits), vsb, vsh, vsl,
+                                   hq, hkv, lq, lk, d, sm_scale, int(causal), int(p_bf16),
+                                   _ptr(rows), rows.shape[0], _ptr(out)), "sage_attn_rows")
+    return out

@@ -1,0 +1,435 @@
+/*
+ * CPU oracle for the quantized DiT hot path (ConvRot W8A8 linear + Sage INT8
+ * attention).
+ *
+ * TEST INFRASTRUCTURE ONLY.  This file is a plain-C restatement of the
+ * reference plugin's arithmetic, used as the checker for the HIP kernels.
+ * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
+ * load it.  The product path (comfyui-turing-utils_amd/) never calls it.
+ *
+ * Build: oracle/Makefile (gcc -O2 -fno-fast-math -ffp-contract=off).  IEEE
+ * fp32 arithmetic without contraction is what makes the restatement bit-exact
+ * for the integer outputs (codes, accumulators).
+ *
+ * Citations are to files under the reference tree
+ * (brahianrosswill/comfyui-turing-utils).
+ *
+ * Parity status per function (how each is pinned is in tests/test_oracle_*.py):
+ *   or_f32_to_bf16_rne        pinned: exhaustive-ish vs torch.bfloat16 cast
+ *   or_convrot_rotate_group   pinned: dense Kronecker matrix (fp64), orthogonality,
+ *                             involution, basis columns, regular-row property
+ *   or_convrot_quant_i8       pinned: invariants + staged==row-buffer KAT
+ *   or_div_markstein_f32      pinned: exhaustive over the quantizer's bf16 domain
+ *                             vs IEEE division (or_check_markstein_quant)
+ *   or_int8_gemm_i32          pinned: numpy int64 matmul (brute force)
+ *   or_int8_epilogue_bf16     pinned: fp64 closed form within bf16 rounding
+ *   or_sage_kmean             pinned: fp64 mean within one bf16 ulp
+ *   or_sage_quant             pinned: invariants (max|q|==127, dequant error)
+ *   or_sage_attn_rows         pinned: fp64 SDPA on dequantized inputs, torch SDPA
+ *                             on raw inputs (reference gate rtol .08 / atol .06)
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define OR_API __attribute__((visibility("default")))
+
+/* ------------------------------------------------------------------------ */
+/* bf16 helpers: convrot_quant.cu:293-309 (same in bf16_epilogue.cu:25-39).   */
+/* ------------------------------------------------------------------------ */
+static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+OR_API uint16_t or_f32_to_bf16_rne(float value) {
+    const uint32_t bits = f2u(value);
+    if ((bits & 0x7fffffffU) > 0x7f800000U) return 0x7fffU; /* canonical NaN */
+    uint16_t upper = (uint16_t)(bits >> 16);
+    const uint32_t rem = bits << 16;
+    if (rem > 0x80000000U || (rem == 0x80000000U && (upper & 1U))) ++upper;
+    return upper;
+}
+
+OR_API float or_bf16_to_f32(uint16_t v) { return u2f((uint32_t)v << 16); }
+
+static inline float bf16_round_f32(float v) { return or_bf16_to_f32(or_f32_to_bf16_rne(v)); }
+
+OR_API void or_f32_to_bf16_n(const float *x, uint16_t *out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = or_f32_to_bf16_rne(x[i]);
+}
+
+/* ------------------------------------------------------------------------ */
+/* ConvRot rotation.                                                         */
+/*                                                                           */
+/* G=256 (reference): R4 (x) R4 (x) R4 (x) R4 with                            */
+/*   R4 = 1/2 [[1,1,1,-1],[1,1,-1,1],[1,-1,1,1],[-1,1,1,1]],                  */
+/* applied digit by digit, stride 1 -> 4 -> 16 -> 64                          */
+/* (convrot_quant.cu:104-116 fht_stage, :311-330 last stage, :384-391 first  */
+/* stage inline).  Exact fp32 add order of each output:                      */
+/*   y0 = 0.5*(((x0+x1)+x2)-x3)   y1 = 0.5*(((x0+x1)-x2)+x3)                  */
+/*   y2 = 0.5*(((x0-x1)+x2)+x3)   y3 = 0.5*(((-x0+x1)+x2)+x3)                 */
+/*                                                                           */
+/* G=128 (build-defined; the reference supports only 256 and no regular      */
+/* Hadamard matrix of order 128 exists): R4 (x) R4 (x) R4 on digits of stride */
+/* 1, 4, 16, then the orthonormal H2 = (1/sqrt2)[[1,1],[1,-1]] on the stride- */
+/* 64 digit: y0 = c*(x0+x1), y1 = c*(x0-x1), c = fp32(1/sqrt(2)).             */
+/* ------------------------------------------------------------------------ */
+static const float kInvSqrt2 = 0.70710678118654752440f;
+
+static void r4_stage(const float *src, float *dst, int stride, int group) {
+    for (int lane = 0; lane < group / 4; ++lane) {
+        const int base = (lane % stride) + (lane / stride) * (4 * stride);
+        const float x0 = src[base];
+        const float x1 = src[base + stride];
+        const float x2 = src[base + 2 * stride];
+        const float x3 = src[base + 3 * stride];
+        dst[base] = 0.5f * (((x0 + x1) + x2) - x3);
+        dst[base + stride] = 0.5f * (((x0 + x1) - x2) + x3);
+        dst[base + 2 * stride] = 0.5f * (((x0 - x1) + x2) + x3);
+        dst[base + 3 * stride] = 0.5f * (((-x0 + x1) + x2) + x3);
+    }
+}
+
+static void h2_stage(const float *src, float *dst, int stride, int group) {
+    for (int lane = 0; lane < group / 2; ++lane) {
+        const int base = (lane % stride) + (lane / stride) * (2 * stride);
+        const float x0 = src[base];
+        const float x1 = src[base + stride];
+        dst[base] = kInvSqrt2 * (x0 + x1);
+        dst[base + stride] = kInvSqrt2 * (x0 - x1);
+    }
+}
+
+/* y = rotation(x) for one group, fp32 (before any bf16 rounding). */
+OR_API int or_convrot_rotate_group(const float *x, float *y, int group) {
+    float a[256], b[256];
+    if (group != 128 && group != 256) return -1;
+    r4_stage(x, a, 1, group);
+    r4_stage(a, b, 4, group);
+    r4_stage(b, a, 16, group);
+    if (group == 256) r4_stage(a, y, 64, group);
+    else h2_stage(a, y, 64, group);
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Input activations folded into the quantizer (convrot_quant.cu:137-156).   */
+/* act 0: none; 2: SwiGLU over [gate | up] halves of a 2K-wide row.          */
+/* (act 1, tanh-GELU, is not restated here: its tanhf is a libm call whose    */
+/* last-ulp behaviour differs between libraries.)                            */
+/* ------------------------------------------------------------------------ */
+static inline float load_act(const uint16_t *row, int64_t col, int64_t k, int act) {
+    if (act == 2) {
+        const float gate = or_bf16_to_f32(row[col]);
+        const float up = or_bf16_to_f32(row[k + col]);
+        return (gate / (1.0f + expf(-gate))) * up;
+    }
+    return or_bf16_to_f32(row[col]);
+}
+
+/* ------------------------------------------------------------------------ */
+/* Row-buffer ConvRot INT8 quantizer: convrot_quant.cu:350-444 (Int4=false). */
+/*   absmax over fp32 y of the whole row (:400-404)                           */
+/*   scale  = max(min(absmax, 3.38953139e38) / 127, 1e-30)   (:408-412)       */
+/*   rs     = bf16(scale)                                     (:417)          */
+/*   q      = clamp(nearbyint(bf16(bf16(y) / rs)), -128, 127) (:431-441)      */
+/* scales[row] keeps the unrounded fp32 scale (:413-415).                     */
+/* staged != 0 selects the staged formulation's scale, absmax*(1/127)        */
+/* (convrot_quant.cu:233-236), the reference's own cross-check partner.      */
+/* ------------------------------------------------------------------------ */
+OR_API int or_convrot_quant_i8(const uint16_t *x, int64_t rows, int64_t k, int group, int act,
+                               int staged, int8_t *q, float *scales) {
+    if ((group != 128 && group != 256) || k <= 0 || k % group) return -1;
+    const int64_t in_width = act == 2 ? 2 * k : k;
+    uint16_t *buf = (uint16_t *)malloc((size_t)k * sizeof(uint16_t));
+    if (!buf) return -2;
+    for (int64_t r = 0; r < rows; ++r) {
+        const uint16_t *row = x + r * in_width;
+        float absmax = 0.0f;
+        for (int64_t g = 0; g < k / group; ++g) {
+            float xin[256], y[256];
+            for (int i = 0; i < group; ++i) xin[i] = load_act(row, g * group + i, k, act);
+            or_convrot_rotate_group(xin, y, group);
+            for (int i = 0; i < group; ++i) {
+                absmax = fmaxf(absmax, fabsf(y[i]));
+                buf[g * group + i] = or_f32_to_bf16_rne(y[i]);
+            }
+        }
+        const float clipped = fminf(absmax, 3.38953139e38f);
+        const float scale = staged ? fmaxf(clipped * (1.0f / 127.0f), 1.0e-30f)
+                                   : fmaxf(clipped / 127.0f, 1.0e-30f);
+        scales[r] = scale;
+        const float rs = bf16_round_f32(scale);
+        for (int64_t c = 0; c < k; ++c) {
+            const float v = or_bf16_to_f32(buf[c]);
+            const float divided = bf16_round_f32(v / rs);
+            float qf = nearbyintf(divided);
+            qf = fminf(127.0f, fmaxf(-128.0f, qf));
+            q[r * k + c] = (int8_t)qf;
+        }
+    }
+    free(buf);
+    return 0;
+}
+
+/* Division by reciprocal plus one FMA correction (Markstein): the GPU
+ * quantizer uses this in place of an IEEE divide.  Exposed so the CPU tests
+ * can compare it with IEEE division over every bf16 x bf16 pair.  The
+ * reciprocal is the correctly rounded 1/b. */
+OR_API float or_div_markstein_f32(float a, float b) {
+    const float y = 1.0f / b;
+    const float q0 = a * y;
+    const float r = fmaf(-q0, b, a);
+    return fmaf(r, y, q0);
+}
+
+/* Exhaustive check of the Markstein quotient on the quantizer's domain:
+ * every divisor b that bf16(scale) can take (positive normal bf16, 1e-30 <=
+ * b <= 2^128/127) and every finite bf16 dividend a with |a| <= 130 b (the
+ * row-buffer invariant |bf16(y)| <= bf16(absmax) <= 128.5 bf16(scale)).
+ * Returns the number of pairs whose INT8 code
+ * clamp(nearbyint(bf16(a / b))) differs between IEEE division and
+ * or_div_markstein_f32; *pairs receives the number of pairs checked and
+ * *fp32_mismatch the number of differing fp32 quotients. */
+static inline int quant_code(float d) {
+    float qf = nearbyintf(bf16_round_f32(d));
+    qf = fminf(127.0f, fmaxf(-128.0f, qf));
+    return (int)qf;
+}
+
+OR_API int64_t or_check_markstein_quant(int64_t *pairs, int64_t *fp32_mismatch) {
+    int64_t bad_code = 0, bad_fp32 = 0, n = 0;
+#pragma omp parallel for schedule(dynamic, 64) reduction(+ : bad_code, bad_fp32, n)
+    for (uint32_t bb = 0x0080; bb < 0x7f80; ++bb) {
+        const float b = u2f(bb << 16);
+        if (b < 1.0e-30f || b > 3.38953139e38f / 127.0f * 1.01f) continue;
+        for (uint32_t ab = 0; ab < 0x10000; ++ab) {
+            if ((ab & 0x7f80) == 0x7f80) continue; /* inf / nan */
+            const float a = u2f(ab << 16);
+            if (fabsf(a) > 130.0f * b) continue;
+            ++n;
+            const float ieee = a / b;
+            const float mk = or_div_markstein_f32(a, b);
+            if (f2u(ieee) != f2u(mk)) ++bad_fp32;
+            if (quant_code(ieee) != quant_code(mk)) ++bad_code;
+        }
+    }
+    if (pairs) *pairs = n;
+    if (fp32_mismatch) *fp32_mismatch = bad_fp32;
+    return bad_code;
+}
+
+/* ------------------------------------------------------------------------ */
+/* INT8 x INT8 -> INT32: acc[m][n] = sum_k A[m][k] * W[n][k].                */
+/* The reference's turing_int8_linear contracts A [M,K] row-major with W     */
+/* [N,K] row-major (w4a8.cu:1185-1219, bindings.cpp:371-421).  Exact integer  */
+/* math: |acc| <= K * 128 * 128 < 2^31 for K < 131072.                        */
+/* ------------------------------------------------------------------------ */
+OR_API int or_int8_gemm_i32(const int8_t *a, const int8_t *w, int64_t m, int64_t n, int64_t k,
+                            int32_t *acc) {
+    if (k >= 131072) return -1;
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < m; ++i) {
+        const int8_t *ar = a + i * k;
+        for (int64_t j = 0; j < n; ++j) {
+            const int8_t *wr = w + j * k;
+            int32_t s = 0;
+            for (int64_t t = 0; t < k; ++t) s += (int32_t)ar[t] * (int32_t)wr[t];
+            acc[i * n + j] = s;
+        }
+    }
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Epilogue: out = bf16_rn(((float(acc) * as[m]) * ws[n]) + bias[n]).        */
+/* Operation order of the CUTLASS EVT tree Mult(Mult(Acc, as), ws) then      */
+/* Plus(., bias) (w4a8.cu:480-525); bias arrives as fp32 (bindings.cpp:379-  */
+/* 383); the no-bias op dequantize_int8_bf16 is the same without the add     */
+/* (bf16_epilogue.cu:105-119).  ws_scalar != 0 broadcasts ws[0].             */
+/* ------------------------------------------------------------------------ */
+OR_API int or_int8_epilogue_bf16(const int32_t *acc, int64_t acc_ld, const float *as,
+                                 const float *ws, int ws_scalar, const float *bias, int64_t m,
+                                 int64_t n, uint16_t *out) {
+    for (int64_t i = 0; i < m; ++i) {
+        for (int64_t j = 0; j < n; ++j) {
+            float v = (float)acc[i * acc_ld + j];
+            v = v * as[i];
+            v = v * ws[ws_scalar ? 0 : j];
+            if (bias) v = v + bias[j];
+            out[i * n + j] = or_f32_to_bf16_rne(v);
+        }
+    }
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Sage K mean (smoothing).  The reference defines smoothing as subtracting  */
+/* a per-(batch, head) channel mean stored in the input type before the       */
+/* block absmax (fused.cu:93-128, sub_mean); it does not define how the mean */
+/* is computed.  This build fixes the fp32 summation order so that the GPU   */
+/* and this restatement agree bit for bit:                                   */
+/*   chunk c covers tokens [128c, 128c+128);                                 */
+/*   rows = 256 / (D/8) lanes-rows, per = 128 / rows tokens per row;          */
+/*   p[r][d]   = sum_{j=0..per-1} x[128c + r + rows*j][d]   (ascending j)    */
+/*   chunk[d]  = sum_{r=0..rows-1} p[r][d]                   (ascending r)    */
+/*   total[d]  = sum_{c ascending} chunk[c][d]                                */
+/*   mean[d]   = bf16_rn(total[d] / (float)L)                                 */
+/* Tokens at or beyond L are skipped.                                         */
+/* x is addressed with element strides (batch, head, seq); channels are       */
+/* contiguous.                                                                */
+/* ------------------------------------------------------------------------ */
+OR_API int or_sage_kmean(const uint16_t *x, int64_t batch, int64_t heads, int64_t len, int64_t dim,
+                         int64_t s_b, int64_t s_h, int64_t s_l, uint16_t *mean /* [B,H,D] */) {
+    if (dim != 64 && dim != 128) return -1;
+    const int rows = 256 / (int)(dim / 8);
+    const int per = 128 / rows;
+    const int64_t chunks = (len + 127) / 128;
+    float *tot = (float *)malloc((size_t)dim * sizeof(float));
+    float *p = (float *)malloc((size_t)rows * dim * sizeof(float));
+    if (!tot || !p) { free(tot); free(p); return -2; }
+    for (int64_t b = 0; b < batch; ++b) {
+        for (int64_t h = 0; h < heads; ++h) {
+            const uint16_t *base = x + b * s_b + h * s_h;
+            for (int64_t d = 0; d < dim; ++d) tot[d] = 0.0f;
+            for (int64_t c = 0; c < chunks; ++c) {
+                for (int r = 0; r < rows; ++r) {
+                    for (int64_t d = 0; d < dim; ++d) {
+                        float s = 0.0f;
+                        for (int j = 0; j < per; ++j) {
+                            const int64_t t = 128 * c + r + (int64_t)rows * j;
+                            if (t < len) s = s + or_bf16_to_f32(base[t * s_l + d]);
+                        }
+                        p[r * dim + d] = s;
+                    }
+                }
+                for (int64_t d = 0; d < dim; ++d) {
+                    float s = 0.0f;
+                    for (int r = 0; r < rows; ++r) s = s + p[r * dim + d];
+                    tot[d] = tot[d] + s;
+                }
+            }
+            for (int64_t d = 0; d < dim; ++d)
+                mean[(b * heads + h) * dim + d] = or_f32_to_bf16_rne(tot[d] / (float)len);
+        }
+    }
+    free(tot);
+    free(p);
+    return 0;
+}
+
+/* cvt.rni.sat.s8.f32 (numeric_conversion.cuh:144-149): round half to even,
+ * saturate to [-128, 127], NaN -> 0. */
+static inline int8_t sat_rne_s8(float v) {
+    if (v != v) return 0;
+    float r = nearbyintf(v);
+    if (r > 127.0f) r = 127.0f;
+    if (r < -128.0f) r = -128.0f;
+    return (int8_t)r;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Sage per-block INT8 quantizer: QuantInt8Kernel (fused.cu:66-200).          */
+/*   v      = float(x) - float(mean[d])  (sub_mean, :97-128)                  */
+/*   amax   = max(1e-7, max |v| over the block's tokens x channels) (:149-159)*/
+/*   scale  = amax / 127            (:166)                                    */
+/*   q      = cvt.rni.sat.s8(v * (127 / amax))   (:171-187)                   */
+/* Tokens past L count as 0 and are not written.  Scale layout [B,H,nblk].    */
+/* The reference builds this extension with --use_fast_math; the restatement */
+/* uses IEEE division (the approximate forms are not reproduced).             */
+/* ------------------------------------------------------------------------ */
+OR_API int or_sage_quant(const uint16_t *x, const uint16_t *mean /* [B,H,D] or NULL */,
+                         int64_t batch, int64_t heads, int64_t len, int64_t dim, int64_t s_b,
+                         int64_t s_h, int64_t s_l, int64_t blk, int8_t *q, int64_t qs_b,
+                         int64_t qs_h, int64_t qs_l, float *scale /* [B,H,nblk] */) {
+    const int64_t nblk = (len + blk - 1) / blk;
+    for (int64_t b = 0; b < batch; ++b) {
+        for (int64_t h = 0; h < heads; ++h) {
+            const uint16_t *xb = x + b * s_b + h * s_h;
+            int8_t *qb = q + b * qs_b + h * qs_h;
+            const uint16_t *mu = mean ? mean + (b * heads + h) * dim : NULL;
+            for (int64_t blkid = 0; blkid < nblk; ++blkid) {
+                float amax = 0.0000001f;
+                for (int64_t t = blkid * blk; t < (blkid + 1) * blk && t < len; ++t)
+                    for (int64_t d = 0; d < dim; ++d) {
+                        float v = or_bf16_to_f32(xb[t * s_l + d]);
+                        if (mu) v = v - or_bf16_to_f32(mu[d]);
+                        amax = fmaxf(amax, fabsf(v));
+                    }
+                scale[(b * heads + h) * nblk + blkid] = amax / 127.0f;
+                const float mult = 127.0f / amax;
+                for (int64_t t = blkid * blk; t < (blkid + 1) * blk && t < len; ++t)
+                    for (int64_t d = 0; d < dim; ++d) {
+                        float v = or_bf16_to_f32(xb[t * s_l + d]);
+                        if (mu) v = v - or_bf16_to_f32(mu[d]);
+                        qb[t * qs_l + d] = sat_rne_s8(v * mult);
+                    }
+            }
+        }
+    }
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Sage attention on quantized Q/K and bf16 V, for a subset of query rows.   */
+/* Reference math (qk_int_sv_f16_cuda_sm75.cu:117-118, :375-381, :411-466;   */
+/* attn_utils.cuh:464-568, :676-703, :920-973):                               */
+/*   s[j]  = float(sum_d q8[i][d] k8[j][d]) * (sm_scale*log2e) * qs * ks      */
+/*   p[j]  = 2^(s[j] - max_j s)   (masked keys excluded)                      */
+/*   P[j]  = round(p[j]) to the PV operand type (bf16 here; the reference's   */
+/*           Turing kernel used fp16)                                         */
+/*   o[d]  = (sum_j P[j] v[j][d]) / (sum_j P[j])                              */
+/* Computed in double from the rounded P; the GPU's online softmax differs   */
+/* from this only by fp32 rounding, which the attention tolerance covers.    */
+/* Causal masking is top-left aligned (kv_idx > q_idx masked,                */
+/* attn_utils.cuh:407-431).  GQA: q head h reads kv head h / (Hq/Hkv).        */
+/* Rows are given as a list of (b, h, i) triples; out is [nrows, D] fp32.     */
+/* ------------------------------------------------------------------------ */
+OR_API int or_sage_attn_rows(const int8_t *q8, int64_t q_sb, int64_t q_sh, int64_t q_sl,
+                             const float *qs, int64_t blkq,
+                             const int8_t *k8, int64_t k_sb, int64_t k_sh, int64_t k_sl,
+                             const float *ks, int64_t blkk,
+                             const uint16_t *v, int64_t v_sb, int64_t v_sh, int64_t v_sl,
+                             int64_t hq, int64_t hkv, int64_t lq, int64_t lk, int64_t dim,
+                             float sm_scale, int causal, int p_bf16,
+                             const int64_t *rows /* [nrows,3] */, int64_t nrows, float *out) {
+    const double log2e = 1.4426950408889634;
+    const int64_t nbq = (lq + blkq - 1) / blkq;
+    const int64_t nbk = (lk + blkk - 1) / blkk;
+    const int64_t groups = hq / hkv;
+#pragma omp parallel
+    {
+        double *s = (double *)malloc((size_t)lk * sizeof(double));
+        double *o = (double *)malloc((size_t)dim * sizeof(double));
+#pragma omp for schedule(dynamic)
+        for (int64_t r = 0; r < nrows; ++r) {
+            const int64_t b = rows[3 * r], h = rows[3 * r + 1], i = rows[3 * r + 2];
+            const int64_t hk = h / groups;
+            const int8_t *qi = q8 + b * q_sb + h * q_sh + i * q_sl;
+            const float qscale = qs[(b * hq + h) * nbq + i / blkq];
+            const int64_t jmax = causal ? (i + 1 < lk ? i + 1 : lk) : lk;
+            double m = -INFINITY;
+            for (int64_t j = 0; j < jmax; ++j) {
+                const int8_t *kj = k8 + b * k_sb + hk * k_sh + j * k_sl;
+                int32_t acc = 0;
+                for (int64_t d = 0; d < dim; ++d) acc += (int32_t)qi[d] * (int32_t)kj[d];
+                const double kscale = ks[(b * hkv + hk) * nbk + j / blkk];
+                s[j] = (double)acc * ((double)sm_scale * log2e) * (double)qscale * kscale;
+                if (s[j] > m) m = s[j];
+            }
+            double l = 0.0;
+            for (int64_t d = 0; d < dim; ++d) o[d] = 0.0;
+            for (int64_t j = 0; j < jmax; ++j) {
+                double p = exp2(s[j] - m);
+                if (p_bf16) p = (double)bf16_round_f32((float)p);
+                l += p;
+                const uint16_t *vj = v + b * v_sb + hk * v_sh + j * v_sl;
+                for (int64_t d = 0; d < dim; ++d) o[d] += p * (double)or_bf16_to_f32(vj[d]);
+            }
+            for (int64_t d = 0; d < dim; ++d) out[r * dim + d] = (float)(o[d] / l);
+        }
+        free(s);
+        free(o);
+    }
+    return 0;
+}

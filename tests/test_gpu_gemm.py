@@ -1,0 +1,93 @@
+"""GPU parity: INT8 GEMM accumulators (bit-exact), the BF16 epilogue (bit-exact
+vs the oracle's operation order) and dequantize_int8_bf16.
+
+Oracle: or_int8_gemm_i32 (exact integer sum) and or_int8_epilogue_bf16
+(w4a8.cu:480-525 operation order: ((acc * as) * ws) + bias, bf16 RNE).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle
+from tests import inputs
+
+pytestmark = pytest.mark.gpu
+
+
+def _rand_i8(shape, seed):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randint(-128, 128, shape, generator=g, dtype=torch.int8)
+
+
+@pytest.mark.parametrize(
+    "m,n,k",
+    [(1, 8, 16), (7, 24, 48), (256, 256, 64), (300, 264, 192), (513, 520, 1040), (64, 8960, 1536), (40, 512, 13824)],
+)
+def test_gemm_i32_exact(gpu_device, m, n, k):
+    print(f"[gemm-i32] m={m} n={n} k={k}", flush=True)
+    a = _rand_i8((m, k), m * 7 + n)
+    w = _rand_i8((n, k), k * 3 + 1)
+    acc = torch.ops.turing_utils.int8_gemm_i32(a.to(gpu_device), w.to(gpu_device))
+    torch.cuda.synchronize(gpu_device)
+    ref = oracle.int8_gemm_i32(a.numpy(), w.numpy())
+    np.testing.assert_array_equal(acc.cpu().numpy(), ref)
+
+
+def test_gemm_i32_extremes(gpu_device):
+    """All -128 times -128 at K=13824: the largest accumulator this path can see."""
+    m, n, k = 32, 16, 13824
+    a = torch.full((m, k), -128, dtype=torch.int8)
+    w = torch.full((n, k), -128, dtype=torch.int8)
+    acc = torch.ops.turing_utils.int8_gemm_i32(a.to(gpu_device), w.to(gpu_device)).cpu()
+    assert int(acc.min()) == int(acc.max()) == 16384 * k
+
+
+@pytest.mark.parametrize("with_bias", [True, False])
+@pytest.mark.parametrize("m,n,k", [(300, 264, 192), (96, 8960, 1536)])
+def test_int8_linear_epilogue_exact(gpu_device, m, n, k, with_bias):
+    print(f"[int8_linear] m={m} n={n} k={k} bias={with_bias}", flush=True)
+    a = _rand_i8((m, k), 5 + m)
+    w, ws, bias = inputs.weights(n, k, 9, with_bias)
+    g = torch.Generator().manual_seed(3)
+    as_ = torch.empty(m).uniform_(1e-3, 1e-1, generator=g)
+    out = torch.ops.turing_utils.int8_linear(
+        a.to(gpu_device), w.to(gpu_device), as_.to(gpu_device), ws.to(gpu_device),
+        None if bias is None else bias.to(gpu_device),
+    )
+    torch.cuda.synchronize(gpu_device)
+    acc = oracle.int8_gemm_i32(a.numpy(), w.numpy())
+    ref = oracle.epilogue_bf16(acc, as_.numpy(), ws.numpy(), None if bias is None else bias.numpy())
+    got = inputs.bits(out)
+    bad = np.argwhere(got != ref)
+    assert bad.size == 0, f"{len(bad)} outputs differ, first {bad[:5].tolist()}"
+
+
+def test_int8_linear_config1_rows(gpu_device):
+    """BASELINE config 1 through the drop-in ops (quantize G=128, then int8_linear);
+    128 sampled rows checked bit-exact against the oracle chain."""
+    x = inputs.activation(4096, 1536, 0)
+    w, ws, bias = inputs.weights(8960, 1536, 0)
+    dev = gpu_device
+    q, s = torch.ops.turing_utils.bf16_int8_convrot_quantize(x.to(dev), 128)
+    out = torch.ops.turing_utils.int8_linear(q, w.to(dev), s, ws.to(dev), bias.to(dev))
+    torch.cuda.synchronize(dev)
+    rows = np.sort(np.random.default_rng(0).choice(4096, 128, replace=False))
+    q_ref, s_ref = oracle.convrot_quant(inputs.bits(x[rows]), 128)
+    np.testing.assert_array_equal(q.cpu().numpy()[rows], q_ref)
+    acc = oracle.int8_gemm_i32(q_ref, w.numpy())
+    ref = oracle.epilogue_bf16(acc, s_ref, ws.numpy(), bias.numpy())
+    np.testing.assert_array_equal(inputs.bits(out)[rows], ref)
+
+
+@pytest.mark.parametrize("cols,scalar", [(264, False), (200, False), (264, True), (131, False)])
+def test_dequantize_exact(gpu_device, cols, scalar):
+    m, ld = 37, 264
+    g = torch.Generator().manual_seed(cols)
+    acc = torch.randint(-(2**30), 2**30, (m, ld), generator=g, dtype=torch.int32)
+    as_ = torch.empty(m).uniform_(1e-4, 1e-2, generator=g)
+    ws = torch.empty(1 if scalar else cols).uniform_(1e-3, 5e-3, generator=g)
+    out = torch.ops.turing_utils.dequantize_int8_bf16(acc.to(gpu_device), as_.to(gpu_device), ws.to(gpu_device), cols)
+    ref = oracle.epilogue_bf16(acc.numpy(), as_.numpy(), ws.numpy(), None, cols=cols)
+    np.testing.assert_array_equal(inputs.bits(out), ref)

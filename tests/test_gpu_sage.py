@@ -1,0 +1,151 @@
+"""GPU parity: Sage prologue (K mean, per-block INT8 Q/K) bit-exact vs the oracle,
+and Sage attention vs the oracle's quantized math within the north-star gate
+(cosine >= 0.999, max-abs <= 2e-2), plus the reference's own SDPA gate.
+
+Oracle: or_sage_kmean, or_sage_quant (fused.cu:66-200), or_sage_attn_rows
+(qk_int_sv_f16_cuda_sm75.cu:117-118, :375-381; attn_utils.cuh:464-568).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from comfyui_turing_utils_kernel.turing_sage import core, quant
+from comfyui_turing_utils_kernel.turing_sage.correctness import (
+    attention_error_metrics,
+    require_attention_correctness,
+)
+from oracle import oracle
+from tests import inputs
+
+pytestmark = pytest.mark.gpu
+
+GATE = dict(max_abs=2e-2, cosine=0.999)
+
+
+@pytest.mark.parametrize("b,h,l,d,seed", [(1, 2, 1, 128, 1), (2, 3, 300, 128, 2), (1, 4, 1000, 64, 3), (1, 12, 8190, 128, 1)])
+def test_kmean_exact(gpu_device, b, h, l, d, seed):
+    print(f"[kmean] b={b} h={h} l={l} d={d}", flush=True)
+    _, k, _ = inputs.attention(b, h, l, d, seed)
+    mean = quant.key_channel_mean(k.to(gpu_device), "HND")
+    np.testing.assert_array_equal(inputs.bits(mean), oracle.sage_kmean(inputs.bits(k)))
+
+
+@pytest.mark.parametrize("blk", [16, 32, 64, 128])
+@pytest.mark.parametrize("smooth", [False, True])
+@pytest.mark.parametrize("b,h,l,d", [(1, 2, 77, 128), (2, 3, 300, 64), (1, 4, 513, 128)])
+def test_quant_exact(gpu_device, blk, smooth, b, h, l, d):
+    print(f"[sage-quant] blk={blk} smooth={smooth} b={b} h={h} l={l} d={d}", flush=True)
+    _, k, _ = inputs.attention(b, h, l, d, blk + l)
+    kd = k.to(gpu_device)
+    mean = quant.key_channel_mean(kd, "HND") if smooth else None
+    q8, sc = quant.quantize_per_block(kd, blk, "HND", mean)
+    mean_ref = oracle.sage_kmean(inputs.bits(k)) if smooth else None
+    q_ref, s_ref = oracle.sage_quant(inputs.bits(k), blk, mean_ref)
+    np.testing.assert_array_equal(sc.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
+    np.testing.assert_array_equal(q8.cpu().numpy(), q_ref)
+
+
+def test_quant_nhd_matches_hnd(gpu_device):
+    _, k, _ = inputs.attention(2, 5, 200, 128, 7)
+    kd = k.to(gpu_device)
+    q_hnd, s_hnd = quant.quantize_per_block(kd, 64, "HND", quant.key_channel_mean(kd, "HND"))
+    kn = kd.transpose(1, 2).contiguous()
+    q_nhd, s_nhd = quant.quantize_per_block(kn, 64, "NHD", quant.key_channel_mean(kn, "NHD"))
+    assert torch.equal(q_hnd, q_nhd.transpose(1, 2))
+    assert torch.equal(s_hnd, s_nhd)
+
+
+def _oracle_rows(q, k, v, rows, blkq, blkk, causal, sm_scale, smooth=True):
+    """Oracle attention for (b, h, i) rows of HND bf16 inputs (head_dim <= 128)."""
+    d = q.size(-1)
+    pad = 128 - d
+    qp, kp, vp = (torch.nn.functional.pad(t, (0, pad)) if pad else t for t in (q, k, v))
+    mean = oracle.sage_kmean(inputs.bits(kp)) if smooth else None
+    q8, qs = oracle.sage_quant(inputs.bits(qp), blkq)
+    k8, ks = oracle.sage_quant(inputs.bits(kp), blkk, mean)
+    out = oracle.sage_attn_rows(q8, qs, blkq, k8, ks, blkk, inputs.bits(vp), sm_scale, rows, causal)
+    return out[:, :d]
+
+
+def _sample_rows(b, h, l, n, seed):
+    rng = np.random.default_rng(seed)
+    rows = np.stack([rng.integers(0, b, n), rng.integers(0, h, n), rng.integers(0, l, n)], 1)
+    rows[: min(n, 2), 2] = [0, l - 1][: min(n, 2)]
+    return rows
+
+
+@pytest.mark.parametrize(
+    "b,h,hkv,lq,lk,d,causal,blkq,blkk",
+    [
+        (1, 2, 2, 256, 256, 128, False, 128, 128),
+        (1, 2, 2, 300, 333, 128, False, 128, 128),
+        (2, 4, 2, 65, 73, 128, False, 16, 64),
+        (1, 2, 1, 1, 64, 128, False, 128, 128),
+        (1, 3, 3, 700, 700, 128, True, 128, 128),
+        (1, 2, 2, 130, 257, 64, False, 32, 64),
+        (1, 2, 2, 129, 200, 96, True, 64, 128),
+    ],
+)
+def test_attention_vs_oracle(gpu_device, b, h, hkv, lq, lk, d, causal, blkq, blkk):
+    print(f"[attn] b={b} h={h} hkv={hkv} lq={lq} lk={lk} d={d} causal={causal} blk=({blkq},{blkk})", flush=True)
+    q, _, _ = inputs.attention(b, h, lq, d, 100 + lq)
+    _, k, v = inputs.attention(b, hkv, lk, d, 200 + lk)
+    sm = d ** -0.5
+    out = core.sageattn(q.to(gpu_device), k.to(gpu_device), v.to(gpu_device), tensor_layout="HND",
+                        is_causal=causal, BLKQ=blkq, BLKK=blkk)
+    torch.cuda.synchronize(gpu_device)
+    rows = _sample_rows(b, h, lq, 96, lq + lk)
+    ref = _oracle_rows(q, k, v, rows, blkq, blkk, causal, sm)
+    got = out.float().cpu()[rows[:, 0], rows[:, 1], rows[:, 2]]
+    res = attention_error_metrics(got, torch.from_numpy(ref), candidate_name="hip", reference_name="oracle")
+    print(f"  cos={res.cosine:.6f} max_abs={res.max_abs:.3e}", flush=True)
+    require_attention_correctness(res, **GATE)
+
+
+def test_attention_config2_rows(gpu_device):
+    """BASELINE config 2 (B1 H12 L8190 D128, seed 1), 256 sampled rows vs the oracle."""
+    q, k, v = inputs.attention(1, 12, 8190, 128, 1)
+    out = core.sageattn(q.to(gpu_device), k.to(gpu_device), v.to(gpu_device), tensor_layout="HND")
+    torch.cuda.synchronize(gpu_device)
+    rows = _sample_rows(1, 12, 8190, 256, 1)
+    ref = _oracle_rows(q, k, v, rows, 128, 128, False, 128 ** -0.5)
+    got = out.float().cpu()[rows[:, 0], rows[:, 1], rows[:, 2]]
+    res = attention_error_metrics(got, torch.from_numpy(ref), candidate_name="hip", reference_name="oracle")
+    print(f"  cos={res.cosine:.6f} max_abs={res.max_abs:.3e}", flush=True)
+    require_attention_correctness(res, **GATE)
+
+
+def test_attention_nhd_and_op(gpu_device):
+    """NHD layout through torch.ops.turing_utils.sage_attention equals the HND facade."""
+    q, k, v = inputs.attention(2, 4, 200, 128, 5)
+    dev = gpu_device
+    hnd = core.sageattn(q.to(dev), k.to(dev), v.to(dev), tensor_layout="HND")
+    nhd = torch.ops.turing_utils.sage_attention(
+        q.transpose(1, 2).contiguous().to(dev), k.transpose(1, 2).contiguous().to(dev),
+        v.transpose(1, 2).contiguous().to(dev), "NHD", False, -1.0,
+    )
+    assert torch.equal(hnd, nhd.transpose(1, 2))
+
+
+def test_attention_reference_sdpa_gate(gpu_device):
+    """The reference preflight's gate (turing_sage/__init__.py:612-663): arange-modulo
+    inputs vs fp32 SDPA, rtol 0.08 / atol 0.05, head_dim 64/96/128, GQA 4:2."""
+    from comfyui_turing_utils_kernel import turing_sage
+
+    turing_sage.preflight(gpu_device)
+
+
+def test_smoothing_invariance(gpu_device):
+    """Subtracting the K mean shifts every score of a row by a constant, so the
+    smoothed and unsmoothed kernels agree within the quantization tolerance."""
+    q, k, v = inputs.attention(1, 4, 512, 128, 9)
+    dev = gpu_device
+    a = core.sageattn(q.to(dev), k.to(dev), v.to(dev), smooth_k=True)
+    b = core.sageattn(q.to(dev), k.to(dev), v.to(dev), smooth_k=False)
+    ref = torch.nn.functional.scaled_dot_product_attention(q.float(), k.float(), v.float())
+    ea = attention_error_metrics(a.float().cpu(), ref)
+    eb = attention_error_metrics(b.float().cpu(), ref)
+    print(f"  smoothed cos={ea.cosine:.6f} raw cos={eb.cosine:.6f}", flush=True)
+    assert ea.cosine >= 0.999 and ea.cosine >= eb.cosine - 1e-4

@@ -95,7 +95,7 @@ def main():
     import comfyui_turing_utils_kernel  # noqa: F401  (registers torch.ops.turing_utils.*)
     from comfyui_turing_utils_kernel import _lib
     from comfyui_turing_utils_kernel.turing_sage import quant as sage_quant
-    from comfyui_turing_utils_kernel.turing_sage.core import sageattn_prequantized
+    from comfyui_turing_utils_kernel.turing_sage.core import attention_from_vt
     from tests import inputs
 
     dev = torch.device("cuda", 0)
@@ -123,7 +123,8 @@ def main():
         mean = timer("sage_kmean", sage_quant.key_channel_mean, k_, "HND")
         q8, qs = timer("sage_quant_q", sage_quant.quantize_per_block, q, BLK, "HND")
         k8, ks = timer("sage_quant_k", sage_quant.quantize_per_block, k_, BLK, "HND", mean)
-        return timer("sage_attn", sageattn_prequantized, q8, qs, k8, ks, v, tensor_layout="HND",
+        vt, _ = timer("sage_v_prep", sage_quant.value_transpose, v, "HND")
+        return timer("sage_attn", attention_from_vt, q8, qs, k8, ks, vt, tensor_layout="HND",
                      sm_scale=sm_scale, blkq=BLK, blkk=BLK)
 
     for _ in range(args.warmup):
@@ -146,7 +147,7 @@ def main():
     # Per-kernel algorithmic work: GEMM 2MNK ops; attention 4BHL^2D ops;
     # ConvRot quantize 2 B/elem read + 1 B/elem write + 4 B/row; Sage quantize
     # 2 B read + 1 B write per element (K also reads its mean: negligible);
-    # K mean 2 B/elem read.
+    # K mean 2 B/elem read; V transpose 2 B read + 2 B write per element.
     work = {}
     for name, k, n, *_ in lin:
         work[f"int8_gemm_{name}"] = ("mfma", 2.0 * M_TOKENS * n * k)
@@ -156,6 +157,7 @@ def main():
     work["sage_quant_q"] = ("hbm", 3.0 * elems)
     work["sage_quant_k"] = ("hbm", 3.0 * elems)
     work["sage_kmean"] = ("hbm", 2.0 * elems)
+    work["sage_v_prep"] = ("hbm", 4.0 * elems)
     for name, rec in kernels.items():
         bound, amount = work[name]
         sec = rec["ms_avg"] * 1e-3

@@ -50,16 +50,20 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
          _c_void_p, _i64, _i64, _i64, _c_void_p, _c_void_p],
     ),
+    "tu_sage_v_prep": (
+        _i32,
+        [_c_void_p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _c_void_p, _i64, _c_void_p],
+    ),
     "tu_sage_attn_fwd": (
         _i32,
-        [_c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p,
+        [_c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p, _i64, _c_void_p, _i64, _c_void_p,
          _i64, _i64, _i64, _i64, _i64, _i64,
-         _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+         _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
          _f32, _i32, _c_void_p],
     ),
 }
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

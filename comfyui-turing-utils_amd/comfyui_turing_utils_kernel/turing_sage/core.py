@@ -25,20 +25,25 @@ from typing import Optional
 import torch
 
 from .. import _lib
-from .quant import SUPPORTED_BLOCKS, _layout_dims, per_block_int8
+from .quant import SUPPORTED_BLOCKS, _layout_dims, per_block_int8, value_transpose
 
 KERNEL_HEAD_DIM = 128
 
 
 @dataclasses.dataclass(frozen=True)
 class PrequantizedSageAttention:
-    """Quantized Q/K plus V, ready for ``sageattn_from_prequantized``."""
+    """Quantized Q/K plus V^T, ready for ``sageattn_from_prequantized``.
+
+    ``value_t`` is [B, Hkv, 128, Lpad] bf16 (keys padded with zeros to a
+    multiple of 64), the layout ``tu_sage_attn_fwd`` reads; the caller may
+    release the original Q/K/V once this object exists.
+    """
 
     query_int8: torch.Tensor
     query_scale: torch.Tensor
     key_int8: torch.Tensor
     key_scale: torch.Tensor
-    value: torch.Tensor
+    value_t: torch.Tensor
     tensor_layout: str
     original_head_dim: int
     is_causal: bool
@@ -112,11 +117,86 @@ def prequantize_sageattn(
         q_int8, q_scale, k_int8, k_scale, _ = per_block_int8(
             qp, kp, BLKQ=BLKQ, BLKK=BLKK, tensor_layout=tensor_layout, smooth_k=smooth_k
         )
+        value_t, _ = value_transpose(vp, tensor_layout)
     return PrequantizedSageAttention(
-        query_int8=q_int8, query_scale=q_scale, key_int8=k_int8, key_scale=k_scale, value=vp,
+        query_int8=q_int8, query_scale=q_scale, key_int8=k_int8, key_scale=k_scale, value_t=value_t,
         tensor_layout=tensor_layout, original_head_dim=head_dim, is_causal=bool(is_causal),
         sm_scale=scale, blkq=BLKQ, blkk=BLKK, output_dtype=output_dtype,
     )
+
+
+def _check_qk(q_int8, q_scale, k_int8, k_scale, tensor_layout, blkq, blkk):
+    if tensor_layout not in ("HND", "NHD"):
+        raise ValueError(f"Unsupported tensor_layout: {tensor_layout}")
+    if q_int8.dtype != torch.int8 or k_int8.dtype != torch.int8:
+        raise TypeError("prequantized Sage Q/K must be int8")
+    if q_scale.dtype != torch.float32 or k_scale.dtype != torch.float32:
+        raise TypeError("prequantized Sage scales must be float32")
+    if q_int8.ndim != 4 or k_int8.ndim != 4:
+        raise ValueError("prequantized Sage Q/K must be four-dimensional")
+    if len({q_int8.device, k_int8.device, q_scale.device, k_scale.device}) != 1:
+        raise ValueError("prequantized Sage tensors must share one device")
+    if q_int8.size(-1) != KERNEL_HEAD_DIM or k_int8.size(-1) != KERNEL_HEAD_DIM:
+        raise ValueError("prequantized Sage requires head_dim 128")
+    if q_int8.stride(-1) != 1 or k_int8.stride(-1) != 1:
+        raise ValueError("the last Q/K dimension must be contiguous")
+    hq, lq, *_ = _layout_dims(q_int8, tensor_layout)
+    hkv, lk, *_ = _layout_dims(k_int8, tensor_layout)
+    batch = q_int8.size(0)
+    if k_int8.size(0) != batch:
+        raise ValueError("prequantized Sage Q/K batch sizes differ")
+    if hkv <= 0 or hq % hkv != 0:
+        raise ValueError("prequantized Sage Q heads must be divisible by KV heads")
+    if blkk % 64 or blkq <= 0:
+        raise ValueError("prequantized Sage needs blkq > 0 and blkk % 64 == 0")
+    if q_scale.shape != (batch, hq, (lq + blkq - 1) // blkq):
+        raise ValueError("prequantized Sage Q scale shape is incompatible")
+    if k_scale.shape != (batch, hkv, (lk + blkk - 1) // blkk):
+        raise ValueError("prequantized Sage K scale shape is incompatible")
+    return batch, hq, hkv, lq, lk
+
+
+def attention_from_vt(
+    q_int8: torch.Tensor,
+    q_scale: torch.Tensor,
+    k_int8: torch.Tensor,
+    k_scale: torch.Tensor,
+    value_t: torch.Tensor,
+    *,
+    tensor_layout: str = "HND",
+    is_causal: bool = False,
+    sm_scale: Optional[float] = None,
+    blkq: int = 128,
+    blkk: int = 128,
+    output: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Attention kernel only: quantized Q/K and V^T from ``value_transpose``."""
+    batch, hq, hkv, lq, lk = _check_qk(q_int8, q_scale, k_int8, k_scale, tensor_layout, blkq, blkk)
+    lpad = (lk + 63) // 64 * 64
+    if value_t.dtype != torch.bfloat16 or value_t.shape != (batch, hkv, KERNEL_HEAD_DIM, lpad):
+        raise ValueError(f"V^T must be bf16 [{batch}, {hkv}, {KERNEL_HEAD_DIM}, {lpad}]")
+    if value_t.device != q_int8.device or not value_t.is_contiguous():
+        raise ValueError("V^T must be contiguous on the Q/K device")
+    scale = float(sm_scale) if sm_scale is not None else KERNEL_HEAD_DIM ** -0.5
+    if output is None:
+        output = torch.empty(q_int8.shape, dtype=torch.bfloat16, device=q_int8.device)
+    elif (output.shape != q_int8.shape or output.dtype != torch.bfloat16 or output.device != q_int8.device
+          or output.stride(-1) != 1):
+        raise ValueError("prequantized Sage output is incompatible")
+    _, _, qsb, qsh, qsl = _layout_dims(q_int8, tensor_layout)
+    _, _, ksb, ksh, ksl = _layout_dims(k_int8, tensor_layout)
+    _, _, osb, osh, osl = _layout_dims(output, tensor_layout)
+    q_scale = q_scale.contiguous()
+    k_scale = k_scale.contiguous()
+    with torch.cuda.device(q_int8.device):
+        _lib.call(
+            "tu_sage_attn_fwd",
+            q_int8.data_ptr(), q_scale.data_ptr(), blkq, k_int8.data_ptr(), k_scale.data_ptr(), blkk,
+            value_t.data_ptr(), lpad, output.data_ptr(), batch, hq, hkv, lq, lk, KERNEL_HEAD_DIM,
+            qsb, qsh, qsl, ksb, ksh, ksl, osb, osh, osl,
+            scale, int(bool(is_causal)), _lib.stream_of(q_int8.device),
+        )
+    return output
 
 
 def sageattn_prequantized(
@@ -133,60 +213,24 @@ def sageattn_prequantized(
     blkk: int = 128,
     output: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
-    """Attention on already-quantized Q/K and bf16 V (all head_dim 128)."""
-    if tensor_layout not in ("HND", "NHD"):
-        raise ValueError(f"Unsupported tensor_layout: {tensor_layout}")
-    if q_int8.dtype != torch.int8 or k_int8.dtype != torch.int8:
-        raise TypeError("prequantized Sage Q/K must be int8")
+    """Attention on already-quantized Q/K and bf16 V (head_dim 128), the
+    counterpart of the reference's ``sageattn_prequantized`` (core.py:573-653)."""
+    batch, hq, hkv, lq, lk = _check_qk(q_int8, q_scale, k_int8, k_scale, tensor_layout, blkq, blkk)
     if v.dtype != torch.bfloat16:
         raise TypeError("prequantized Sage V must be bfloat16")
-    if q_scale.dtype != torch.float32 or k_scale.dtype != torch.float32:
-        raise TypeError("prequantized Sage scales must be float32")
-    if q_int8.ndim != 4 or k_int8.ndim != 4 or v.ndim != 4:
-        raise ValueError("prequantized Sage Q/K/V must be four-dimensional")
-    devices = {q_int8.device, k_int8.device, v.device, q_scale.device, k_scale.device}
-    if len(devices) != 1:
-        raise ValueError("prequantized Sage tensors must share one device")
-    if q_int8.size(-1) != KERNEL_HEAD_DIM or k_int8.size(-1) != KERNEL_HEAD_DIM or v.size(-1) != KERNEL_HEAD_DIM:
-        raise ValueError("prequantized Sage requires head_dim 128")
-    hq, lq, qsb, qsh, qsl = _layout_dims(q_int8, tensor_layout)
-    hkv, lk, ksb, ksh, ksl = _layout_dims(k_int8, tensor_layout)
-    vh, vl, vsb, vsh, vsl = _layout_dims(v, tensor_layout)
-    batch = q_int8.size(0)
-    if k_int8.size(0) != batch or v.size(0) != batch or vh != hkv or vl != lk:
+    if v.ndim != 4 or v.device != q_int8.device or v.stride(-1) != 1:
+        raise ValueError("prequantized Sage V must be 4D, contiguous in channels, on the Q/K device")
+    vh, vl, *_ = _layout_dims(v, tensor_layout)
+    if v.size(0) != batch or vh != hkv or vl != lk or v.size(-1) != KERNEL_HEAD_DIM:
         raise ValueError("prequantized Sage Q/K/V shapes are incompatible")
-    if hkv <= 0 or hq % hkv != 0:
-        raise ValueError("prequantized Sage Q heads must be divisible by KV heads")
-    if blkk % 64 or blkq <= 0:
-        raise ValueError("prequantized Sage needs blkq > 0 and blkk % 64 == 0")
-    if q_scale.shape != (batch, hq, (lq + blkq - 1) // blkq):
-        raise ValueError("prequantized Sage Q scale shape is incompatible")
-    if k_scale.shape != (batch, hkv, (lk + blkk - 1) // blkk):
-        raise ValueError("prequantized Sage K scale shape is incompatible")
-    if any(t.stride(-1) != 1 for t in (q_int8, k_int8, v)):
-        raise ValueError("the last Q/K/V dimension must be contiguous")
-    scale = float(sm_scale) if sm_scale is not None else KERNEL_HEAD_DIM ** -0.5
-    if output is None:
-        output = torch.empty(q_int8.shape, dtype=torch.bfloat16, device=v.device)
-    elif output.shape != q_int8.shape or output.dtype != torch.bfloat16 or output.device != v.device or output.stride(-1) != 1:
-        raise ValueError("prequantized Sage output is incompatible")
-    _, _, osb, osh, osl = _layout_dims(output, tensor_layout)
-    q_scale = q_scale.contiguous()
-    k_scale = k_scale.contiguous()
-    with torch.cuda.device(v.device):
-        _lib.call(
-            "tu_sage_attn_fwd",
-            q_int8.data_ptr(), q_scale.data_ptr(), blkq, k_int8.data_ptr(), k_scale.data_ptr(), blkk,
-            v.data_ptr(), output.data_ptr(), batch, hq, hkv, lq, lk, KERNEL_HEAD_DIM,
-            qsb, qsh, qsl, ksb, ksh, ksl, vsb, vsh, vsl, osb, osh, osl,
-            scale, int(bool(is_causal)), _lib.stream_of(v.device),
-        )
-    return output
+    value_t, _ = value_transpose(v, tensor_layout)
+    return attention_from_vt(q_int8, q_scale, k_int8, k_scale, value_t, tensor_layout=tensor_layout,
+                             is_causal=is_causal, sm_scale=sm_scale, blkq=blkq, blkk=blkk, output=output)
 
 
 def sageattn_from_prequantized(quantized: PrequantizedSageAttention) -> torch.Tensor:
-    out = sageattn_prequantized(
-        quantized.query_int8, quantized.query_scale, quantized.key_int8, quantized.key_scale, quantized.value,
+    out = attention_from_vt(
+        quantized.query_int8, quantized.query_scale, quantized.key_int8, quantized.key_scale, quantized.value_t,
         tensor_layout=quantized.tensor_layout, is_causal=quantized.is_causal, sm_scale=quantized.sm_scale,
         blkq=quantized.blkq, blkk=quantized.blkk,
     )

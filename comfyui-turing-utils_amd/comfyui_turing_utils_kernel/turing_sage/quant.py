@@ -75,3 +75,16 @@ def per_block_int8(
     q_int8, q_scale = quantize_per_block(q, BLKQ, tensor_layout)
     k_int8, k_scale = quantize_per_block(k, BLKK, tensor_layout, mean)
     return q_int8, q_scale, k_int8, k_scale, mean
+
+
+def value_transpose(v: torch.Tensor, tensor_layout: str = "HND") -> tuple[torch.Tensor, int]:
+    """V^T [B, H, D, Lpad] (keys padded with zeros to a multiple of 64), the
+    PV operand layout of the attention kernel.  Returns (vt, lpad)."""
+    heads, tokens, sb, sh, sl = _layout_dims(v, tensor_layout)
+    batch, dim = v.size(0), v.size(-1)
+    lpad = (tokens + 63) // 64 * 64
+    vt = torch.empty((batch, heads, dim, lpad), dtype=torch.bfloat16, device=v.device)
+    with torch.cuda.device(v.device):
+        _lib.call("tu_sage_v_prep", v.data_ptr(), batch, heads, tokens, dim, sb, sh, sl, vt.data_ptr(), lpad,
+                  _lib.stream_of(v.device))
+    return vt, lpad

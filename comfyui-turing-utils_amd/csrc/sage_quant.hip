@@ -74,8 +74,18 @@ __global__ __launch_bounds__(128) void kmean_final_kernel(const float *__restric
     if (d >= dim) return;
     const int64_t bh = blockIdx.x;
     const float *src = chunk_sums + bh * chunks * dim + d;
+    // Loads are issued 16 at a time to hide their latency; the additions stay
+    // in ascending chunk order.
     float tot = 0.0f;
-    for (int64_t c = 0; c < chunks; ++c) tot = tot + src[c * dim];
+    int64_t c = 0;
+    for (; c + 16 <= chunks; c += 16) {
+        float v[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) v[j] = src[(c + j) * dim];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) tot = tot + v[j];
+    }
+    for (; c < chunks; ++c) tot = tot + src[c * dim];
     mean[bh * dim + d] = static_cast<uint16_t>(bf16_rne_bits(tot / static_cast<float>(len)));
 }
 

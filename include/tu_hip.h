@@ -114,6 +114,17 @@ int32_t tu_sage_quant(const void *x_bf16, const void *mean_bf16, int64_t batch, 
                       int64_t blk, int8_t *q, int64_t q_b, int64_t q_h, int64_t q_l,
                       float *scale, void *stream);
 
+/* Sage attention: V layout prologue ----------------------------------------- */
+
+/* Writes V^T: vt[b][h][d][lpad] = v[b][h][key][d] for key < len and 0 for
+ * len <= key < lpad (lpad % 64 == 0, lpad >= len).  v: bf16 with element
+ * strides (s_b, s_h, s_l), channels contiguous; dim == 128.  This is the PV
+ * operand layout of tu_sage_attn_fwd (keys contiguous per channel).  It plays
+ * the role of the reference's V staging in shared memory
+ * (kernel/csrc/turing/sage/attn_utils.cuh:125-136, load_v_global_to_share). */
+int32_t tu_sage_v_prep(const void *v_bf16, int64_t batch, int64_t heads, int64_t len, int64_t dim,
+                       int64_t s_b, int64_t s_h, int64_t s_l, void *vt_bf16, int64_t lpad, void *stream);
+
 /* Sage attention: forward --------------------------------------------------- */
 
 /* O = softmax(Q K^T * sm_scale) V on INT8 Q/K and bf16 V:
@@ -121,19 +132,19 @@ int32_t tu_sage_quant(const void *x_bf16, const void *mean_bf16, int64_t batch, 
  *   online softmax in base 2, P rounded to bf16, O accumulated in fp32 by
  *   bf16 MFMA, O / rowsum(P) stored as bf16.
  * q8: int8 [batch, hq, lq, dim] addressed by strides (q_sb, q_sh, q_sl);
- * k8: int8, v: bf16, o: bf16 likewise (kv heads hkv, hq % hkv == 0, GQA).
+ * k8: int8 likewise with hkv heads (hq % hkv == 0, GQA); vt: bf16
+ * [batch, hkv, dim, lpad] from tu_sage_v_prep; o: bf16 by strides.
  * q_scale: fp32 [batch, hq, ceil(lq/blkq)]; k_scale: fp32 [batch, hkv, ceil(lk/blkk)].
  * dim == 128; blkq >= 1; blkk % 64 == 0.  causal: top-left aligned.
  * Replaces qk_int8_sv_f16_accum_f32_attn
  * (kernel/csrc/turing/sage/qk_int_sv_f16_cuda_sm75.cu:984-1123), the kernel
  * behind turing_utils::sage_attention (turing_sage/custom_ops.py:137-168). */
 int32_t tu_sage_attn_fwd(const int8_t *q8, const float *q_scale, int64_t blkq, const int8_t *k8,
-                         const float *k_scale, int64_t blkk, const void *v_bf16, void *o_bf16,
-                         int64_t batch, int64_t hq, int64_t hkv, int64_t lq, int64_t lk,
+                         const float *k_scale, int64_t blkk, const void *vt_bf16, int64_t lpad,
+                         void *o_bf16, int64_t batch, int64_t hq, int64_t hkv, int64_t lq, int64_t lk,
                          int64_t dim, int64_t q_sb, int64_t q_sh, int64_t q_sl, int64_t k_sb,
-                         int64_t k_sh, int64_t k_sl, int64_t v_sb, int64_t v_sh, int64_t v_sl,
-                         int64_t o_sb, int64_t o_sh, int64_t o_sl, float sm_scale, int32_t causal,
-                         void *stream);
+                         int64_t k_sh, int64_t k_sl, int64_t o_sb, int64_t o_sh, int64_t o_sl,
+                         float sm_scale, int32_t causal, void *stream);
 
 #ifdef __cplusplus
 }

@@ -8,16 +8,18 @@
 // contiguous load along K.
 //
 // MI355X mapping
-//   * Workgroup tile 256 (n) x 256 (m) x 64 (k), 4 wave64 in a 2 x 2 grid, each
-//     wave owning a 128 x 128 output tile = 8 x 8 v_mfma_i32_16x16x64_i8 per
-//     K step (256 accumulator registers, AGPR-resident).
+//   * Workgroup tile 256 (n) x 256 (m) x 128 (k), 4 wave64 in a 2 x 2 grid,
+//     each wave owning a 128 x 128 output tile = 2 x 8 x 8
+//     v_mfma_i32_16x16x64_i8 per K step (256 accumulator registers).
 //   * The W tile is the MFMA A operand and the activation tile the B operand,
 //     so each lane ends with 4 consecutive output columns of one row: the
 //     epilogue issues one 8-byte store per 16 x 16 sub-tile.
-//   * LDS double buffer (2 x 32 KiB).  Rows are 64 B; the 16-byte chunk index
-//     is XOR-swizzled with row bits 2..3 so the 16 lanes that read one chunk
-//     column of 16 consecutive rows hit distinct banks.  Global loads for
-//     step k+1 are issued before the MFMAs of step k.
+//   * K steps of 128 bytes through a 2-stage LDS ring (2 x 64 KiB) filled by
+//     global_load_lds_dwordx4 (direct to LDS, no staging registers) one step
+//     ahead of the MFMAs.  Rows are 128 B; the 16-byte chunk index is
+//     XOR-swizzled with row bits 1..3 (applied through each lane's source
+//     address).  A partial last K step (K % 128 != 0) is staged through
+//     registers with zero fill.
 //   * Tiles are renumbered so each XCD (workgroup id mod 8) owns a contiguous
 //     range, walked in groups of 8 m-tiles for L2 reuse of the A and W panels.
 #include "tu_common.h"
@@ -27,15 +29,26 @@ namespace {
 
 constexpr int kBM = 256;  // activation rows per workgroup
 constexpr int kBN = 256;  // weight rows (output columns) per workgroup
-constexpr int kBK = 64;   // bytes of K per step
-constexpr int kThreads = 256;
+constexpr int kBK = 128;  // bytes of K per step (two 64-deep MFMA slices)
+// Waves per workgroup: 2 along the weight rows x kWavesM along the activation
+// rows; each wave owns a 128 x (256 / kWavesM) output tile.
+#ifndef TU_GEMM_WAVES_M
+#define TU_GEMM_WAVES_M 4
+#endif
+constexpr int kWavesM = TU_GEMM_WAVES_M;
+constexpr int kWaves = 2 * kWavesM;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kFragsM = kBM / kWavesM / 16;  // 16-row activation fragments per wave
 constexpr int kGroupM = 8;
 
-__device__ __forceinline__ int swz(int row, int chunk) { return row * kBK + ((chunk ^ ((row >> 2) & 3)) << 4); }
+// LDS panel layout: 128-byte rows, the 16-byte chunk index XOR-swizzled with
+// row bits 1..3 (measured bank-conflict free for 16 lanes reading one chunk
+// of 16 consecutive rows; 64-byte rows with a 2-bit swizzle were not).
+__device__ __forceinline__ int swz(int row, int chunk) { return row * kBK + ((chunk ^ ((row >> 1) & 7)) << 4); }
 
 struct TileLoad {
-    i32x4 a[4];
-    i32x4 w[4];
+    i32x4 a[2048 / kThreads];
+    i32x4 w[2048 / kThreads];
 };
 
 // Loads the 256 x 64 B activation and weight panels of step k0 into registers.
@@ -45,10 +58,10 @@ __device__ __forceinline__ void load_tiles(TileLoad &t, const int8_t *__restrict
                                            const int8_t *__restrict__ w, int64_t m0, int64_t n0,
                                            int64_t m, int64_t n, int64_t k, int64_t k0, int tid) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < 2048 / kThreads; ++i) {
         const int id = tid + kThreads * i;
-        const int row = id >> 2;
-        const int chunk = id & 3;
+        const int row = id >> 3;
+        const int chunk = id & 7;
         const int64_t kk = k0 + chunk * 16;
         const int64_t ra = min(m0 + row, m - 1);
         const int64_t rw = min(n0 + row, n - 1);
@@ -64,10 +77,10 @@ __device__ __forceinline__ void load_tiles(TileLoad &t, const int8_t *__restrict
 
 __device__ __forceinline__ void store_tiles(const TileLoad &t, int8_t *lds_a, int8_t *lds_w, int tid) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < 2048 / kThreads; ++i) {
         const int id = tid + kThreads * i;
-        const int row = id >> 2;
-        const int chunk = id & 3;
+        const int row = id >> 3;
+        const int chunk = id & 7;
         *reinterpret_cast<i32x4 *>(lds_a + swz(row, chunk)) = t.a[i];
         *reinterpret_cast<i32x4 *>(lds_w + swz(row, chunk)) = t.w[i];
     }
@@ -89,68 +102,150 @@ __device__ __forceinline__ void tile_coords(int bid, int tiles_m, int tiles_n, i
     tn = in_group / gsm;
 }
 
+constexpr int kStages = 2;
+constexpr int kStageBytes = 2 * kBM * kBK;  // activation panel + weight panel
+typedef __attribute__((address_space(3))) void lds_void;
+
+// s_waitcnt immediate: at most n vector-memory operations outstanding (gfx9
+// encoding: vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
+constexpr int vmcnt_imm(int n) { return (n & 0xf) | (0x7 << 4) | (0xf << 8) | ((n >> 4) << 14); }
+
+// Per-lane source offsets of the direct-to-LDS loads.  Wave w fills the 1 KiB
+// blocks w * kBlocksPerWave .. of each panel; in block b, lane l writes LDS row
+// 8 b + l / 8, physical chunk l % 8, which holds logical chunk
+// (l % 8) ^ ((row >> 1) & 7) of that row.  Offsets are relative to the
+// panel's first row at K offset 0 (32-bit: a panel row index times K plus a
+// chunk offset; rows past the end are clamped, their results never stored).
+constexpr int kBlocksPerWave = 32 / kWaves;  // 1 KiB blocks of each 32 KiB panel
+
+struct LoadGeom {
+    uint32_t a_off[kBlocksPerWave];
+    uint32_t w_off[kBlocksPerWave];
+};
+
+__device__ __forceinline__ LoadGeom load_geom(int64_t m0, int64_t n0, int64_t m, int64_t n, int64_t k, int wave,
+                                              int lane) {
+    LoadGeom gm;
+#pragma unroll
+    for (int i = 0; i < kBlocksPerWave; ++i) {
+        const int row = 8 * (kBlocksPerWave * wave + i) + (lane >> 3);
+        const int c = (lane & 7) ^ ((row >> 1) & 7);
+        gm.a_off[i] = static_cast<uint32_t>((min(m0 + row, m - 1) - m0) * k + c * 16);
+        gm.w_off[i] = static_cast<uint32_t>((min(n0 + row, n - 1) - n0) * k + c * 16);
+    }
+    return gm;
+}
+
+// Direct-to-LDS loads of one full K step (k0 + 128 <= K) into a ring stage.
+__device__ __forceinline__ void issue_step(int8_t *stage, const int8_t *a_panel, const int8_t *w_panel,
+                                           const LoadGeom &gm, int64_t k0, int wave) {
+    const int8_t *ab = a_panel + k0;
+    const int8_t *wb = w_panel + k0;
+#pragma unroll
+    for (int i = 0; i < kBlocksPerWave; ++i) {
+        const int block = kBlocksPerWave * wave + i;
+        __builtin_amdgcn_global_load_lds(ab + gm.a_off[i], (lds_void *)(stage + block * 1024), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(wb + gm.w_off[i], (lds_void *)(stage + kBM * kBK + block * 1024), 16, 0, 0);
+    }
+}
+
+struct Frags {
+    i32x4 a[8];        // weight rows (MFMA A operand)
+    i32x4 b[kFragsM];  // activation rows (MFMA B operand)
+};
+
 template <bool kI32Out>
-__global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(
+__global__ __launch_bounds__(kThreads, kWaves / 4) void int8_gemm_kernel(
     const int8_t *__restrict__ a, const int8_t *__restrict__ w, const float *__restrict__ as,
     const float *__restrict__ ws, const float *__restrict__ bias, void *__restrict__ out,
     int64_t m, int64_t n, int64_t k, int tiles_m, int tiles_n) {
-    __shared__ __align__(16) int8_t lds[2][2][kBM * kBK];  // [buffer][a|w][rows*64]
+    __shared__ __align__(1024) int8_t lds[kStages][kStageBytes];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int wn = wave >> 1;  // which 128-row half of the W tile
-    const int wm = wave & 1;   // which 128-row half of the activation tile
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wn = wave / kWavesM;  // which 128-row half of the W tile
+    const int wm = wave % kWavesM;  // which activation-row slice of the tile
 
     int tm, tn;
     tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
     const int64_t m0 = static_cast<int64_t>(tm) * kBM;
     const int64_t n0 = static_cast<int64_t>(tn) * kBN;
+    const int8_t *a_panel = a + m0 * k;
+    const int8_t *w_panel = w + n0 * k;
+    const LoadGeom gm = load_geom(m0, n0, m, n, k, wave, lane);
 
-    i32x4 acc[8][8];
+    i32x4 acc[8][kFragsM];
 #pragma unroll
     for (int i = 0; i < 8; ++i)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[i][j] = i32x4{0, 0, 0, 0};
-
-    const int steps = static_cast<int>((k + kBK - 1) / kBK);
-    TileLoad t;
-    load_tiles(t, a, w, m0, n0, m, n, k, 0, tid);
-    store_tiles(t, lds[0][0], lds[0][1], tid);
-    __syncthreads();
+        for (int j = 0; j < kFragsM; ++j) acc[i][j] = i32x4{0, 0, 0, 0};
 
     const int frag_row = lane & 15;
     const int frag_chunk = lane >> 4;
-
-    for (int s = 0; s < steps; ++s) {
-        const int cur = s & 1;
-        if (s + 1 < steps) load_tiles(t, a, w, m0, n0, m, n, k, static_cast<int64_t>(s + 1) * kBK, tid);
-
-        const int8_t *la = lds[cur][0];
-        const int8_t *lw = lds[cur][1];
-        i32x4 bfrag[8];
+    // Fragments of 64-deep slice kk (0 or 1) of a stage.
+    auto load_frags = [&](Frags &f, const int8_t *stage, int kk) {
+        const int8_t *la = stage;
+        const int8_t *lw = stage + kBM * kBK;
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
-            bfrag[j] = *reinterpret_cast<const i32x4 *>(la + swz(wm * 128 + j * 16 + frag_row, frag_chunk));
+        for (int j = 0; j < kFragsM; ++j)
+            f.b[j] = *reinterpret_cast<const i32x4 *>(
+                la + swz(wm * 16 * kFragsM + j * 16 + frag_row, 4 * kk + frag_chunk));
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const i32x4 afrag =
-                *reinterpret_cast<const i32x4 *>(lw + swz(wn * 128 + i * 16 + frag_row, frag_chunk));
+        for (int i = 0; i < 8; ++i)
+            f.a[i] = *reinterpret_cast<const i32x4 *>(lw + swz(wn * 128 + i * 16 + frag_row, 4 * kk + frag_chunk));
+    };
+    auto mma = [&](const Frags &f) {
 #pragma unroll
-            for (int j = 0; j < 8; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(afrag, bfrag[j], acc[i][j], 0, 0, 0);
-        }
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+            for (int j = 0; j < kFragsM; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(f.a[i], f.b[j], acc[i][j], 0, 0, 0);
+    };
 
-        if (s + 1 < steps) store_tiles(t, lds[cur ^ 1][0], lds[cur ^ 1][1], tid);
+    const int full = static_cast<int>(k / kBK);
+    if (full > 0) {
+        issue_step(lds[0], a_panel, w_panel, gm, 0, wave);
+        if (full > 1) issue_step(lds[1], a_panel, w_panel, gm, kBK, wave);
+        if (full > 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * kBlocksPerWave));
+        else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
         __syncthreads();
+        Frags f0, f1;
+        load_frags(f0, lds[0], 0);
+#pragma clang loop unroll(disable)
+        for (int s = 0; s < full; ++s) {
+            // Slice 0 of step s on the MFMAs while slice 1 is read from LDS.
+            load_frags(f1, lds[s & 1], 1);
+            mma(f0);
+            // Step s + 1 resident and every wave done reading stage s.
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+            __syncthreads();
+            if (s + 2 < full) issue_step(lds[s & 1], a_panel, w_panel, gm, static_cast<int64_t>(s + 2) * kBK, wave);
+            // Slice 1 of step s on the MFMAs while slice 0 of step s + 1 is read.
+            if (s + 1 < full) load_frags(f0, lds[(s + 1) & 1], 0);
+            mma(f1);
+        }
+    }
+    if (full * kBK < k) {
+        // Partial last step: register loads with zero fill past K.
+        __syncthreads();
+        TileLoad t;
+        load_tiles(t, a, w, m0, n0, m, n, k, static_cast<int64_t>(full) * kBK, tid);
+        store_tiles(t, lds[0], lds[0] + kBM * kBK, tid);
+        __syncthreads();
+        Frags f;
+        load_frags(f, lds[0], 0);
+        mma(f);
+        load_frags(f, lds[0], 1);
+        mma(f);
     }
 
-    // acc[i][j][r] = C[m = m0 + wm*128 + 16j + (lane & 15)]
+    // acc[i][j][r] = C[m = m0 + wm*16*kFragsM + 16j + (lane & 15)]
     //                  [n = n0 + wn*128 + 16i + 4*(lane >> 4) + r]
     const int g = lane >> 4;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const int64_t row = m0 + wm * 128 + j * 16 + (lane & 15);
+    for (int j = 0; j < kFragsM; ++j) {
+        const int64_t row = m0 + wm * 16 * kFragsM + j * 16 + (lane & 15);
         if (row >= m) continue;
         float arow = 0.0f;
         if constexpr (!kI32Out) arow = as[row];

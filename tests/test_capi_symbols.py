@@ -1,0 +1,78 @@
+"""The C ABI: every entry point declared in include/tu_hip.h is exported by
+libtu_hip.so and described identically (argument count, return type) in the
+ctypes binding.  Nothing here launches GPU work."""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from comfyui_turing_utils_kernel import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "tu_hip.h")
+
+
+def _declarations():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    out = {}
+    for ret, name, args in re.findall(r"(const char \*|int32_t)\s*(tu_\w+)\(([^)]*)\);", text):
+        args = args.strip()
+        n = 0 if args in ("", "void") else len(args.split(","))
+        out[name] = (ret.strip(), n)
+    return out
+
+
+def test_header_parses():
+    decls = _declarations()
+    assert len(decls) >= 11
+    assert "tu_sage_attn_fwd" in decls and "tu_int8_gemm_bf16" in decls
+
+
+def test_binding_matches_header():
+    decls = _declarations()
+    assert set(decls) == set(_lib.SIGNATURES)
+    for name, (ret, nargs) in decls.items():
+        restype, argtypes = _lib.SIGNATURES[name]
+        assert len(argtypes) == nargs, name
+        assert restype is (ctypes.c_char_p if ret.startswith("const char") else ctypes.c_int32), name
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.fail(f"{_lib.LIB_PATH} is missing: {_lib.BUILD_HINT}")
+    return _lib.load()
+
+
+def test_library_exports_every_symbol(lib):
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True, text=True, check=True)
+    exported = {line.split()[-1] for line in out.stdout.splitlines() if " T " in line}
+    missing = set(_declarations()) - exported
+    assert not missing, missing
+    for name in _declarations():
+        assert hasattr(lib, name)
+
+
+def test_abi_version_and_error_channel(lib):
+    assert lib.tu_abi_version() == _lib.ABI_VERSION
+    assert isinstance(lib.tu_last_error(), bytes)
+
+
+def test_argument_errors_are_reported_without_launching(lib):
+    """Shape checks run on the host before any HIP call: a bad group size is
+    rejected with a message, and no device is touched."""
+    rc = lib.tu_convrot_quant_i8(None, None, None, 4, 100, 96, 0, None)
+    assert rc != 0
+    assert b"group" in lib.tu_last_error().lower()
+
+
+def test_package_import_fails_loudly_without_library(monkeypatch, tmp_path):
+    monkeypatch.setattr(_lib, "LIB_PATH", str(tmp_path / "missing.so"))
+    monkeypatch.setattr(_lib, "_lib", None)
+    with pytest.raises(RuntimeError, match="libtu_hip|build"):
+        _lib.load()

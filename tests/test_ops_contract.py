@@ -1,0 +1,122 @@
+"""Fake-tensor contracts, fullgraph-leaf behaviour and host-side error paths of
+the registered ops, mirroring the reference's contract tests
+(tests/test_kernel_custom_ops.py:194-266, tests/test_turing_sage_quant.py:88-122,
+tests/test_attention_correctness.py).  CPU only: meta tensors never reach the
+HIP library, and CPU tensors must be refused before any launch."""
+from __future__ import annotations
+
+import pytest
+import torch
+
+import comfyui_turing_utils_kernel as kernel
+from comfyui_turing_utils_kernel import ops, turing_sage  # noqa: F401
+from comfyui_turing_utils_kernel.turing_sage import core, quant
+from comfyui_turing_utils_kernel.turing_sage.correctness import (
+    attention_error_metrics,
+    require_attention_correctness,
+)
+
+META = "meta"
+
+
+@pytest.mark.parametrize("group", [128, 256])
+def test_convrot_fake_contract(group):
+    x = torch.empty((3, 512), dtype=torch.bfloat16, device=META)
+    q, s = torch.ops.turing_utils.bf16_int8_convrot_quantize(x, group)
+    assert q.shape == (3, 512) and q.dtype == torch.int8 and q.device.type == META
+    assert s.shape == (3, 1) and s.dtype == torch.float32
+
+
+def test_linear_and_epilogue_fake_contracts():
+    activation = torch.empty((7, 128), dtype=torch.int8, device=META)
+    weight = torch.empty((64, 128), dtype=torch.int8, device=META)
+    row_scale = torch.empty((7,), dtype=torch.float32, device=META)
+    column_scale = torch.empty((64,), dtype=torch.float32, device=META)
+    out = torch.ops.turing_utils.int8_linear(activation, weight, row_scale, column_scale)
+    assert out.shape == (7, 64) and out.dtype == torch.bfloat16
+    acc = torch.ops.turing_utils.int8_gemm_i32(activation, weight)
+    assert acc.shape == (7, 64) and acc.dtype == torch.int32
+    accumulator = torch.empty((7, 80), dtype=torch.int32, device=META)
+    epi = torch.ops.turing_utils.dequantize_int8_bf16(accumulator, row_scale, column_scale, 64)
+    assert epi.shape == (7, 64) and epi.dtype == torch.bfloat16
+    epi = torch.ops.turing_utils.dequantize_int8_bf16(accumulator, row_scale, column_scale)
+    assert epi.shape == (7, 80)
+
+
+def test_sage_fake_contract_and_fullgraph_leaf():
+    q = torch.empty((1, 4, 129, 128), dtype=torch.bfloat16, device=META)
+    k = torch.empty((1, 2, 151, 128), dtype=torch.bfloat16, device=META)
+    out = turing_sage.sageattn_compiled(q, k, k)
+    assert out.shape == q.shape and out.dtype == q.dtype and out.device.type == META
+    compiled = torch.compile(lambda a, b, c: turing_sage.sageattn_compiled(a, b, c), backend="eager", fullgraph=True)
+    assert compiled(q, k, k).shape == q.shape
+
+
+def test_linear_chain_is_a_fullgraph_leaf():
+    def chain(x, w, ws):
+        q, s = torch.ops.turing_utils.bf16_int8_convrot_quantize(x, 128)
+        return torch.ops.turing_utils.int8_linear(q, w, s.reshape(-1), ws)
+
+    x = torch.empty((5, 256), dtype=torch.bfloat16, device=META)
+    w = torch.empty((48, 256), dtype=torch.int8, device=META)
+    ws = torch.empty((48,), dtype=torch.float32, device=META)
+    out = torch.compile(chain, backend="eager", fullgraph=True)(x, w, ws)
+    assert out.shape == (5, 48) and out.dtype == torch.bfloat16
+
+
+def test_cpu_tensors_are_refused():
+    x = torch.zeros((4, 256), dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="CUDA|HIP"):
+        torch.ops.turing_utils.bf16_int8_convrot_quantize(x, 256)
+    a = torch.zeros((4, 128), dtype=torch.int8)
+    with pytest.raises(RuntimeError, match="CUDA|HIP"):
+        torch.ops.turing_utils.int8_linear(a, a, torch.ones(4), torch.ones(4))
+    q = torch.zeros((1, 2, 64, 128), dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="CUDA"):  # reference core.py raises ValueError here
+        core.sageattn(q, q, q)
+    with pytest.raises((RuntimeError, ValueError)):
+        quant.per_block_int8(q, q)
+
+
+def test_public_sage_api():
+    assert turing_sage.__all__ == [
+        "available", "w8a8_available", "split_prequantization_available", "fused_qk_preprocessing_available",
+        "sageattn", "sageattn_compiled", "prequantize_sageattn", "sageattn_from_prequantized", "preflight",
+    ]
+    assert turing_sage.w8a8_available() is False
+    assert kernel.__version__
+
+
+def test_preflight_refuses_cpu():
+    with pytest.raises(RuntimeError, match="GPU"):
+        turing_sage.preflight(torch.device("cpu"))
+
+
+# correctness gate (reference tests/test_attention_correctness.py:19-51)
+def test_metrics_accept_identical_tensors():
+    ref = torch.tensor(((1.0, -2.0), (0.5, 4.0)))
+    res = attention_error_metrics(ref.clone(), ref)
+    assert res.finite and res.max_abs == 0.0 and res.relative_l2 == 0.0
+    assert abs(res.cosine - 1.0) < 1e-6
+    require_attention_correctness(res, max_abs=0.0, relative_l2=0.0, cosine=0.999)
+
+
+def test_gate_reports_every_failed_bound():
+    res = attention_error_metrics(torch.tensor((1.0, float("nan"))), torch.tensor((0.0, 1.0)),
+                                  candidate_name="sol", reference_name="sage", selected_blocks=3, possible_blocks=4)
+    with pytest.raises(AssertionError, match="non-finite output") as raised:
+        require_attention_correctness(res, max_abs=0.1, relative_l2=0.1, cosine=0.99)
+    assert "selected 3/4" in str(raised.value)
+
+
+def test_gate_names_each_bound():
+    res = attention_error_metrics(torch.tensor((1.0, 0.0)), torch.tensor((0.0, 1.0)))
+    with pytest.raises(AssertionError) as raised:
+        require_attention_correctness(res, max_abs=0.1, relative_l2=0.1, cosine=0.99)
+    text = str(raised.value)
+    assert "max_abs" in text and "relative_l2" in text and "cosine" in text
+
+
+def test_shape_mismatch_fails_before_reduction():
+    with pytest.raises(AssertionError, match="shape"):
+        attention_error_metrics(torch.zeros(2), torch.zeros(3))

@@ -1,0 +1,150 @@
+"""Pins the ConvRot part of the CPU oracle (oracle/tu_oracle.c) without the GPU.
+
+Checks are chosen so that plausible mistakes fail one of them:
+  * the staged butterflies equal the dense Kronecker matrix of the reference's
+    R4 (convrot_quant.cu:104-116) -> catches a wrong sign pattern, stride or
+    stage order that changes the transform;
+  * orthogonality / involution / basis columns / the regular-row property;
+  * quantizer invariants and an independent re-derivation with torch's bf16
+    cast and numpy rint;
+  * the reference's own cross-check: staged and row-buffer quantizers give
+    bit-equal codes and scales within rtol 1e-6 (validate_compatible.py:43-64);
+  * the exhaustive proof that the GPU's reciprocal+FMA quotient gives the same
+    INT8 codes as IEEE division.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle
+from tests import inputs
+
+R4 = 0.5 * np.array([[1, 1, 1, -1], [1, 1, -1, 1], [1, -1, 1, 1], [-1, 1, 1, 1]], dtype=np.float64)
+H2 = np.array([[1, 1], [1, -1]], dtype=np.float64) / np.sqrt(2.0)
+
+
+def dense(group: int) -> np.ndarray:
+    """Dense transform; np.kron's first factor acts on the most significant digit
+    (stride 64), the last on the stride-1 digit."""
+    if group == 256:
+        return np.kron(R4, np.kron(R4, np.kron(R4, R4)))
+    return np.kron(H2, np.kron(R4, np.kron(R4, R4)))
+
+
+@pytest.mark.parametrize("group", [128, 256])
+def test_rotation_matches_dense_matrix(group):
+    rng = np.random.default_rng(group)
+    m = dense(group)
+    for _ in range(20):
+        x = rng.standard_normal(group).astype(np.float32) * rng.choice([1e-3, 1.0, 50.0])
+        y = oracle.rotate_group(x, group)
+        ref = m @ x.astype(np.float64)
+        np.testing.assert_allclose(y, ref, rtol=0, atol=4e-7 * np.abs(x).max() * 4)
+
+
+@pytest.mark.parametrize("group", [128, 256])
+def test_rotation_is_orthogonal_and_involutive(group):
+    m = dense(group)
+    np.testing.assert_allclose(m @ m.T, np.eye(group), atol=1e-12)
+    np.testing.assert_allclose(m, m.T, atol=1e-15)  # symmetric -> involution
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal(group).astype(np.float32)
+    twice = oracle.rotate_group(oracle.rotate_group(x, group), group)
+    np.testing.assert_allclose(twice, x, rtol=0, atol=2e-6 * np.abs(x).max())
+
+
+@pytest.mark.parametrize("group", [128, 256])
+def test_rotation_basis_columns_exact(group):
+    """e_i maps to column i; every entry is +-1/16 (G=256) or +-fp32(1/sqrt2)/8 (G=128),
+    exactly representable, so the comparison is bit-exact."""
+    m = dense(group)
+    c = np.float32(0.70710678118654752440)
+    for i in range(0, group, 7):
+        e = np.zeros(group, np.float32)
+        e[i] = 1.0
+        col = m[:, i]
+        expect = (np.sign(col) * (np.float32(1 / 16) if group == 256 else c / np.float32(8))).astype(np.float32)
+        np.testing.assert_array_equal(oracle.rotate_group(e, group), expect)
+
+
+def test_regular_row_property_distinguishes_groups():
+    """Every R4 row sums to 1, so a constant row is a fixed point of the G=256
+    transform; the G=128 transform (H2 on the top digit) is not regular."""
+    x = np.full(256, 3.0, np.float32)
+    np.testing.assert_array_equal(oracle.rotate_group(x, 256), x)
+    y = oracle.rotate_group(np.full(128, 3.0, np.float32), 128)
+    assert np.all(y[64:] == 0) and np.allclose(y[:64], 3.0 * np.sqrt(2), rtol=1e-6)
+
+
+def test_bf16_rounding_matches_torch():
+    rng = np.random.default_rng(3)
+    x = np.concatenate([
+        (rng.standard_normal(200000) * 10.0 ** rng.integers(-30, 30, 200000)).astype(np.float32),
+        np.array([0.0, -0.0, 1.0, -1.0, 3.3895313e38, -3.3895313e38, 1e-40, -1e-40, np.inf, -np.inf], np.float32),
+        # ties: mantissa low half exactly 0x8000 with even and odd upper halves
+        np.array([0x3f808000, 0x3f818000, 0xbf808000, 0x00008000], np.uint32).view(np.float32),
+    ]).astype(np.float32)
+    got = oracle.f32_to_bf16_bits(x)
+    ref = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    np.testing.assert_array_equal(got, ref)
+    assert oracle.f32_to_bf16_bits(np.array([np.nan], np.float32))[0] == 0x7FFF  # canonical NaN
+
+
+def _rows_y(x_bits: np.ndarray, group: int) -> np.ndarray:
+    xf = oracle.bf16_bits_to_f32(x_bits).reshape(x_bits.shape)
+    m, k = xf.shape
+    y = np.empty_like(xf)
+    for r in range(m):
+        for g in range(k // group):
+            y[r, g * group:(g + 1) * group] = oracle.rotate_group(xf[r, g * group:(g + 1) * group], group)
+    return y
+
+
+@pytest.mark.parametrize("group", [128, 256])
+def test_quantizer_invariants_and_rederivation(group):
+    x = inputs.activation(24, 1536, 11)
+    xb = inputs.bits(x)
+    q, s = oracle.convrot_quant(xb, group)
+    y = _rows_y(xb, group)
+    absmax = np.abs(y).max(axis=1)
+    expect_scale = np.maximum(np.minimum(absmax, np.float32(3.38953139e38)) / np.float32(127), np.float32(1e-30))
+    np.testing.assert_array_equal(s.view(np.uint32), expect_scale.astype(np.float32).view(np.uint32))
+    # independent re-derivation with torch's bf16 cast and numpy rint
+    yb = torch.from_numpy(y).to(torch.bfloat16).float()
+    rs = torch.from_numpy(s).to(torch.bfloat16).float()[:, None]
+    ref = torch.clamp(torch.round((yb / rs).to(torch.bfloat16).float()), -128, 127).to(torch.int8).numpy()
+    np.testing.assert_array_equal(q, ref)
+    assert q.min() >= -128 and q.max() <= 127
+    assert np.all(np.abs(q.astype(np.int32)).max(axis=1) >= 126)
+    # dequantization error bound: half a code plus the bf16 double rounding
+    err = np.abs(q.astype(np.float64) - y.astype(np.float64) / rs.numpy())
+    assert np.all(err <= 0.5 + np.abs(y / rs.numpy()) * 2.0 ** -7 + 1e-6)
+
+
+def test_quantizer_zero_and_extreme_rows():
+    x = np.zeros((3, 256), np.float32)
+    x[1, 5] = 1e4
+    x[2, :] = -2.5e38
+    q, s = oracle.convrot_quant(oracle.f32_to_bf16_bits(x), 256)
+    assert np.all(q[0] == 0) and s[0] == np.float32(1e-30)
+    assert np.abs(q[1].astype(int)).max() == 127
+    assert np.isfinite(s[2]) and np.abs(q[2].astype(int)).max() >= 126
+
+
+@pytest.mark.parametrize("group", [128, 256])
+def test_staged_equals_row_buffer(group):
+    """The reference's own KAT: staged and row-buffer quantizers produce bit-equal
+    codes, scales within rtol 1e-6 (kernel/scripts/validate_compatible.py:43-64)."""
+    xb = inputs.bits(inputs.activation(64, 5120, 21))
+    q1, s1 = oracle.convrot_quant(xb, group, staged=False)
+    q2, s2 = oracle.convrot_quant(xb, group, staged=True)
+    np.testing.assert_array_equal(q1, q2)
+    np.testing.assert_allclose(s1, s2, rtol=1e-6, atol=5e-8)
+
+
+def test_markstein_quotient_is_code_exact_on_the_quantizer_domain():
+    bad, pairs, fp32_diff = oracle.check_markstein_quant()
+    assert pairs > 1_000_000_000
+    assert bad == 0, f"{bad} (value, scale) pairs give a different INT8 code"

@@ -12,13 +12,18 @@ in HBM:
     INT8 quantization, INT8 QK^T + online softmax + bf16 PV.
 value = (sum of 2MNK over the linears + 4 B H L^2 D) / step time, in TOPS.
 
-Per-kernel average durations come from HIP events recorded on the launch
-stream inside the timed region.  The roofline entry is for the kernel with the
-largest total time.  cpu_baseline times the CPU oracle (oracle/, a plain-C
-restatement of the reference arithmetic) on a bounded sample of the same
-workload on this host's cores.
+Per-kernel average durations come from HIP events recorded on torch's current
+stream, which is the stream every op of this package launches on, inside the
+timed region.  The roofline entry is for the kernel with the largest total
+time; its ``traffic`` (HBM bytes per launch) is read from profiles/traffic.json,
+written from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes of this script
+(``--copy-calibration`` adds the 1 GiB reference copy those passes scale by).
+cpu_baseline times the CPU oracle (oracle/, a plain-C restatement of the
+reference arithmetic) on a bounded sample of the same workload on this host's
+cores, next to the reference's PyTorch CPU fallback on the same sample.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+                       [--cpu-seconds S] [--copy-calibration]
 """
 from __future__ import annotations
 
@@ -48,7 +53,9 @@ def parse_args():
     p.add_argument("--steps", type=int, default=10)
     p.add_argument("--warmup", type=int, default=2)
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--cpu-seconds", type=float, default=15.0, help="approximate CPU baseline budget")
+    p.add_argument("--cpu-seconds", type=float, default=30.0, help="approximate CPU baseline budget (s)")
+    p.add_argument("--copy-calibration", action="store_true",
+                   help="after the timed steps, copy 1 GiB once (HBM-counter calibration for rocprofv3 --pmc)")
     return p.parse_args()
 
 
@@ -138,6 +145,15 @@ def main():
     t1 = time.perf_counter()
     ms_per_step = (t1 - t0) * 1e3 / args.steps
     kernels = timer.summary(args.steps)
+    if args.copy_calibration:
+        # one elementwise kernel that reads and writes exactly 1 GiB: the
+        # reference point for the FETCH_SIZE / WRITE_SIZE counters
+        src = torch.ones(1 << 28, dtype=torch.int32, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+        del src, dst
 
     lin_ops = sum(2.0 * M_TOKENS * n * k for _, k, n, *_ in lin)
     attn_ops = 4.0 * ATTN["b"] * ATTN["h"] * ATTN["l"] ** 2 * ATTN["d"]
@@ -178,7 +194,7 @@ def main():
         "peak": peak,
         "unit": "TFLOP/s" if bound == "mfma" else "GB/s",
         "frac": achieved / peak,
-        "traffic": None,
+        "traffic": measured_traffic(dominant),
     }
 
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds)
@@ -212,58 +228,110 @@ def main():
     return 0
 
 
-def cpu_baseline(budget_s: float):
-    """CPU oracle (port) on a bounded sample of the same workload.
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 
-    Sample: ffn-up linear on S rows (ConvRot quantize G=128 + exact int GEMM +
-    epilogue, K=5120, N=13824) and the Sage attention oracle on R query rows of
-    config 3 (full 32760-key softmax per row).  Both are expressed as TOPS of
-    the same op count the GPU figure uses, and combined with the GPU step's
-    op mix (linears vs attention) into one step-equivalent rate.
+
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of ``kernel`` at this workload, from the committed
+    rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes (scaled by the same counters
+    on a 1 GiB copy), or None when no such measurement is committed."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            entry = json.load(f).get(kernel)
+    except (OSError, ValueError):
+        return None
+    return None if entry is None else float(entry["bytes_per_launch"])
+
+
+def cpu_baseline(budget_s: float):
+    """CPU baseline on a bounded sample of the same workload, on this host's cores.
+
+    ``value`` is the CPU oracle (oracle/, the plain-C restatement of the
+    reference arithmetic; kind "port"): ConvRot quantize (G=128) + exact INT8
+    GEMM + epilogue of the ffn-up linear (K=5120, N=13824) on a sample of rows,
+    and Sage attention (K mean, per-128-token INT8 Q/K, softmax over all 32760
+    keys, bf16 P) on a sample of query rows of head 0 of config 3.  Sample sizes
+    are calibrated so the whole baseline takes about ``budget_s`` seconds.  The
+    two rates are combined with the GPU step's op mix into one step-equivalent
+    rate.  ``torch_fallback`` times the reference's PyTorch CPU fallback on the
+    same sample (bf16 linear on the dequantized weight; bf16 SDPA).
     """
     import numpy as np
+    import torch
 
     from oracle import oracle
     from tests import inputs
 
-    threads = os.cpu_count() or 1
+    threads = oracle.num_threads()
     k, n = 5120, 13824
-    rows = 64
-    x = inputs.activation(rows, k, 5)
+    x_all = inputs.activation(4096, k, 5)
     w, ws, _ = inputs.weights(n, k, 5, with_bias=False)
-    xb, wn, wsn = inputs.bits(x), w.numpy(), ws.numpy()
-    t0 = time.perf_counter()
-    qa, sa = oracle.convrot_quant(xb, GROUP)
-    acc = oracle.int8_gemm_i32(qa, wn)
-    oracle.epilogue_bf16(acc, sa, wsn)
-    t_lin = time.perf_counter() - t0
+    wn, wsn = w.numpy(), ws.numpy()
+
+    def oracle_linear(rows):
+        t0 = time.perf_counter()
+        qa, sa = oracle.convrot_quant(inputs.bits(x_all[:rows]), GROUP)
+        oracle.epilogue_bf16(oracle.int8_gemm_i32(qa, wn), sa, wsn)
+        return time.perf_counter() - t0
+
+    probe = oracle_linear(16)
+    rows = int(min(4096, max(16, 0.35 * budget_s / probe * 16)))
+    t_lin = oracle_linear(rows)
     lin_tops = 2.0 * rows * n * k / t_lin / 1e12
 
     l, d = ATTN["l"], ATTN["d"]
-    g = np.random.default_rng(0)
-    q8 = g.integers(-127, 128, (1, 1, 256, d), dtype=np.int8)
-    k8 = g.integers(-127, 128, (1, 1, l, d), dtype=np.int8)
-    vb = inputs.bits(inputs.attention(1, 1, l, d, 2)[2])
-    qs = np.full((1, 1, 2), 1e-3, np.float32)
-    ks = np.full((1, 1, (l + 127) // 128), 1e-3, np.float32)
-    rows_a = max(threads, 16)
-    sel = np.stack([np.zeros(rows_a, np.int64), np.zeros(rows_a, np.int64), np.arange(rows_a) % 256], 1)
-    t0 = time.perf_counter()
-    oracle.sage_attn_rows(q8, qs, 128, k8, ks, 128, vb, d ** -0.5, sel)
-    t_att = time.perf_counter() - t0
+    q, kk, v = inputs.attention(1, 1, l, d, 2)
+    qb, kb, vb = inputs.bits(q), inputs.bits(kk), inputs.bits(v)
+
+    def oracle_attention(nrows):
+        t0 = time.perf_counter()
+        mean = oracle.sage_kmean(kb)
+        k8, ks = oracle.sage_quant(kb, BLK, mean)
+        q8, qs = oracle.sage_quant(qb[:, :, :nrows], BLK)
+        sel = np.stack([np.zeros(nrows, np.int64), np.zeros(nrows, np.int64), np.arange(nrows)], 1)
+        oracle.sage_attn_rows(q8, qs, BLK, k8, ks, BLK, vb, d ** -0.5, sel)
+        return time.perf_counter() - t0
+
+    probe = oracle_attention(threads)
+    rows_a = int(min(l, max(threads, 0.35 * budget_s / probe * threads)))
+    t_att = oracle_attention(rows_a)
     att_tops = 4.0 * rows_a * l * d / t_att / 1e12
 
-    lin_ops = sum(2.0 * M_TOKENS * nn * kk for _, kk, nn in LINEARS)
+    lin_ops = sum(2.0 * M_TOKENS * nn * kk_ for _, kk_, nn in LINEARS)
     attn_ops = 4.0 * ATTN["b"] * ATTN["h"] * ATTN["l"] ** 2 * d
     step_s = lin_ops / (lin_tops * 1e12) + attn_ops / (att_tops * 1e12)
+
+    # reference's PyTorch CPU fallback on the same sample
+    wd = (w.float() * ws[:, None]).to(torch.bfloat16)
+    xs = x_all[:rows]
+    torch.nn.functional.linear(xs[:16], wd)
+    t0 = time.perf_counter()
+    torch.nn.functional.linear(xs, wd)
+    t_tl = time.perf_counter() - t0
+    qs_ = q[:, :, :rows_a]
+    torch.nn.functional.scaled_dot_product_attention(qs_[:, :, :16], kk, v)
+    t0 = time.perf_counter()
+    torch.nn.functional.scaled_dot_product_attention(qs_, kk, v)
+    t_ta = time.perf_counter() - t0
+    tl_tops = 2.0 * rows * n * k / t_tl / 1e12
+    ta_tops = 4.0 * rows_a * l * d / t_ta / 1e12
+    torch_step = lin_ops / (tl_tops * 1e12) + attn_ops / (ta_tops * 1e12)
     return {
         "value": (lin_ops + attn_ops) / step_s / 1e12,
         "unit": "TOPS",
         "cores": threads,
         "kind": "port",
-        "sample": f"oracle ffn-up linear on {rows} rows ({t_lin:.2f} s, {lin_tops:.4f} TOPS) and Sage "
-                  f"attention oracle on {rows_a} query rows x 32760 keys ({t_att:.2f} s, {att_tops:.4f} TOPS), "
-                  f"combined with the step's op mix; projected step {step_s:.0f} s",
+        "sample": f"CPU oracle: ffn-up ConvRot W8A8 linear on {rows} of 32760 rows ({t_lin:.2f} s, "
+                  f"{lin_tops:.4f} TOPS) and Sage attention on {rows_a} query rows x 32760 keys of one head "
+                  f"({t_att:.2f} s, {att_tops:.4f} TOPS), combined with the step's op mix; "
+                  f"projected step {step_s:.0f} s",
+        "torch_fallback": {
+            "value": (lin_ops + attn_ops) / torch_step / 1e12,
+            "unit": "TOPS",
+            "cores": torch.get_num_threads(),
+            "sample": f"bf16 linear on the dequantized weight ({rows} rows, {tl_tops:.3f} TFLOP/s) and bf16 "
+                      f"SDPA ({rows_a} query rows, {ta_tops:.3f} TFLOP/s); projected step {torch_step:.1f} s",
+        },
     }
 
 

@@ -42,6 +42,8 @@ def lib():
             if not os.path.exists(LIB_PATH):
                 build()
             L = ctypes.CDLL(LIB_PATH)
+            L.or_num_threads.restype = _i32
+            L.or_num_threads.argtypes = []
             L.or_f32_to_bf16_rne.restype = ctypes.c_uint16
             L.or_f32_to_bf16_rne.argtypes = [ctypes.c_float]
             L.or_bf16_to_f32.restype = ctypes.c_float
@@ -73,6 +75,11 @@ def lib():
                                             _p, _i64, _p]
             _lib = L
     return _lib
+
+
+def num_threads() -> int:
+    """OpenMP threads the oracle's parallel loops run on."""
+    return int(lib().or_num_threads())
 
 
 def _ptr(a: np.ndarray) -> int:

@@ -29,6 +29,7 @@
  *                             on raw inputs (reference gate rtol .08 / atol .06)
  */
 #include <math.h>
+#include <omp.h>
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
@@ -51,6 +52,9 @@ OR_API uint16_t or_f32_to_bf16_rne(float value) {
 }
 
 OR_API float or_bf16_to_f32(uint16_t v) { return u2f((uint32_t)v << 16); }
+
+/* Threads the OpenMP loops below use (OMP_NUM_THREADS or the core count). */
+OR_API int or_num_threads(void) { return omp_get_max_threads(); }
 
 static inline float bf16_round_f32(float v) { return or_bf16_to_f32(or_f32_to_bf16_rne(v)); }
 

@@ -39,6 +39,7 @@ for _p in (ROOT, os.path.join(ROOT, "comfyui-turing-utils_amd")):
         sys.path.insert(0, _p)
 
 PEAK_INT8_TOPS = 5000.0     # MI355X published dense INT8 MFMA, 5.0 POP/s
+PEAK_BF16_TFLOPS = 2500.0   # MI355X published dense BF16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E, 8 TB/s
 M_TOKENS = 32760
 LINEARS = (("qkv", 5120, 15360), ("out", 5120, 5120), ("ffn_up", 5120, 13824), ("ffn_down", 13824, 5120))
@@ -50,8 +51,8 @@ BLK = 128
 def parse_args():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=10)
-    p.add_argument("--warmup", type=int, default=2)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=30.0, help="approximate CPU baseline budget (s)")
     p.add_argument("--copy-calibration", action="store_true",
@@ -145,6 +146,7 @@ def main():
     t1 = time.perf_counter()
     ms_per_step = (t1 - t0) * 1e3 / args.steps
     kernels = timer.summary(args.steps)
+    copy_gbs = copy_bandwidth(torch, dev)
     if args.copy_calibration:
         # one elementwise kernel that reads and writes exactly 1 GiB: the
         # reference point for the FETCH_SIZE / WRITE_SIZE counters
@@ -183,6 +185,12 @@ def main():
         else:
             rec["gbs"] = amount / sec / 1e9
             rec["frac_hbm_peak"] = rec["gbs"] / PEAK_HBM_GBS
+            rec["frac_copy"] = rec["gbs"] / copy_gbs
+    # attention: half its ops are INT8 (QK^T), half BF16 (PV); time at the
+    # mixed peak relative to the measured time
+    rec = kernels["sage_attn"]
+    rec["frac_mixed_peak"] = (attn_ops / 2 / (PEAK_INT8_TOPS * 1e12) + attn_ops / 2 / (PEAK_BF16_TFLOPS * 1e12)) / (
+        rec["ms_avg"] * 1e-3)
     dominant = max(kernels, key=lambda n: kernels[n]["ms_per_step"])
     bound, amount = work[dominant]
     achieved = kernels[dominant]["tops"] if bound == "mfma" else kernels[dominant]["gbs"]
@@ -222,10 +230,29 @@ def main():
         },
         "kernels": kernels,
         "roofline": roofline,
+        "hbm_copy_gbs": copy_gbs,
         "cpu_baseline": cpu,
     }
     print(json.dumps(record))
     return 0
+
+
+def copy_bandwidth(torch, dev) -> float:
+    """Achievable HBM bandwidth on this GPU: GB/s of a 1 GiB read + 1 GiB write
+    elementwise kernel (median of 5, HIP events), outside the timed region."""
+    src = torch.ones(1 << 28, dtype=torch.int32, device=dev)
+    dst = torch.empty_like(src)
+    times = []
+    for _ in range(6):
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        torch.neg(src, out=dst)
+        b.record()
+        b.synchronize()
+        times.append(a.elapsed_time(b))
+    del src, dst
+    return 2.0 * (1 << 30) / (sorted(times[1:])[2] * 1e-3) / 1e9
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
@@ -316,11 +343,19 @@ def cpu_baseline(budget_s: float):
     tl_tops = 2.0 * rows * n * k / t_tl / 1e12
     ta_tops = 4.0 * rows_a * l * d / t_ta / 1e12
     torch_step = lin_ops / (tl_tops * 1e12) + attn_ops / (ta_tops * 1e12)
+    cpu_model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            cpu_model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), "")
+    except OSError:
+        pass
     return {
         "value": (lin_ops + attn_ops) / step_s / 1e12,
         "unit": "TOPS",
         "cores": threads,
         "kind": "port",
+        "cpu_model": cpu_model,
+        "host_cpu_count": os.cpu_count(),
         "sample": f"CPU oracle: ffn-up ConvRot W8A8 linear on {rows} of 32760 rows ({t_lin:.2f} s, "
                   f"{lin_tops:.4f} TOPS) and Sage attention on {rows_a} query rows x 32760 keys of one head "
                   f"({t_att:.2f} s, {att_tops:.4f} TOPS), combined with the step's op mix; "

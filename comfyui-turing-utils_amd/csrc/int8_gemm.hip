@@ -8,15 +8,19 @@
 // contiguous load along K.
 //
 // MI355X mapping
-//   * Workgroup tile 256 (n) x 256 (m) x 128 (k), 4 wave64 in a 2 x 2 grid,
-//     each wave owning a 128 x 128 output tile = 2 x 8 x 8
-//     v_mfma_i32_16x16x64_i8 per K step (256 accumulator registers).
+//   * Workgroup tile 256 (n) x 256 (m) x 128 (k), 8 wave64 in a 2 (n) x 4 (m)
+//     grid, each wave owning a 128 x 64 output tile = 2 x 8 x 4
+//     v_mfma_i32_16x16x64_i8 per K step (128 accumulator registers).  One
+//     workgroup per CU, two waves per SIMD, so one wave's LDS fragment reads
+//     and barrier waits overlap the other's MFMAs.
 //   * The W tile is the MFMA A operand and the activation tile the B operand,
 //     so each lane ends with 4 consecutive output columns of one row: the
 //     epilogue issues one 8-byte store per 16 x 16 sub-tile.
 //   * K steps of 128 bytes through a 2-stage LDS ring (2 x 64 KiB) filled by
 //     global_load_lds_dwordx4 (direct to LDS, no staging registers) one step
-//     ahead of the MFMAs.  Rows are 128 B; the 16-byte chunk index is
+//     ahead of the MFMAs.  Within a step the two 64-deep fragment sets are
+//     double-buffered in registers: slice 1 is read from LDS while slice 0 is
+//     on the MFMAs, and slice 0 of the next step while slice 1 is.  Rows are 128 B; the 16-byte chunk index is
 //     XOR-swizzled with row bits 1..3 (applied through each lane's source
 //     address).  A partial last K step (K % 128 != 0) is staged through
 //     registers with zero fill.

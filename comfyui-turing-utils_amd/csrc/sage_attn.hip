@@ -11,12 +11,14 @@
 // to bf16 for the CDNA4 bf16 MFMA.
 //
 // MI355X mapping
-//   * Workgroup = 4 wave64 = 256 query rows (64 per wave) of one (batch,
-//     head); two workgroups per CU (256 registers per lane each), so the two
-//     waves sharing a SIMD overlap one's softmax VALU work with the other's
-//     MFMAs.
-//   * Keys stream in tiles of 64 through a double-buffered LDS filled with
-//     global_load_lds_dwordx4 (no staging registers).  V arrives
+//   * Workgroup = 4 wave64 = 64 QT query rows (16 QT per wave, QT = 2 by
+//     default) of one (batch, head); two workgroups per CU (256 registers per
+//     lane each), so the two waves sharing a SIMD overlap one's softmax VALU
+//     work with the other's MFMAs.
+//   * Keys stream in tiles of 64 through a 3-stage LDS ring (24 KiB a stage)
+//     filled with global_load_lds_dwordx4 (no staging registers), two tiles
+//     ahead of the MFMAs.  For pairs of unmasked tiles the QK^T of the next
+//     tile is issued before the softmax and PV of the current one.  V arrives
 //     pre-transposed (V^T, [d][key], keys padded to a multiple of 64 with
 //     zeros) from tu_sage_v_prep, so every MFMA operand is a plain LDS read.
 //   * Each tile is processed in two 32-key halves.  S^T = K Q^T runs on

@@ -49,10 +49,11 @@ int32_t tu_device_supported(int32_t device);
  * or 256), then quantizes per row to symmetric INT8:
  *   scale[r] = max(min(absmax_r, 3.38953139e38) / 127, 1e-30)
  *   q[r][c]  = clamp(rne(bf16(bf16(y[r][c]) / bf16(scale[r]))), -128, 127)
- * x: bf16 [rows, cols] (act 0) or [rows, 2*cols] (act 2, SwiGLU over the
- * [gate | up] halves), row-major contiguous.  q: int8 [rows, cols];
- * scale: fp32 [rows].  cols % group == 0.
- * act: 0 none, 2 SwiGLU.  (1, tanh-GELU, is reserved and rejected.)
+ * x: bf16 [rows, cols], row-major contiguous.  q: int8 [rows, cols];
+ * scale: fp32 [rows].  cols % group == 0; x and q 8-byte aligned.
+ * act must be 0 (no input activation).  1 (tanh-GELU) and 2 (SwiGLU over
+ * [gate | up] halves) are reserved for the fused-activation variants of the
+ * reference (convrot_quant.cu:145-156, :332-344) and are rejected.
  * Replaces turing_utils::bf16_int8_convrot_quantize
  * (kernel/comfyui_turing_utils_kernel/ops.py:257-282 ->
  *  kernel/csrc/bindings.cpp:603-646 -> kernel/csrc/turing/convrot_quant.cu:566-589). */

@@ -1,0 +1,96 @@
+"""GPU parity at BASELINE's full single-GPU sizes (configs 3 and 4) and at the
+empty-input edges.
+
+Full-size outputs are too large for the oracle to recompute in seconds, so
+each check combines sampled rows recomputed bit for bit (or within the
+attention gate) by the oracle with a size-independent property: rows of the
+linear and heads of the attention are independent, so the full-size run must
+equal, bit for bit, a run on a slice.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from comfyui_turing_utils_kernel.turing_sage import core
+from comfyui_turing_utils_kernel.turing_sage.correctness import (
+    attention_error_metrics,
+    require_attention_correctness,
+)
+from oracle import oracle
+from tests import inputs
+
+pytestmark = pytest.mark.gpu
+
+C4 = [("qkv", 5120, 15360), ("out", 5120, 5120), ("ffn_up", 5120, 13824), ("ffn_down", 13824, 5120)]
+M = 32760
+
+
+@pytest.mark.parametrize("idx", range(len(C4)))
+def test_c4_linear_full_size(gpu_device, idx):
+    name, k, n = C4[idx]
+    print(f"[c4 linear] {name} M={M} K={k} N={n}", flush=True)
+    x = inputs.activation(M, k, 3 + idx)
+    w, ws, _ = inputs.weights(n, k, 3 + idx, with_bias=False)
+    dev = gpu_device
+    xd, wd, wsd = x.to(dev), w.to(dev), ws.to(dev)
+    q, s = torch.ops.turing_utils.bf16_int8_convrot_quantize(xd, 128)
+    out = torch.ops.turing_utils.int8_linear(q, wd, s, wsd, None)
+    torch.cuda.synchronize(dev)
+    rows = np.sort(np.random.default_rng(idx).choice(M, 48, replace=False))
+    rows[-1] = M - 1  # last, partial M tile
+    q_ref, s_ref = oracle.convrot_quant(inputs.bits(x[rows]), 128)
+    np.testing.assert_array_equal(q[rows].cpu().numpy(), q_ref)
+    np.testing.assert_array_equal(s[rows].cpu().numpy().reshape(-1).view(np.uint32), s_ref.view(np.uint32))
+    ref = oracle.epilogue_bf16(oracle.int8_gemm_i32(q_ref, w.numpy()), s_ref, ws.numpy())
+    np.testing.assert_array_equal(inputs.bits(out[rows]), ref)
+    # row independence: a 1000-row slice starting mid-tile gives the same bits
+    lo = 12345
+    q2, s2 = torch.ops.turing_utils.bf16_int8_convrot_quantize(xd[lo:lo + 1000].contiguous(), 128)
+    out2 = torch.ops.turing_utils.int8_linear(q2, wd, s2, wsd, None)
+    assert torch.equal(q2, q[lo:lo + 1000]) and torch.equal(out2, out[lo:lo + 1000])
+
+
+def test_linear_empty_rows(gpu_device):
+    q = torch.empty((0, 256), dtype=torch.int8, device=gpu_device)
+    w = torch.zeros((64, 256), dtype=torch.int8, device=gpu_device)
+    out = torch.ops.turing_utils.int8_linear(q, w, torch.empty(0, device=gpu_device), torch.ones(64, device=gpu_device))
+    assert out.shape == (0, 64) and out.dtype == torch.bfloat16
+
+
+def test_attention_empty_sequence_is_refused(gpu_device):
+    q = torch.zeros((1, 2, 0, 128), dtype=torch.bfloat16, device=gpu_device)
+    k = torch.zeros((1, 2, 16, 128), dtype=torch.bfloat16, device=gpu_device)
+    with pytest.raises(ValueError, match="non-empty"):
+        core.sageattn(q, k, k)
+
+
+def test_c3_attention_full_size(gpu_device):
+    """Config 3 (B1 H40 L32760 D128, seed 2): 160 sampled rows vs the oracle
+    within the gate, and heads 5..7 recomputed alone equal the full run."""
+    print("[c3 attention] B1 H40 L32760 D128", flush=True)
+    q, k, v = inputs.attention(1, 40, 32760, 128, 2)
+    dev = gpu_device
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    out = core.sageattn(qd, kd, vd, tensor_layout="HND")
+    torch.cuda.synchronize(dev)
+    rng = np.random.default_rng(3)
+    rows = np.stack([np.zeros(160, np.int64), rng.integers(0, 40, 160), rng.integers(0, 32760, 160)], 1)
+    rows[0, 2], rows[1, 2] = 0, 32759
+    heads = np.unique(rows[:, 1])
+    # oracle on the sampled heads only (heads are independent)
+    remap = {h: i for i, h in enumerate(heads)}
+    qs_, ks_, vs_ = (t[:, torch.from_numpy(heads)] for t in (q, k, v))
+    kb = inputs.bits(ks_)
+    q8, qsc = oracle.sage_quant(inputs.bits(qs_), 128)
+    k8, ksc = oracle.sage_quant(kb, 128, oracle.sage_kmean(kb))
+    sub = rows.copy()
+    sub[:, 1] = [remap[h] for h in rows[:, 1]]
+    ref = oracle.sage_attn_rows(q8, qsc, 128, k8, ksc, 128, inputs.bits(vs_), 128 ** -0.5, sub)
+    got = out.float().cpu()[rows[:, 0], rows[:, 1], rows[:, 2]]
+    res = attention_error_metrics(got, torch.from_numpy(ref), candidate_name="hip", reference_name="oracle")
+    print(f"  cos={res.cosine:.6f} max_abs={res.max_abs:.3e}", flush=True)
+    require_attention_correctness(res, max_abs=2e-2, cosine=0.999)
+    part = core.sageattn(qd[:, 5:8].contiguous(), kd[:, 5:8].contiguous(), vd[:, 5:8].contiguous())
+    assert torch.equal(part, out[:, 5:8])

@@ -11,46 +11,45 @@
 // to bf16 for the CDNA4 bf16 MFMA.
 //
 // MI355X mapping
-//   * Workgroup = 4 wave64 = 64 QT query rows (16 QT per wave, QT = 2 by
-//     default) of one (batch, head); two workgroups per CU (256 registers per
-//     lane each), so the two waves sharing a SIMD overlap one's softmax VALU
-//     work with the other's MFMAs.
-//   * Keys stream in tiles of 64 through a 3-stage LDS ring (24 KiB a stage)
-//     filled with global_load_lds_dwordx4 (no staging registers), two tiles
-//     ahead of the MFMAs.  For pairs of unmasked tiles the QK^T of the next
-//     tile is issued before the softmax and PV of the current one.  V arrives
-//     pre-transposed (V^T, [d][key], keys padded to a multiple of 64 with
-//     zeros) from tu_sage_v_prep, so every MFMA operand is a plain LDS read.
-//   * Each tile is processed in two 32-key halves.  S^T = K Q^T runs on
-//     v_mfma_i32_16x16x64_i8 with the wave's Q rows resident as the B
-//     operand; a lane then holds 4 keys x 1 query per 16x16 block, so the row
-//     max is an integer max3 tree plus two cross-lane steps.  O^T = V^T P runs
-//     on v_mfma_f32_16x16x32_bf16 with P taken straight from registers.
-//   * Masking (Lk tail, causal diagonal) is compiled only into the tiles
-//     that need it.  The O rescale is lazy: the exponent base m_used only
-//     moves when a row maximum exceeds it by more than 8 (p <= 2^8), which
-//     after the first tiles is rare.
+//   * Workgroup = 8 wave64 = 256 query rows of one (batch, head): two groups
+//     of 4 waves, 32 rows (two 16-row fragments) per wave, one wave of each
+//     group per SIMD.  The groups run the same program one phase apart
+//     (ping-pong): while one group issues its MFMA cluster, the other runs its
+//     softmax VALU cluster on the same SIMD; a workgroup barrier separates the
+//     phases.
+//   * Keys stream in tiles of 64 through a 5-stage LDS ring (24 KiB a stage)
+//     filled by buffer_load_dwordx4 ... lds (no staging registers) from group
+//     0, four tiles ahead of the MFMAs.  V arrives pre-transposed (V^T,
+//     [d][key], keys padded to a multiple of 64 with zeros) from
+//     tu_sage_v_prep, so every MFMA operand is a plain LDS read.
+//   * S^T = K Q^T runs on v_mfma_i32_16x16x64_i8 with the wave's Q rows
+//     resident as the B operand, accumulators starting at the bit pattern of
+//     1.5 * 2^23 so that the result reads as a float with one subtraction; a
+//     lane then holds 4 keys x 1 query per 16x16 block, so the row max is an
+//     integer max3 tree plus two cross-lane steps.  O^T = V^T P runs on
+//     v_mfma_f32_16x16x32_bf16 with P taken straight from registers.
+//   * Masking (Lk tail, causal diagonal) is an integer pre-pass compiled only
+//     into the steps that need it.  The O rescale is lazy: the exponent base
+//     m_used only moves when a row maximum exceeds it by more than 8
+//     (p <= 2^8), which after the first tiles is rare.
 //   * LDS rows are 128 B with 16-byte chunks XOR-swizzled by row bits 1..3,
 //     conflict-free for the 16 lanes that read one chunk column.
 #include <type_traits>
-
-#ifndef TU_ATTN_QT
-#define TU_ATTN_QT 2
-#endif
 
 #include "tu_common.h"
 
 namespace tu {
 namespace {
 
-constexpr int kThreads = 256;
+constexpr int kThreads = 512;  // 8 waves: two groups of 4
 constexpr int kD = 128;
-// Query rows per wave = 16 * QT (template parameter); 4 waves per workgroup.
-constexpr int kBKey = 64;     // keys per tile
+constexpr int kQT = 2;                   // 16-row query fragments per wave
+constexpr int kWaveQ = 16 * kQT;         // query rows per wave
+constexpr int kBQ = 8 * kWaveQ;          // query rows per workgroup
+constexpr int kBKey = 64;                // keys per tile
 constexpr int kKTileBytes = kBKey * kD;      // int8 K tile, 8 KiB
 constexpr int kVTileBytes = kD * kBKey * 2;  // bf16 V^T tile, 16 KiB
 constexpr int kStageBytes = kKTileBytes + kVTileBytes;
-constexpr int kStages = 3;                   // LDS ring: current tile plus two in flight
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kRescaleSlack = 8.0f;        // log2 of the largest p allowed
 
@@ -62,6 +61,8 @@ typedef __attribute__((address_space(3))) void lds_void;
 // outstanding and leaves the other counters alone (gfx9 encoding: vmcnt in
 // bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
 constexpr int vmcnt_imm(int n) { return (n & 0xf) | (0x7 << 4) | (0xf << 8) | ((n >> 4) << 14); }
+// s_waitcnt immediate: at most n LDS/scalar-memory operations outstanding.
+constexpr int lgkmcnt_imm(int n) { return 0xf | (0x7 << 4) | ((n & 0xf) << 8) | (0x3 << 14); }
 
 // Row maxima / sums across the 4 lane groups (xor 16, xor 32) with the
 // gfx950 permlane swaps: VALU only, no LDS traffic.
@@ -92,21 +93,19 @@ __device__ __forceinline__ int kperm(int p) {
 
 // Per-lane constants of the tile loads and the MFMA operand reads.
 struct LaneGeom {
-    int k_row[2];        // K tile LDS row filled by this lane's two loads
-    uint32_t k_src[2];   // kperm(row) and byte offset of the source chunk
-    uint32_t v_src[4];   // byte offset of this lane's four V^T source chunks
+    uint32_t k_src[2];   // byte offset (from key0's row) of this lane's two K source chunks
+    uint32_t v_src[4];   // byte offset (from key0's column) of this lane's four V^T source chunks
     uint32_t k_rd[2];    // LDS byte offset of the K operand, chunk g / 4 + g
     uint32_t v_rd[2];    // LDS byte offset of the V^T operand, half 0 / 1
 };
 
-__device__ __forceinline__ LaneGeom lane_geom(int wave, int lane, int64_t lpad) {
+__device__ __forceinline__ LaneGeom lane_geom(int wave, int lane, int64_t k_sl, int64_t lpad) {
     LaneGeom gm;
     const int g = lane >> 4, lc = lane & 15, sw = (lc >> 1) & 7;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         const int row = (2 * wave + i) * 8 + (lane >> 3);
-        gm.k_row[i] = kperm(row);
-        gm.k_src[i] = static_cast<uint32_t>(((lane & 7) ^ ((row >> 1) & 7)) * 16);
+        gm.k_src[i] = static_cast<uint32_t>(kperm(row) * k_sl + ((lane & 7) ^ ((row >> 1) & 7)) * 16);
         gm.k_rd[i] = static_cast<uint32_t>(lc * 128 + (((4 * i + g) ^ sw) << 4));
         gm.v_rd[i] = static_cast<uint32_t>(kKTileBytes + lc * 128 + (((4 * i + g) ^ sw) << 4));
     }
@@ -118,37 +117,50 @@ __device__ __forceinline__ LaneGeom lane_geom(int wave, int lane, int64_t lpad) 
     return gm;
 }
 
-// Direct-to-LDS loads of the K and V^T tiles at key0 into one ring stage.
-// Each global_load_lds_dwordx4 moves 64 lanes x 16 B into 1 KiB of contiguous
-// LDS; the row permutation and chunk swizzle come from the source offsets.
-__device__ __forceinline__ void issue_tile(int8_t *stage, const int8_t *__restrict__ kp,
-                                           const uint16_t *__restrict__ vtp, const LaneGeom &gm, int64_t k_sl,
-                                           int64_t key0, int64_t lk, int wave) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int64_t key = min(key0 + gm.k_row[i], lk - 1);
-        const uint32_t off = static_cast<uint32_t>(key * k_sl) + gm.k_src[i];
-        __builtin_amdgcn_global_load_lds(kp + off, (lds_void *)(stage + (2 * wave + i) * 1024), 16, 0, 0);
-    }
-    const int8_t *vbase = reinterpret_cast<const int8_t *>(vtp + key0);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-        __builtin_amdgcn_global_load_lds(vbase + gm.v_src[i], (lds_void *)(stage + kKTileBytes + (4 * wave + i) * 1024),
-                                         16, 0, 0);
+// Buffer resource over [base, base + bytes): raw (stride 0) dword access;
+// reads at or past `bytes` return zeros.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), static_cast<short>(0), static_cast<int>(bytes),
+                                             0x00020000);
 }
 
-// S^T for one tile: s[kt][qt][r] = score of key 32 (kt >> 1) + 8 g + 4 (kt & 1) + r
-// and query 16 qt + lc of the wave.
-template <int QT>
-__device__ __forceinline__ void qk_tile(const int8_t *stage, const LaneGeom &gm, const i32x4 (&qf)[QT][2],
-                                        i32x4 (&s)[4][QT]) {
+// Direct-to-LDS buffer loads of the K and V^T tiles at key0 into one ring
+// stage.  Each buffer_load_dwordx4 ... lds moves 64 lanes x 16 B into 1 KiB of
+// contiguous LDS; the K row permutation and the chunk swizzle come from the
+// per-lane source offsets.  K rows at or past lk read as zeros (the buffer
+// range ends there); those keys are masked by the softmax.
+__device__ __forceinline__ void issue_tile(int8_t *stage, __amdgpu_buffer_rsrc_t krs, __amdgpu_buffer_rsrc_t vrs,
+                                           const LaneGeom &gm, uint32_t k_sl, uint32_t key0, int wave) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_void *)(stage + (2 * wave + i) * 1024), 16, gm.k_src[i],
+                                                 key0 * k_sl, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_void *)(stage + kKTileBytes + (4 * wave + i) * 1024), 16,
+                                                 gm.v_src[i], key0 * 2, 0, 0);
+}
+
+// The QK^T accumulators start at kBias, the bit pattern of 1.5 * 2^23, so
+// each int32 result is the float 1.5 * 2^23 + dot exactly (|dot| <= 2^21 for
+// D = 128 int8 codes): float(dot) is then one exact subtraction instead of a
+// conversion, and integer comparisons of the biased values still order the
+// dots.
+constexpr int kBias = 0x4B400000;
+constexpr float kBiasF = 12582912.0f;
+
+// S^T for one tile: s[kt][qt][r] = biased score of key 32 (kt >> 1) + 8 g +
+// 4 (kt & 1) + r and query 16 qt + lc of the wave.
+__device__ __forceinline__ void qk_tile(const int8_t *stage, const LaneGeom &gm, const i32x4 (&qf)[kQT][2],
+                                        i32x4 (&s)[4][kQT]) {
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt) {
         const i32x4 kf0 = *reinterpret_cast<const i32x4 *>(stage + gm.k_rd[0] + kt * 16 * 128);
         const i32x4 kf1 = *reinterpret_cast<const i32x4 *>(stage + gm.k_rd[1] + kt * 16 * 128);
 #pragma unroll
-        for (int qt = 0; qt < QT; ++qt) {
-            const i32x4 z = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf0, qf[qt][0], i32x4{0, 0, 0, 0}, 0, 0, 0);
+        for (int qt = 0; qt < kQT; ++qt) {
+            const i32x4 z = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf0, qf[qt][0], i32x4{kBias, kBias, kBias, kBias},
+                                                                  0, 0, 0);
             s[kt][qt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf1, qf[qt][1], z, 0, 0, 0);
         }
     }
@@ -157,72 +169,118 @@ __device__ __forceinline__ void qk_tile(const int8_t *stage, const LaneGeom &gm,
 // Softmax state of the wave: exponent base per query block, O^T and the row
 // sums (l, accumulated by an MFMA against a ones operand so every lane ends
 // with the complete sum for its query column).
-template <int QT>
 struct SoftmaxState {
-    float m_used[QT];
-    f32x4 acc_o[8][QT];
-    f32x4 acc_l[QT];
+    float m_used[kQT];
+    f32x4 acc_o[8][kQT];
+    f32x4 acc_l[kQT];
 };
 
-// Scales (and masks) the tile's raw scores into sf and returns per-query-block
-// row maxima in scaled units.  Masked tiles produce -inf for padded keys and,
-// for causal attention, keys after the query.
-template <int QT, bool kMask, bool kCausal>
-__device__ __forceinline__ void tile_rowmax(i32x4 (&s)[4][QT], const float (&f)[QT], float (&mrow)[QT], int key_lim,
-                                            int q_rel, int g, int lc) {
+// Masks a tile's biased scores in place: masked keys (key >= key_lim, and for
+// causal attention key > query) get the int bit pattern of -inf, which is
+// below every biased score as an integer and stays -inf through the
+// subtraction of the bias, so the row max ignores it and its p is 0.
+template <bool kCausal>
+__device__ __forceinline__ void mask_tile(i32x4 (&s)[4][kQT], int key_lim, int q_rel, int g, int lc) {
+    constexpr int kNegInf = static_cast<int>(0xFF800000u);
+    // key = c + 8 g with c a constant; key is masked iff c > t, with t the
+    // lane's last visible key minus 8 g.  The select is done with integer
+    // arithmetic (sign of t - c) to keep lane masks out of scalar registers.
 #pragma unroll
-    for (int qt = 0; qt < QT; ++qt) {
-        if constexpr (kMask) {
-            const int qi = q_rel + 16 * qt + lc;
-            float mx = -INFINITY;
+    for (int qt = 0; qt < kQT; ++qt) {
+        int t = key_lim - 1 - 8 * g;
+        if constexpr (kCausal) t = min(t, q_rel + 16 * qt + lc - 8 * g);
 #pragma unroll
-            for (int kt = 0; kt < 4; ++kt)
+        for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int key = 32 * (kt >> 1) + 8 * g + 4 * (kt & 1) + r;
-                    bool masked = key >= key_lim;
-                    if constexpr (kCausal) masked = masked || key > qi;
-                    const float x = masked ? -INFINITY : static_cast<float>(s[kt][qt][r]);
-                    s[kt][qt][r] = __float_as_int(x);  // masked tiles carry floats from here on
-                    mx = fmaxf(mx, x);
-                }
-            mrow[qt] = xmax_f32(mx) * f[qt];
-        } else {
-            int mi = imax3(s[0][qt][0], s[0][qt][1], s[0][qt][2]);
-            mi = imax3(mi, s[0][qt][3], s[1][qt][0]);
-            mi = imax3(mi, s[1][qt][1], s[1][qt][2]);
-            mi = imax3(mi, s[1][qt][3], s[2][qt][0]);
-            mi = imax3(mi, s[2][qt][1], s[2][qt][2]);
-            mi = imax3(mi, s[2][qt][3], s[3][qt][0]);
-            mi = imax3(mi, s[3][qt][1], s[3][qt][2]);
-            mi = max(mi, s[3][qt][3]);
-            mrow[qt] = static_cast<float>(xmax_i32(mi)) * f[qt];
-        }
+            for (int r = 0; r < 4; ++r) {
+                const int c = 32 * (kt >> 1) + 4 * (kt & 1) + r;
+                const int m = (t - c) >> 31;  // all ones when masked
+                s[kt][qt][r] = (s[kt][qt][r] & ~m) | (kNegInf & m);
+            }
     }
 }
 
-template <int QT>
-__device__ __forceinline__ void maybe_rescale(SoftmaxState<QT> &st, const float (&mrow)[QT]) {
+// Softmax of one tile: lazy rescale of O and l, then P = 2^(dot f - m_used)
+// rounded to bf16, packed as the PV B operands p[h][qt] (keys 32 h + 8 g ..
+// + 7 of query 16 qt + lc).
+//
+// The exponent base m_used of a query row only moves when some score of the
+// row exceeds it by more than kRescaleSlack; each lane tests its own 16
+// scores (an integer max tree on the biased values), and only when some lane
+// of the wave fails is the exact row maximum reduced across the 4 lanes that
+// hold the row.
+//
+// x = dot f - m_used is formed as fma(biased, f, c) with
+// c = -(1.5 * 2^23 f + m_used) when |c| < 2^12, which keeps the rounding of c
+// below 2^-13 in the exponent; otherwise the bias is subtracted exactly first.
+__device__ __forceinline__ void softmax_tile(const i32x4 (&s)[4][kQT], const float (&f)[kQT], SoftmaxState &st,
+                                             bf16x8 (&p)[2][kQT]) {
+    float mlane[kQT];
     bool need = false;
 #pragma unroll
-    for (int qt = 0; qt < QT; ++qt) need = need || (mrow[qt] > st.m_used[qt] + kRescaleSlack);
+    for (int qt = 0; qt < kQT; ++qt) {
+        int mi = imax3(s[0][qt][0], s[0][qt][1], s[0][qt][2]);
+        mi = imax3(mi, s[0][qt][3], s[1][qt][0]);
+        mi = imax3(mi, s[1][qt][1], s[1][qt][2]);
+        mi = imax3(mi, s[1][qt][3], s[2][qt][0]);
+        mi = imax3(mi, s[2][qt][1], s[2][qt][2]);
+        mi = imax3(mi, s[2][qt][3], s[3][qt][0]);
+        mi = imax3(mi, s[3][qt][1], s[3][qt][2]);
+        mi = max(mi, s[3][qt][3]);
+        mlane[qt] = (__int_as_float(mi) - kBiasF) * f[qt];
+        need = need || (mlane[qt] > st.m_used[qt] + kRescaleSlack);
+    }
     if (__any(need)) {
 #pragma unroll
-        for (int qt = 0; qt < QT; ++qt) {
-            const float m_new = fmaxf(st.m_used[qt], mrow[qt]);
-            const float alpha = __builtin_amdgcn_exp2f(st.m_used[qt] - m_new);
+        for (int qt = 0; qt < kQT; ++qt) {
+            const float m_new = fmaxf(st.m_used[qt], xmax_f32(mlane[qt]));
+            // a row with no visible key yet keeps m_used = -inf and alpha = 1
+            const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(st.m_used[qt] - m_new);
             st.m_used[qt] = m_new;
             st.acc_l[qt] *= alpha;
 #pragma unroll
             for (int ds = 0; ds < 8; ++ds) st.acc_o[ds][qt] *= alpha;
         }
     }
+    float c[kQT];
+    bool exact = false;
+#pragma unroll
+    for (int qt = 0; qt < kQT; ++qt) {
+        c[qt] = -__builtin_fmaf(kBiasF, f[qt], st.m_used[qt]);
+        exact = exact || !(fabsf(c[qt]) < 4096.0f);
+    }
+    auto make_p = [&](auto exact_tag) {
+#pragma unroll
+        for (int qt = 0; qt < kQT; ++qt) {
+            const float nm = -st.m_used[qt];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                u32x4 packed;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    float p2[2];
+#pragma unroll
+                    for (int t = 0; t < 2; ++t) {
+                        const int e = 2 * j + t;  // keys 32 h + 8 g + e
+                        const float v = __int_as_float(s[2 * h + (e >> 2)][qt][e & 3]);
+                        const float x = decltype(exact_tag)::value ? __builtin_fmaf(v - kBiasF, f[qt], nm)
+                                                                   : __builtin_fmaf(v, f[qt], c[qt]);
+                        p2[t] = __builtin_amdgcn_exp2f(x);
+                    }
+                    packed[j] =
+                        __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{p2[0], p2[1]}), bf16x2_t));
+                }
+                p[h][qt] = __builtin_bit_cast(bf16x8, packed);
+            }
+        }
+    };
+    if (__any(exact)) make_p(std::true_type{});
+    else make_p(std::false_type{});
 }
 
-// P = 2^(s f - m_used) as bf16 B operands and O^T += V^T P, l += 1 P.
-template <int QT, bool kMask>
-__device__ __forceinline__ void tile_pv(const int8_t *stage, const LaneGeom &gm, const i32x4 (&s)[4][QT],
-                                        const float (&f)[QT], SoftmaxState<QT> &st, const bf16x8 &ones) {
+// O^T += V^T P and l += 1 P for one tile.
+__device__ __forceinline__ void pv_tile(const int8_t *stage, const LaneGeom &gm, const bf16x8 (&p)[2][kQT],
+                                        SoftmaxState &st, const bf16x8 &ones) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         bf16x8 vf[8];
@@ -230,32 +288,99 @@ __device__ __forceinline__ void tile_pv(const int8_t *stage, const LaneGeom &gm,
         for (int ds = 0; ds < 8; ++ds)
             vf[ds] = *reinterpret_cast<const bf16x8 *>(stage + gm.v_rd[h] + ds * 16 * 128);
 #pragma unroll
-        for (int qt = 0; qt < QT; ++qt) {
-            const float nm = -st.m_used[qt];
-            u32x4 packed;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                float p2[2];
-#pragma unroll
-                for (int t = 0; t < 2; ++t) {
-                    const int e = 2 * j + t;           // keys 32 h + 8 g + e
-                    const int v = s[2 * h + (e >> 2)][qt][e & 3];
-                    const float x = kMask ? __int_as_float(v) : static_cast<float>(v);
-                    p2[t] = __builtin_amdgcn_exp2f(__builtin_fmaf(x, f[qt], nm));
-                }
-                packed[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{p2[0], p2[1]}), bf16x2_t));
-            }
-            const bf16x8 pf = __builtin_bit_cast(bf16x8, packed);
+        for (int qt = 0; qt < kQT; ++qt) {
 #pragma unroll
             for (int ds = 0; ds < 8; ++ds)
-                st.acc_o[ds][qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[ds], pf, st.acc_o[ds][qt], 0, 0, 0);
-            st.acc_l[qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pf, st.acc_l[qt], 0, 0, 0);
+                st.acc_o[ds][qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[ds], p[h][qt], st.acc_o[ds][qt], 0, 0, 0);
+            st.acc_l[qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, p[h][qt], st.acc_l[qt], 0, 0, 0);
         }
     }
 }
 
-template <int QT, bool kCausal>
-__global__ __launch_bounds__(kThreads, QT == 4 ? 1 : 2) void sage_attn_kernel(
+// MFMA cluster of a steady-state step: QK^T of the tile in kst and PV of the
+// tile in vst, with the LDS fragment reads issued a group of MFMAs ahead of
+// their first use.
+__device__ __forceinline__ void mfma_cluster(const int8_t *kst, const int8_t *vst, const LaneGeom &gm,
+                                             const i32x4 (&qf)[kQT][2], i32x4 (&s)[4][kQT],
+                                             const bf16x8 (&p)[2][kQT], SoftmaxState &st, const bf16x8 &ones) {
+    i32x4 kf[4][2];
+    bf16x8 va[8], vb[8];
+    // first-slice K fragments first: the first QK^T MFMAs only need those
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) kf[kt][i] = *reinterpret_cast<const i32x4 *>(kst + gm.k_rd[i] + kt * 16 * 128);
+#pragma unroll
+    for (int ds = 0; ds < 8; ++ds) va[ds] = *reinterpret_cast<const bf16x8 *>(vst + gm.v_rd[0] + ds * 16 * 128);
+    i32x4 z[4][kQT];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int qt = 0; qt < kQT; ++qt)
+            z[kt][qt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf[kt][0], qf[qt][0], i32x4{kBias, kBias, kBias, kBias},
+                                                              0, 0, 0);
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int qt = 0; qt < kQT; ++qt)
+            s[kt][qt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf[kt][1], qf[qt][1], z[kt][qt], 0, 0, 0);
+#pragma unroll
+    for (int ds = 0; ds < 8; ++ds) vb[ds] = *reinterpret_cast<const bf16x8 *>(vst + gm.v_rd[1] + ds * 16 * 128);
+#pragma unroll
+    for (int qt = 0; qt < kQT; ++qt) {
+#pragma unroll
+        for (int ds = 0; ds < 8; ++ds)
+            st.acc_o[ds][qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[ds], p[0][qt], st.acc_o[ds][qt], 0, 0, 0);
+        st.acc_l[qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, p[0][qt], st.acc_l[qt], 0, 0, 0);
+    }
+#pragma unroll
+    for (int qt = 0; qt < kQT; ++qt) {
+#pragma unroll
+        for (int ds = 0; ds < 8; ++ds)
+            st.acc_o[ds][qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vb[ds], p[1][qt], st.acc_o[ds][qt], 0, 0, 0);
+        st.acc_l[qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, p[1][qt], st.acc_l[qt], 0, 0, 0);
+    }
+    // Issue order, keeping at most 12 LDS reads in flight (the wait counter
+    // holds 15; past that the compiler can only wait for all of them):
+    // K reads, first QK^T MFMAs, first V^T half, second QK^T MFMAs, 4 PV
+    // MFMAs, second V^T half, remaining PV MFMAs.
+    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 12, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 32, 0);
+}
+
+// Workgroup barrier that does not wait for memory (the LDS ring hand-off is
+// ordered by an explicit s_waitcnt vmcnt before it) and that no instruction
+// is scheduled across: the ping-pong phases must not leak MFMAs into the
+// other group's VALU phase.
+__device__ __forceinline__ void wg_barrier() {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// Ping-pong schedule.  A workgroup is 8 waves in two groups of 4 (one wave of
+// each group per SIMD), 256 query rows of one (batch, head).  Each wave runs
+// the same sequence of clusters over the key tiles t = 0 .. T-1:
+//   C0 = QK(0), C1 = softmax(0), then per tile
+//   M_t = { QK(t+1), PV(t) }   (MFMA cluster; also LDS operand reads)
+//   V_t = { softmax(t+1) }     (VALU cluster)
+// with a workgroup barrier after every cluster.  Group 1 starts one barrier
+// later than group 0, so while one group is in an MFMA cluster the other is
+// in a VALU cluster on the same SIMD.  Group 0 alone streams the K and V^T
+// tiles through a kStages-deep LDS ring, kAhead tiles ahead, and waits for
+// the tile the next MFMA cluster reads before the barrier that opens it.
+constexpr int kStages = 5;
+constexpr int kAhead = kStages - 1;
+constexpr int kLoadsPerTile = 6;  // per group-0 wave: 2 K + 4 V^T 1 KiB blocks
+
+template <bool kCausal>
+__global__ __launch_bounds__(kThreads, 1) void sage_attn_kernel(
     const int8_t *__restrict__ q8, const float *__restrict__ q_scale, int blkq, const int8_t *__restrict__ k8,
     const float *__restrict__ k_scale, int kscale_shift, const uint16_t *__restrict__ vt, uint16_t *__restrict__ o,
     int hq, int groups, int64_t lq, int64_t lk, int64_t lpad, int64_t q_sb, int64_t q_sh, int64_t q_sl,
@@ -265,16 +390,16 @@ __global__ __launch_bounds__(kThreads, QT == 4 ? 1 : 2) void sage_attn_kernel(
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int grp = wave >> 2;
+    const int w4 = wave & 3;
     const int g = lane >> 4;
     const int lc = lane & 15;
 
     const int64_t bh = blockIdx.y;
     const int64_t b = bh / hq, h = bh % hq, hk = h / groups;
     const int64_t hkv = hq / groups;
-    constexpr int kWaveQ = 16 * QT;
-    constexpr int kBQ = 4 * kWaveQ;
     const int64_t qblock0 = static_cast<int64_t>(blockIdx.x) * kBQ;
-    const int64_t q0 = qblock0 + wave * kWaveQ;
+    const int64_t q0 = qblock0 + grp * (kBQ / 2) + w4 * kWaveQ;
 
     const int8_t *qp = q8 + b * q_sb + h * q_sh;
     const int8_t *kp = k8 + b * k_sb + hk * k_sh;
@@ -286,26 +411,39 @@ __global__ __launch_bounds__(kThreads, QT == 4 ? 1 : 2) void sage_attn_kernel(
     int64_t key_end = lk;
     if constexpr (kCausal) key_end = min(lk, qblock0 + kBQ);
     const int tiles = static_cast<int>((key_end + kBKey - 1) / kBKey);
-    const LaneGeom gm = lane_geom(wave, lane, lpad);
-    // Tiles past the last one re-load it (their results are never used), so
-    // the ring needs no guards.
-    auto tile_key0 = [&](int it) { return static_cast<int64_t>(min(it, tiles - 1)) * kBKey; };
-    issue_tile(lds[0], kp, vtp, gm, k_sl, tile_key0(0), lk, wave);
-    issue_tile(lds[1], kp, vtp, gm, k_sl, tile_key0(1), lk, wave);
+    // Tiles this wave computes: all of them, or up to its last query's
+    // diagonal when causal.  Later tiles only keep the barrier count.
+    int my_tiles = tiles;
+    if constexpr (kCausal)
+        my_tiles = static_cast<int>(min<int64_t>(tiles, max<int64_t>(1, (min(q0 + kWaveQ, lq) + kBKey - 1) / kBKey)));
+    // Tiles at or past this one need the Lk-tail or causal mask.
+    int64_t mask_from = lk / kBKey;
+    if constexpr (kCausal) mask_from = min(mask_from, q0 / kBKey);
+    const int first_masked = static_cast<int>(min<int64_t>(tiles, mask_from));
 
-    i32x4 qf[QT][2];
-    float qsc[QT];
+    const LaneGeom gm = lane_geom(w4, lane, k_sl, lpad);
+    const __amdgpu_buffer_rsrc_t krs = make_rsrc(kp, static_cast<uint32_t>(lk * k_sl));
+    const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vtp, static_cast<uint32_t>(kD * lpad * 2));
+    const uint32_t k_sl32 = static_cast<uint32_t>(k_sl);
+    auto tile_key0 = [&](int it) { return static_cast<uint32_t>(min(it, tiles - 1) * kBKey); };
+
+    i32x4 qf[kQT][2];
+    float qsc[kQT];
 #pragma unroll
-    for (int qt = 0; qt < QT; ++qt) {
+    for (int qt = 0; qt < kQT; ++qt) {
         const int64_t qi = min(q0 + 16 * qt + lc, lq - 1);
 #pragma unroll
         for (int ds = 0; ds < 2; ++ds)
             qf[qt][ds] = *reinterpret_cast<const i32x4 *>(qp + qi * q_sl + 64 * ds + 16 * g);
         qsc[qt] = q_scale[(b * hq + h) * nbq + qi / blkq] * sm_log2;
     }
-    SoftmaxState<QT> st;
+    if (grp == 0) {
 #pragma unroll
-    for (int qt = 0; qt < QT; ++qt) {
+        for (int j = 0; j < kAhead; ++j) issue_tile(lds[j], krs, vrs, gm, k_sl32, tile_key0(j), w4);
+    }
+    SoftmaxState st;
+#pragma unroll
+    for (int qt = 0; qt < kQT; ++qt) {
         st.m_used[qt] = -INFINITY;
         st.acc_l[qt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -315,79 +453,71 @@ __global__ __launch_bounds__(kThreads, QT == 4 ? 1 : 2) void sage_attn_kernel(
 #pragma unroll
     for (int e = 0; e < 8; ++e) ones[e] = static_cast<__bf16>(1.0f);
 
-    // Tiles at or past this key index need the Lk-tail or causal mask.
-    int64_t mask_from = (lk / kBKey) * kBKey;
-    if constexpr (kCausal) mask_from = min(mask_from, (q0 / kBKey) * kBKey);
-    const int first_masked = static_cast<int>(min<int64_t>(tiles, mask_from / kBKey));
+    i32x4 s[4][kQT];
+    bf16x8 pb[2][kQT];
 
-    // Software pipeline over key tiles.  Entering step(it), S(it) is in s_cur,
-    // tile it sits in stage it % 3 and tile it + 1's loads are in flight.
-    // The step waits for tile it + 1, refills the stage of tile it - 1 with
-    // tile it + 2, then overlaps QK(it + 1) (MFMA) with the row max of S(it)
-    // (VALU) and P(it) (VALU) with PV(it) (MFMA).
-    auto step = [&](int it, i32x4 (&s_cur)[4][QT], i32x4 (&s_next)[4][QT], auto mask_tag) {
-        constexpr bool kMask = decltype(mask_tag)::value;
-        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-        __syncthreads();
-        issue_tile(lds[(it + 2) % kStages], kp, vtp, gm, k_sl, tile_key0(it + 2), lk, wave);
-        const int64_t key0 = static_cast<int64_t>(it) * kBKey;
+    // softmax of tile it (it < my_tiles) into pb; mask_tag false promises
+    // it < first_masked.
+    auto softmax = [&](int it, auto mask_tag) {
         const float kscale = ks_row[it >> kscale_shift];
-        float f[QT];
+        float f[kQT];
 #pragma unroll
-        for (int qt = 0; qt < QT; ++qt) f[qt] = qsc[qt] * kscale;
-        const int key_lim = static_cast<int>(min(lk - key0, static_cast<int64_t>(kBKey)));
-        const int q_rel = static_cast<int>(max(min(q0 - key0, static_cast<int64_t>(kBKey)), static_cast<int64_t>(-kBQ)));
-        qk_tile<QT>(lds[(it + 1) % kStages], gm, qf, s_next);
-        float mrow[QT];
-        tile_rowmax<QT, kMask, kCausal>(s_cur, f, mrow, key_lim, q_rel, g, lc);
-        maybe_rescale<QT>(st, mrow);
-        tile_pv<QT, kMask>(lds[it % kStages], gm, s_cur, f, st, ones);
-    };
-    // Non-pipelined step for the boundary tiles (Lk tail, causal diagonal) and
-    // an odd leftover: it waits for every outstanding load, then computes
-    // QK(it), the row max, P and PV of the same tile.
-    auto step_single = [&](int it, auto mask_tag) {
-        constexpr bool kMask = decltype(mask_tag)::value;
-        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-        __syncthreads();
-        issue_tile(lds[(it + 2) % kStages], kp, vtp, gm, k_sl, tile_key0(it + 2), lk, wave);
-        const int64_t key0 = static_cast<int64_t>(it) * kBKey;
-        const float kscale = ks_row[it >> kscale_shift];
-        float f[QT];
-#pragma unroll
-        for (int qt = 0; qt < QT; ++qt) f[qt] = qsc[qt] * kscale;
-        const int key_lim = static_cast<int>(min(lk - key0, static_cast<int64_t>(kBKey)));
-        const int q_rel = static_cast<int>(max(min(q0 - key0, static_cast<int64_t>(kBKey)), static_cast<int64_t>(-kBQ)));
-        i32x4 s1[4][QT];
-        qk_tile<QT>(lds[it % kStages], gm, qf, s1);
-        float mrow[QT];
-        tile_rowmax<QT, kMask, kCausal>(s1, f, mrow, key_lim, q_rel, g, lc);
-        maybe_rescale<QT>(st, mrow);
-        tile_pv<QT, kMask>(lds[it % kStages], gm, s1, f, st, ones);
-    };
-
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-    __syncthreads();
-    int it = 0;
-    if (first_masked >= 2) {
-        i32x4 sa[4][QT], sb[4][QT];
-        qk_tile<QT>(lds[0], gm, qf, sa);
-#pragma clang loop unroll(disable)
-        for (; it + 2 <= first_masked; it += 2) {
-            step(it, sa, sb, std::false_type{});
-            step(it + 1, sb, sa, std::false_type{});
+        for (int qt = 0; qt < kQT; ++qt) f[qt] = qsc[qt] * kscale;
+        if (decltype(mask_tag)::value && it >= first_masked) {
+            const int64_t key0 = static_cast<int64_t>(it) * kBKey;
+            const int key_lim = static_cast<int>(min(lk - key0, static_cast<int64_t>(kBKey)));
+            const int q_rel =
+                static_cast<int>(max(min(q0 - key0, static_cast<int64_t>(kBKey)), static_cast<int64_t>(-kBQ)));
+            mask_tile<kCausal>(s, key_lim, q_rel, g, lc);
         }
+        softmax_tile(s, f, st, pb);
+    };
+
+    // Group 0 has tile 0 (and the Q loads) resident before the first barrier.
+    if (grp == 0) __builtin_amdgcn_s_waitcnt(vmcnt_imm((kAhead - 1) * kLoadsPerTile));
+    wg_barrier();
+    if (grp == 1) wg_barrier();
+    // C0 = QK(0), C1 = softmax(0); group 0 then waits for tile 1.
+    qk_tile(lds[0], gm, qf, s);
+    wg_barrier();
+    softmax(0, std::true_type{});
+    if (grp == 0) __builtin_amdgcn_s_waitcnt(vmcnt_imm((kAhead - 2) * kLoadsPerTile));
+    wg_barrier();
+    // Steady-state steps: M_it = QK(it + 1), PV(it); V_it = unmasked
+    // softmax(it + 1).  Group 0 issues tile it + kAhead in M_it and, before
+    // the barrier that ends V_it, waits for tile it + 2, which M_{it + 1}
+    // reads.
+    const int main_steps = max(0, min(my_tiles, first_masked) - 1);
+#pragma clang loop unroll(disable)
+    for (int it = 0; it < main_steps; ++it) {
+        mfma_cluster(lds[(it + 1) % kStages], lds[it % kStages], gm, qf, s, pb, st, ones);
+        if (grp == 0)
+            issue_tile(lds[(it + kAhead) % kStages], krs, vrs, gm, k_sl32, tile_key0(it + kAhead), w4);
+        wg_barrier();
+        softmax(it + 1, std::false_type{});
+        if (grp == 0) __builtin_amdgcn_s_waitcnt(vmcnt_imm((kAhead - 2) * kLoadsPerTile));
+        wg_barrier();
     }
+    // Remaining steps: masked tiles, the last tile, and (causal) tiles past
+    // this wave's diagonal, which only keep the barrier count.
 #pragma clang loop unroll(disable)
-    for (; it < first_masked; ++it) step_single(it, std::false_type{});
-#pragma clang loop unroll(disable)
-    for (; it < tiles; ++it) step_single(it, std::true_type{});
+    for (int it = main_steps; it < tiles; ++it) {
+        if (grp == 0)
+            issue_tile(lds[(it + kAhead) % kStages], krs, vrs, gm, k_sl32, tile_key0(it + kAhead), w4);
+        if (it + 1 < my_tiles) qk_tile(lds[(it + 1) % kStages], gm, qf, s);
+        if (it < my_tiles) pv_tile(lds[it % kStages], gm, pb, st, ones);
+        wg_barrier();
+        if (it + 1 < my_tiles) softmax(it + 1, std::true_type{});
+        if (grp == 0) __builtin_amdgcn_s_waitcnt(vmcnt_imm((kAhead - 2) * kLoadsPerTile));
+        wg_barrier();
+    }
+    if (grp == 0) wg_barrier();
     __builtin_amdgcn_s_waitcnt(0);
 
     // acc_o[ds][qt][r] = O[q0 + 16 qt + lc][16 ds + 4 g + r]; acc_l[qt][*] = l.
     uint16_t *op = o + b * o_sb + h * o_sh;
 #pragma unroll
-    for (int qt = 0; qt < QT; ++qt) {
+    for (int qt = 0; qt < kQT; ++qt) {
         const int64_t qi = q0 + 16 * qt + lc;
         const float inv = 1.0f / st.acc_l[qt][0];
         if (qi >= lq) continue;
@@ -472,7 +602,9 @@ extern "C" int32_t tu_sage_attn_fwd(const int8_t *q8, const float *q_scale, int6
     TU_REQUIRE(blkq > 0 && blkk > 0 && blkk % kBKey == 0 && ((blkk / kBKey) & (blkk / kBKey - 1)) == 0,
                "Sage attention needs blkq > 0 and blkk = 64 * 2^n");
     TU_REQUIRE(blkq <= 0x7fffffff && blkk <= 0x7fffffff, "Sage attention block sizes out of range");
-    TU_REQUIRE((lq + 127) / 128 <= 0x7fffffff && batch * hq <= 65535, "Sage attention grid too large");
+    TU_REQUIRE((lq + kBQ - 1) / kBQ <= 0x7fffffff && batch * hq <= 65535, "Sage attention grid too large");
+    TU_REQUIRE(lk * k_sl < (int64_t{1} << 32) && kD * lpad * 2 < (int64_t{1} << 32),
+               "Sage attention: one head's K or V^T exceeds 4 GiB of addressable bytes");
     TU_REQUIRE(q8 && q_scale && k8 && k_scale && vt_bf16 && o_bf16, "Sage attention pointers must be non-null");
     TU_REQUIRE(sm_scale > 0.0f, "Sage attention sm_scale must be positive");
     TU_REQUIRE(q_sl % 16 == 0 && q_sh % 16 == 0 && q_sb % 16 == 0 && (reinterpret_cast<uintptr_t>(q8) & 15) == 0 &&
@@ -482,8 +614,7 @@ extern "C" int32_t tu_sage_attn_fwd(const int8_t *q8, const float *q_scale, int6
                    (reinterpret_cast<uintptr_t>(o_bf16) & 7) == 0,
                "Sage attention V^T/O must be aligned");
     if (require_gfx950()) return -1;
-    constexpr int kQT = TU_ATTN_QT;
-    const dim3 grid(static_cast<unsigned>((lq + 64 * kQT - 1) / (64 * kQT)), static_cast<unsigned>(batch * hq));
+    const dim3 grid(static_cast<unsigned>((lq + kBQ - 1) / kBQ), static_cast<unsigned>(batch * hq));
     const float sm_log2 = sm_scale * kLog2e;
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int groups = static_cast<int>(hq / hkv);
@@ -493,8 +624,8 @@ extern "C" int32_t tu_sage_attn_fwd(const int8_t *q8, const float *q_scale, int6
     q8, q_scale, static_cast<int>(blkq), k8, k_scale, kscale_shift, static_cast<const uint16_t *>(vt_bf16),      \
         static_cast<uint16_t *>(o_bf16), static_cast<int>(hq), groups, lq, lk, lpad, q_sb, q_sh, q_sl, k_sb, k_sh,  \
         k_sl, o_sb, o_sh, o_sl, sm_log2
-    if (causal) sage_attn_kernel<kQT, true><<<grid, kThreads, 0, s>>>(TU_ATTN_ARGS);
-    else sage_attn_kernel<kQT, false><<<grid, kThreads, 0, s>>>(TU_ATTN_ARGS);
+    if (causal) sage_attn_kernel<true><<<grid, kThreads, 0, s>>>(TU_ATTN_ARGS);
+    else sage_attn_kernel<false><<<grid, kThreads, 0, s>>>(TU_ATTN_ARGS);
 #undef TU_ATTN_ARGS
     return check_launch("tu_sage_attn_fwd");
 }

@@ -11,10 +11,13 @@ Importing the package registers the ops; it does not load the shared library
 (the first op call does, and raises RuntimeError if it is missing).
 """
 from .ops import (
+    turing_bf16_gelu_int8_convrot_quantize,
     turing_bf16_int8_convrot_quantize,
     turing_dequantize_int8_bf16,
+    turing_gelu_int8_convrot_quantize,
     turing_int8_gemm_i32,
     turing_int8_linear,
+    turing_swiglu_int8_convrot_quantize,
 )
 from . import turing_sage
 
@@ -24,9 +27,12 @@ from . import turing_sage
 __version__ = "0.29.1"
 
 __all__ = [
+    "turing_bf16_gelu_int8_convrot_quantize",
     "turing_bf16_int8_convrot_quantize",
     "turing_dequantize_int8_bf16",
+    "turing_gelu_int8_convrot_quantize",
     "turing_int8_gemm_i32",
     "turing_int8_linear",
     "turing_sage",
+    "turing_swiglu_int8_convrot_quantize",
 ]

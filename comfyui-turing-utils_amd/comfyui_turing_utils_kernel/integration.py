@@ -3,8 +3,9 @@
 The reference plugin reaches the kernel package from two places:
 
 * ``comfyui_turing_utils/quantization/dispatch.py:618-670`` -- ``int8_linear``:
-  reshape to 2D, ConvRot-quantize the activation, run the W8A8 GEMM, reshape
-  back.  Calls it cannot serve are handed to comfy-kitchen.
+  reshape to 2D, ConvRot-quantize the activation (optionally folding a
+  tanh-GELU or SwiGLU input activation), run the W8A8 GEMM, reshape back.
+  Calls it cannot serve are handed to comfy-kitchen.
 * ``comfyui_turing_utils/attention/stable.py:83-200, :593-711`` -- the
   attention override: inspect the call, fall back to the caller's attention
   for anything unsupported (mask, head_dim > 128, dtype/device mismatch,
@@ -50,22 +51,28 @@ def int8_linear(
     convrot_groupsize: int = 128,
     input_act: str | None = None,
 ) -> torch.Tensor:
-    """ConvRot W8A8 linear: y = dequant(int8(R x) @ W^T) * s_x * s_w + bias.
+    """ConvRot W8A8 linear: y = dequant(int8(R act(x)) @ W^T) * s_x * s_w + bias.
 
-    x: bf16 [..., K]; weight: int8 [N, K]; weight_scale: fp32 scalar or [N];
-    bias: [N] or None.  Returns [..., N] in ``out_dtype`` (default x.dtype).
+    x: bf16 [..., K] ([..., 2K] for ``input_act="swiglu"``); weight: int8 [N, K];
+    weight_scale: fp32 scalar or [N]; bias: [N] or None; input_act: None /
+    "none", "gelu_tanh" or "swiglu" (dispatch.py:326-393), folded into the
+    quantizer.  Returns [..., N] in ``out_dtype`` (default x.dtype).
     """
+    if input_act not in (None, "none", "swiglu", "gelu_tanh"):
+        raise ValueError(f"unsupported fused INT8 activation: {input_act!r}")
     if x.dtype != torch.bfloat16:
         raise NotImplementedError("gfx950 W8A8 linear takes bfloat16 activations")
     if not convrot:
         raise NotImplementedError("gfx950 W8A8 linear requires ConvRot activations")
-    if input_act not in (None, "none"):
-        raise NotImplementedError(f"input activation {input_act!r} is not fused on gfx950")
     if not is_supported_device(x.device):
         raise NotImplementedError(f"{x.device} is not a gfx950 device")
     original_shape = x.shape
     x2d = x.reshape(-1, original_shape[-1]).contiguous()
-    q, s_x = torch.ops.turing_utils.bf16_int8_convrot_quantize(x2d, convrot_groupsize)
+    if input_act == "gelu_tanh":
+        q, s_x = torch.ops.turing_utils.bf16_gelu_int8_convrot_quantize(x2d, convrot_groupsize)
+    else:
+        q, s_x = torch.ops.turing_utils.bf16_int8_convrot_quantize(x2d, convrot_groupsize,
+                                                                    swiglu=input_act == "swiglu")
     n = weight.shape[0]
     w_scale = weight_scale.to(device=x.device, dtype=torch.float32).reshape(-1)
     if w_scale.numel() == 1:

@@ -7,8 +7,11 @@ that dispatch through ``torch.ops.turing_utils.*`` or the package attributes
 
 Differences from the reference, by design of this MI355X build:
   * the device predicate is gfx950 instead of sm75;
-  * ``bf16_int8_convrot_quantize`` accepts ``group_size`` 128 (this build's
+  * the ConvRot quantizers accept ``group_size`` 128 (this build's
     block-Hadamard extension) as well as 256 (the reference's only size);
+  * tanh and exp inside the fused GELU / SwiGLU activations are this
+    build's fixed fp32 sequences (bit-identical to the CPU oracle), not
+    CUDA's tanhf / expf;
   * ``int8_gemm_i32`` is an extra op exposing the raw INT32 accumulator of
     the same GEMM kernel, used for bit-exact parity checks.
 """
@@ -159,9 +162,36 @@ def _turing_dequantize_int8_bf16_fake(accumulator, activation_scale, weight_scal
 
 
 # ---------------------------------------------------------------------------
-# ConvRot INT8 activation quantizer (reference ops.py:257-282)
+# ConvRot INT8 activation quantizer (reference ops.py:257-282, :313-331)
 # ---------------------------------------------------------------------------
 SUPPORTED_GROUP_SIZES = (128, 256)
+ACT_NONE, ACT_GELU_TANH, ACT_SWIGLU = 0, 1, 2
+STAGED_SCALE = 0x100  # scale = absmax * (1/127), the two-pass kernels' formula
+
+
+def _convrot_quantize(x: torch.Tensor, group_size: int, act: int, what: str,
+                      staged: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
+    _require_device(x, what)
+    if x.dtype != torch.bfloat16:
+        # the reference's two-pass ops also take float16; only bf16 is built here
+        raise TypeError(f"{what} input must be bfloat16")
+    if x.ndim != 2:
+        raise ValueError(f"{what} input must be 2D")
+    if group_size not in SUPPORTED_GROUP_SIZES:
+        raise ValueError(f"{what} supports group_size {SUPPORTED_GROUP_SIZES}, got {group_size}")
+    x = x.contiguous()
+    rows, width = x.shape
+    if act == ACT_SWIGLU and width % 2:
+        raise ValueError(f"{what} SwiGLU input width must be even")
+    hidden = width // 2 if act == ACT_SWIGLU else width
+    if rows <= 0 or hidden <= 0 or hidden % group_size:
+        raise ValueError(f"{what} width must be positive and divisible by {group_size}")
+    q = torch.empty((rows, hidden), dtype=torch.int8, device=x.device)
+    scales = torch.empty((rows, 1), dtype=torch.float32, device=x.device)
+    with torch.cuda.device(x.device):
+        _lib.call("tu_convrot_quant_i8", x.data_ptr(), q.data_ptr(), scales.data_ptr(), rows, hidden,
+                  group_size, act | (STAGED_SCALE if staged else 0), _lib.stream_of(x.device))
+    return q, scales
 
 
 @torch.library.custom_op("turing_utils::bf16_int8_convrot_quantize", mutates_args=())
@@ -171,26 +201,9 @@ def turing_bf16_int8_convrot_quantize(
     *,
     swiglu: bool = False,
 ) -> tuple[torch.Tensor, torch.Tensor]:
-    """Whole-row BF16 ConvRot rotation + per-token symmetric INT8 quantization."""
-    _require_device(x, "BF16 row-buffer ConvRot")
-    if x.dtype != torch.bfloat16:
-        raise TypeError("BF16 row-buffer ConvRot input must be bfloat16")
-    if x.ndim != 2:
-        raise ValueError("BF16 row-buffer ConvRot input must be 2D")
-    if swiglu:
-        raise RuntimeError("SwiGLU folding is not available in the gfx950 ConvRot quantizer")
-    if group_size not in SUPPORTED_GROUP_SIZES:
-        raise ValueError(f"BF16 row-buffer ConvRot supports group_size {SUPPORTED_GROUP_SIZES}, got {group_size}")
-    x = x.contiguous()
-    rows, hidden = x.shape
-    if rows <= 0 or hidden <= 0 or hidden % group_size:
-        raise ValueError(f"BF16 row-buffer ConvRot width must be positive and divisible by {group_size}")
-    q = torch.empty((rows, hidden), dtype=torch.int8, device=x.device)
-    scales = torch.empty((rows, 1), dtype=torch.float32, device=x.device)
-    with torch.cuda.device(x.device):
-        _lib.call("tu_convrot_quant_i8", x.data_ptr(), q.data_ptr(), scales.data_ptr(), rows, hidden,
-                  group_size, 0, _lib.stream_of(x.device))
-    return q, scales
+    """Whole-row BF16 ConvRot rotation + per-token symmetric INT8 quantization.
+    swiglu=True folds SwiGLU over the [gate | up] halves of each row first."""
+    return _convrot_quantize(x, group_size, ACT_SWIGLU if swiglu else ACT_NONE, "BF16 row-buffer ConvRot")
 
 
 @turing_bf16_int8_convrot_quantize.register_fake
@@ -198,5 +211,64 @@ def _turing_bf16_int8_convrot_quantize_fake(x, group_size=256, *, swiglu=False):
     hidden = x.size(1) // 2 if swiglu else x.size(1)
     return (
         torch.empty((x.size(0), hidden), dtype=torch.int8, device=x.device),
+        torch.empty((x.size(0), 1), dtype=torch.float32, device=x.device),
+    )
+
+
+@torch.library.custom_op("turing_utils::bf16_gelu_int8_convrot_quantize", mutates_args=())
+def turing_bf16_gelu_int8_convrot_quantize(
+    x: torch.Tensor,
+    group_size: int = 256,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Whole-row BF16 tanh-GELU + ConvRot INT8 quantization (reference ops.py:313-331):
+    GELU is applied on load and rounded to bf16 before the rotation."""
+    return _convrot_quantize(x, group_size, ACT_GELU_TANH, "BF16 GELU ConvRot")
+
+
+@turing_bf16_gelu_int8_convrot_quantize.register_fake
+def _turing_bf16_gelu_int8_convrot_quantize_fake(x, group_size=256):
+    return (
+        torch.empty(x.shape, dtype=torch.int8, device=x.device),
+        torch.empty((x.size(0), 1), dtype=torch.float32, device=x.device),
+    )
+
+
+# ---------------------------------------------------------------------------
+# Two-pass ("staged") fused-activation quantizers (reference ops.py:163-186,
+# :215-233; bindings.cpp:474-510, :550-600).  The reference computes these in
+# two kernels through a global bf16 copy of the rotated rows; here the same
+# single-pass kernel runs with the staged scale formula, so codes and scales
+# equal the reference's two-pass results.
+# ---------------------------------------------------------------------------
+@torch.library.custom_op("turing_utils::swiglu_int8_convrot_quantize", mutates_args=())
+def turing_swiglu_int8_convrot_quantize(
+    x: torch.Tensor,
+    group_size: int = 256,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """SwiGLU over the [gate | up] halves of each row, then ConvRot INT8 quantization."""
+    return _convrot_quantize(x, group_size, ACT_SWIGLU, "SwiGLU ConvRot", staged=True)
+
+
+@turing_swiglu_int8_convrot_quantize.register_fake
+def _turing_swiglu_int8_convrot_quantize_fake(x, group_size=256):
+    return (
+        torch.empty((x.size(0), x.size(1) // 2), dtype=torch.int8, device=x.device),
+        torch.empty((x.size(0), 1), dtype=torch.float32, device=x.device),
+    )
+
+
+@torch.library.custom_op("turing_utils::gelu_int8_convrot_quantize", mutates_args=())
+def turing_gelu_int8_convrot_quantize(
+    x: torch.Tensor,
+    group_size: int = 256,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """tanh-GELU (rounded to bf16), then ConvRot INT8 quantization."""
+    return _convrot_quantize(x, group_size, ACT_GELU_TANH, "GELU ConvRot", staged=True)
+
+
+@turing_gelu_int8_convrot_quantize.register_fake
+def _turing_gelu_int8_convrot_quantize_fake(x, group_size=256):
+    return (
+        torch.empty(x.shape, dtype=torch.int8, device=x.device),
         torch.empty((x.size(0), 1), dtype=torch.float32, device=x.device),
     )

@@ -10,6 +10,9 @@
 //      bf16 (round-to-nearest-even);
 //   3. scale = max(min(absmax, bf16 max) / 127, 1e-30);
 //      q = clamp(rne(bf16(bf16(y) / bf16(scale))), -128, 127).
+// With the staged-scale flag the scale is absmax * (1/127) instead, as in the
+// reference's two-pass kernels (convrot_quant.cu:233-236) behind the
+// gelu_/swiglu_int8_convrot_quantize ops; everything else is identical.
 // G = 128 is this build's extension: three radix-4 digits then the
 // orthonormal radix-2 digit (1/sqrt2)[[1,1],[1,-1]] on stride 64.
 //
@@ -66,6 +69,46 @@ __device__ __forceinline__ float div_markstein(float a, float b, float y) {
     return __builtin_isinf(a) ? a : q;
 }
 
+// Input activations, operation for operation the fixed fp32 sequences of the
+// CPU oracle (exp by Cody-Waite reduction and a degree-7 Taylor polynomial,
+// tanh from exp), so activation outputs are bit-identical to it:
+//   tanh-GELU: bf16((0.5 x) (1 + tanh(a (x + ((b x) x) x))))  (convrot_quant.cu:145-156)
+//   SwiGLU:    (g / (1 + exp(-g))) u                           (convrot_quant.cu:137-143)
+__device__ __forceinline__ float exp_det(float v) {
+    if (v != v) return v;
+    if (v > 88.72f) return __builtin_inff();
+    if (v < -87.0f) return 0.0f;
+    const float n = __builtin_rintf(v * 1.44269504f);
+    const float r = (v - n * 0.693145752f) - n * 1.42860677e-6f;
+    float p = 1.98412698e-4f;
+    p = p * r + 1.38888889e-3f;
+    p = p * r + 8.33333377e-3f;
+    p = p * r + 4.16666679e-2f;
+    p = p * r + 1.66666672e-1f;
+    p = p * r + 0.5f;
+    p = p * r + 1.0f;
+    p = p * r + 1.0f;
+    return __builtin_ldexpf(p, static_cast<int>(n));
+}
+
+__device__ __forceinline__ float tanh_det(float u) {
+    if (u != u) return u;
+    const float a = fabsf(u);
+    const float e = exp_det(2.0f * fminf(a, 9.0f));
+    float t = 1.0f - 2.0f / (e + 1.0f);
+    t = a < 0.000244140625f ? a : t;
+    t = a > 9.0f ? 1.0f : t;
+    return __builtin_copysignf(t, u);
+}
+
+__device__ __forceinline__ float gelu_tanh_bf16(float x) {
+    const float inner = 0.7978845608028654f * (x + ((0.044715f * x) * x) * x);
+    const float act = (0.5f * x) * (1.0f + tanh_det(inner));
+    return bf16_round(act);
+}
+
+__device__ __forceinline__ float swiglu(float gate, float up) { return (gate / (1.0f + exp_det(-gate))) * up; }
+
 __device__ __forceinline__ int32_t quant_code(float v, float rs, float ry) {
     const float divided = bf16_round(div_markstein(v, rs, ry));
     float qf = __builtin_rintf(divided);
@@ -73,10 +116,11 @@ __device__ __forceinline__ int32_t quant_code(float v, float rs, float ry) {
     return static_cast<int32_t>(qf);
 }
 
-template <int G>
+// kAct: 0 none, 1 tanh-GELU, 2 SwiGLU (x rows are [gate | up], 2k wide).
+template <int G, int kAct>
 __global__ __launch_bounds__(kThreads) void convrot_quant_i8_kernel(
     const uint16_t *__restrict__ x, int8_t *__restrict__ q, float *__restrict__ scales, int k,
-    int row_buffer_bytes) {
+    int row_buffer_bytes, int staged_scale) {
     extern __shared__ __align__(16) unsigned char smem[];
     uint16_t *row_buf = reinterpret_cast<uint16_t *>(smem);
     __shared__ float wave_amax[kWaves];
@@ -92,7 +136,7 @@ __global__ __launch_bounds__(kThreads) void convrot_quant_i8_kernel(
     float *buf = reinterpret_cast<float *>(smem + row_buffer_bytes) + wave * 256 + gsub * G;
 
     const int64_t row = blockIdx.x;
-    const uint16_t *xrow = x + row * static_cast<int64_t>(k);
+    const uint16_t *xrow = x + row * static_cast<int64_t>(kAct == 2 ? 2 * k : k);
     const int groups = k / G;
     float absmax = 0.0f;
 
@@ -107,6 +151,18 @@ __global__ __launch_bounds__(kThreads) void convrot_quant_i8_kernel(
             x1 = bf16_bits_to_f32(v.x >> 16);
             x2 = bf16_bits_to_f32(v.y & 0xffffu);
             x3 = bf16_bits_to_f32(v.y >> 16);
+            if constexpr (kAct == 1) {
+                x0 = gelu_tanh_bf16(x0);
+                x1 = gelu_tanh_bf16(x1);
+                x2 = gelu_tanh_bf16(x2);
+                x3 = gelu_tanh_bf16(x3);
+            } else if constexpr (kAct == 2) {
+                const u32x2 u = *reinterpret_cast<const u32x2 *>(xrow + k + col);
+                x0 = swiglu(x0, bf16_bits_to_f32(u.x & 0xffffu));
+                x1 = swiglu(x1, bf16_bits_to_f32(u.x >> 16));
+                x2 = swiglu(x2, bf16_bits_to_f32(u.y & 0xffffu));
+                x3 = swiglu(x3, bf16_bits_to_f32(u.y >> 16));
+            }
         }
         // Stride-1 digit in registers (convrot_quant.cu:384-391).
         f32x4 y;
@@ -163,7 +219,8 @@ __global__ __launch_bounds__(kThreads) void convrot_quant_i8_kernel(
     float amax = wave_amax[0];
 #pragma unroll
     for (int w = 1; w < kWaves; ++w) amax = fmaxf(amax, wave_amax[w]);
-    const float scale = fmaxf(fminf(amax, 3.38953139e38f) / 127.0f, 1.0e-30f);
+    const float clipped = fminf(amax, 3.38953139e38f);
+    const float scale = fmaxf(staged_scale ? clipped * (1.0f / 127.0f) : clipped / 127.0f, 1.0e-30f);
     if (tid == 0) scales[row] = scale;
     const float rs = bf16_round(scale);
     const float ry = 1.0f / rs;
@@ -197,7 +254,10 @@ extern "C" int32_t tu_convrot_quant_i8(const void *x_bf16, int8_t *q, float *sca
                                        int64_t cols, int32_t group, int32_t act, void *stream) {
     using namespace tu;
     TU_REQUIRE(group == 128 || group == 256, "ConvRot group_size must be 128 or 256, got %d", group);
-    TU_REQUIRE(act == 0, "ConvRot input activation %d is not supported (only 0 = none)", act);
+    const int staged_scale = (act & TU_CONVROT_STAGED_SCALE) != 0;
+    act &= ~TU_CONVROT_STAGED_SCALE;
+    TU_REQUIRE(act >= TU_ACT_NONE && act <= TU_ACT_SWIGLU,
+               "ConvRot input activation must be 0 (none), 1 (tanh-GELU) or 2 (SwiGLU), got %d", act);
     TU_REQUIRE(rows >= 0 && cols > 0 && cols % group == 0,
                "ConvRot width must be positive and divisible by %d, got %lld", group,
                static_cast<long long>(cols));
@@ -213,12 +273,17 @@ extern "C" int32_t tu_convrot_quant_i8(const void *x_bf16, int8_t *q, float *sca
     TU_REQUIRE(lds <= 160 * 1024 - 64, "ConvRot row of %d columns exceeds LDS", k);
     hipStream_t s = static_cast<hipStream_t>(stream);
     const dim3 grid(static_cast<unsigned>(rows));
+    const auto *xp = static_cast<const uint16_t *>(x_bf16);
+#define TU_CONVROT_LAUNCH(G, A) convrot_quant_i8_kernel<G, A><<<grid, kThreads, lds, s>>>(xp, q, scale, k, row_buffer_bytes, staged_scale)
     if (group == 256) {
-        convrot_quant_i8_kernel<256><<<grid, kThreads, lds, s>>>(
-            static_cast<const uint16_t *>(x_bf16), q, scale, k, row_buffer_bytes);
+        if (act == 0) TU_CONVROT_LAUNCH(256, 0);
+        else if (act == 1) TU_CONVROT_LAUNCH(256, 1);
+        else TU_CONVROT_LAUNCH(256, 2);
     } else {
-        convrot_quant_i8_kernel<128><<<grid, kThreads, lds, s>>>(
-            static_cast<const uint16_t *>(x_bf16), q, scale, k, row_buffer_bytes);
+        if (act == 0) TU_CONVROT_LAUNCH(128, 0);
+        else if (act == 1) TU_CONVROT_LAUNCH(128, 1);
+        else TU_CONVROT_LAUNCH(128, 2);
     }
+#undef TU_CONVROT_LAUNCH
     return check_launch("tu_convrot_quant_i8");
 }

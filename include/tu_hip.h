@@ -45,18 +45,33 @@ int32_t tu_device_supported(int32_t device);
 
 /* ConvRot INT8 activation quantizer -------------------------------------- */
 
-/* Rotates each row of x by the block-Hadamard ConvRot transform (group 128
- * or 256), then quantizes per row to symmetric INT8:
+/* Input activation applied on load (low byte of `act`). */
+#define TU_ACT_NONE 0      /* a = x */
+#define TU_ACT_GELU_TANH 1 /* a = bf16(0.5x(1 + tanh(0.7978845608028654(x + 0.044715x^3)))) */
+#define TU_ACT_SWIGLU 2    /* a = silu(gate) * up; x rows are [gate | up], 2*cols wide */
+/* OR-ed into `act`: scale = absmax * (1/127) (the two-pass kernels' formula,
+ * convrot_quant.cu:233-236) instead of absmax / 127. */
+#define TU_CONVROT_STAGED_SCALE 0x100
+
+/* Rotates each row of the activated input a = act(x) by the block-Hadamard
+ * ConvRot transform (group 128 or 256), then quantizes per row to symmetric
+ * INT8:
+ *   y        = rotate(a) in fp32, absmax_r = max |y[r][:]|
  *   scale[r] = max(min(absmax_r, 3.38953139e38) / 127, 1e-30)
  *   q[r][c]  = clamp(rne(bf16(bf16(y[r][c]) / bf16(scale[r]))), -128, 127)
- * x: bf16 [rows, cols], row-major contiguous.  q: int8 [rows, cols];
- * scale: fp32 [rows].  cols % group == 0; x and q 8-byte aligned.
- * act must be 0 (no input activation).  1 (tanh-GELU) and 2 (SwiGLU over
- * [gate | up] halves) are reserved for the fused-activation variants of the
- * reference (convrot_quant.cu:145-156, :332-344) and are rejected.
- * Replaces turing_utils::bf16_int8_convrot_quantize
- * (kernel/comfyui_turing_utils_kernel/ops.py:257-282 ->
- *  kernel/csrc/bindings.cpp:603-646 -> kernel/csrc/turing/convrot_quant.cu:566-589). */
+ * x: bf16 [rows, cols] (TU_ACT_SWIGLU: [rows, 2*cols]), row-major contiguous.
+ * q: int8 [rows, cols]; scale: fp32 [rows].  cols % group == 0; x and q 8-byte
+ * aligned.  tanh and exp inside the activations are fixed fp32 sequences
+ * (range reduction by ln2 and a degree-7 Taylor polynomial; tanh(u) =
+ * 1 - 2/(e^2u + 1)), bit-identical to the CPU oracle.
+ * Replaces turing_utils::bf16_int8_convrot_quantize (act 0 and 2;
+ * kernel/comfyui_turing_utils_kernel/ops.py:257-282 ->
+ * kernel/csrc/bindings.cpp:603-646 -> kernel/csrc/turing/convrot_quant.cu:566-589),
+ * turing_utils::bf16_gelu_int8_convrot_quantize (act 1; ops.py:313-331 ->
+ * convrot_quant.cu:145-156, :332-344, :616-630) and, with
+ * TU_CONVROT_STAGED_SCALE, turing_utils::gelu_int8_convrot_quantize /
+ * swiglu_int8_convrot_quantize (ops.py:163-186, :215-233 ->
+ * bindings.cpp:474-510, :550-600 -> convrot_quant.cu:158-248, :470-563). */
 int32_t tu_convrot_quant_i8(const void *x_bf16, int8_t *q, float *scale, int64_t rows,
                             int64_t cols, int32_t group, int32_t act, void *stream);
 

@@ -42,6 +42,11 @@ def lib():
             if not os.path.exists(LIB_PATH):
                 build()
             L = ctypes.CDLL(LIB_PATH)
+            for fn in ("or_exp_det", "or_tanh_det", "or_gelu_tanh_bf16"):
+                getattr(L, fn).restype = ctypes.c_float
+                getattr(L, fn).argtypes = [ctypes.c_float]
+            L.or_swiglu.restype = ctypes.c_float
+            L.or_swiglu.argtypes = [ctypes.c_float, ctypes.c_float]
             L.or_num_threads.restype = _i32
             L.or_num_threads.argtypes = []
             L.or_f32_to_bf16_rne.restype = ctypes.c_uint16
@@ -114,14 +119,37 @@ def rotate_group(x: np.ndarray, group: int) -> np.ndarray:
     return y
 
 
-def convrot_quant(x_bits: np.ndarray, group: int, staged: bool = False) -> tuple[np.ndarray, np.ndarray]:
-    """(int8 codes [M, K], fp32 scales [M]) of the row-buffer quantizer."""
+ACT_NONE, ACT_GELU_TANH, ACT_SWIGLU = 0, 1, 2
+
+
+def convrot_quant(x_bits: np.ndarray, group: int, staged: bool = False,
+                  act: int = ACT_NONE) -> tuple[np.ndarray, np.ndarray]:
+    """(int8 codes [M, K], fp32 scales [M]) of the row-buffer quantizer.
+    act: 0 none, 1 tanh-GELU, 2 SwiGLU (input [M, 2K] = [gate | up])."""
     x_bits = np.ascontiguousarray(x_bits, dtype=np.uint16)
-    m, k = x_bits.shape
+    m, width = x_bits.shape
+    k = width // 2 if act == ACT_SWIGLU else width
     q = np.empty((m, k), dtype=np.int8)
     s = np.empty(m, dtype=np.float32)
-    _check(lib().or_convrot_quant_i8(_ptr(x_bits), m, k, group, 0, int(staged), _ptr(q), _ptr(s)), "convrot_quant")
+    _check(lib().or_convrot_quant_i8(_ptr(x_bits), m, k, group, act, int(staged), _ptr(q), _ptr(s)),
+           "convrot_quant")
     return q, s
+
+
+def exp_det(v: float) -> float:
+    return float(lib().or_exp_det(v))
+
+
+def tanh_det(u: float) -> float:
+    return float(lib().or_tanh_det(u))
+
+
+def gelu_tanh_bf16(x: float) -> float:
+    return float(lib().or_gelu_tanh_bf16(x))
+
+
+def swiglu(gate: float, up: float) -> float:
+    return float(lib().or_swiglu(gate, up))
 
 
 def div_markstein(a: float, b: float) -> float:

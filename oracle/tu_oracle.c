@@ -117,17 +117,61 @@ OR_API int or_convrot_rotate_group(const float *x, float *y, int group) {
 }
 
 /* ------------------------------------------------------------------------ */
-/* Input activations folded into the quantizer (convrot_quant.cu:137-156).   */
-/* act 0: none; 2: SwiGLU over [gate | up] halves of a 2K-wide row.          */
-/* (act 1, tanh-GELU, is not restated here: its tanhf is a libm call whose    */
-/* last-ulp behaviour differs between libraries.)                            */
+/* Input activations folded into the quantizer (convrot_quant.cu:137-156,    */
+/* :332-344):                                                                 */
+/*   act 1, tanh-GELU:  bf16( (0.5 x) (1 + tanh(a (x + ((b x) x) x))) ),     */
+/*                      a = 0.7978845608028654, b = 0.044715 (:145-156)       */
+/*   act 2, SwiGLU:     (g / (1 + exp(-g))) u over the [g | u] halves of a   */
+/*                      2K-wide row (:137-143), not rounded before the FHT    */
+/* The reference calls CUDA's tanhf / expf, whose last-ulp behaviour is not   */
+/* reproducible off-GPU.  This build defines exp and tanh by the fixed fp32   */
+/* sequences below (the GPU kernel executes the same operations in the same   */
+/* order, so activation outputs are bit-identical between the two):         */
+/*   exp_det(v): Cody-Waite reduction n = rint(v log2 e),                     */
+/*     r = (v - n ln2_hi) - n ln2_lo, degree-7 Taylor polynomial of e^r in    */
+/*     Horner form, scaled by 2^n; 0 below -87, +inf above 88.72.             */
+/*   tanh_det(u) = sign(u) (1 - 2 / (exp_det(2|u|) + 1)), |u| for            */
+/*     |u| < 2^-12, 1 for |u| > 9.                                            */
+/* Both are pinned against double-precision exp / tanh by error bounds.      */
 /* ------------------------------------------------------------------------ */
+OR_API float or_exp_det(float v) {
+    if (v != v) return v;
+    if (v > 88.72f) return INFINITY;
+    if (v < -87.0f) return 0.0f;
+    const float n = nearbyintf(v * 1.44269504f);
+    const float r = (v - n * 0.693145752f) - n * 1.42860677e-6f;
+    float p = 1.98412698e-4f;
+    p = p * r + 1.38888889e-3f;
+    p = p * r + 8.33333377e-3f;
+    p = p * r + 4.16666679e-2f;
+    p = p * r + 1.66666672e-1f;
+    p = p * r + 0.5f;
+    p = p * r + 1.0f;
+    p = p * r + 1.0f;
+    return ldexpf(p, (int)n);
+}
+
+OR_API float or_tanh_det(float u) {
+    if (u != u) return u;
+    const float a = fabsf(u);
+    const float e = or_exp_det(2.0f * fminf(a, 9.0f));
+    float t = 1.0f - 2.0f / (e + 1.0f);
+    t = a < 0.000244140625f ? a : t;
+    t = a > 9.0f ? 1.0f : t;
+    return copysignf(t, u);
+}
+
+OR_API float or_gelu_tanh_bf16(float x) {
+    const float inner = 0.7978845608028654f * (x + ((0.044715f * x) * x) * x);
+    const float act = (0.5f * x) * (1.0f + or_tanh_det(inner));
+    return bf16_round_f32(act);
+}
+
+OR_API float or_swiglu(float gate, float up) { return (gate / (1.0f + or_exp_det(-gate))) * up; }
+
 static inline float load_act(const uint16_t *row, int64_t col, int64_t k, int act) {
-    if (act == 2) {
-        const float gate = or_bf16_to_f32(row[col]);
-        const float up = or_bf16_to_f32(row[k + col]);
-        return (gate / (1.0f + expf(-gate))) * up;
-    }
+    if (act == 2) return or_swiglu(or_bf16_to_f32(row[col]), or_bf16_to_f32(row[k + col]));
+    if (act == 1) return or_gelu_tanh_bf16(or_bf16_to_f32(row[col]));
     return or_bf16_to_f32(row[col]);
 }
 

@@ -69,3 +69,52 @@ def test_convrot_rejects_bad_width(gpu_device):
     x = torch.zeros(2, 200, dtype=torch.bfloat16, device=gpu_device)
     with pytest.raises(ValueError):
         torch.ops.turing_utils.bf16_int8_convrot_quantize(x, 128)
+
+
+# ---------------------------------------------------------------------------
+# fused input activations: tanh-GELU (turing_utils::bf16_gelu_int8_convrot_quantize)
+# and SwiGLU (bf16_int8_convrot_quantize(swiglu=True)), bit-exact vs the oracle
+# ---------------------------------------------------------------------------
+def _edge_values(m, k, seed):
+    x = inputs.activation(m, k, seed).float()
+    g = torch.Generator().manual_seed(seed + 1)
+    x[0, : k // 2] = torch.linspace(-12, 12, k // 2)                 # the whole tanh range
+    x[1, :8] = torch.tensor([0.0, -0.0, 1e-30, -1e-30, 3e38, -3e38, 1e4, -1e4])
+    x[2] = torch.randn(k, generator=g) * 1e-3                           # tiny row
+    return x.to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("group", [128, 256])
+@pytest.mark.parametrize("m,k,seed", [(5, 512, 41), (64, 5120, 42), (32, 13824, 43)])
+def test_gelu_quant_exact(gpu_device, group, m, k, seed):
+    print(f"[convrot gelu] m={m} k={k} group={group}", flush=True)
+    x = _edge_values(m, k, seed)
+    q, s = torch.ops.turing_utils.bf16_gelu_int8_convrot_quantize(x.to(gpu_device), group)
+    q_ref, s_ref = oracle.convrot_quant(inputs.bits(x), group, act=oracle.ACT_GELU_TANH)
+    np.testing.assert_array_equal(s.cpu().numpy().reshape(-1).view(np.uint32), s_ref.view(np.uint32))
+    np.testing.assert_array_equal(q.cpu().numpy(), q_ref)
+
+
+@pytest.mark.parametrize("group", [128, 256])
+@pytest.mark.parametrize("m,k,seed", [(5, 512, 51), (48, 5120, 52)])
+def test_swiglu_quant_exact(gpu_device, group, m, k, seed):
+    print(f"[convrot swiglu] m={m} k={k} group={group}", flush=True)
+    x = _edge_values(m, 2 * k, seed)
+    q, s = torch.ops.turing_utils.bf16_int8_convrot_quantize(x.to(gpu_device), group, swiglu=True)
+    q_ref, s_ref = oracle.convrot_quant(inputs.bits(x), group, act=oracle.ACT_SWIGLU)
+    assert q.shape == (m, k)
+    np.testing.assert_array_equal(s.cpu().numpy().reshape(-1).view(np.uint32), s_ref.view(np.uint32))
+    np.testing.assert_array_equal(q.cpu().numpy(), q_ref)
+
+
+@pytest.mark.parametrize("act,name", [(1, "gelu_int8_convrot_quantize"), (2, "swiglu_int8_convrot_quantize")])
+@pytest.mark.parametrize("group", [128, 256])
+def test_staged_ops_exact(gpu_device, act, name, group):
+    """The two-pass op names: staged scale formula, same codes contract."""
+    m, k = 37, 5120
+    print(f"[convrot staged] {name} m={m} k={k} group={group}", flush=True)
+    x = _edge_values(m, 2 * k if act == 2 else k, 60 + act)
+    q, s = getattr(torch.ops.turing_utils, name)(x.to(gpu_device), group)
+    q_ref, s_ref = oracle.convrot_quant(inputs.bits(x), group, staged=True, act=act)
+    np.testing.assert_array_equal(s.cpu().numpy().reshape(-1).view(np.uint32), s_ref.view(np.uint32))
+    np.testing.assert_array_equal(q.cpu().numpy(), q_ref)

@@ -112,6 +112,11 @@ def test_int8_linear_contract(monkeypatch):
     assert out.dtype == torch.float16
     with pytest.raises(ValueError, match="scalar or have 48"):
         integration.int8_linear(x, w, torch.empty((7,), device="meta"))
+    out = integration.int8_linear(x, w, torch.empty((48,), device="meta"), input_act="gelu_tanh")
+    assert out.shape == (2, 5, 48)
+    xs = torch.empty((2, 5, 512), dtype=torch.bfloat16, device="meta")
+    out = integration.int8_linear(xs, w, torch.empty((48,), device="meta"), input_act="swiglu")
+    assert out.shape == (2, 5, 48)
 
 
 def test_int8_linear_declines_what_it_cannot_serve():
@@ -124,5 +129,5 @@ def test_int8_linear_declines_what_it_cannot_serve():
         integration.int8_linear(x.float(), w, s)
     with pytest.raises(NotImplementedError, match="ConvRot"):
         integration.int8_linear(x, w, s, convrot=False)
-    with pytest.raises(NotImplementedError, match="gelu"):
+    with pytest.raises(ValueError, match="activation"):
         integration.int8_linear(x, w, s, input_act="gelu")

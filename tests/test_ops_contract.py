@@ -25,6 +25,16 @@ def test_convrot_fake_contract(group):
     q, s = torch.ops.turing_utils.bf16_int8_convrot_quantize(x, group)
     assert q.shape == (3, 512) and q.dtype == torch.int8 and q.device.type == META
     assert s.shape == (3, 1) and s.dtype == torch.float32
+    # reference tests/test_kernel_custom_ops.py:194-217
+    q, s = torch.ops.turing_utils.bf16_gelu_int8_convrot_quantize(x, group)
+    assert q.shape == (3, 512) and s.shape == (3, 1) and q.dtype == torch.int8
+    q, s = kernel.turing_bf16_int8_convrot_quantize(x, group, swiglu=True)
+    assert q.shape == (3, 256) and s.shape == (3, 1)
+    # two-pass op names (reference ops.py:163-186, :215-233)
+    q, s = kernel.turing_gelu_int8_convrot_quantize(x, group)
+    assert q.shape == (3, 512) and s.shape == (3, 1) and q.dtype == torch.int8
+    q, s = kernel.turing_swiglu_int8_convrot_quantize(x, group)
+    assert q.shape == (3, 256) and s.shape == (3, 1) and s.dtype == torch.float32
 
 
 def test_linear_and_epilogue_fake_contracts():
@@ -66,8 +76,10 @@ def test_linear_chain_is_a_fullgraph_leaf():
 
 def test_cpu_tensors_are_refused():
     x = torch.zeros((4, 256), dtype=torch.bfloat16)
-    with pytest.raises(RuntimeError, match="CUDA|HIP"):
-        torch.ops.turing_utils.bf16_int8_convrot_quantize(x, 256)
+    for op in (torch.ops.turing_utils.bf16_int8_convrot_quantize, torch.ops.turing_utils.bf16_gelu_int8_convrot_quantize,
+               torch.ops.turing_utils.gelu_int8_convrot_quantize, torch.ops.turing_utils.swiglu_int8_convrot_quantize):
+        with pytest.raises(RuntimeError, match="CUDA|HIP"):
+            op(x, 256)
     a = torch.zeros((4, 128), dtype=torch.int8)
     with pytest.raises(RuntimeError, match="CUDA|HIP"):
         torch.ops.turing_utils.int8_linear(a, a, torch.ones(4), torch.ones(4))

@@ -148,3 +148,100 @@ def test_markstein_quotient_is_code_exact_on_the_quantizer_domain():
     bad, pairs, fp32_diff = oracle.check_markstein_quant()
     assert pairs > 1_000_000_000
     assert bad == 0, f"{bad} (value, scale) pairs give a different INT8 code"
+
+
+# ---------------------------------------------------------------------------
+# fused input activations (convrot_quant.cu:137-156): this build's fixed fp32
+# exp / tanh, pinned against double precision
+# ---------------------------------------------------------------------------
+def test_exp_det_accuracy_and_edges():
+    v = np.concatenate([np.linspace(-87.0, 88.7, 40001), np.linspace(-1, 1, 2001)]).astype(np.float32)
+    got = np.array([oracle.exp_det(float(t)) for t in v], np.float64)
+    rel = np.abs(got / np.exp(v.astype(np.float64)) - 1)
+    assert rel.max() < 1.5e-7  # ~1.3 ulp
+    assert oracle.exp_det(0.0) == 1.0
+    assert oracle.exp_det(100.0) == np.inf and oracle.exp_det(-100.0) == 0.0
+    assert np.isnan(oracle.exp_det(float("nan")))
+
+
+def test_tanh_det_accuracy_and_symmetry():
+    u = np.concatenate([np.linspace(-12, 12, 48001), np.geomspace(1e-8, 1e-2, 2000)]).astype(np.float32)
+    got = np.array([oracle.tanh_det(float(t)) for t in u], np.float64)
+    assert np.abs(got - np.tanh(u.astype(np.float64))).max() < 1.3e-7
+    neg = np.array([oracle.tanh_det(float(-t)) for t in u], np.float64)
+    np.testing.assert_array_equal(neg, -got)
+    assert oracle.tanh_det(0.0) == 0.0 and oracle.tanh_det(20.0) == 1.0
+
+
+def _gelu64(x):
+    x = x.astype(np.float64)
+    return 0.5 * x * (1 + np.tanh(0.7978845608028654 * (x + 0.044715 * x ** 3)))
+
+
+def test_gelu_tanh_matches_fp64_and_torch():
+    rng = np.random.default_rng(4)
+    x = np.concatenate([rng.standard_normal(20000) * 3, np.linspace(-6, 6, 4001)]).astype(np.float32)
+    x = oracle.bf16_bits_to_f32(oracle.f32_to_bf16_bits(x))  # bf16 inputs, as the kernel sees them
+    got = np.array([oracle.gelu_tanh_bf16(float(t)) for t in x], np.float32)
+    # bf16 output: within one bf16 step of the fp64 value (plus the reference
+    # formula's own cancellation near x << 0, where values are ~1e-7)
+    ref = _gelu64(x)
+    assert np.all(np.abs(got - ref) <= np.abs(ref) * 2.0 ** -8 + 1e-6)
+    # and equal to torch's tanh-GELU in fp32 rounded to bf16 except at rare
+    # rounding ties (tanh differs in the last fp32 ulp) and around x ~ -5, where
+    # 1 + tanh cancels and each library's last tanh ulp shows in the bf16 result
+    tg = torch.nn.functional.gelu(torch.from_numpy(x), approximate="tanh").to(torch.bfloat16).float().numpy()
+    assert np.mean(tg[x > -4] == got[x > -4]) > 0.999
+    assert np.all(np.abs(tg - got) <= np.abs(tg) * 2.0 ** -6 + 1e-6)
+
+
+def test_swiglu_matches_fp64():
+    rng = np.random.default_rng(5)
+    g = (rng.standard_normal(20000) * 4).astype(np.float32)
+    u = rng.standard_normal(20000).astype(np.float32)
+    got = np.array([oracle.swiglu(float(a), float(b)) for a, b in zip(g, u)], np.float64)
+    ref = g.astype(np.float64) / (1 + np.exp(-g.astype(np.float64))) * u.astype(np.float64)
+    assert np.all(np.abs(got - ref) <= np.abs(ref) * 6e-7 + 1e-30)
+    assert oracle.swiglu(-200.0, 1.0) == 0.0 and oracle.swiglu(200.0, 2.0) == 400.0
+
+
+@pytest.mark.parametrize("group", [128, 256])
+def test_gelu_quantizer_is_gelu_then_quantizer(group):
+    """act 1 = bf16 tanh-GELU applied elementwise, then the plain quantizer."""
+    xb = inputs.bits(inputs.activation(16, 1024, 31))
+    xf = oracle.bf16_bits_to_f32(xb).reshape(xb.shape)
+    gb = oracle.f32_to_bf16_bits(np.vectorize(oracle.gelu_tanh_bf16, otypes=[np.float32])(xf))
+    q1, s1 = oracle.convrot_quant(xb, group, act=oracle.ACT_GELU_TANH)
+    q0, s0 = oracle.convrot_quant(gb, group)
+    np.testing.assert_array_equal(q1, q0)
+    np.testing.assert_array_equal(s1.view(np.uint32), s0.view(np.uint32))
+
+
+@pytest.mark.parametrize("group", [128, 256])
+def test_swiglu_quantizer_bounds(group):
+    """act 2 on [gate | up] rows: scales = amax/127 of the rotated fp64 SwiGLU
+    within fp32 rounding, codes within half a step of the exact quotient plus
+    the three bf16 roundings (y, scale, quotient; 2^-8 relative each)."""
+    rng = np.random.default_rng(group)
+    x = (rng.standard_normal((8, 2 * 512)) * 2).astype(np.float32)
+    xb = oracle.f32_to_bf16_bits(x)
+    xf = oracle.bf16_bits_to_f32(xb).reshape(xb.shape).astype(np.float64)
+    q, s = oracle.convrot_quant(xb, group, act=oracle.ACT_SWIGLU)
+    assert q.shape == (8, 512)
+    act = xf[:, :512] / (1 + np.exp(-xf[:, :512])) * xf[:, 512:]
+    y = (act.reshape(8, -1, group) @ dense(group).T).reshape(8, 512)
+    np.testing.assert_allclose(s, np.abs(y).max(axis=1) / 127, rtol=1e-5)
+    err = np.abs(q - y / s[:, None])
+    assert np.all(err <= 0.5 + np.abs(y / s[:, None]) * 3 * 2.0 ** -8 + 1e-3)
+
+
+@pytest.mark.parametrize("act", [1, 2])
+def test_staged_equals_row_buffer_with_activation(act):
+    """The same cross-check for the fused activations (validate_wan_fusions.py:45-80
+    compares the fused GELU codes against a two-pass quantizer)."""
+    k = 1024
+    xb = inputs.bits(inputs.activation(32, 2 * k if act == 2 else k, 22 + act))
+    q1, s1 = oracle.convrot_quant(xb, 256, staged=False, act=act)
+    q2, s2 = oracle.convrot_quant(xb, 256, staged=True, act=act)
+    np.testing.assert_array_equal(q1, q2)
+    np.testing.assert_allclose(s1, s2, rtol=1e-6, atol=5e-8)

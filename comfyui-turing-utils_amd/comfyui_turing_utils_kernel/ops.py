@@ -167,6 +167,7 @@ def _turing_dequantize_int8_bf16_fake(accumulator, activation_scale, weight_scal
 SUPPORTED_GROUP_SIZES = (128, 256)
 ACT_NONE, ACT_GELU_TANH, ACT_SWIGLU = 0, 1, 2
 STAGED_SCALE = 0x100  # scale = absmax * (1/127), the two-pass kernels' formula
+MAX_CONVROT_COLUMNS = 65536  # activated width; the kernel keeps a whole row in registers
 
 
 def _convrot_quantize(x: torch.Tensor, group_size: int, act: int, what: str,
@@ -186,6 +187,10 @@ def _convrot_quantize(x: torch.Tensor, group_size: int, act: int, what: str,
     hidden = width // 2 if act == ACT_SWIGLU else width
     if rows <= 0 or hidden <= 0 or hidden % group_size:
         raise ValueError(f"{what} width must be positive and divisible by {group_size}")
+    if hidden > MAX_CONVROT_COLUMNS:
+        raise ValueError(f"{what} width {hidden} exceeds the {MAX_CONVROT_COLUMNS}-column limit")
+    if x.data_ptr() % 16:
+        x = x.clone()  # the kernel reads 16-byte vectors
     q = torch.empty((rows, hidden), dtype=torch.int8, device=x.device)
     scales = torch.empty((rows, 1), dtype=torch.float32, device=x.device)
     with torch.cuda.device(x.device):

@@ -16,22 +16,37 @@
 // G = 128 is this build's extension: three radix-4 digits then the
 // orthonormal radix-2 digit (1/sqrt2)[[1,1],[1,-1]] on stride 64.
 //
-// MI355X mapping: one workgroup (4 wave64) per row.  Each wave rotates whole
-// groups in its own 1 KiB LDS scratch (no workgroup barrier between stages),
-// writes the bf16 row into an LDS row buffer and reduces the absmax with
-// cross-lane max; one workgroup barrier, then every thread quantizes 8
-// contiguous columns (16 B LDS read, 8 B global store).  The division by
-// bf16(scale) is a reciprocal multiply plus one FMA correction (Markstein),
-// which the CPU tests prove yields the same INT8 code as IEEE division for
-// every (value, scale) pair the quantizer can produce.
+// MI355X mapping: one workgroup per row; the row is cut into 1024-column
+// chunks and each wave takes up to four of them (ceil(chunks / 4) waves),
+// loading all of its input with 16-byte loads before any arithmetic.  Few
+// waves per row keep the per-row barrier short and let more rows share a CU
+// (measured faster than one chunk per wave).  A lane holds 16 consecutive
+// columns of one group, so the stride-1 and
+// stride-4 digits are register arithmetic.  One wave-local LDS transpose
+// (fp32, padded so reads are conflict-free) then gives each lane the 16
+// elements that share their two low digits, and the stride-16 and stride-64
+// digits are register arithmetic again.  The rotated values stay in
+// registers as packed bf16 while the row absmax is reduced (cross-lane max,
+// one workgroup barrier); each lane then quantizes its own values and a
+// second, byte-sized wave-local transpose puts the codes back in column order
+// for 16-byte stores.  The division by bf16(scale) is a reciprocal multiply
+// plus one FMA correction (Markstein), which the CPU tests prove yields the
+// same INT8 code as IEEE division for every (value, scale) pair the quantizer
+// can produce.
+#include <type_traits>
+
 #include "tu_common.h"
 
 namespace tu {
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kWaves = kThreads / 64;
+constexpr int kChunk = 1024;      // columns per wave pass: 64 lanes x 16
+constexpr int kMaxWaves = 16;
+constexpr int kMaxPasses = 4;     // so a row holds at most 65536 columns
+constexpr int kMaxCols = kChunk * kMaxWaves * kMaxPasses;
+constexpr int kScratchBytes = 8 * 144 * 4;  // per wave: the larger of the two padded layouts
 constexpr float kInvSqrt2 = 0.70710678118654752440f;
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ void lds_wave_sync() {
     // LDS operations of one wave complete in order; this stops the compiler
@@ -39,19 +54,16 @@ __device__ __forceinline__ void lds_wave_sync() {
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 }
 
-// One radix-4 digit in place on buf (G floats): lane gl owns the 4 elements
-// base + {0, 1, 2, 3} * S, base = (gl % S) + (gl / S) * 4S.
-template <int S>
-__device__ __forceinline__ void r4_stage_lds(float *buf, int gl) {
-    const int base = (gl % S) + (gl / S) * (4 * S);
-    const float x0 = buf[base];
-    const float x1 = buf[base + S];
-    const float x2 = buf[base + 2 * S];
-    const float x3 = buf[base + 3 * S];
-    buf[base] = 0.5f * (((x0 + x1) + x2) - x3);
-    buf[base + S] = 0.5f * (((x0 + x1) - x2) + x3);
-    buf[base + 2 * S] = 0.5f * (((x0 - x1) + x2) + x3);
-    buf[base + 3 * S] = 0.5f * (((-x0 + x1) + x2) + x3);
+// One radix-4 butterfly in the reference's add order (convrot_quant.cu:104-116).
+__device__ __forceinline__ void r4(float &x0, float &x1, float &x2, float &x3) {
+    const float y0 = 0.5f * (((x0 + x1) + x2) - x3);
+    const float y1 = 0.5f * (((x0 + x1) - x2) + x3);
+    const float y2 = 0.5f * (((x0 - x1) + x2) + x3);
+    const float y3 = 0.5f * (((-x0 + x1) + x2) + x3);
+    x0 = y0;
+    x1 = y1;
+    x2 = y2;
+    x3 = y3;
 }
 
 __device__ __forceinline__ float wave_max(float v) {
@@ -109,116 +121,178 @@ __device__ __forceinline__ float gelu_tanh_bf16(float x) {
 
 __device__ __forceinline__ float swiglu(float gate, float up) { return (gate / (1.0f + exp_det(-gate))) * up; }
 
+// Round-to-nearest-even to bf16 by the gfx950 conversion instruction
+// (v_cvt_pk_bf16_f32).  Identical to bf16_rne_bits for every non-NaN input;
+// a NaN keeps an unspecified NaN payload, which is harmless where this is
+// used: the rotated row buffer and the quotient only feed the division,
+// rint and clamp, where any NaN yields the same code.
+__device__ __forceinline__ uint16_t hw_bf16_bits(float v) {
+    return __builtin_bit_cast(uint16_t, static_cast<__bf16>(v));
+}
+// Through the bit pattern, so the compiler does not re-round a later rint in
+// bf16 arithmetic.
+__device__ __forceinline__ float hw_bf16_round(float v) { return bf16_bits_to_f32(hw_bf16_bits(v)); }
+
 __device__ __forceinline__ int32_t quant_code(float v, float rs, float ry) {
-    const float divided = bf16_round(div_markstein(v, rs, ry));
+    const float divided = hw_bf16_round(div_markstein(v, rs, ry));
     float qf = __builtin_rintf(divided);
     qf = fminf(127.0f, fmaxf(-128.0f, qf));
     return static_cast<int32_t>(qf);
 }
 
-// kAct: 0 none, 1 tanh-GELU, 2 SwiGLU (x rows are [gate | up], 2k wide).
-template <int G, int kAct>
-__global__ __launch_bounds__(kThreads) void convrot_quant_i8_kernel(
-    const uint16_t *__restrict__ x, int8_t *__restrict__ q, float *__restrict__ scales, int k,
-    int row_buffer_bytes, int staged_scale) {
-    extern __shared__ __align__(16) unsigned char smem[];
-    uint16_t *row_buf = reinterpret_cast<uint16_t *>(smem);
-    __shared__ float wave_amax[kWaves];
+__device__ __forceinline__ float activate(float v, float up, std::integral_constant<int, 0>) { return v; }
+__device__ __forceinline__ float activate(float v, float up, std::integral_constant<int, 1>) { return gelu_tanh_bf16(v); }
+__device__ __forceinline__ float activate(float v, float up, std::integral_constant<int, 2>) { return swiglu(v, up); }
 
-    constexpr int kLanesPerGroup = G / 4;           // each lane holds 4 elements
-    constexpr int kGroupsPerWave = 64 / kLanesPerGroup;
+// Raw bf16 input of one lane for one pass: 16 columns (and 16 "up" columns
+// for SwiGLU).
+template <int kAct>
+struct LaneInput {
+    u32x4 x[2];
+    u32x4 up[kAct == 2 ? 2 : 1];
+};
+
+template <int kAct>
+__device__ __forceinline__ void load_lane(LaneInput<kAct> &in, const uint16_t *xrow, int k, int col) {
+    in.x[0] = u32x4{0u, 0u, 0u, 0u};
+    in.x[1] = u32x4{0u, 0u, 0u, 0u};
+    if constexpr (kAct == 2) {
+        in.up[0] = u32x4{0u, 0u, 0u, 0u};
+        in.up[1] = u32x4{0u, 0u, 0u, 0u};
+    }
+    if (col < k) {
+        in.x[0] = *reinterpret_cast<const u32x4 *>(xrow + col);
+        in.x[1] = *reinterpret_cast<const u32x4 *>(xrow + col + 8);
+        if constexpr (kAct == 2) {
+            in.up[0] = *reinterpret_cast<const u32x4 *>(xrow + k + col);
+            in.up[1] = *reinterpret_cast<const u32x4 *>(xrow + k + col + 8);
+        }
+    }
+}
+
+// kAct: 0 none, 1 tanh-GELU, 2 SwiGLU (x rows are [gate | up], 2k wide).
+// kPasses: 1024-column chunks per wave (wave w takes chunks w, w + waves, ...).
+//
+// Lane layout in a pass: lane l of the wave covers columns c0 + 16 l .. +15
+// (c0 = chunk * 1024), i.e. group gi = l / (G/16) and, inside the group,
+// element index 16 L + p with L = l % (G/16), p = d0 + 4 d1.  After the
+// transpose a lane holds, for G = 256, p = L and t = d2 + 4 d3 = 0..15; for
+// G = 128, p = 2L and 2L + 1 (z[t] and z[8 + t]) with t = d2 + 4 d3 = 0..7.
+template <int G, int kAct, int kPasses>
+__global__ __launch_bounds__(1024) void convrot_quant_i8_kernel(
+    const uint16_t *__restrict__ x, int8_t *__restrict__ q, float *__restrict__ scales, int k, int staged_scale) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ float wave_amax[kMaxWaves];
+    constexpr int kLanesPerGroup = G / 16;
+    // Transpose scratch: group gi starts at dword gi * kGroupDwords (padded so
+    // the groups of a wave fall on different banks); element p of source lane
+    // L sits at 16 L + 4 ((p / 4 + L / 4) % 4) + p % 4 (16-byte chunks rotated
+    // by L / 4, so the 16-byte writes of lanes L and L + 4 hit different banks).
+    constexpr int kGroupDwords = G == 128 ? 144 : 272;
+    constexpr int kCodeGroupBytes = G + 16;  // code scratch, padded likewise
 
     const int tid = threadIdx.x;
-    const int wave = tid >> 6;
     const int lane = tid & 63;
-    const int gsub = lane / kLanesPerGroup;
-    const int gl = lane % kLanesPerGroup;
-    float *buf = reinterpret_cast<float *>(smem + row_buffer_bytes) + wave * 256 + gsub * G;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int waves = blockDim.x >> 6;
+    const int gi = lane / kLanesPerGroup;
+    const int L = lane % kLanesPerGroup;
+    float *scr = reinterpret_cast<float *>(smem + wave * kScratchBytes);
+    unsigned char *scr8 = smem + wave * kScratchBytes;
+    float *grp = scr + gi * kGroupDwords;
+    const int nchunks = (k + kChunk - 1) / kChunk;
+    const int64_t in_stride = kAct == 2 ? 2 * static_cast<int64_t>(k) : k;
 
     const int64_t row = blockIdx.x;
-    const uint16_t *xrow = x + row * static_cast<int64_t>(kAct == 2 ? 2 * k : k);
-    const int groups = k / G;
+    const uint16_t *xrow = x + row * in_stride;
+    LaneInput<kAct> in[kPasses];
+#pragma unroll
+    for (int pass = 0; pass < kPasses; ++pass)
+        if (wave + pass * waves < nchunks) load_lane<kAct>(in[pass], xrow, k, (wave + pass * waves) * kChunk + 16 * lane);
     float absmax = 0.0f;
+    uint32_t packed[kPasses][8];
+#pragma unroll
+    for (int pass = 0; pass < kPasses; ++pass) {
+        const int chunk = wave + pass * waves;
+        if (chunk >= nchunks) break;  // uniform across the wave
+        const bool active = chunk * kChunk + 16 * lane < k;  // whole groups are in or out (k % G == 0)
+        float v[16];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t w = in[pass].x[j / 4][j % 4];
+            const uint32_t u = kAct == 2 ? in[pass].up[(j / 4) % (kAct == 2 ? 2 : 1)][j % 4] : 0u;
+            v[2 * j] = activate(bf16_bits_to_f32(w & 0xffffu), bf16_bits_to_f32(u & 0xffffu),
+                                std::integral_constant<int, kAct>{});
+            v[2 * j + 1] = activate(bf16_bits_to_f32(w >> 16), bf16_bits_to_f32(u >> 16),
+                                    std::integral_constant<int, kAct>{});
+        }
+        // Digits d0 (stride 1) and d1 (stride 4) in registers (convrot_quant.cu:384-391).
+#pragma unroll
+        for (int d1 = 0; d1 < 4; ++d1) r4(v[4 * d1], v[4 * d1 + 1], v[4 * d1 + 2], v[4 * d1 + 3]);
+#pragma unroll
+        for (int d0 = 0; d0 < 4; ++d0) r4(v[d0], v[d0 + 4], v[d0 + 8], v[d0 + 12]);
 
-    for (int g0 = wave * kGroupsPerWave; g0 < groups; g0 += kWaves * kGroupsPerWave) {
-        const int g = g0 + gsub;
-        const bool active = g < groups;
-        const int col = g * G + 4 * gl;
-        float x0 = 0.0f, x1 = 0.0f, x2 = 0.0f, x3 = 0.0f;
-        if (active) {
-            const u32x2 v = *reinterpret_cast<const u32x2 *>(xrow + col);
-            x0 = bf16_bits_to_f32(v.x & 0xffffu);
-            x1 = bf16_bits_to_f32(v.x >> 16);
-            x2 = bf16_bits_to_f32(v.y & 0xffffu);
-            x3 = bf16_bits_to_f32(v.y >> 16);
-            if constexpr (kAct == 1) {
-                x0 = gelu_tanh_bf16(x0);
-                x1 = gelu_tanh_bf16(x1);
-                x2 = gelu_tanh_bf16(x2);
-                x3 = gelu_tanh_bf16(x3);
-            } else if constexpr (kAct == 2) {
-                const u32x2 u = *reinterpret_cast<const u32x2 *>(xrow + k + col);
-                x0 = swiglu(x0, bf16_bits_to_f32(u.x & 0xffffu));
-                x1 = swiglu(x1, bf16_bits_to_f32(u.x >> 16));
-                x2 = swiglu(x2, bf16_bits_to_f32(u.y & 0xffffu));
-                x3 = swiglu(x3, bf16_bits_to_f32(u.y >> 16));
+        // Wave-local transpose through LDS.
+        lds_wave_sync();  // earlier reads of the scratch are done
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            *reinterpret_cast<f32x4 *>(grp + 16 * L + 4 * ((c + (L >> 2)) & 3)) =
+                f32x4{v[4 * c], v[4 * c + 1], v[4 * c + 2], v[4 * c + 3]};
+        lds_wave_sync();
+        float z[16];
+        if constexpr (G == 256) {
+#pragma unroll
+            for (int t = 0; t < 16; ++t) z[t] = grp[16 * t + 4 * (((L >> 2) + (t >> 2)) & 3) + (L & 3)];
+        } else {
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                const f32x2 pair = *reinterpret_cast<const f32x2 *>(
+                    grp + 16 * t + 4 * (((L >> 1) + (t >> 2)) & 3) + ((2 * L) & 3));
+                z[t] = pair.x;
+                z[8 + t] = pair.y;
             }
         }
-        // Stride-1 digit in registers (convrot_quant.cu:384-391).
-        f32x4 y;
-        y.x = 0.5f * (((x0 + x1) + x2) - x3);
-        y.y = 0.5f * (((x0 + x1) - x2) + x3);
-        y.z = 0.5f * (((x0 - x1) + x2) + x3);
-        y.w = 0.5f * (((-x0 + x1) + x2) + x3);
-        *reinterpret_cast<f32x4 *>(buf + 4 * gl) = y;
-        lds_wave_sync();
-        r4_stage_lds<4>(buf, gl);
-        lds_wave_sync();
-        r4_stage_lds<16>(buf, gl);
-        lds_wave_sync();
+
+        // Digits d2 (stride 16) and d3 (stride 64) in registers (convrot_quant.cu:311-330).
         if constexpr (G == 256) {
-            // Stride-64 digit, stored as bf16 (convrot_quant.cu:311-330).
-            const int base = gl;
-            const float a0 = buf[base], a1 = buf[base + 64], a2 = buf[base + 128],
-                        a3 = buf[base + 192];
-            const float o0 = 0.5f * (((a0 + a1) + a2) - a3);
-            const float o1 = 0.5f * (((a0 + a1) - a2) + a3);
-            const float o2 = 0.5f * (((a0 - a1) + a2) + a3);
-            const float o3 = 0.5f * (((-a0 + a1) + a2) + a3);
-            if (active) {
-                absmax = fmaxf(absmax, fmaxf(fmaxf(fabsf(o0), fabsf(o1)), fmaxf(fabsf(o2), fabsf(o3))));
-                uint16_t *dst = row_buf + g * G + base;
-                dst[0] = static_cast<uint16_t>(bf16_rne_bits(o0));
-                dst[64] = static_cast<uint16_t>(bf16_rne_bits(o1));
-                dst[128] = static_cast<uint16_t>(bf16_rne_bits(o2));
-                dst[192] = static_cast<uint16_t>(bf16_rne_bits(o3));
-            }
+#pragma unroll
+            for (int d3 = 0; d3 < 4; ++d3) r4(z[4 * d3], z[4 * d3 + 1], z[4 * d3 + 2], z[4 * d3 + 3]);
+#pragma unroll
+            for (int d2 = 0; d2 < 4; ++d2) r4(z[d2], z[d2 + 4], z[d2 + 8], z[d2 + 12]);
         } else {
-            // Radix-2 digit on stride 64: lane gl owns pairs (b, b + 64) for
-            // b = gl and b = gl + 32.
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-                const int base = gl + 32 * h;
-                const float a0 = buf[base], a1 = buf[base + 64];
-                const float o0 = kInvSqrt2 * (a0 + a1);
-                const float o1 = kInvSqrt2 * (a0 - a1);
-                if (active) {
-                    absmax = fmaxf(absmax, fmaxf(fabsf(o0), fabsf(o1)));
-                    uint16_t *dst = row_buf + g * G + base;
-                    dst[0] = static_cast<uint16_t>(bf16_rne_bits(o0));
-                    dst[64] = static_cast<uint16_t>(bf16_rne_bits(o1));
+#pragma unroll
+                for (int d3 = 0; d3 < 2; ++d3)
+                    r4(z[8 * h + 4 * d3], z[8 * h + 4 * d3 + 1], z[8 * h + 4 * d3 + 2], z[8 * h + 4 * d3 + 3]);
+                // Radix-2 digit on stride 64: (1/sqrt2) [[1, 1], [1, -1]].
+#pragma unroll
+                for (int d2 = 0; d2 < 4; ++d2) {
+                    const float a0 = z[8 * h + d2], a1 = z[8 * h + d2 + 4];
+                    z[8 * h + d2] = kInvSqrt2 * (a0 + a1);
+                    z[8 * h + d2 + 4] = kInvSqrt2 * (a0 - a1);
                 }
             }
         }
-        lds_wave_sync();
+        if (active) {
+#pragma unroll
+            for (int t = 0; t < 16; ++t) absmax = fmaxf(absmax, fabsf(z[t]));
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            // G = 256: t = 2j, 2j + 1 of p = L.  G = 128: p = 2L (low), 2L + 1 (high) of t = j.
+            const float lo = G == 256 ? z[2 * j] : z[j];
+            const float hi = G == 256 ? z[2 * j + 1] : z[8 + j];
+            packed[pass][j] =
+                static_cast<uint32_t>(hw_bf16_bits(lo)) | (static_cast<uint32_t>(hw_bf16_bits(hi)) << 16);
+        }
     }
 
     absmax = wave_max(absmax);
     if (lane == 0) wave_amax[wave] = absmax;
     __syncthreads();
     float amax = wave_amax[0];
-#pragma unroll
-    for (int w = 1; w < kWaves; ++w) amax = fmaxf(amax, wave_amax[w]);
+    for (int w = 1; w < waves; ++w) amax = fmaxf(amax, wave_amax[w]);
     const float clipped = fminf(amax, 3.38953139e38f);
     const float scale = fmaxf(staged_scale ? clipped * (1.0f / 127.0f) : clipped / 127.0f, 1.0e-30f);
     if (tid == 0) scales[row] = scale;
@@ -226,24 +300,30 @@ __global__ __launch_bounds__(kThreads) void convrot_quant_i8_kernel(
     const float ry = 1.0f / rs;
 
     int8_t *qrow = q + row * static_cast<int64_t>(k);
-    for (int c = tid * 8; c < k; c += kThreads * 8) {
-        const u32x4 v = *reinterpret_cast<const u32x4 *>(row_buf + c);
-        uint32_t packed[2];
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const uint32_t w0 = h ? v.z : v.x;
-            const uint32_t w1 = h ? v.w : v.y;
-            const int32_t c0 = quant_code(bf16_bits_to_f32(w0 & 0xffffu), rs, ry);
-            const int32_t c1 = quant_code(bf16_bits_to_f32(w0 >> 16), rs, ry);
-            const int32_t c2 = quant_code(bf16_bits_to_f32(w1 & 0xffffu), rs, ry);
-            const int32_t c3 = quant_code(bf16_bits_to_f32(w1 >> 16), rs, ry);
-            packed[h] = (static_cast<uint32_t>(c0) & 0xffu) | ((static_cast<uint32_t>(c1) & 0xffu) << 8) |
-                        ((static_cast<uint32_t>(c2) & 0xffu) << 16) | (static_cast<uint32_t>(c3) << 24);
+    for (int pass = 0; pass < kPasses; ++pass) {
+        const int chunk = wave + pass * waves;
+        if (chunk >= nchunks) break;
+        const int col = chunk * kChunk + 16 * lane;
+        // Codes back to column order: element 16 t + p of group gi is byte
+        // gi * kCodeGroupBytes + 16 t + p of the wave's scratch.
+        lds_wave_sync();  // the scratch is free (transposed reads consumed)
+        unsigned char *gb = scr8 + gi * kCodeGroupBytes;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t w = packed[pass][j];
+            const uint32_t c0 = static_cast<uint32_t>(quant_code(bf16_bits_to_f32(w & 0xffffu), rs, ry)) & 0xffu;
+            const uint32_t c1 = static_cast<uint32_t>(quant_code(bf16_bits_to_f32(w >> 16), rs, ry)) & 0xffu;
+            if constexpr (G == 256) {
+                gb[32 * j + L] = static_cast<unsigned char>(c0);
+                gb[32 * j + 16 + L] = static_cast<unsigned char>(c1);
+            } else {
+                *reinterpret_cast<uint16_t *>(gb + 16 * j + 2 * L) = static_cast<uint16_t>(c0 | (c1 << 8));
+            }
         }
-        u32x2 out;
-        out.x = packed[0];
-        out.y = packed[1];
-        *reinterpret_cast<u32x2 *>(qrow + c) = out;
+        lds_wave_sync();
+        const u32x4 codes = *reinterpret_cast<const u32x4 *>(gb + 16 * L);
+        if (col < k) *reinterpret_cast<u32x4 *>(qrow + col) = codes;
     }
 }
 
@@ -263,18 +343,30 @@ extern "C" int32_t tu_convrot_quant_i8(const void *x_bf16, int8_t *q, float *sca
                static_cast<long long>(cols));
     TU_REQUIRE(rows <= 0x7fffffff && cols <= (1 << 20), "ConvRot dimensions out of range");
     TU_REQUIRE(x_bf16 && q && scale, "ConvRot pointers must be non-null");
-    TU_REQUIRE((reinterpret_cast<uintptr_t>(x_bf16) & 7) == 0 && (reinterpret_cast<uintptr_t>(q) & 7) == 0,
-               "ConvRot input must be 8-byte aligned");
+    TU_REQUIRE((reinterpret_cast<uintptr_t>(x_bf16) & 15) == 0 && (reinterpret_cast<uintptr_t>(q) & 15) == 0,
+               "ConvRot input and codes must be 16-byte aligned");
     if (require_gfx950()) return -1;
     if (rows == 0) return 0;
     const int k = static_cast<int>(cols);
-    const int row_buffer_bytes = (k * 2 + 15) / 16 * 16;
-    const size_t lds = static_cast<size_t>(row_buffer_bytes) + kWaves * 256 * sizeof(float);
-    TU_REQUIRE(lds <= 160 * 1024 - 64, "ConvRot row of %d columns exceeds LDS", k);
+    TU_REQUIRE(k <= kMaxCols, "ConvRot row of %d columns exceeds the %d-column limit", k, kMaxCols);
+    // Few waves per row, each carrying up to kMaxPasses chunks: measured
+    // faster than one chunk per wave (shorter barrier, more rows per CU).
+    const int nchunks = (k + kChunk - 1) / kChunk;
+    const int passes = nchunks < kMaxPasses ? nchunks : kMaxPasses;
+    const int waves = (nchunks + passes - 1) / passes;
+    const size_t lds = static_cast<size_t>(waves) * kScratchBytes;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    const dim3 grid(static_cast<unsigned>(rows));
     const auto *xp = static_cast<const uint16_t *>(x_bf16);
-#define TU_CONVROT_LAUNCH(G, A) convrot_quant_i8_kernel<G, A><<<grid, kThreads, lds, s>>>(xp, q, scale, k, row_buffer_bytes, staged_scale)
+    const dim3 grid(static_cast<unsigned>(rows));
+#define TU_CONVROT_LAUNCH(G, A)                                                                                \
+    do {                                                                                                      \
+        switch (passes) {                                                                                     \
+            case 1: convrot_quant_i8_kernel<G, A, 1><<<grid, waves * 64, lds, s>>>(xp, q, scale, k, staged_scale); break; \
+            case 2: convrot_quant_i8_kernel<G, A, 2><<<grid, waves * 64, lds, s>>>(xp, q, scale, k, staged_scale); break; \
+            case 3: convrot_quant_i8_kernel<G, A, 3><<<grid, waves * 64, lds, s>>>(xp, q, scale, k, staged_scale); break; \
+            default: convrot_quant_i8_kernel<G, A, 4><<<grid, waves * 64, lds, s>>>(xp, q, scale, k, staged_scale); break; \
+        }                                                                                                     \
+    } while (0)
     if (group == 256) {
         if (act == 0) TU_CONVROT_LAUNCH(256, 0);
         else if (act == 1) TU_CONVROT_LAUNCH(256, 1);

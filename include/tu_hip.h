@@ -60,10 +60,10 @@ int32_t tu_device_supported(int32_t device);
  *   scale[r] = max(min(absmax_r, 3.38953139e38) / 127, 1e-30)
  *   q[r][c]  = clamp(rne(bf16(bf16(y[r][c]) / bf16(scale[r]))), -128, 127)
  * x: bf16 [rows, cols] (TU_ACT_SWIGLU: [rows, 2*cols]), row-major contiguous.
- * q: int8 [rows, cols]; scale: fp32 [rows].  cols % group == 0; x and q 8-byte
- * aligned.  tanh and exp inside the activations are fixed fp32 sequences
- * (range reduction by ln2 and a degree-7 Taylor polynomial; tanh(u) =
- * 1 - 2/(e^2u + 1)), bit-identical to the CPU oracle.
+ * q: int8 [rows, cols]; scale: fp32 [rows].  cols % group == 0, cols <= 65536;
+ * x and q 16-byte aligned.  tanh and exp inside the activations are fixed
+ * fp32 sequences (range reduction by ln2 and a degree-7 Taylor polynomial;
+ * tanh(u) = 1 - 2/(e^2u + 1)), bit-identical to the CPU oracle.
  * Replaces turing_utils::bf16_int8_convrot_quantize (act 0 and 2;
  * kernel/comfyui_turing_utils_kernel/ops.py:257-282 ->
  * kernel/csrc/bindings.cpp:603-646 -> kernel/csrc/turing/convrot_quant.cu:566-589),

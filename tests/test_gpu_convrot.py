@@ -32,7 +32,8 @@ def _assert_exact(x: torch.Tensor, group: int, dev, label: str):
 
 
 @pytest.mark.parametrize("group", [128, 256])
-@pytest.mark.parametrize("m,k,seed", [(1, 256, 11), (3, 512, 12), (17, 1536, 13), (64, 5120, 14), (8, 13824, 15)])
+@pytest.mark.parametrize("m,k,seed", [(1, 256, 11), (3, 512, 12), (17, 1536, 13), (64, 5120, 14), (8, 13824, 15),
+                                      (5, 20480, 16), (3, 32768, 17), (2, 65536, 19)])
 def test_convrot_random(gpu_device, group, m, k, seed):
     _assert_exact(inputs.activation(m, k, seed), group, gpu_device, f"random m={m} k={k}")
 
@@ -69,6 +70,20 @@ def test_convrot_rejects_bad_width(gpu_device):
     x = torch.zeros(2, 200, dtype=torch.bfloat16, device=gpu_device)
     with pytest.raises(ValueError):
         torch.ops.turing_utils.bf16_int8_convrot_quantize(x, 128)
+    x = torch.zeros(2, 65536 + 128, dtype=torch.bfloat16, device=gpu_device)
+    with pytest.raises(ValueError, match="limit"):
+        torch.ops.turing_utils.bf16_int8_convrot_quantize(x, 128)
+
+
+def test_convrot_misaligned_view(gpu_device):
+    """A view whose data pointer is not 16-byte aligned is copied, not refused."""
+    base = inputs.activation(1, 4 * 256 + 8, 18).reshape(-1)
+    view = base.to(gpu_device)[1:1 + 4 * 256].reshape(4, 256)
+    assert view.data_ptr() % 16 != 0
+    q, s = torch.ops.turing_utils.bf16_int8_convrot_quantize(view, 128)
+    q_ref, s_ref = oracle.convrot_quant(inputs.bits(base[1:1 + 4 * 256].reshape(4, 256).contiguous()), 128)
+    np.testing.assert_array_equal(q.cpu().numpy(), q_ref)
+    np.testing.assert_array_equal(s.cpu().numpy().reshape(-1).view(np.uint32), s_ref.view(np.uint32))
 
 
 # ---------------------------------------------------------------------------

@@ -61,9 +61,18 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
          _f32, _i32, _c_void_p],
     ),
+    "tu_qk_rms_rope_int8": (
+        _i32,
+        [_c_void_p, _c_void_p, _i32, _i64, _i64, _i64, _i64, _i64, _i64,
+         _i64, _i64, _i64, _i64, _i64, _i64,
+         _c_void_p, _c_void_p, _i32, _f32, _c_void_p, _i64, _i32, _i64, _i64,
+         _i64, _i64, _i64, _i64, _i64,
+         _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _c_void_p, _i64, _i64, _i64,
+         _c_void_p, _c_void_p, _c_void_p],
+    ),
 }
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

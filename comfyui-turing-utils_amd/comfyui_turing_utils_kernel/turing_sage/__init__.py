@@ -36,8 +36,10 @@ def split_prequantization_available() -> bool:
 
 
 def fused_qk_preprocessing_available() -> bool:
-    """Fused RMSNorm+RoPE+INT8 Q/K preprocessing is not built for gfx950."""
-    return False
+    """True when the library (with ``tu_qk_rms_rope_int8``) loads: the fused
+    RMSNorm + RoPE + INT8 Q/K preprocessing of the reference's
+    ``quant_qk_rms_rope_int8_cuda`` (turing_sage/__init__.py:98-107)."""
+    return available()
 
 
 def sageattn(*args, **kwargs):
@@ -48,6 +50,18 @@ def sageattn(*args, **kwargs):
 
 def prequantize_sageattn(*args, **kwargs):
     from .core import prequantize_sageattn as implementation
+
+    return implementation(*args, **kwargs)
+
+
+def prequantize_rms_rope_qk(*args, **kwargs):
+    from .core import prequantize_rms_rope_qk as implementation
+
+    return implementation(*args, **kwargs)
+
+
+def prequantize_sageattn_from_qk(*args, **kwargs):
+    from .core import prequantize_sageattn_from_qk as implementation
 
     return implementation(*args, **kwargs)
 
@@ -112,6 +126,8 @@ __all__ = [
     "sageattn",
     "sageattn_compiled",
     "prequantize_sageattn",
+    "prequantize_rms_rope_qk",
+    "prequantize_sageattn_from_qk",
     "sageattn_from_prequantized",
     "preflight",
 ]

@@ -25,7 +25,7 @@ from typing import Optional
 import torch
 
 from .. import _lib
-from .quant import SUPPORTED_BLOCKS, _layout_dims, per_block_int8, value_transpose
+from .quant import SUPPORTED_BLOCKS, _layout_dims, per_block_int8, rms_rope_per_warp_int8, value_transpose
 
 KERNEL_HEAD_DIM = 128
 
@@ -51,6 +51,22 @@ class PrequantizedSageAttention:
     blkq: int
     blkk: int
     output_dtype: torch.dtype
+
+
+@dataclasses.dataclass(frozen=True)
+class PrequantizedQK:
+    """Fused-preprocessing result (``prequantize_rms_rope_qk``): INT8 Q with
+    16-token scales [B, Hq, ceil(Lq / 64) * 4] and INT8 K with 64-token scales
+    [B, Hk, ceil(Lk / 64)], the reference's dataclass (core.py:39-47)."""
+
+    query_int8: torch.Tensor
+    query_scale: torch.Tensor
+    key_int8: torch.Tensor
+    key_scale: torch.Tensor
+    tensor_layout: str
+    input_dtype: torch.dtype
+    original_head_dim: int
+    route_original_basis: bool = False
 
 
 def _validate(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, tensor_layout: str) -> None:
@@ -258,3 +274,95 @@ def sageattn(
         smooth_k=smooth_k, BLKQ=BLKQ, BLKK=BLKK,
     )
     return sageattn_from_prequantized(quantized)
+
+
+def prequantize_rms_rope_qk(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    q_norm: torch.Tensor,
+    k_norm: torch.Tensor,
+    freqs: Optional[torch.Tensor],
+    *,
+    epsilon: float,
+    rot_dim: int,
+    tensor_layout: str = "HND",
+    norm_scope: str = "head",
+    split_half: bool = False,
+    rotate_qk: bool = False,
+    stabilize_k: bool = False,
+) -> PrequantizedQK:
+    """Normalized, rotated and quantized Q/K without materializing bf16
+    intermediates (reference core.py:222-289), through
+    ``torch.ops.turing_utils.qk_rms_rope_int8``."""
+    if not q.is_cuda or not k.is_cuda:
+        raise ValueError("Q/K inputs must be on CUDA")
+    if q.device != k.device:
+        raise ValueError("Q/K inputs must share one CUDA device")
+    if q.dtype not in (torch.float16, torch.bfloat16) or k.dtype != q.dtype:
+        raise TypeError("fused Q/K preprocessing requires matching FP16 or BF16 inputs")
+    if q.ndim != 4 or k.ndim != 4 or q.shape[0] != k.shape[0] or q.shape[-1] != k.shape[-1]:
+        raise ValueError("fused Q/K preprocessing requires compatible four-dimensional tensors")
+    if q.stride(-1) != 1 or k.stride(-1) != 1:
+        raise ValueError("the last Q/K dimension must be contiguous")
+    head_dim = int(q.shape[-1])
+    if head_dim not in (64, 128):
+        raise ValueError("fused Q/K preprocessing requires head_dim 64 or 128")
+    q_norm = q_norm.to(device=q.device, dtype=q.dtype).contiguous()
+    k_norm = k_norm.to(device=q.device, dtype=q.dtype).contiguous()
+    freqs = (torch.empty(0, device=q.device, dtype=q.dtype) if freqs is None
+             else freqs.to(device=q.device, dtype=q.dtype))
+    from .custom_ops import qk_rms_rope_int8
+
+    q_int8, q_scale, k_int8, k_scale = qk_rms_rope_int8(
+        q, k, q_norm, k_norm, freqs, float(epsilon), int(rot_dim), tensor_layout, norm_scope,
+        bool(split_half), bool(rotate_qk), bool(stabilize_k),
+    )
+    return PrequantizedQK(
+        query_int8=q_int8, query_scale=q_scale, key_int8=k_int8, key_scale=k_scale,
+        tensor_layout=tensor_layout, input_dtype=q.dtype, original_head_dim=head_dim,
+        route_original_basis=bool(rotate_qk),
+    )
+
+
+def prequantize_sageattn_from_qk(
+    qk: PrequantizedQK,
+    value: torch.Tensor,
+    *,
+    is_causal: bool = False,
+    sm_scale: Optional[float] = None,
+) -> PrequantizedSageAttention:
+    """Attach V to a fused Q/K preprocessing result without rereading Q/K
+    (reference core.py:477-513).  Q/K codes of head_dim 64 are zero-padded to
+    the kernel's 128 channels (dot products unchanged)."""
+    if qk.tensor_layout not in ("HND", "NHD"):
+        raise ValueError(f"Unsupported tensor_layout: {qk.tensor_layout}")
+    if qk.route_original_basis:
+        raise ValueError("rotated Q/K belong to the w8a8 attention variant, which is not built for gfx950")
+    if value.dtype != qk.input_dtype:
+        raise TypeError("preprocessed Q/K and V must have matching logical dtypes")
+    if value.device != qk.query_int8.device:
+        raise ValueError("preprocessed Q/K and V must share one CUDA device")
+    if value.ndim != 4 or value.stride(-1) != 1:
+        raise ValueError("preprocessed Sage V must be four-dimensional with contiguous channels")
+    head_axis = 1 if qk.tensor_layout == "HND" else 2
+    seq_axis = 2 if qk.tensor_layout == "HND" else 1
+    if (value.size(0) != qk.key_int8.size(0) or value.size(head_axis) != qk.key_int8.size(head_axis)
+            or value.size(seq_axis) != qk.key_int8.size(seq_axis) or value.size(-1) != qk.key_int8.size(-1)):
+        raise ValueError("preprocessed Q/K and V shapes are incompatible")
+    scale = float(sm_scale) if sm_scale is not None else qk.original_head_dim ** -0.5
+    q_int8, k_int8 = qk.query_int8, qk.key_int8
+    pad = KERNEL_HEAD_DIM - q_int8.size(-1)
+    if pad:
+        q_int8 = torch.nn.functional.pad(q_int8, (0, pad))
+        k_int8 = torch.nn.functional.pad(k_int8, (0, pad))
+    lq = q_int8.size(seq_axis)
+    # the fused producer pads Q scales to 4 per 64 tokens; the kernel indexes
+    # them as ceil(Lq / 16) per head
+    q_scale = qk.query_scale[..., : (lq + 15) // 16].contiguous()
+    with torch.cuda.device(value.device):
+        value_t, _ = value_transpose(_prepare(value), qk.tensor_layout)
+    return PrequantizedSageAttention(
+        query_int8=q_int8, query_scale=q_scale, key_int8=k_int8, key_scale=qk.key_scale, value_t=value_t,
+        tensor_layout=qk.tensor_layout, original_head_dim=qk.original_head_dim, is_causal=bool(is_causal),
+        sm_scale=scale, blkq=16, blkk=64, output_dtype=value.dtype,
+    )

@@ -88,3 +88,89 @@ def value_transpose(v: torch.Tensor, tensor_layout: str = "HND") -> tuple[torch.
         _lib.call("tu_sage_v_prep", v.data_ptr(), batch, heads, tokens, dim, sb, sh, sl, vt.data_ptr(), lpad,
                   _lib.stream_of(v.device))
     return vt, lpad
+
+
+def rms_rope_per_warp_int8(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    q_norm: torch.Tensor,
+    k_norm: torch.Tensor,
+    freqs: torch.Tensor | None,
+    *,
+    epsilon: float,
+    rot_dim: int,
+    tensor_layout: str,
+    norm_scope: str,
+    split_half: bool,
+    rotate_qk: bool = False,
+    stabilize_k: bool = False,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Fused Q/K RMSNorm + RoPE + INT8 (Q per 16 tokens, K per 64 tokens), the
+    reference's ``rms_rope_per_warp_int8`` (turing_sage/quant.py:6-87).
+
+    Q scales are [B, Hq, ceil(Lq / 64) * 4], K scales [B, Hk, ceil(Lk / 64)].
+    ``rotate_qk`` / ``stabilize_k`` belong to the w8a8 attention variant,
+    which this build does not provide.
+    """
+    if rotate_qk or stabilize_k:
+        raise ValueError("rotate_qk / stabilize_k need the w8a8 attention variant, which is not built for gfx950")
+    if tensor_layout not in ("HND", "NHD"):
+        raise ValueError(f"Unknown tensor layout: {tensor_layout}")
+    if norm_scope not in ("head", "row"):
+        raise ValueError("norm_scope must be head or row")
+    if q.dtype not in (torch.float16, torch.bfloat16) or k.dtype != q.dtype:
+        raise TypeError("fused Q/K preprocessing requires matching FP16 or BF16 inputs")
+    if q.ndim != 4 or k.ndim != 4 or q.size(0) != k.size(0) or q.size(-1) != k.size(-1):
+        raise ValueError("fused Q/K preprocessing requires compatible four-dimensional tensors")
+    head_dim = q.size(-1)
+    if head_dim not in (64, 128):
+        raise ValueError("fused RMSNorm+RoPE Q/K quantization requires head_dim 64 or 128")
+    if q.stride(-1) != 1 or k.stride(-1) != 1:
+        raise ValueError("the last Q/K dimension must be contiguous")
+    hq, lq, qsb, qsh, qsl = _layout_dims(q, tensor_layout)
+    hk, lk, ksb, ksh, ksl = _layout_dims(k, tensor_layout)
+    batch = q.size(0)
+    if rot_dim < 0 or rot_dim > head_dim or rot_dim % 2:
+        raise ValueError("rot_dim must be even and within head_dim")
+    expect_q = head_dim if norm_scope == "head" else hq * head_dim
+    expect_k = head_dim if norm_scope == "head" else hk * head_dim
+    if q_norm.numel() != expect_q or k_norm.numel() != expect_k:
+        raise ValueError("Q/K norm weight shapes are incompatible")
+    q_norm = q_norm.to(device=q.device, dtype=q.dtype).contiguous()
+    k_norm = k_norm.to(device=q.device, dtype=q.dtype).contiguous()
+    fb = fl = 1
+    fstrides = (0, 0, 0, 0, 0)
+    if rot_dim > 0:
+        if freqs is None or freqs.ndim != 6:
+            raise ValueError("RoPE frequencies must be [B|1, L|1, 1, rot_dim / 2, 2, 2]")
+        freqs = freqs.to(device=q.device, dtype=q.dtype)
+        if freqs.size(2) != 1 or freqs.size(3) != rot_dim // 2 or freqs.size(4) != 2 or freqs.size(5) != 2:
+            raise ValueError("RoPE frequency shape is incompatible")
+        fb, fl = freqs.size(0), freqs.size(1)
+        if not ((fb == 1 or fb == batch) and (fl == 1 or (fl == lq and lq == lk))):
+            raise ValueError("RoPE batch/sequence broadcasting is incompatible")
+        fstrides = (freqs.stride(0), freqs.stride(1), freqs.stride(3), freqs.stride(4), freqs.stride(5))
+    if any(t.data_ptr() % 16 or any(s % 8 for s in t.stride()[:-1]) for t in (q, k)):
+        q, k = q.contiguous(), k.contiguous()
+        hq, lq, qsb, qsh, qsl = _layout_dims(q, tensor_layout)
+        hk, lk, ksb, ksh, ksl = _layout_dims(k, tensor_layout)
+    q_int8 = torch.empty(q.shape, dtype=torch.int8, device=q.device)
+    k_int8 = torch.empty(k.shape, dtype=torch.int8, device=k.device)
+    _, _, qob, qoh, qol = _layout_dims(q_int8, tensor_layout)
+    _, _, kob, koh, kol = _layout_dims(k_int8, tensor_layout)
+    q_scale = torch.empty((batch, hq, (lq + 63) // 64 * 4), dtype=torch.float32, device=q.device)
+    k_scale = torch.empty((batch, hk, (lk + 63) // 64), dtype=torch.float32, device=k.device)
+    q_rrms = k_rrms = None
+    if norm_scope == "row":
+        q_rrms = torch.empty((batch, lq), dtype=torch.float32, device=q.device)
+        k_rrms = torch.empty((batch, lk), dtype=torch.float32, device=k.device)
+    with torch.cuda.device(q.device):
+        _lib.call(
+            "tu_qk_rms_rope_int8",
+            q.data_ptr(), k.data_ptr(), 1 if q.dtype == torch.float16 else 0, batch, hq, hk, lq, lk, head_dim,
+            qsb, qsh, qsl, ksb, ksh, ksl, q_norm.data_ptr(), k_norm.data_ptr(), 1 if norm_scope == "row" else 0,
+            float(epsilon), _lib.ptr(freqs) if rot_dim > 0 else None, int(rot_dim), int(bool(split_half)), fb, fl,
+            *fstrides, _lib.ptr(q_rrms), _lib.ptr(k_rrms), q_int8.data_ptr(), qob, qoh, qol,
+            k_int8.data_ptr(), kob, koh, kol, q_scale.data_ptr(), k_scale.data_ptr(), _lib.stream_of(q.device),
+        )
+    return q_int8, q_scale, k_int8, k_scale

@@ -1,0 +1,328 @@
+// Fused Q/K RMSNorm + RoPE + per-tile INT8 quantization for gfx950: the
+// producer of Sage attention's Q/K in a Wan block.
+//
+// Semantics follow the reference's quantize_qk_kernel / quantize_tile
+// (kernel/csrc/turing/sage/qk_preprocess.cu:417-629) without its Hadamard /
+// anchor variant:
+//   rrms = 1 / sqrt(sumsq / n + eps)   per token: over the head's D channels
+//          (head scope) or over all H*D channels of the token (row scope)
+//   a_c  = T((x_c * rrms) * w_c)       T = the input type (bf16 or fp16)
+//   y_c  = T(fma(f1, a_second, f0 * a_first)) for c < rot_dim (interleaved
+//          or split-half pairs; (f0, f1) the row of the pair's 2x2 matrix
+//          that produces channel c), y_c = a_c otherwise
+//   per tile (Q: 16 tokens, K: 64 tokens) of one (batch, head):
+//   amax = max(1e-7, max |y|), scale = amax / 127,
+//   q = clamp(rint(y * (127 / amax)), -127, 127).
+// The sum of squares has a fixed order (8-channel FMA chains, then a
+// butterfly across a head's packs; heads added in order for the row scope),
+// and square root and divisions are IEEE, so the CPU oracle restates it bit
+// for bit.  The reference uses rsqrtf, which is not reproduced.
+//
+// MI355X mapping: one workgroup (4 wave64) per tile.  A thread owns 8
+// consecutive channels ("pack") of a token; the packs of one token are
+// consecutive lanes, so the head-scope sum is a lane butterfly.  The
+// normalized tile goes through LDS once so RoPE can take its pair partner
+// from any pack (split-half pairs and partial rot_dim included); the tile
+// amax is a wave max plus one LDS exchange.  Row-scope rrms comes from a
+// one-wave-per-token pre-pass into caller scratch.
+#include <type_traits>
+
+#include "tu_common.h"
+
+namespace tu {
+namespace {
+
+constexpr int kQkThreads = 256;
+constexpr int kQTile = 16;
+constexpr int kKTile = 64;
+constexpr int kMaxIters = kKTile * 16 / kQkThreads;  // packs per thread for a D = 128 K tile
+
+// bf16 (kFp16 = false) or fp16 bit patterns <-> fp32.
+template <bool kFp16>
+__device__ __forceinline__ float t_to_f32(uint32_t bits16) {
+    if constexpr (kFp16) return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits16)));
+    else return __uint_as_float(bits16 << 16);
+}
+// Round to the input type (RNE, the hardware conversion) and back.  The
+// empty asm pins v as an fp32 value first: without it the compiler folds the
+// conversion into the producing multiply or FMA (v_fma_mixlo_f16), which
+// rounds the exact result to fp16 once instead of rounding to fp32 and then
+// to fp16 as the reference does, and differs at fp32 values that are fp16
+// rounding ties.
+template <bool kFp16>
+__device__ __forceinline__ float t_round(float v) {
+    asm volatile("" : "+v"(v));
+    if constexpr (kFp16) return static_cast<float>(static_cast<_Float16>(v));
+    else return __uint_as_float(static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(v))) << 16);
+}
+
+struct QkArgs {
+    const uint16_t *x[2];        // Q, K
+    const uint16_t *norm[2];
+    float *rrms[2];              // row scope: [B, L] per tensor
+    int8_t *out[2];
+    float *scale[2];
+    const uint16_t *freqs;
+    int64_t heads[2], len[2];
+    int64_t x_sb[2], x_sh[2], x_sl[2];
+    int64_t o_sb[2], o_sh[2], o_sl[2];
+    int64_t ntiles[2];           // scale entries per (batch, head)
+    int64_t f_sb, f_sl, f_sp, f_sr, f_sc;
+    int64_t f_batches, f_len;
+    int rot_dim;
+    float eps;
+};
+
+template <bool kFp16, int D, bool kSplit, bool kRow>
+__global__ __launch_bounds__(kQkThreads) void qk_rope_quant_kernel(QkArgs args) {
+    constexpr int kPacks = D / 8;  // lanes per token
+    __shared__ __align__(16) float tile_a[kKTile * D];
+    __shared__ float wave_amax[kQkThreads / 64];
+
+    const int tid = threadIdx.x;
+    const int64_t b = blockIdx.y;
+    // Tasks: Q tiles of every head first, then K tiles.
+    int64_t task = blockIdx.x;
+    const int which = task < args.heads[0] * args.ntiles[0] ? 0 : 1;
+    if (which) task -= args.heads[0] * args.ntiles[0];
+    const int64_t head = task / args.ntiles[which];
+    const int64_t tile_id = task - head * args.ntiles[which];
+    const int tile = which ? kKTile : kQTile;
+    const int64_t len = args.len[which];
+    const int64_t t0 = tile_id * tile;
+    const int iters = (tile * kPacks + kQkThreads - 1) / kQkThreads;
+    const uint16_t *xbase = args.x[which] + b * args.x_sb[which] + head * args.x_sh[which];
+    const uint16_t *norm = args.norm[which] + (kRow ? head * D : 0);
+    const int pairs = args.rot_dim / 2;
+
+    // Pass 1: RMSNorm into the LDS tile.
+#pragma unroll
+    for (int it = 0; it < kMaxIters; ++it) {
+        if (it >= iters) break;
+        const int pidx = tid + it * kQkThreads;
+        const int to = pidx / kPacks, pack = pidx % kPacks;
+        const bool in_tile = to < tile;
+        const int64_t t = t0 + to;
+        const bool valid = in_tile && t < len;
+        u32x4 raw = u32x4{0u, 0u, 0u, 0u};
+        if (valid) raw = *reinterpret_cast<const u32x4 *>(xbase + t * args.x_sl[which] + pack * 8);
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            v[2 * j] = t_to_f32<kFp16>(raw[j] & 0xffffu);
+            v[2 * j + 1] = t_to_f32<kFp16>(raw[j] >> 16);
+        }
+        float rrms;
+        if constexpr (kRow) {
+            rrms = valid ? args.rrms[which][b * len + t] : 0.0f;
+        } else {
+            // Every lane of the token's pack group takes part, valid or not.
+            float s = 0.0f;
+#pragma unroll
+            for (int c = 0; c < 8; ++c) s = __builtin_fmaf(v[c], v[c], s);
+#pragma unroll
+            for (int off = kPacks / 2; off > 0; off >>= 1) s = s + __shfl_xor(s, off, kPacks);
+            rrms = 1.0f / __builtin_sqrtf(s / static_cast<float>(D) + args.eps);
+        }
+        if (in_tile) {
+            const u32x4 wraw = *reinterpret_cast<const u32x4 *>(norm + pack * 8);
+            float a[8];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                a[2 * j] = t_round<kFp16>((v[2 * j] * rrms) * t_to_f32<kFp16>(wraw[j] & 0xffffu));
+                a[2 * j + 1] = t_round<kFp16>((v[2 * j + 1] * rrms) * t_to_f32<kFp16>(wraw[j] >> 16));
+            }
+            float *dst = tile_a + to * D + pack * 8;
+            *reinterpret_cast<f32x4 *>(dst) = f32x4{a[0], a[1], a[2], a[3]};
+            *reinterpret_cast<f32x4 *>(dst + 4) = f32x4{a[4], a[5], a[6], a[7]};
+        }
+    }
+    __syncthreads();
+
+    // Pass 2: RoPE, tile amax.
+    float y[kMaxIters][8];
+    float amax = 0.0000001f;
+#pragma unroll
+    for (int it = 0; it < kMaxIters; ++it) {
+        if (it >= iters) break;
+        const int pidx = tid + it * kQkThreads;
+        const int to = pidx / kPacks, pack = pidx % kPacks;
+        const int64_t t = t0 + to;
+        const bool valid = to < tile && t < len;
+        if (!valid) continue;
+        const float *arow = tile_a + to * D;
+        const uint16_t *frow = args.rot_dim == 0 ? nullptr
+                                                 : args.freqs + (args.f_batches == 1 ? 0 : b) * args.f_sb +
+                                                       (args.f_len == 1 ? 0 : t) * args.f_sl;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int c = pack * 8 + j;
+            float val = arow[c];
+            if (c < args.rot_dim) {
+                const int pair = kSplit ? (c < pairs ? c : c - pairs) : c >> 1;
+                const int first = kSplit ? pair : 2 * pair;
+                const int second = kSplit ? pair + pairs : first + 1;
+                const int comp = kSplit ? (c >= pairs) : (c & 1);
+                const uint16_t *fp = frow + pair * args.f_sp + comp * args.f_sr;
+                const float f0 = t_to_f32<kFp16>(fp[0]);
+                const float f1 = t_to_f32<kFp16>(fp[args.f_sc]);
+                val = t_round<kFp16>(__builtin_fmaf(f1, arow[second], f0 * arow[first]));
+            }
+            y[it][j] = val;
+            amax = fmaxf(amax, fabsf(val));
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+    if ((tid & 63) == 0) wave_amax[tid >> 6] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(wave_amax[0], wave_amax[1]), fmaxf(wave_amax[2], wave_amax[3]));
+    if (tid == 0) args.scale[which][(b * args.heads[which] + head) * args.ntiles[which] + tile_id] = amax / 127.0f;
+    const float inv = 127.0f / amax;
+
+    // Pass 3: codes, one 8-byte store per pack.
+    int8_t *obase = args.out[which] + b * args.o_sb[which] + head * args.o_sh[which];
+#pragma unroll
+    for (int it = 0; it < kMaxIters; ++it) {
+        if (it >= iters) break;
+        const int pidx = tid + it * kQkThreads;
+        const int to = pidx / kPacks, pack = pidx % kPacks;
+        const int64_t t = t0 + to;
+        if (!(to < tile && t < len)) continue;
+        uint32_t w[2] = {0u, 0u};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float r = fminf(127.0f, fmaxf(-127.0f, __builtin_rintf(y[it][j] * inv)));
+            w[j >> 2] |= (static_cast<uint32_t>(static_cast<int32_t>(r)) & 0xffu) << (8 * (j & 3));
+        }
+        *reinterpret_cast<u32x2 *>(obase + t * args.o_sl[which] + pack * 8) = u32x2{w[0], w[1]};
+    }
+}
+
+// Row-scope rrms: one wave per (token, batch) of Q then K.  Each group of
+// D/8 lanes reduces one head's sum of squares (same order as the head
+// scope); the head sums are then added in head order.
+template <bool kFp16, int D>
+__global__ __launch_bounds__(64) void row_rrms_kernel(QkArgs args) {
+    constexpr int kPacks = D / 8;
+    constexpr int kHeadsPerPass = 64 / kPacks;
+    const int lane = threadIdx.x;
+    const int64_t b = blockIdx.y;
+    int64_t t = blockIdx.x;
+    const int which = t < args.len[0] ? 0 : 1;
+    if (which) t -= args.len[0];
+    const int64_t heads = args.heads[which];
+    const uint16_t *xrow = args.x[which] + b * args.x_sb[which] + t * args.x_sl[which];
+    const int grp = lane / kPacks, pack = lane % kPacks;
+    float total = 0.0f;
+    for (int64_t h0 = 0; h0 < heads; h0 += kHeadsPerPass) {
+        const int64_t h = h0 + grp;
+        u32x4 raw = u32x4{0u, 0u, 0u, 0u};
+        if (h < heads) raw = *reinterpret_cast<const u32x4 *>(xrow + h * args.x_sh[which] + pack * 8);
+        float s = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float lo = t_to_f32<kFp16>(raw[j] & 0xffffu), hi = t_to_f32<kFp16>(raw[j] >> 16);
+            s = __builtin_fmaf(lo, lo, s);
+            s = __builtin_fmaf(hi, hi, s);
+        }
+#pragma unroll
+        for (int off = kPacks / 2; off > 0; off >>= 1) s = s + __shfl_xor(s, off, kPacks);
+        // Heads of this pass in order (group leaders at lanes g * kPacks).
+#pragma unroll
+        for (int g = 0; g < kHeadsPerPass; ++g) {
+            const float hs = __shfl(s, g * kPacks, 64);
+            if (h0 + g < heads) total = total + hs;
+        }
+    }
+    if (lane == 0) {
+        const float r = 1.0f / __builtin_sqrtf(total / static_cast<float>(heads * D) + args.eps);
+        args.rrms[which][b * args.len[which] + t] = r;
+    }
+}
+
+template <bool kFp16, int D>
+int32_t launch_qk(const QkArgs &args, int64_t batch, bool split, bool row, hipStream_t s) {
+    if (row) {
+        const dim3 g(static_cast<unsigned>(args.len[0] + args.len[1]), static_cast<unsigned>(batch));
+        row_rrms_kernel<kFp16, D><<<g, 64, 0, s>>>(args);
+    }
+    const dim3 grid(static_cast<unsigned>(args.heads[0] * args.ntiles[0] + args.heads[1] * args.ntiles[1]),
+                    static_cast<unsigned>(batch));
+    if (split) {
+        if (row) qk_rope_quant_kernel<kFp16, D, true, true><<<grid, kQkThreads, 0, s>>>(args);
+        else qk_rope_quant_kernel<kFp16, D, true, false><<<grid, kQkThreads, 0, s>>>(args);
+    } else {
+        if (row) qk_rope_quant_kernel<kFp16, D, false, true><<<grid, kQkThreads, 0, s>>>(args);
+        else qk_rope_quant_kernel<kFp16, D, false, false><<<grid, kQkThreads, 0, s>>>(args);
+    }
+    return check_launch("tu_qk_rms_rope_int8");
+}
+
+}  // namespace
+}  // namespace tu
+
+extern "C" int32_t tu_qk_rms_rope_int8(
+    const void *q, const void *k, int32_t dtype, int64_t batch, int64_t hq, int64_t hk, int64_t lq, int64_t lk,
+    int64_t dim, int64_t q_sb, int64_t q_sh, int64_t q_sl, int64_t k_sb, int64_t k_sh, int64_t k_sl,
+    const void *q_norm, const void *k_norm, int32_t norm_scope, float eps, const void *freqs, int64_t rot_dim,
+    int32_t split_half, int64_t f_batches, int64_t f_len, int64_t f_sb, int64_t f_sl, int64_t f_sp, int64_t f_sr,
+    int64_t f_sc, float *q_rrms, float *k_rrms, int8_t *q8, int64_t qo_sb, int64_t qo_sh, int64_t qo_sl,
+    int8_t *k8, int64_t ko_sb, int64_t ko_sh, int64_t ko_sl, float *q_scale, float *k_scale, void *stream) {
+    using namespace tu;
+    TU_REQUIRE(dtype == 0 || dtype == 1, "Q/K preprocessing dtype must be 0 (bf16) or 1 (fp16), got %d", dtype);
+    TU_REQUIRE(dim == 64 || dim == 128, "Q/K preprocessing requires head_dim 64 or 128, got %lld",
+               static_cast<long long>(dim));
+    TU_REQUIRE(batch > 0 && batch <= 65535 && hq > 0 && hk > 0 && lq > 0 && lk > 0,
+               "Q/K preprocessing dimensions must be positive");
+    TU_REQUIRE(norm_scope == 0 || norm_scope == 1, "norm_scope must be 0 (head) or 1 (row)");
+    TU_REQUIRE(rot_dim >= 0 && rot_dim <= dim && rot_dim % 2 == 0, "rot_dim must be even and within head_dim");
+    TU_REQUIRE(q && k && q_norm && k_norm && q8 && k8 && q_scale && k_scale, "Q/K preprocessing pointers must be non-null");
+    TU_REQUIRE(rot_dim == 0 || freqs, "RoPE frequencies are required when rot_dim > 0");
+    TU_REQUIRE(rot_dim == 0 || ((f_batches == 1 || f_batches == batch) &&
+                                (f_len == 1 || (f_len == lq && lq == lk))),
+               "RoPE batch/sequence broadcasting is incompatible");
+    TU_REQUIRE(norm_scope == 0 || (q_rrms && k_rrms), "row-scope RMSNorm needs rrms scratch");
+    const auto aligned16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+    TU_REQUIRE(aligned16(q) && aligned16(k) && aligned16(q_norm) && aligned16(k_norm) && q_sl % 8 == 0 &&
+                   q_sh % 8 == 0 && q_sb % 8 == 0 && k_sl % 8 == 0 && k_sh % 8 == 0 && k_sb % 8 == 0,
+               "Q/K preprocessing inputs must be 16-byte aligned rows");
+    TU_REQUIRE((reinterpret_cast<uintptr_t>(q8) & 7) == 0 && (reinterpret_cast<uintptr_t>(k8) & 7) == 0 &&
+                   qo_sl % 8 == 0 && qo_sh % 8 == 0 && qo_sb % 8 == 0 && ko_sl % 8 == 0 && ko_sh % 8 == 0 &&
+                   ko_sb % 8 == 0,
+               "Q/K preprocessing outputs must be 8-byte aligned rows");
+    const int64_t nqt = (lq + 63) / 64 * 4, nkt = (lk + 63) / 64;
+    TU_REQUIRE(hq * nqt + hk * nkt < 0x7fffffff && lq + lk < 0x7fffffff, "Q/K preprocessing grid too large");
+    if (require_gfx950()) return -1;
+    QkArgs a{};
+    a.x[0] = static_cast<const uint16_t *>(q);
+    a.x[1] = static_cast<const uint16_t *>(k);
+    a.norm[0] = static_cast<const uint16_t *>(q_norm);
+    a.norm[1] = static_cast<const uint16_t *>(k_norm);
+    a.rrms[0] = q_rrms;
+    a.rrms[1] = k_rrms;
+    a.out[0] = q8;
+    a.out[1] = k8;
+    a.scale[0] = q_scale;
+    a.scale[1] = k_scale;
+    a.freqs = static_cast<const uint16_t *>(freqs);
+    a.heads[0] = hq;
+    a.heads[1] = hk;
+    a.len[0] = lq;
+    a.len[1] = lk;
+    a.x_sb[0] = q_sb, a.x_sh[0] = q_sh, a.x_sl[0] = q_sl;
+    a.x_sb[1] = k_sb, a.x_sh[1] = k_sh, a.x_sl[1] = k_sl;
+    a.o_sb[0] = qo_sb, a.o_sh[0] = qo_sh, a.o_sl[0] = qo_sl;
+    a.o_sb[1] = ko_sb, a.o_sh[1] = ko_sh, a.o_sl[1] = ko_sl;
+    a.ntiles[0] = nqt;
+    a.ntiles[1] = nkt;
+    a.f_sb = f_sb, a.f_sl = f_sl, a.f_sp = f_sp, a.f_sr = f_sr, a.f_sc = f_sc;
+    a.f_batches = f_batches;
+    a.f_len = f_len;
+    a.rot_dim = static_cast<int>(rot_dim);
+    a.eps = eps;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const bool split = split_half != 0, row = norm_scope == 1;
+    if (dtype == 1) return dim == 128 ? launch_qk<true, 128>(a, batch, split, row, s) : launch_qk<true, 64>(a, batch, split, row, s);
+    return dim == 128 ? launch_qk<false, 128>(a, batch, split, row, s) : launch_qk<false, 64>(a, batch, split, row, s);
+}

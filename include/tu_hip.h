@@ -162,6 +162,40 @@ int32_t tu_sage_attn_fwd(const int8_t *q8, const float *q_scale, int64_t blkq, c
                          int64_t k_sh, int64_t k_sl, int64_t o_sb, int64_t o_sh, int64_t o_sl,
                          float sm_scale, int32_t causal, void *stream);
 
+/* Sage attention: fused Q/K preprocessing -------------------------------- */
+
+/* RMSNorm + RoPE + per-tile INT8 of Q and K in one pass, the producer of the
+ * attention's Q/K (Q per 16-token tile, K per 64-token tile):
+ *   rrms  = 1 / sqrt(sumsq / n + eps)    norm_scope 0: the token's head row
+ *           (n = dim); 1: all heads of the token (n = heads * dim), computed
+ *           into q_rrms / k_rrms (fp32 [batch, len] scratch)
+ *   a_c   = T((x_c * rrms) * w_c)        T = bf16 (dtype 0) or fp16 (dtype 1);
+ *           w = norm[c] (scope 0) or norm[head * dim + c] (scope 1)
+ *   c < rot_dim: y_c = T(fma(f[pair][comp][1], a_second, f[pair][comp][0] * a_first))
+ *           with pairs (2p, 2p + 1) or, split_half, (p, p + rot_dim / 2), and
+ *           comp the channel's position in its pair; else y_c = a_c
+ *   tile: amax = max(1e-7, max |y|); scale = amax / 127;
+ *           q = clamp(rint(y * 127 / amax), -127, 127)
+ * q, k: T with element strides (s_b, s_h, s_l), channels contiguous,
+ * 16-byte aligned rows; dim in {64, 128}.  freqs: T [f_batches, f_len, 1,
+ * rot_dim / 2, 2, 2] by element strides (f_sb, f_sl, pair f_sp, row f_sr,
+ * column f_sc); f_batches in {1, batch}, f_len in {1, lq == lk}.  q8, k8:
+ * int8 by strides.  q_scale: fp32 [batch, hq, ceil(lq / 64) * 4] (tiles past
+ * lq get 1e-7 / 127); k_scale: fp32 [batch, hk, ceil(lk / 64)].
+ * Replaces turing_utils::qk_rms_rope_int8 without its rotate_qk /
+ * stabilize_k variant (kernel/comfyui_turing_utils_kernel/turing_sage/
+ * custom_ops.py:63-134 -> quant.py:6-87 -> kernel/csrc/turing/sage/
+ * qk_preprocess.cu:417-629, :632-753). */
+int32_t tu_qk_rms_rope_int8(const void *q, const void *k, int32_t dtype, int64_t batch, int64_t hq,
+                            int64_t hk, int64_t lq, int64_t lk, int64_t dim, int64_t q_sb, int64_t q_sh,
+                            int64_t q_sl, int64_t k_sb, int64_t k_sh, int64_t k_sl, const void *q_norm,
+                            const void *k_norm, int32_t norm_scope, float eps, const void *freqs,
+                            int64_t rot_dim, int32_t split_half, int64_t f_batches, int64_t f_len,
+                            int64_t f_sb, int64_t f_sl, int64_t f_sp, int64_t f_sr, int64_t f_sc,
+                            float *q_rrms, float *k_rrms, int8_t *q8, int64_t qo_sb, int64_t qo_sh,
+                            int64_t qo_sl, int8_t *k8, int64_t ko_sb, int64_t ko_sh, int64_t ko_sl,
+                            float *q_scale, float *k_scale, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

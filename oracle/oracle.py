@@ -78,6 +78,13 @@ def lib():
                                             _p, _i64, _i64, _i64,
                                             _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _i32, _i32,
                                             _p, _i64, _p]
+            L.or_f32_to_f16_rne.restype = ctypes.c_uint16
+            L.or_f32_to_f16_rne.argtypes = [ctypes.c_float]
+            L.or_f16_to_f32.restype = ctypes.c_float
+            L.or_f16_to_f32.argtypes = [ctypes.c_uint16]
+            L.or_qk_rms_rope_int8.restype = _i32
+            L.or_qk_rms_rope_int8.argtypes = [_p, _i32, _i64, _i64, _i64, _i64, _p, _i32, ctypes.c_float,
+                                              _p, _i64, _i64, _i64, _i32, _i64, _i64, _p, _p]
             _lib = L
     return _lib
 
@@ -241,3 +248,42 @@ def sage_attn_rows(q8: np.ndarray, qs: np.ndarray, blkq: int, k8: np.ndarray, ks
                                    hq, hkv, lq, lk, d, sm_scale, int(causal), int(p_bf16),
                                    _ptr(rows), rows.shape[0], _ptr(out)), "sage_attn_rows")
     return out
+
+
+# --- fused Q/K RMSNorm + RoPE + INT8 (qk_preprocess.cu) ---------------------
+
+DTYPE_BF16, DTYPE_FP16 = 0, 1
+
+
+def f32_to_f16_bits(v: float) -> int:
+    return int(lib().or_f32_to_f16_rne(v))
+
+
+def f16_bits_to_f32(h: int) -> float:
+    return float(lib().or_f16_to_f32(h))
+
+
+def qk_rms_rope_int8(x_bits: np.ndarray, dtype: int, norm_bits: np.ndarray, norm_scope: str, eps: float,
+                     freqs: np.ndarray | None, rot_dim: int, split_half: bool,
+                     tile: int, ntiles: int) -> tuple[np.ndarray, np.ndarray]:
+    """One tensor (Q or K) of the fused preprocessor.  x_bits: [B, H, L, D]
+    bf16/fp16 bit patterns; freqs: fp32 [fb, fs, rot_dim / 2, 2, 2] or None.
+    Returns (int8 [B, H, L, D], fp32 scales [B, H, ntiles])."""
+    x_bits = np.ascontiguousarray(x_bits, dtype=np.uint16)
+    norm_bits = np.ascontiguousarray(norm_bits, dtype=np.uint16)
+    b, h, l, d = x_bits.shape
+    if freqs is not None:
+        freqs = np.ascontiguousarray(freqs, dtype=np.float32)
+        fb, fs = freqs.shape[0], freqs.shape[1]
+        assert freqs.shape[2:] == (rot_dim // 2, 2, 2)
+    else:
+        fb = fs = 1
+        assert rot_dim == 0
+    q = np.empty(x_bits.shape, dtype=np.int8)
+    s = np.empty((b, h, ntiles), dtype=np.float32)
+    _check(lib().or_qk_rms_rope_int8(_ptr(x_bits), dtype, b, h, l, d, _ptr(norm_bits),
+                                     1 if norm_scope == "row" else 0, eps,
+                                     _ptr(freqs) if freqs is not None else None, fb, fs, rot_dim,
+                                     int(split_half), tile, ntiles, _ptr(q), _ptr(s)),
+           "qk_rms_rope_int8")
+    return q, s

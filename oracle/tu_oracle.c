@@ -27,6 +27,11 @@
  *   or_sage_quant             pinned: invariants (max|q|==127, dequant error)
  *   or_sage_attn_rows         pinned: fp64 SDPA on dequantized inputs, torch SDPA
  *                             on raw inputs (reference gate rtol .08 / atol .06)
+ *   or_f32_to_f16_rne         pinned: every fp32 class vs numpy float16 casts
+ *   or_qk_rms_rope_int8       pinned: the reference's own KAT (torch restatement of
+ *                             validate_compatible.py:241-286 + per-warp INT8,
+ *                             codes within 2 LSB, scales rtol .015), fp64 RMSNorm,
+ *                             identity / rotation-by-angle RoPE closed forms
  */
 #include <math.h>
 #include <omp.h>
@@ -479,5 +484,155 @@ OR_API int or_sage_attn_rows(const int8_t *q8, int64_t q_sb, int64_t q_sh, int64
         free(s);
         free(o);
     }
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* IEEE binary16 conversions (round to nearest even, subnormals kept).        */
+/* ------------------------------------------------------------------------ */
+OR_API uint16_t or_f32_to_f16_rne(float value) {
+    const uint32_t bits = f2u(value);
+    const uint32_t sign = (bits >> 16) & 0x8000U;
+    const uint32_t absb = bits & 0x7fffffffU;
+    if (absb > 0x7f800000U) return (uint16_t)(sign | 0x7e00U); /* NaN */
+    if (absb >= 0x477ff000U) return (uint16_t)(sign | 0x7c00U); /* rounds to inf */
+    if (absb < 0x38800000U) {                                   /* half subnormal or 0 */
+        /* value = absb-float; subnormal unit 2^-24: round(v * 2^24) half-even */
+        const float v = u2f(absb) * 16777216.0f; /* exact scaling by 2^24 */
+        const float r = nearbyintf(v);
+        return (uint16_t)(sign | (uint32_t)r);
+    }
+    /* normal: rebias exponent, round the 13 dropped mantissa bits */
+    uint32_t m = absb - 0x38000000U; /* exponent 127 -> 15 */
+    const uint32_t rem = m & 0x1fffU;
+    m >>= 13;
+    if (rem > 0x1000U || (rem == 0x1000U && (m & 1U))) ++m;
+    return (uint16_t)(sign | m);
+}
+
+OR_API float or_f16_to_f32(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h & 0x8000U) << 16;
+    const uint32_t e = (h >> 10) & 0x1fU, m = h & 0x3ffU;
+    if (e == 0) {
+        const float v = (float)m * 5.9604644775390625e-8f; /* m * 2^-24, exact */
+        return sign ? -v : v;
+    }
+    if (e == 31) return u2f(sign | 0x7f800000U | (m << 13));
+    return u2f(sign | ((e + 112U) << 23) | (m << 13));
+}
+
+static inline float t_to_f32(uint16_t v, int dtype) { return dtype ? or_f16_to_f32(v) : or_bf16_to_f32(v); }
+static inline float t_round(float v, int dtype) {
+    return dtype ? or_f16_to_f32(or_f32_to_f16_rne(v)) : bf16_round_f32(v);
+}
+
+/* Sum of squares of one head row (D channels) in the order the GPU uses:    */
+/* packs of 8 channels each accumulate x*x by FMA from 0, then the D/8 pack  */
+/* sums are combined by a butterfly: s[p] += s[p ^ off] for off = D/16 .. 1  */
+/* (qk_preprocess.cu:530-537 uses the same order).                           */
+static float head_sumsq(const uint16_t *row, int64_t dim, int dtype) {
+    float s[16];
+    const int packs = (int)(dim / 8);
+    for (int p = 0; p < packs; ++p) {
+        float acc = 0.0f;
+        for (int c = 0; c < 8; ++c) {
+            const float v = t_to_f32(row[p * 8 + c], dtype);
+            acc = fmaf(v, v, acc);
+        }
+        s[p] = acc;
+    }
+    for (int off = packs / 2; off > 0; off >>= 1) {
+        float t[16];
+        for (int p = 0; p < packs; ++p) t[p] = s[p] + s[p ^ off];
+        memcpy(s, t, sizeof(float) * (size_t)packs);
+    }
+    return s[0];
+}
+
+/* ------------------------------------------------------------------------ */
+/* Fused Q/K RMSNorm + RoPE + per-tile INT8, one tensor (Q or K):            */
+/* quantize_tile / processed_tile_value (qk_preprocess.cu:99-197, :417-552). */
+/*   rrms  = 1 / sqrt(sumsq / n + eps)   head scope: n = D, sum of the head  */
+/*           row (head_sumsq); row scope: n = H*D, the heads' head_sumsq      */
+/*           added in head order (the reference uses rsqrtf; here IEEE)      */
+/*   a_c   = T((x_c * rrms) * w)   w = norm[c] or norm[h*D + c]               */
+/*   c < rot_dim: pair = split ? c mod pairs : c / 2, first/second = the     */
+/*           pair's channels (split: pair, pair + pairs; else 2 pair, +1),   */
+/*           comp = split ? c >= pairs : c & 1,                              */
+/*           y_c = T(fma(f[pair][comp][1], a_second, f[pair][comp][0] * a_first)) */
+/*   else  y_c = a_c                                                          */
+/*   per tile of `tile` tokens: amax = max(1e-7, max |y|), scale = amax / 127 */
+/*           q = clamp(rint(y * (127 / amax)), -127, 127)                     */
+/* x: [B][H][L][D] contiguous (dtype 0 bf16, 1 fp16 bit patterns); freqs:    */
+/* f32 [fb][fs][rot_dim/2][2][2] (fb, fs in {1, B}, {1, L}); q: [B][H][L][D];*/
+/* scales: [B][H][ntiles] (tiles past L get 1e-7 / 127).                     */
+/* ------------------------------------------------------------------------ */
+OR_API int or_qk_rms_rope_int8(const uint16_t *x, int dtype, int64_t batch, int64_t heads, int64_t len,
+                               int64_t dim, const uint16_t *norm, int norm_scope, float eps,
+                               const float *freqs, int64_t fb, int64_t fs, int64_t rot_dim,
+                               int split_half, int64_t tile, int64_t ntiles, int8_t *q, float *scales) {
+    if ((dim != 64 && dim != 128) || rot_dim < 0 || rot_dim > dim || (rot_dim & 1)) return -1;
+    if (ntiles * tile < len) return -1;
+    const int64_t pairs = rot_dim / 2;
+    float *rrms = (float *)malloc(sizeof(float) * (size_t)(batch * heads * len));
+    float *y = (float *)malloc(sizeof(float) * (size_t)(tile * dim));
+    if (!rrms || !y) { free(rrms); free(y); return -2; }
+    for (int64_t b = 0; b < batch; ++b)
+        for (int64_t t = 0; t < len; ++t) {
+            if (norm_scope) {
+                float total = 0.0f;
+                for (int64_t h = 0; h < heads; ++h)
+                    total += head_sumsq(x + ((b * heads + h) * len + t) * dim, dim, dtype);
+                const float r = 1.0f / sqrtf(total / (float)(heads * dim) + eps);
+                for (int64_t h = 0; h < heads; ++h) rrms[(b * heads + h) * len + t] = r;
+            } else {
+                for (int64_t h = 0; h < heads; ++h) {
+                    const float s = head_sumsq(x + ((b * heads + h) * len + t) * dim, dim, dtype);
+                    rrms[(b * heads + h) * len + t] = 1.0f / sqrtf(s / (float)dim + eps);
+                }
+            }
+        }
+    for (int64_t b = 0; b < batch; ++b)
+        for (int64_t h = 0; h < heads; ++h)
+            for (int64_t ti = 0; ti < ntiles; ++ti) {
+                float amax = 0.0000001f;
+                const int64_t t0 = ti * tile;
+                for (int64_t to = 0; to < tile && t0 + to < len; ++to) {
+                    const int64_t t = t0 + to;
+                    const uint16_t *row = x + ((b * heads + h) * len + t) * dim;
+                    const float r = rrms[(b * heads + h) * len + t];
+                    const float *fr = freqs ? freqs + ((fb == 1 ? 0 : b) * fs + (fs == 1 ? 0 : t)) * pairs * 4 : NULL;
+                    for (int64_t c = 0; c < dim; ++c) {
+                        const int64_t wi = norm_scope ? h * dim + c : c;
+                        const float a = t_round((t_to_f32(row[c], dtype) * r) * t_to_f32(norm[wi], dtype), dtype);
+                        float v = a;
+                        if (c < rot_dim) {
+                            const int64_t pair = split_half ? (c < pairs ? c : c - pairs) : c / 2;
+                            const int64_t first = split_half ? pair : 2 * pair;
+                            const int64_t second = split_half ? pair + pairs : first + 1;
+                            const int comp = split_half ? (c >= pairs) : (int)(c & 1);
+                            const int64_t w0 = norm_scope ? h * dim + first : first;
+                            const int64_t w1 = norm_scope ? h * dim + second : second;
+                            const float x0 = t_round((t_to_f32(row[first], dtype) * r) * t_to_f32(norm[w0], dtype), dtype);
+                            const float x1 = t_round((t_to_f32(row[second], dtype) * r) * t_to_f32(norm[w1], dtype), dtype);
+                            const float f0 = fr[pair * 4 + comp * 2 + 0];
+                            const float f1 = fr[pair * 4 + comp * 2 + 1];
+                            v = t_round(fmaf(f1, x1, f0 * x0), dtype);
+                        }
+                        y[to * dim + c] = v;
+                        amax = fmaxf(amax, fabsf(v));
+                    }
+                }
+                scales[(b * heads + h) * ntiles + ti] = amax / 127.0f;
+                const float inv = 127.0f / amax;
+                for (int64_t to = 0; to < tile && t0 + to < len; ++to)
+                    for (int64_t c = 0; c < dim; ++c) {
+                        float r = nearbyintf(y[to * dim + c] * inv);
+                        r = fminf(127.0f, fmaxf(-127.0f, r));
+                        q[((b * heads + h) * len + t0 + to) * dim + c] = (int8_t)r;
+                    }
+            }
+    free(rrms);
+    free(y);
     return 0;
 }

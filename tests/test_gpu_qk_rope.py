@@ -1,0 +1,168 @@
+"""GPU parity: fused Q/K RMSNorm + RoPE + INT8 (HIP, tu_qk_rms_rope_int8) vs the
+CPU oracle, bit-exact codes and scales, and the reference's own known-answer
+check against its preprocessing formula (kernel/scripts/validate_compatible.py
+:241-421: codes within 2 LSB, scales rtol 0.015 / atol 0.0011).
+
+Oracle: oracle/tu_oracle.c or_qk_rms_rope_int8, a restatement of
+kernel/csrc/turing/sage/qk_preprocess.cu:99-197, :417-629.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle
+from tests.test_oracle_qk_rope import _per_block_int8, _reference_formula
+
+pytestmark = pytest.mark.gpu
+
+
+def _bits(t: torch.Tensor) -> np.ndarray:
+    return t.contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def _hnd(t: torch.Tensor, layout: str) -> torch.Tensor:
+    return t if layout == "HND" else t.transpose(1, 2)
+
+
+def _case(b, hq, hk, l, d, dtype, scope, rot, fb, fl, seed, layout="HND"):
+    g = torch.Generator().manual_seed(seed)
+    shape_q = (b, hq, l, d) if layout == "HND" else (b, l, hq, d)
+    shape_k = (b, hk, l, d) if layout == "HND" else (b, l, hk, d)
+    q = (torch.randn(shape_q, generator=g) * 2).to(dtype)
+    k = (torch.randn(shape_k, generator=g) * 2).to(dtype)
+    qw = torch.randn(d if scope == "head" else hq * d, generator=g).to(dtype)
+    kw = torch.randn(d if scope == "head" else hk * d, generator=g).to(dtype)
+    freqs = torch.randn((fb, fl, 1, rot // 2, 2, 2), generator=g).to(dtype) if rot else None
+    return q, k, qw, kw, freqs
+
+
+def _check_exact(q, k, qw, kw, freqs, rot, scope, split, layout, dev):
+    from comfyui_turing_utils_kernel.turing_sage.custom_ops import qk_rms_rope_int8
+
+    empty = torch.empty(0, dtype=q.dtype)
+    out = qk_rms_rope_int8(q.to(dev), k.to(dev), qw.to(dev), kw.to(dev),
+                           (freqs if freqs is not None else empty).to(dev), 1e-6, rot, layout, scope, split,
+                           False, False)
+    torch.cuda.synchronize(dev)
+    qi, qs, ki, ks = (t.cpu() for t in out)
+    dt = oracle.DTYPE_FP16 if q.dtype == torch.float16 else oracle.DTYPE_BF16
+    f32 = freqs.float()[:, :, 0].numpy() if freqs is not None else None
+    for x, w, got_q, got_s, blk in ((q, qw, qi, qs, 16), (k, kw, ki, ks, 64)):
+        xh = _hnd(x, layout)
+        nt = got_s.shape[-1]
+        ref_q, ref_s = oracle.qk_rms_rope_int8(_bits(xh), dt, _bits(w), scope, 1e-6, f32, rot, split, blk, nt)
+        np.testing.assert_array_equal(got_s.numpy().view(np.uint32), ref_s.view(np.uint32))
+        np.testing.assert_array_equal(_hnd(got_q, layout).contiguous().numpy(), ref_q)
+    return qi, qs, ki, ks
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("d,scope,split,rot", [(128, "row", False, 128), (128, "head", True, 96),
+                                               (64, "head", False, 64), (64, "row", True, 32), (128, "head", False, 0)])
+def test_exact_vs_oracle(gpu_device, dtype, d, scope, split, rot):
+    print(f"[qk-rope] {dtype} d={d} {scope} split={split} rot={rot}", flush=True)
+    q, k, qw, kw, freqs = _case(2, 4, 2, 129, d, dtype, scope, rot, 2, 129, 100 + d + rot)
+    _check_exact(q, k, qw, kw, freqs, rot, scope, split, "HND", gpu_device)
+
+
+@pytest.mark.parametrize("scope", ["head", "row"])
+def test_nhd_strided_and_broadcast_freqs(gpu_device, scope):
+    """Wan's call: HND views of an NHD projection ([B, L, H, D].transpose(1, 2)),
+    interleaved full-width RoPE, frequencies shared by the batch."""
+    print(f"[qk-rope] nhd-view {scope}", flush=True)
+    q, k, qw, kw, freqs = _case(2, 5, 5, 70, 128, torch.bfloat16, scope, 128, 1, 70, 7, layout="NHD")
+    qv, kv = q.transpose(1, 2), k.transpose(1, 2)  # strided HND views
+    _check_exact(qv, kv, qw, kw, freqs, 128, scope, False, "HND", gpu_device)
+    _check_exact(q, k, qw, kw, freqs, 128, scope, False, "NHD", gpu_device)
+    # one frequency row for every token
+    q, k, qw, kw, freqs = _case(1, 2, 2, 33, 128, torch.bfloat16, scope, 64, 1, 1, 8)
+    _check_exact(q, k, qw, kw, freqs, 64, scope, True, "HND", gpu_device)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("d,scope,split", [(64, "head", True), (128, "head", True), (64, "row", False),
+                                           (128, "row", False)])
+def test_reference_known_answer(gpu_device, dtype, d, scope, split):
+    """validate_compatible.py:289-383 on the GPU result."""
+    from comfyui_turing_utils_kernel.turing_sage import prequantize_rms_rope_qk
+
+    print(f"[qk-rope] kat {dtype} d={d} {scope}", flush=True)
+    g = torch.Generator().manual_seed(4700 + d + (100 if scope == "row" else 0))
+    b, h, l = 1, 3, 129
+    q = torch.randn((b, h, l, d), generator=g).to(dtype)
+    k = torch.randn((b, h, l, d), generator=g).to(dtype)
+    nsz = d if scope == "head" else h * d
+    qw = torch.randn(nsz, generator=g).to(dtype)
+    kw = torch.randn(nsz, generator=g).to(dtype)
+    rot = d if scope == "row" else d - 32
+    freqs = torch.randn((b, l, 1, rot // 2, 2, 2), generator=g).to(dtype)
+    fused = prequantize_rms_rope_qk(q.to(gpu_device), k.to(gpu_device), qw, kw, freqs, epsilon=1e-6, rot_dim=rot,
+                                    norm_scope=scope, split_half=split)
+    for x, w, gq, gs, blk in ((q, qw, fused.query_int8, fused.query_scale, 16),
+                              (k, kw, fused.key_int8, fused.key_scale, 64)):
+        ref_q, ref_s = _per_block_int8(_reference_formula(x, w, freqs, 1e-6, rot, scope, split), blk, gs.shape[-1])
+        assert int((gq.cpu().to(torch.int16) - ref_q.to(torch.int16)).abs().max()) <= 2
+        np.testing.assert_allclose(gs.cpu().numpy(), ref_s.numpy(), rtol=0.015, atol=0.0011)
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_prequantized_qk_attention(gpu_device, d):
+    """prequantize_rms_rope_qk -> prequantize_sageattn_from_qk -> attention, against
+    the oracle's attention on the same codes (16-token Q / 64-token K scales)."""
+    from comfyui_turing_utils_kernel.turing_sage import (prequantize_rms_rope_qk, prequantize_sageattn_from_qk,
+                                                           sageattn_from_prequantized)
+    from comfyui_turing_utils_kernel.turing_sage.correctness import (attention_error_metrics,
+                                                                      require_attention_correctness)
+
+    print(f"[qk-rope] attention d={d}", flush=True)
+    q, k, qw, kw, freqs = _case(1, 4, 2, 200, d, torch.bfloat16, "row", d, 1, 200, 11)
+    v = torch.randn((1, 2, 200, d), generator=torch.Generator().manual_seed(12)).to(torch.bfloat16)
+    qk = prequantize_rms_rope_qk(q.to(gpu_device), k.to(gpu_device), qw, kw, freqs, epsilon=1e-6, rot_dim=d,
+                                 norm_scope="row")
+    out = sageattn_from_prequantized(prequantize_sageattn_from_qk(qk, v.to(gpu_device))).float().cpu()
+    assert out.shape == (1, 4, 200, d)
+    q8 = qk.query_int8.cpu().numpy()
+    k8 = qk.key_int8.cpu().numpy()
+    pad = 128 - d
+    q8p = np.pad(q8, ((0, 0), (0, 0), (0, 0), (0, pad)))
+    k8p = np.pad(k8, ((0, 0), (0, 0), (0, 0), (0, pad)))
+    vp = np.pad(_bits(v), ((0, 0), (0, 0), (0, 0), (0, pad)))
+    qs = qk.query_scale.cpu().numpy()[..., : (200 + 15) // 16].copy()
+    ks = qk.key_scale.cpu().numpy()
+    rows = np.array([[0, h, i] for h in range(4) for i in (0, 1, 15, 16, 63, 64, 127, 199)])
+    ref = oracle.sage_attn_rows(q8p, qs, 16, k8p, ks, 64, vp, d ** -0.5, rows)[:, :d]
+    got = out[rows[:, 0], rows[:, 1], rows[:, 2]]
+    require_attention_correctness(attention_error_metrics(got, torch.from_numpy(ref)), max_abs=2e-2, cosine=0.999)
+
+
+def test_wan_shape_slices(gpu_device):
+    """Wan-14B self-attention producer at full size (B1 H40 L32760 D128, row
+    scope, interleaved full-width RoPE): two token slices checked bit-exactly
+    (row-scope rrms and tile scales depend only on the slice's tokens)."""
+    from comfyui_turing_utils_kernel.turing_sage.custom_ops import qk_rms_rope_int8
+
+    print("[qk-rope] wan B1 H40 L32760", flush=True)
+    h, l, d = 40, 32760, 128
+    g = torch.Generator().manual_seed(21)
+    x = torch.randn((1, l, h, d), generator=g).to(torch.bfloat16)  # one projection serves as Q and K
+    w = (1 + 0.1 * torch.randn(h * d, generator=g)).to(torch.bfloat16)
+    theta = torch.rand((1, l, 1, d // 2), generator=g) * 6.28
+    freqs = torch.stack([torch.stack([theta.cos(), -theta.sin()], -1),
+                         torch.stack([theta.sin(), theta.cos()], -1)], -2).to(torch.bfloat16)
+    xd = x.to(gpu_device).transpose(1, 2)
+    qi, qs, ki, ks = (t.cpu() for t in qk_rms_rope_int8(xd, xd, w.to(gpu_device), w.to(gpu_device),
+                                                          freqs.to(gpu_device), 1e-6, d, "HND", "row", False,
+                                                          False, False))
+    assert qs.shape == (1, h, (l + 63) // 64 * 4) and ks.shape == (1, h, (l + 63) // 64)
+    f32 = freqs.float()[:, :, 0].numpy()
+    for t0, t1 in ((0, 1024), (31744, l)):  # the last slice ends on the ragged tiles
+        xs = x[:, t0:t1].transpose(1, 2).contiguous()
+        fs = f32[:, t0:t1]
+        rq, rs = oracle.qk_rms_rope_int8(_bits(xs), 0, _bits(w), "row", 1e-6, fs, d, False, 16, (t1 - t0 + 15) // 16)
+        np.testing.assert_array_equal(qi[:, :, t0:t1].numpy(), rq)
+        np.testing.assert_array_equal(qs[:, :, t0 // 16:(t1 + 15) // 16].numpy().view(np.uint32), rs.view(np.uint32))
+        rk, rks = oracle.qk_rms_rope_int8(_bits(xs), 0, _bits(w), "row", 1e-6, fs, d, False, 64, (t1 - t0 + 63) // 64)
+        np.testing.assert_array_equal(ki[:, :, t0:t1].numpy(), rk)
+        np.testing.assert_array_equal(ks[:, :, t0 // 64:(t1 + 63) // 64].numpy().view(np.uint32), rks.view(np.uint32))

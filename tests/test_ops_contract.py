@@ -93,7 +93,8 @@ def test_cpu_tensors_are_refused():
 def test_public_sage_api():
     assert turing_sage.__all__ == [
         "available", "w8a8_available", "split_prequantization_available", "fused_qk_preprocessing_available",
-        "sageattn", "sageattn_compiled", "prequantize_sageattn", "sageattn_from_prequantized", "preflight",
+        "sageattn", "sageattn_compiled", "prequantize_sageattn", "prequantize_rms_rope_qk",
+        "prequantize_sageattn_from_qk", "sageattn_from_prequantized", "preflight",
     ]
     assert turing_sage.w8a8_available() is False
     assert kernel.__version__
@@ -132,3 +133,40 @@ def test_gate_names_each_bound():
 def test_shape_mismatch_fails_before_reduction():
     with pytest.raises(AssertionError, match="shape"):
         attention_error_metrics(torch.zeros(2), torch.zeros(3))
+
+
+def test_qk_rms_rope_fake_contract_and_fullgraph_leaf():
+    """Reference tests/test_turing_sage_quant.py:22-90."""
+    from comfyui_turing_utils_kernel.turing_sage.custom_ops import qk_rms_rope_int8
+
+    query = torch.empty((2, 4, 129, 128), dtype=torch.bfloat16, device=META)
+    key = torch.empty((2, 2, 129, 128), dtype=torch.bfloat16, device=META)
+    norm = torch.empty((128,), dtype=torch.bfloat16, device=META)
+    freqs = torch.empty((1, 129, 1, 64, 2, 2), dtype=torch.bfloat16, device=META)
+    qi, qs, ki, ks = qk_rms_rope_int8(query, key, norm, norm, freqs, 1e-6, 128, "HND", "head", True, False, False)
+    assert qi.shape == query.shape and qi.dtype == torch.int8 and qs.shape == (2, 4, 12)
+    assert ki.shape == key.shape and ks.shape == (2, 2, 3) and ks.dtype == torch.float32
+    q64 = torch.empty((1, 129, 4, 64), dtype=torch.float16, device=META)
+    k64 = torch.empty((1, 129, 2, 64), dtype=torch.float16, device=META)
+    n64 = torch.empty((64,), dtype=torch.float16, device=META)
+    compiled = torch.compile(
+        lambda q, k, qw, kw, f: qk_rms_rope_int8(q, k, qw, kw, f, 1e-6, 0, "NHD", "head", False, False, False),
+        backend="eager", fullgraph=True)
+    qi, qs, ki, ks = compiled(q64, k64, n64, n64, torch.empty((0,), dtype=torch.float16, device=META))
+    assert qi.shape == q64.shape and qs.shape == (1, 4, 12) and ks.shape == (1, 2, 3)
+
+
+def test_qk_rms_rope_refuses_what_is_not_built():
+    from comfyui_turing_utils_kernel.turing_sage.quant import rms_rope_per_warp_int8
+
+    x = torch.zeros((1, 2, 16, 128), dtype=torch.bfloat16)
+    w = torch.ones(128, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="w8a8"):
+        rms_rope_per_warp_int8(x, x, w, w, None, epsilon=1e-6, rot_dim=0, tensor_layout="HND", norm_scope="head",
+                               split_half=False, rotate_qk=True, stabilize_k=True)
+    with pytest.raises(ValueError, match="head_dim"):
+        rms_rope_per_warp_int8(x[..., :96], x[..., :96], w, w, None, epsilon=1e-6, rot_dim=0,
+                               tensor_layout="HND", norm_scope="head", split_half=False)
+    with pytest.raises(ValueError, match="norm weight"):
+        rms_rope_per_warp_int8(x, x, w, w, None, epsilon=1e-6, rot_dim=0, tensor_layout="HND", norm_scope="row",
+                               split_half=False)

@@ -205,6 +205,7 @@ def main():
         "traffic": measured_traffic(dominant),
     }
 
+    extras = extra_kernels(torch, dev, ops, lin, q, k_, copy_gbs)
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds)
 
     record = {
@@ -229,12 +230,53 @@ def main():
             "ops_per_step": total_ops,
         },
         "kernels": kernels,
+        "extra_kernels": extras,
         "roofline": roofline,
         "hbm_copy_gbs": copy_gbs,
         "cpu_baseline": cpu,
     }
     print(json.dumps(record))
     return 0
+
+
+def extra_kernels(torch, dev, ops, lin, q, k, copy_gbs) -> dict:
+    """Kernels of the path's next rows, timed outside the headline step (the
+    metric's workload is the four linears and the attention): the GELU-fused
+    ConvRot quantizer at FFN-down (K13824) and the fused Q/K RMSNorm + RoPE +
+    INT8 producer at the attention shape (row-scope RMSNorm, interleaved
+    full-width RoPE, as in a Wan block)."""
+    from comfyui_turing_utils_kernel.turing_sage.custom_ops import qk_rms_rope_int8
+
+    def timed(fn, reps=10):
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    out = {}
+    x = next(t[3] for t in lin if t[1] == 13824)
+    ms = timed(lambda: ops.bf16_gelu_int8_convrot_quantize(x, GROUP))
+    nbytes = 3.0 * x.numel() + 4.0 * x.shape[0]
+    out["gelu_convrot_quant_k13824"] = {"ms_avg": ms, "gbs": nbytes / ms / 1e6,
+                                        "frac_copy": nbytes / ms / 1e6 / copy_gbs}
+    b, h, l, d = q.shape
+    g = torch.Generator().manual_seed(31)
+    w = (1 + 0.1 * torch.randn(h * d, generator=g)).to(torch.bfloat16).to(dev)
+    theta = torch.rand((1, l, 1, d // 2), generator=g) * 6.28
+    freqs = torch.stack([torch.stack([theta.cos(), -theta.sin()], -1),
+                         torch.stack([theta.sin(), theta.cos()], -1)], -2).to(torch.bfloat16).to(dev)
+    ms = timed(lambda: qk_rms_rope_int8(q, k, w, w, freqs, 1e-6, d, "HND", "row", False, False, False))
+    # Q and K: 2 B read + 1 B write per element (the row-scope pre-pass reads
+    # them once more: 2 B per element, not counted as algorithmic work)
+    nbytes = 2 * 3.0 * q.numel()
+    out["qk_rms_rope_int8"] = {"ms_avg": ms, "gbs": nbytes / ms / 1e6, "frac_copy": nbytes / ms / 1e6 / copy_gbs,
+                               "shape": [b, h, l, d], "norm_scope": "row", "rot_dim": d}
+    return out
 
 
 def copy_bandwidth(torch, dev) -> float:

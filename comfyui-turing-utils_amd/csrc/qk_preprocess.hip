@@ -18,13 +18,14 @@
 // and square root and divisions are IEEE, so the CPU oracle restates it bit
 // for bit.  The reference uses rsqrtf, which is not reproduced.
 //
-// MI355X mapping: one workgroup (4 wave64) per tile.  A thread owns 8
+// MI355X mapping: one workgroup (4 wave64) per 64-token chunk of a head (four
+// Q tiles or one K tile; a Q tile is whole waves, so its amax is a wave max
+// plus one LDS exchange shared by the four).  A thread owns 8
 // consecutive channels ("pack") of a token; the packs of one token are
 // consecutive lanes, so the head-scope sum is a lane butterfly.  The
 // normalized tile goes through LDS once so RoPE can take its pair partner
-// from any pack (split-half pairs and partial rot_dim included); the tile
-// amax is a wave max plus one LDS exchange.  Row-scope rrms comes from a
-// one-wave-per-token pre-pass into caller scratch.
+// from any pack (split-half pairs and partial rot_dim included).  Row-scope
+// rrms comes from a one-wave-per-token pre-pass into caller scratch.
 #include <type_traits>
 
 #include "tu_common.h"
@@ -33,9 +34,8 @@ namespace tu {
 namespace {
 
 constexpr int kQkThreads = 256;
-constexpr int kQTile = 16;
-constexpr int kKTile = 64;
-constexpr int kMaxIters = kKTile * 16 / kQkThreads;  // packs per thread for a D = 128 K tile
+constexpr int kQTile = 16;   // Q scale granularity (tokens)
+constexpr int kChunk = 64;   // tokens per workgroup = the K scale granularity
 
 // bf16 (kFp16 = false) or fp16 bit patterns <-> fp32.
 template <bool kFp16>
@@ -68,6 +68,7 @@ struct QkArgs {
     int64_t o_sb[2], o_sh[2], o_sl[2];
     int64_t ntiles[2];           // scale entries per (batch, head)
     int64_t f_sb, f_sl, f_sp, f_sr, f_sc;
+    int f_contig;                // [.., pair, 2, 2] contiguous, 16-byte aligned rows
     int64_t f_batches, f_len;
     int rot_dim;
     float eps;
@@ -75,35 +76,38 @@ struct QkArgs {
 
 template <bool kFp16, int D, bool kSplit, bool kRow>
 __global__ __launch_bounds__(kQkThreads) void qk_rope_quant_kernel(QkArgs args) {
-    constexpr int kPacks = D / 8;  // lanes per token
-    __shared__ __align__(16) float tile_a[kKTile * D];
-    __shared__ float wave_amax[kQkThreads / 64];
+    constexpr int kPacks = D / 8;                        // lanes per token
+    constexpr int kIters = kChunk * kPacks / kQkThreads;  // packs per thread
+    constexpr int kSubs = kChunk / kQTile;                // 16-token sub-tiles per chunk
+    // Split-half pairs take their partner from another pack through LDS;
+    // interleaved pairs are inside a pack and stay in registers.
+    __shared__ __align__(16) float tile_a[kSplit ? kChunk * D : 4];
+    __shared__ float wave_amax[kQkThreads / 64][kSubs];
 
     const int tid = threadIdx.x;
     const int64_t b = blockIdx.y;
-    // Tasks: Q tiles of every head first, then K tiles.
+    // Tasks: 64-token chunks of every Q head first, then of every K head.
     int64_t task = blockIdx.x;
-    const int which = task < args.heads[0] * args.ntiles[0] ? 0 : 1;
-    if (which) task -= args.heads[0] * args.ntiles[0];
-    const int64_t head = task / args.ntiles[which];
-    const int64_t tile_id = task - head * args.ntiles[which];
-    const int tile = which ? kKTile : kQTile;
+    const int64_t nch_q = (args.len[0] + kChunk - 1) / kChunk;
+    const int which = task < args.heads[0] * nch_q ? 0 : 1;
+    if (which) task -= args.heads[0] * nch_q;
     const int64_t len = args.len[which];
-    const int64_t t0 = tile_id * tile;
-    const int iters = (tile * kPacks + kQkThreads - 1) / kQkThreads;
+    const int64_t nch = (len + kChunk - 1) / kChunk;
+    const int64_t head = task / nch;
+    const int64_t chunk = task - head * nch;
+    const int64_t t0 = chunk * kChunk;
     const uint16_t *xbase = args.x[which] + b * args.x_sb[which] + head * args.x_sh[which];
     const uint16_t *norm = args.norm[which] + (kRow ? head * D : 0);
     const int pairs = args.rot_dim / 2;
 
-    // Pass 1: RMSNorm into the LDS tile.
+    // Pass 1: RMSNorm (into the LDS tile for split-half pairs).
+    float av[kIters][8];
 #pragma unroll
-    for (int it = 0; it < kMaxIters; ++it) {
-        if (it >= iters) break;
+    for (int it = 0; it < kIters; ++it) {
         const int pidx = tid + it * kQkThreads;
         const int to = pidx / kPacks, pack = pidx % kPacks;
-        const bool in_tile = to < tile;
         const int64_t t = t0 + to;
-        const bool valid = in_tile && t < len;
+        const bool valid = t < len;
         u32x4 raw = u32x4{0u, 0u, 0u, 0u};
         if (valid) raw = *reinterpret_cast<const u32x4 *>(xbase + t * args.x_sl[which] + pack * 8);
         float v[8];
@@ -124,75 +128,140 @@ __global__ __launch_bounds__(kQkThreads) void qk_rope_quant_kernel(QkArgs args) 
             for (int off = kPacks / 2; off > 0; off >>= 1) s = s + __shfl_xor(s, off, kPacks);
             rrms = 1.0f / __builtin_sqrtf(s / static_cast<float>(D) + args.eps);
         }
-        if (in_tile) {
-            const u32x4 wraw = *reinterpret_cast<const u32x4 *>(norm + pack * 8);
-            float a[8];
+        const u32x4 wraw = *reinterpret_cast<const u32x4 *>(norm + pack * 8);
+        float *a = av[it];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                a[2 * j] = t_round<kFp16>((v[2 * j] * rrms) * t_to_f32<kFp16>(wraw[j] & 0xffffu));
-                a[2 * j + 1] = t_round<kFp16>((v[2 * j + 1] * rrms) * t_to_f32<kFp16>(wraw[j] >> 16));
-            }
+        for (int j = 0; j < 4; ++j) {
+            a[2 * j] = t_round<kFp16>((v[2 * j] * rrms) * t_to_f32<kFp16>(wraw[j] & 0xffffu));
+            a[2 * j + 1] = t_round<kFp16>((v[2 * j + 1] * rrms) * t_to_f32<kFp16>(wraw[j] >> 16));
+        }
+        if constexpr (kSplit) {
             float *dst = tile_a + to * D + pack * 8;
             *reinterpret_cast<f32x4 *>(dst) = f32x4{a[0], a[1], a[2], a[3]};
             *reinterpret_cast<f32x4 *>(dst + 4) = f32x4{a[4], a[5], a[6], a[7]};
         }
     }
-    __syncthreads();
+    if constexpr (kSplit) __syncthreads();
 
-    // Pass 2: RoPE, tile amax.
-    float y[kMaxIters][8];
-    float amax = 0.0000001f;
+    // Pass 2: RoPE, amax per 16-token sub-tile (a sub-tile is whole waves:
+    // 16 tokens x kPacks lanes = 256 or 128 lanes).
+    float y[kIters][8];
+    float amax[kSubs];
 #pragma unroll
-    for (int it = 0; it < kMaxIters; ++it) {
-        if (it >= iters) break;
+    for (int sub = 0; sub < kSubs; ++sub) amax[sub] = 0.0000001f;
+#pragma unroll
+    for (int it = 0; it < kIters; ++it) {
         const int pidx = tid + it * kQkThreads;
         const int to = pidx / kPacks, pack = pidx % kPacks;
         const int64_t t = t0 + to;
-        const bool valid = to < tile && t < len;
-        if (!valid) continue;
-        const float *arow = tile_a + to * D;
         const uint16_t *frow = args.rot_dim == 0 ? nullptr
                                                  : args.freqs + (args.f_batches == 1 ? 0 : b) * args.f_sb +
                                                        (args.f_len == 1 ? 0 : t) * args.f_sl;
+        const float *a = av[it];
+        float pmax = 0.0f;
+        const bool rope = t < len && pack * 8 < args.rot_dim;
+        if (rope && args.f_contig && pack * 8 + 8 <= args.rot_dim && (!kSplit || pairs % 8 == 0)) {
+            // The pack's frequency rows as 16-byte loads ([pair][row][col]
+            // contiguous): interleaved, pairs 4 pack .. + 3 (all four values);
+            // split-half, 8 pairs of one row.
+            if constexpr (!kSplit) {
+                const u32x4 f01 = *reinterpret_cast<const u32x4 *>(frow + pack * 16);
+                const u32x4 f23 = *reinterpret_cast<const u32x4 *>(frow + pack * 16 + 8);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int c = pack * 8 + j;
-            float val = arow[c];
-            if (c < args.rot_dim) {
-                const int pair = kSplit ? (c < pairs ? c : c - pairs) : c >> 1;
-                const int first = kSplit ? pair : 2 * pair;
-                const int second = kSplit ? pair + pairs : first + 1;
-                const int comp = kSplit ? (c >= pairs) : (c & 1);
-                const uint16_t *fp = frow + pair * args.f_sp + comp * args.f_sr;
-                const float f0 = t_to_f32<kFp16>(fp[0]);
-                const float f1 = t_to_f32<kFp16>(fp[args.f_sc]);
-                val = t_round<kFp16>(__builtin_fmaf(f1, arow[second], f0 * arow[first]));
+                for (int j = 0; j < 8; ++j) {
+                    const int i = j >> 1, comp = j & 1;
+                    const uint32_t word = (i < 2 ? f01 : f23)[(i & 1) * 2 + comp];
+                    const float f0 = t_to_f32<kFp16>(word & 0xffffu), f1 = t_to_f32<kFp16>(word >> 16);
+                    const float val = t_round<kFp16>(__builtin_fmaf(f1, a[2 * i + 1], f0 * a[2 * i]));
+                    y[it][j] = val;
+                    pmax = fmaxf(pmax, fabsf(val));
+                }
+            } else {
+                const int comp = pack * 8 >= pairs;
+                const int pb = pack * 8 - (comp ? pairs : 0);
+                const float *arow = tile_a + to * D;
+                u32x4 fv[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) fv[r] = *reinterpret_cast<const u32x4 *>(frow + pb * 4 + r * 8);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const uint32_t word = fv[j >> 1][(j & 1) * 2 + comp];
+                    const float f0 = t_to_f32<kFp16>(word & 0xffffu), f1 = t_to_f32<kFp16>(word >> 16);
+                    const float val = t_round<kFp16>(__builtin_fmaf(f1, arow[pb + j + pairs], f0 * arow[pb + j]));
+                    y[it][j] = val;
+                    pmax = fmaxf(pmax, fabsf(val));
+                }
             }
-            y[it][j] = val;
-            amax = fmaxf(amax, fabsf(val));
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int c = pack * 8 + j;
+                float val = a[j];
+                if (c < args.rot_dim && t < len) {
+                    const int pair = kSplit ? (c < pairs ? c : c - pairs) : c >> 1;
+                    const int comp = kSplit ? (c >= pairs) : (c & 1);
+                    const uint16_t *fp = frow + pair * args.f_sp + comp * args.f_sr;
+                    const float f0 = t_to_f32<kFp16>(fp[0]);
+                    const float f1 = t_to_f32<kFp16>(fp[args.f_sc]);
+                    float x0, x1;
+                    if constexpr (kSplit) {
+                        x0 = tile_a[to * D + pair];
+                        x1 = tile_a[to * D + pair + pairs];
+                    } else {
+                        x0 = a[j & ~1];
+                        x1 = a[j | 1];
+                    }
+                    val = t_round<kFp16>(__builtin_fmaf(f1, x1, f0 * x0));
+                }
+                y[it][j] = val;
+                pmax = fmaxf(pmax, fabsf(val));
+            }
+        }
+        if (t < len) {
+            const int sub = to / kQTile;
+#pragma unroll
+            for (int s2 = 0; s2 < kSubs; ++s2) amax[s2] = sub == s2 ? fmaxf(amax[s2], pmax) : amax[s2];
         }
     }
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
-    if ((tid & 63) == 0) wave_amax[tid >> 6] = amax;
+    for (int sub = 0; sub < kSubs; ++sub) {
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) amax[sub] = fmaxf(amax[sub], __shfl_xor(amax[sub], off, 64));
+        if ((tid & 63) == 0) wave_amax[tid >> 6][sub] = amax[sub];
+    }
     __syncthreads();
-    amax = fmaxf(fmaxf(wave_amax[0], wave_amax[1]), fmaxf(wave_amax[2], wave_amax[3]));
-    if (tid == 0) args.scale[which][(b * args.heads[which] + head) * args.ntiles[which] + tile_id] = amax / 127.0f;
-    const float inv = 127.0f / amax;
+    float inv[kSubs];
+    float kmax = 0.0000001f;
+#pragma unroll
+    for (int sub = 0; sub < kSubs; ++sub) {
+        const float m = fmaxf(fmaxf(wave_amax[0][sub], wave_amax[1][sub]), fmaxf(wave_amax[2][sub], wave_amax[3][sub]));
+        kmax = fmaxf(kmax, m);
+        inv[sub] = 127.0f / m;
+        if (which == 0 && tid == sub)
+            args.scale[0][(b * args.heads[0] + head) * args.ntiles[0] + chunk * kSubs + sub] = m / 127.0f;
+    }
+    if (which == 1) {
+        if (tid == 0) args.scale[1][(b * args.heads[1] + head) * args.ntiles[1] + chunk] = kmax / 127.0f;
+        const float kinv = 127.0f / kmax;
+#pragma unroll
+        for (int sub = 0; sub < kSubs; ++sub) inv[sub] = kinv;
+    }
 
     // Pass 3: codes, one 8-byte store per pack.
     int8_t *obase = args.out[which] + b * args.o_sb[which] + head * args.o_sh[which];
 #pragma unroll
-    for (int it = 0; it < kMaxIters; ++it) {
-        if (it >= iters) break;
+    for (int it = 0; it < kIters; ++it) {
         const int pidx = tid + it * kQkThreads;
         const int to = pidx / kPacks, pack = pidx % kPacks;
         const int64_t t = t0 + to;
-        if (!(to < tile && t < len)) continue;
+        if (t >= len) continue;
+        float iv = inv[0];
+#pragma unroll
+        for (int sub = 1; sub < kSubs; ++sub) iv = to / kQTile == sub ? inv[sub] : iv;
         uint32_t w[2] = {0u, 0u};
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            const float r = fminf(127.0f, fmaxf(-127.0f, __builtin_rintf(y[it][j] * inv)));
+            const float r = fminf(127.0f, fmaxf(-127.0f, __builtin_rintf(y[it][j] * iv)));
             w[j >> 2] |= (static_cast<uint32_t>(static_cast<int32_t>(r)) & 0xffu) << (8 * (j & 3));
         }
         *reinterpret_cast<u32x2 *>(obase + t * args.o_sl[which] + pack * 8) = u32x2{w[0], w[1]};
@@ -247,7 +316,8 @@ int32_t launch_qk(const QkArgs &args, int64_t batch, bool split, bool row, hipSt
         const dim3 g(static_cast<unsigned>(args.len[0] + args.len[1]), static_cast<unsigned>(batch));
         row_rrms_kernel<kFp16, D><<<g, 64, 0, s>>>(args);
     }
-    const dim3 grid(static_cast<unsigned>(args.heads[0] * args.ntiles[0] + args.heads[1] * args.ntiles[1]),
+    // one workgroup per 64-token chunk of each head: ntiles is 4 chunks' worth for Q, one for K
+    const dim3 grid(static_cast<unsigned>(args.heads[0] * (args.ntiles[0] / 4) + args.heads[1] * args.ntiles[1]),
                     static_cast<unsigned>(batch));
     if (split) {
         if (row) qk_rope_quant_kernel<kFp16, D, true, true><<<grid, kQkThreads, 0, s>>>(args);
@@ -318,6 +388,8 @@ extern "C" int32_t tu_qk_rms_rope_int8(
     a.ntiles[1] = nkt;
     a.f_sb = f_sb, a.f_sl = f_sl, a.f_sp = f_sp, a.f_sr = f_sr, a.f_sc = f_sc;
     a.f_batches = f_batches;
+    a.f_contig = rot_dim > 0 && f_sc == 1 && f_sr == 2 && f_sp == 4 && f_sl % 8 == 0 && f_sb % 8 == 0 &&
+                 (reinterpret_cast<uintptr_t>(freqs) & 15) == 0;
     a.f_len = f_len;
     a.rot_dim = static_cast<int>(rot_dim);
     a.eps = eps;

@@ -70,9 +70,30 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _c_void_p, _i64, _i64, _i64,
          _c_void_p, _c_void_p, _c_void_p],
     ),
+    "tu_w8a8_quant_qk": (
+        _i32,
+        [_c_void_p, _c_void_p, _i32, _i64, _i64, _i64, _i64, _i64, _i64,
+         _i64, _i64, _i64, _i64, _i64, _i64,
+         _c_void_p, _i64, _i64, _i64, _c_void_p, _i64, _i64, _i64,
+         _c_void_p, _c_void_p, _c_void_p, _i32, _c_void_p],
+    ),
+    "tu_w8a8_quant_v_workspace": (_i64, [_i64, _i64, _i64, _i64]),
+    "tu_w8a8_quant_v": (
+        _i32,
+        [_c_void_p, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _c_void_p, _i64,
+         _c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p],
+    ),
+    "tu_w8a8_attn_fwd": (
+        _i32,
+        [_c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p,
+         _c_void_p, _i64, _c_void_p, _i32,
+         _i64, _i64, _i64, _i64, _i64, _i64,
+         _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+         _f32, _i32, _c_void_p],
+    ),
 }
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

@@ -25,7 +25,15 @@ from typing import Optional
 import torch
 
 from .. import _lib
-from .quant import SUPPORTED_BLOCKS, _layout_dims, per_block_int8, rms_rope_per_warp_int8, value_transpose
+from .quant import (
+    SUPPORTED_BLOCKS,
+    _layout_dims,
+    per_block_int8,
+    per_warp_int8_hadamard,
+    quantize_v_int8,
+    rms_rope_per_warp_int8,
+    value_transpose,
+)
 
 KERNEL_HEAD_DIM = 128
 
@@ -366,3 +374,287 @@ def prequantize_sageattn_from_qk(
         tensor_layout=qk.tensor_layout, original_head_dim=qk.original_head_dim, is_causal=bool(is_causal),
         sm_scale=scale, blkq=16, blkk=64, output_dtype=value.dtype,
     )
+
+
+# ---------------------------------------------------------------------------
+# Dense W8A8 attention (the reference's loader-default ``w8a8`` backend)
+# ---------------------------------------------------------------------------
+
+@dataclasses.dataclass(frozen=True)
+class PrequantizedW8A8Attention:
+    """INT8 Q/K (Hadamard-rotated, 16-/64-token scales) and channel-wise INT8
+    V^T, ready for ``w8a8attn_from_prequantized``: the dense (force_dense,
+    use_w8a8) subset of the reference's PrequantizedSolAttention
+    (core.py:50-72).  All tensors are HND with the kernel's 128 channels;
+    ``value_int8`` is [B, Hkv, 128, Lpad] with keys in natural order and
+    ``value_prefix`` the per-channel prefix sums of its codes over 64-key
+    tiles [B, Hkv, Lpad / 64 + 1, 128]."""
+
+    query_int8: torch.Tensor
+    query_scale: torch.Tensor
+    key_int8: torch.Tensor
+    key_scale: torch.Tensor
+    value_int8: torch.Tensor
+    value_scale: torch.Tensor
+    value_prefix: torch.Tensor
+    output_dtype: torch.dtype
+    sm_scale: float
+    original_head_dim: int
+    key_tile_tokens: int
+    is_causal: bool
+    route_original_basis: bool
+
+
+def _validate_fixed_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, tensor_layout: str) -> None:
+    """The reference's fixed-length Q/K/V contract (core.py:292-309)."""
+    if tensor_layout not in ("HND", "NHD"):
+        raise ValueError(f"Unsupported tensor_layout: {tensor_layout}")
+    if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
+        raise ValueError("fixed-length Q/K/V must be four-dimensional")
+    head_dim = q.size(-1)
+    if k.size(-1) != head_dim or v.size(-1) != head_dim:
+        raise ValueError("Q/K/V head dimensions must match")
+    head_axis = 1 if tensor_layout == "HND" else 2
+    seq_axis = 2 if tensor_layout == "HND" else 1
+    if q.size(0) != k.size(0) or q.size(0) != v.size(0):
+        raise ValueError("Q/K/V batch sizes must match")
+    if k.size(head_axis) != v.size(head_axis) or k.size(seq_axis) != v.size(seq_axis):
+        raise ValueError("K/V head counts and sequence lengths must match")
+    if k.size(head_axis) == 0 or q.size(head_axis) % k.size(head_axis) != 0:
+        raise ValueError("the Q head count must be divisible by the KV head count")
+    if q.size(seq_axis) == 0 or k.size(seq_axis) == 0:
+        raise ValueError("empty Q/K sequences are not supported")
+
+
+def _key_tile_tokens(key_tile_tokens: int, key_length: int) -> int:
+    """The reference's key-tile validation (core.py:740-745).  The dense path
+    runs 64-key tiles whatever the value; the resolved value is kept."""
+    key_tile_tokens = int(key_tile_tokens)
+    if key_tile_tokens not in (0, 64, 128):
+        raise ValueError("key_tile_tokens must be 0 (auto), 64, or 128")
+    if key_tile_tokens == 0:
+        key_tile_tokens = 128 if key_length > 1024 else 64
+    return key_tile_tokens
+
+
+def _pad_channels(x: torch.Tensor, width: int) -> torch.Tensor:
+    pad = width - x.size(-1)
+    return torch.nn.functional.pad(x, (0, pad)) if pad else x
+
+
+def prequantize_w8a8attn_from_qk(
+    qk: PrequantizedQK,
+    value: torch.Tensor,
+    *,
+    sm_scale: Optional[float] = None,
+    key_tile_tokens: int = 0,
+    is_causal: bool = False,
+) -> PrequantizedW8A8Attention:
+    """Attach channel-wise INT8 V to already quantized Q/K, the dense W8A8
+    branch of the reference's prequantize_sol_sageattn_from_qk (core.py
+    :711-839 with use_w8a8=True, force_dense=True)."""
+    if qk.tensor_layout != "HND":
+        raise ValueError("prequantized Sol/W8A8 attention requires HND layout")
+    if value.dtype != qk.input_dtype:
+        raise TypeError("preprocessed Q/K and V must have matching logical dtypes")
+    if value.device != qk.query_int8.device:
+        raise ValueError("preprocessed Q/K and V must share one CUDA device")
+    if value.ndim != 4 or value.stride(-1) != 1:
+        raise ValueError("preprocessed Sol V must be four-dimensional with contiguous channels")
+    if value.shape != qk.key_int8.shape:
+        raise ValueError("preprocessed Q/K and V shapes are incompatible")
+    tile = _key_tile_tokens(key_tile_tokens, qk.key_int8.size(2))
+    with torch.cuda.device(value.device):
+        value_int8, value_scale, value_prefix = quantize_v_int8(value)
+        if value_int8.size(2) != KERNEL_HEAD_DIM:
+            pad = KERNEL_HEAD_DIM - value_int8.size(2)
+            value_int8 = torch.nn.functional.pad(value_int8, (0, 0, 0, pad))
+            value_scale = torch.nn.functional.pad(value_scale, (0, pad), value=1.0e-12)
+            value_prefix = _pad_channels(value_prefix, KERNEL_HEAD_DIM)
+        q_int8 = _pad_channels(qk.query_int8, KERNEL_HEAD_DIM)
+        k_int8 = _pad_channels(qk.key_int8, KERNEL_HEAD_DIM)
+    scale = float(sm_scale) if sm_scale is not None else qk.original_head_dim ** -0.5
+    return PrequantizedW8A8Attention(
+        query_int8=q_int8, query_scale=qk.query_scale, key_int8=k_int8, key_scale=qk.key_scale,
+        value_int8=value_int8, value_scale=value_scale, value_prefix=value_prefix, output_dtype=value.dtype,
+        sm_scale=scale, original_head_dim=qk.original_head_dim, key_tile_tokens=tile,
+        is_causal=bool(is_causal), route_original_basis=bool(qk.route_original_basis),
+    )
+
+
+def prequantize_w8a8attn(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    *,
+    tensor_layout: str = "HND",
+    sm_scale: Optional[float] = None,
+    key_tile_tokens: int = 0,
+    rotate_qk: bool = True,
+    stabilize_k: bool = True,
+    is_causal: bool = False,
+) -> PrequantizedW8A8Attention:
+    """Q/K/V quantization of the dense W8A8 path before the output exists,
+    the reference's prequantize_sol_sageattn (core.py:841-913) with
+    use_w8a8=True, force_dense=True: head_dim padded to 64 or 128, Q/K
+    through the rotated (and, with ``stabilize_k``, anchored) quantizer,
+    V per channel."""
+    if not q.is_cuda:
+        raise ValueError("Input tensors must be on CUDA")
+    if tensor_layout != "HND":
+        raise ValueError("Sol sparse attention currently requires HND layout")
+    if q.dtype not in (torch.float16, torch.bfloat16):
+        raise TypeError("Sol sparse Q/K/V must be float16 or bfloat16")
+    if q.device != k.device or q.device != v.device:
+        raise ValueError("Q/K/V must be on the same device")
+    if q.dtype != k.dtype or q.dtype != v.dtype:
+        raise TypeError("Q/K/V must have matching dtypes")
+    _validate_fixed_qkv(q, k, v, tensor_layout)
+    head_dim = q.size(-1)
+    if not 0 < head_dim <= 128:
+        raise ValueError("Sol sparse attention requires head_dim in [1, 128]")
+    if q.stride(-1) != 1 or k.stride(-1) != 1 or v.stride(-1) != 1:
+        raise ValueError("the last Q/K/V dimension must be contiguous")
+    kernel_head_dim = 64 if head_dim <= 64 else 128
+    with torch.cuda.device(q.device):
+        q, k, v = (_pad_channels(t, kernel_head_dim) for t in (q, k, v))
+        q_int8, q_scale, k_int8, k_scale = per_warp_int8_hadamard(
+            q, k, tensor_layout="HND", stabilize_k=bool(stabilize_k) and bool(rotate_qk), rotate=bool(rotate_qk))
+    qk = PrequantizedQK(
+        query_int8=q_int8, query_scale=q_scale, key_int8=k_int8, key_scale=k_scale, tensor_layout="HND",
+        input_dtype=v.dtype, original_head_dim=head_dim, route_original_basis=bool(rotate_qk),
+    )
+    return prequantize_w8a8attn_from_qk(qk, v, sm_scale=sm_scale, key_tile_tokens=key_tile_tokens,
+                                        is_causal=is_causal)
+
+
+def w8a8attn_from_prequantized(quantized: PrequantizedW8A8Attention) -> torch.Tensor:
+    """Runs the dense W8A8 kernel (reference sol_sparse_sageattn_from_prequantized,
+    core.py:916-982, W8A8 force-dense branch).  Output [B, Hq, Lq, head_dim]
+    in the input dtype."""
+    q8, k8 = quantized.query_int8, quantized.key_int8
+    batch, hq, lq, dim = q8.shape
+    hkv, lk = k8.size(1), k8.size(2)
+    device = q8.device
+    if quantized.output_dtype not in (torch.float16, torch.bfloat16):
+        raise TypeError("W8A8 output must be float16 or bfloat16")
+    with torch.cuda.device(device):
+        out = torch.empty((batch, hq, lq, dim), dtype=quantized.output_dtype, device=device)
+        _lib.call(
+            "tu_w8a8_attn_fwd", q8.data_ptr(), quantized.query_scale.data_ptr(), quantized.query_scale.size(-1),
+            k8.data_ptr(), quantized.key_scale.data_ptr(), quantized.key_scale.size(-1),
+            quantized.value_int8.data_ptr(), quantized.value_scale.data_ptr(), quantized.value_prefix.data_ptr(),
+            quantized.value_int8.size(-1), out.data_ptr(), int(quantized.output_dtype == torch.float16),
+            batch, hq, hkv, lq, lk, dim, q8.stride(0), q8.stride(1), q8.stride(2),
+            k8.stride(0), k8.stride(1), k8.stride(2), out.stride(0), out.stride(1), out.stride(2),
+            float(quantized.sm_scale), int(quantized.is_causal), _lib.stream_of(device),
+        )
+    return out[..., : quantized.original_head_dim]
+
+
+def w8a8attn(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    *,
+    tensor_layout: str = "HND",
+    is_causal: bool = False,
+    sm_scale: Optional[float] = None,
+    key_tile_tokens: int = 0,
+    rotate_qk: bool = True,
+    stabilize_k: bool = True,
+) -> torch.Tensor:
+    """Dense INT8 QK / INT8 PV attention, the reference's ``w8a8attn``
+    (core.py:657-708): NHD inputs are made HND-contiguous, Q/K rotated by
+    the shared Hadamard transform (K centred on its anchor), V quantized per
+    channel, P packed to unsigned 8 bits with the exp2 offset log2(255)."""
+    if tensor_layout not in {"HND", "NHD"}:
+        raise ValueError(f"Unsupported tensor_layout: {tensor_layout}")
+    if tensor_layout == "NHD":
+        q_hnd, k_hnd, v_hnd = (t.transpose(1, 2).contiguous() for t in (q, k, v))
+    else:
+        q_hnd, k_hnd, v_hnd = q, k, v
+    _validate_fixed_qkv(q_hnd, k_hnd, v_hnd, "HND")
+    if q_hnd.dtype not in (torch.float16, torch.bfloat16):
+        raise TypeError("Turing W8A8 Q/K/V must be float16 or bfloat16")
+    if q_hnd.dtype != k_hnd.dtype or q_hnd.dtype != v_hnd.dtype:
+        raise TypeError("Turing W8A8 Q/K/V must have matching dtypes")
+    if not 0 < q_hnd.size(-1) <= 128:
+        raise ValueError("Turing W8A8 requires head_dim in [1, 128]")
+    quantized = prequantize_w8a8attn(
+        q_hnd, k_hnd, v_hnd, tensor_layout="HND", sm_scale=sm_scale, key_tile_tokens=key_tile_tokens,
+        rotate_qk=rotate_qk, stabilize_k=stabilize_k, is_causal=bool(is_causal),
+    )
+    output = w8a8attn_from_prequantized(quantized)
+    return output.transpose(1, 2) if tensor_layout == "NHD" else output
+
+
+# The reference's split API names for the dense W8A8 path (the calls
+# comfyui_turing_utils/attention/stable.py:430-518 makes).  Only the
+# configuration that path uses is built: use_w8a8=True with force_dense=True
+# (the Sol sparse router is out of scope); everything else is refused.
+
+def _require_dense_w8a8(use_w8a8: bool, force_dense: bool, dense_query_ranges, exact_kv_ranges,
+                        residual_subblocks: int) -> None:
+    if not (use_w8a8 and force_dense):
+        raise ValueError("only dense W8A8 (use_w8a8=True, force_dense=True) of the Sol path is built for gfx950")
+    if int(residual_subblocks) not in (1, 2):
+        raise ValueError("residual_subblocks must be 1 or 2")
+    # Sol routing ranges only steer the sparse router; dense attention reads
+    # every key, so they are validated for shape and otherwise unused.
+    for ranges in (dense_query_ranges, exact_kv_ranges):
+        for item in ranges or ():
+            if not isinstance(item, (tuple, list)) or len(item) != 2:
+                raise ValueError("Sol policy ranges must contain (start, stop) pairs")
+
+
+def prequantize_sol_sageattn_from_qk(
+    qk: PrequantizedQK,
+    value: torch.Tensor,
+    *,
+    sm_scale: Optional[float] = None,
+    dense_query_ranges=(),
+    exact_kv_ranges=(),
+    threshold_sigma: float = 1.0,
+    residual_subblocks: int = 1,
+    use_w8a8: bool = False,
+    force_dense: bool = False,
+    key_tile_tokens: int = 0,
+    is_causal: bool = False,
+) -> PrequantizedW8A8Attention:
+    """Reference core.py:711-839, dense W8A8 configuration only."""
+    _require_dense_w8a8(use_w8a8, force_dense, dense_query_ranges, exact_kv_ranges, residual_subblocks)
+    return prequantize_w8a8attn_from_qk(qk, value, sm_scale=sm_scale, key_tile_tokens=key_tile_tokens,
+                                        is_causal=is_causal)
+
+
+def prequantize_sol_sageattn(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    *,
+    tensor_layout: str = "HND",
+    sm_scale: Optional[float] = None,
+    dense_query_ranges=(),
+    exact_kv_ranges=(),
+    threshold_sigma: float = 1.0,
+    residual_subblocks: int = 1,
+    use_w8a8: bool = False,
+    force_dense: bool = False,
+    key_tile_tokens: int = 0,
+    rotate_qk: bool = True,
+    stabilize_k: bool = True,
+    is_causal: bool = False,
+) -> PrequantizedW8A8Attention:
+    """Reference core.py:841-913, dense W8A8 configuration only."""
+    _require_dense_w8a8(use_w8a8, force_dense, dense_query_ranges, exact_kv_ranges, residual_subblocks)
+    return prequantize_w8a8attn(q, k, v, tensor_layout=tensor_layout, sm_scale=sm_scale,
+                                key_tile_tokens=key_tile_tokens, rotate_qk=rotate_qk, stabilize_k=stabilize_k,
+                                is_causal=is_causal)
+
+
+def sol_sparse_sageattn_from_prequantized(quantized: PrequantizedW8A8Attention, *, return_stats: bool = False):
+    """Reference core.py:916-982 for a dense W8A8 state.  With
+    ``return_stats`` the dense path reports no routed blocks: (output, 0, 0)."""
+    output = w8a8attn_from_prequantized(quantized)
+    return (output, 0, 0) if return_stats else output

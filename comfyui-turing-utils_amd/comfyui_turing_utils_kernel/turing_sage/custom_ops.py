@@ -1,10 +1,13 @@
-"""``torch.ops.turing_utils.sage_attention`` and ``qk_rms_rope_int8`` on gfx950.
+"""``torch.ops.turing_utils.sage_attention``, ``w8a8_attention`` and
+``qk_rms_rope_int8`` on gfx950.
 
 Same names, signatures and fake implementations as the reference
 (``turing_sage/custom_ops.py:63-168``).  ``sage_attention``: ``sm_scale <= 0``
 selects the default ``head_dim ** -0.5`` and the output is
 ``empty_like(query)``; the implementation is this build's Sage path (K
 smoothing on, 128-token Q/K blocks, bf16 PV), see ``core.sageattn``.
+``w8a8_attention``: dense INT8 QK / INT8 PV attention (``core.w8a8attn``);
+``sm_scale <= 0`` selects the default.
 ``qk_rms_rope_int8``: fused RMSNorm + RoPE + INT8 of Q (16-token scales,
 padded to multiples of 4 per 64 tokens) and K (64-token scales).
 """
@@ -36,6 +39,40 @@ def sage_attention(
 
 @sage_attention.register_fake
 def _sage_attention_fake(query, key, value, tensor_layout, is_causal, sm_scale):
+    return torch.empty_like(query)
+
+
+@torch.library.custom_op("turing_utils::w8a8_attention", mutates_args=())
+def w8a8_attention(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    tensor_layout: str,
+    is_causal: bool,
+    sm_scale: float,
+    key_tile_tokens: int,
+    rotate_qk: bool,
+    stabilize_k: bool,
+) -> torch.Tensor:
+    """Reference turing_sage/custom_ops.py:171-195."""
+    from .core import w8a8attn
+
+    return w8a8attn(
+        query,
+        key,
+        value,
+        tensor_layout=tensor_layout,
+        is_causal=is_causal,
+        sm_scale=sm_scale if sm_scale > 0.0 else None,
+        key_tile_tokens=key_tile_tokens,
+        rotate_qk=rotate_qk,
+        stabilize_k=stabilize_k,
+    )
+
+
+@w8a8_attention.register_fake
+def _w8a8_attention_fake(query, key, value, tensor_layout, is_causal, sm_scale, key_tile_tokens, rotate_qk,
+                         stabilize_k):
     return torch.empty_like(query)
 
 

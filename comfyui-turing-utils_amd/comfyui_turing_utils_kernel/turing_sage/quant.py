@@ -174,3 +174,82 @@ def rms_rope_per_warp_int8(
             k_int8.data_ptr(), kob, koh, kol, q_scale.data_ptr(), k_scale.data_ptr(), _lib.stream_of(q.device),
         )
     return q_int8, q_scale, k_int8, k_scale
+
+
+def per_warp_int8_hadamard(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    BLKQ: int = 64,
+    WARPQ: int = 16,
+    BLKK: int = 64,
+    tensor_layout: str = "HND",
+    stabilize_k: bool = True,
+    rotate: bool = True,
+):
+    """Shared randomized Hadamard rotation fused into Q/K INT8 quantization,
+    the reference's ``per_warp_int8_hadamard`` (turing_sage/quant.py:182-242):
+    Q per 16-token tile with ceil(Lq / 64) * 4 scales, K per 64-token tile,
+    K first centred on its stabilisation anchor when ``stabilize_k``.
+    Returns (q_int8, q_scale, k_int8, k_scale); codes keep the input layout.
+    ``rotate=False`` gives the plain per-warp codes (the reference's
+    ``rotate_qk=False`` route, quant.py:95-118)."""
+    if (BLKQ, WARPQ, BLKK) != (64, 16, 64):
+        raise ValueError("the W8A8 quantizer uses BLKQ=64, WARPQ=16, BLKK=64")
+    qh, ql, qsb, qsh, qsl = _layout_dims(q, tensor_layout)
+    kh, kl, ksb, ksh, ksl = _layout_dims(k, tensor_layout)
+    if q.dtype not in (torch.float16, torch.bfloat16) or k.dtype != q.dtype:
+        raise TypeError("W8A8 Q/K must be matching float16 or bfloat16 tensors")
+    if q.ndim != 4 or k.ndim != 4 or q.size(0) != k.size(0) or q.size(-1) != k.size(-1):
+        raise ValueError("W8A8 Q/K must be compatible four-dimensional tensors")
+    dim = q.size(-1)
+    if dim not in (64, 128):
+        raise ValueError("the W8A8 Q/K quantizer requires head_dim 64 or 128")
+    if q.stride(-1) != 1 or k.stride(-1) != 1:
+        raise ValueError("the last Q/K dimension must be contiguous")
+    if not q.is_cuda or k.device != q.device:
+        raise ValueError("W8A8 Q/K must be CUDA tensors on one device")
+    batch = q.size(0)
+    q_int8 = torch.empty(q.shape, dtype=torch.int8, device=q.device)
+    k_int8 = torch.empty(k.shape, dtype=torch.int8, device=k.device)
+    _, _, q8b, q8h, q8l = _layout_dims(q_int8, tensor_layout)
+    _, _, k8b, k8h, k8l = _layout_dims(k_int8, tensor_layout)
+    q_scale = torch.empty((batch, qh, (ql + BLKQ - 1) // BLKQ * (BLKQ // WARPQ)), dtype=torch.float32,
+                          device=q.device)
+    k_scale = torch.empty((batch, kh, (kl + BLKK - 1) // BLKK), dtype=torch.float32, device=q.device)
+    anchors = torch.empty((batch, kh), dtype=torch.int32, device=q.device) if stabilize_k else None
+    with torch.cuda.device(q.device):
+        _lib.call("tu_w8a8_quant_qk", q.data_ptr(), k.data_ptr(), 1 if q.dtype == torch.float16 else 0,
+                  batch, qh, kh, ql, kl, dim, qsb, qsh, qsl, ksb, ksh, ksl,
+                  q_int8.data_ptr(), q8b, q8h, q8l, k_int8.data_ptr(), k8b, k8h, k8l,
+                  q_scale.data_ptr(), k_scale.data_ptr(), _lib.ptr(anchors), int(bool(rotate)),
+                  _lib.stream_of(q.device))
+    return q_int8, q_scale, k_int8, k_scale
+
+
+def quantize_v_int8(value: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Channel-wise signed INT8 of HND V, the reference's quantize_v_int8_sm75
+    (turing_sage/core.py:772-784): (codes [B, H, D, ceil(L/64)*64] with keys
+    in natural order and zero padding, fp32 scales [B, H, D], int32 prefix
+    sums of the codes over 64-key tiles [B, H, ceil(L/64) + 1, D])."""
+    if value.ndim != 4 or value.stride(-1) != 1:
+        raise ValueError("W8A8 V must be four-dimensional with contiguous channels")
+    if value.dtype not in (torch.float16, torch.bfloat16):
+        raise TypeError("W8A8 V must be float16 or bfloat16")
+    batch, heads, length, dim = value.shape
+    if dim not in (64, 128):
+        raise ValueError("the W8A8 V quantizer requires head_dim 64 or 128")
+    if value.data_ptr() % 16 or any(s % 8 for s in value.stride()[:-1]):
+        value = value.contiguous()
+    lpad = (length + 63) // 64 * 64
+    codes = torch.empty((batch, heads, dim, lpad), dtype=torch.int8, device=value.device)
+    scale = torch.empty((batch, heads, dim), dtype=torch.float32, device=value.device)
+    prefix = torch.empty((batch, heads, lpad // 64 + 1, dim), dtype=torch.int32, device=value.device)
+    lib = _lib.load()
+    ws_bytes = int(lib.tu_w8a8_quant_v_workspace(batch, heads, length, dim))
+    workspace = torch.empty((ws_bytes,), dtype=torch.uint8, device=value.device)
+    with torch.cuda.device(value.device):
+        _lib.call("tu_w8a8_quant_v", value.data_ptr(), 1 if value.dtype == torch.float16 else 0, batch, heads,
+                  length, dim, value.stride(0), value.stride(1), value.stride(2), codes.data_ptr(), lpad,
+                  scale.data_ptr(), prefix.data_ptr(), workspace.data_ptr(), ws_bytes,
+                  _lib.stream_of(value.device))
+    return codes, scale, prefix

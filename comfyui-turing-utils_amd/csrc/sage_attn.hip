@@ -36,7 +36,7 @@
 //     conflict-free for the 16 lanes that read one chunk column.
 #include <type_traits>
 
-#include "tu_common.h"
+#include "attn_common.h"
 
 namespace tu {
 namespace {
@@ -50,36 +50,7 @@ constexpr int kBKey = 64;                // keys per tile
 constexpr int kKTileBytes = kBKey * kD;      // int8 K tile, 8 KiB
 constexpr int kVTileBytes = kD * kBKey * 2;  // bf16 V^T tile, 16 KiB
 constexpr int kStageBytes = kKTileBytes + kVTileBytes;
-constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kRescaleSlack = 8.0f;        // log2 of the largest p allowed
-
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-typedef __attribute__((address_space(3))) void lds_void;
-
-// s_waitcnt immediate that waits until at most n vector-memory operations are
-// outstanding and leaves the other counters alone (gfx9 encoding: vmcnt in
-// bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
-constexpr int vmcnt_imm(int n) { return (n & 0xf) | (0x7 << 4) | (0xf << 8) | ((n >> 4) << 14); }
-// s_waitcnt immediate: at most n LDS/scalar-memory operations outstanding.
-constexpr int lgkmcnt_imm(int n) { return 0xf | (0x7 << 4) | ((n & 0xf) << 8) | (0x3 << 14); }
-
-// Row maxima / sums across the 4 lane groups (xor 16, xor 32) with the
-// gfx950 permlane swaps: VALU only, no LDS traffic.
-__device__ __forceinline__ int xmax_i32(int v) {
-    auto a = __builtin_amdgcn_permlane16_swap(static_cast<unsigned>(v), static_cast<unsigned>(v), false, false);
-    v = max(static_cast<int>(a[0]), static_cast<int>(a[1]));
-    auto b = __builtin_amdgcn_permlane32_swap(static_cast<unsigned>(v), static_cast<unsigned>(v), false, false);
-    return max(static_cast<int>(b[0]), static_cast<int>(b[1]));
-}
-__device__ __forceinline__ float xmax_f32(float v) {
-    auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
-    auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
-}
-
-__device__ __forceinline__ int imax3(int a, int b, int c) { return max(max(a, b), c); }
 
 // K tile LDS row p holds key kperm(p): within each 32-key half, row
 // 16 kt + i holds key 8 (i >> 2) + 4 kt + (i & 3).  The QK MFMA reads 16
@@ -117,13 +88,6 @@ __device__ __forceinline__ LaneGeom lane_geom(int wave, int lane, int64_t k_sl, 
     return gm;
 }
 
-// Buffer resource over [base, base + bytes): raw (stride 0) dword access;
-// reads at or past `bytes` return zeros.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), static_cast<short>(0), static_cast<int>(bytes),
-                                             0x00020000);
-}
-
 // Direct-to-LDS buffer loads of the K and V^T tiles at key0 into one ring
 // stage.  Each buffer_load_dwordx4 ... lds moves 64 lanes x 16 B into 1 KiB of
 // contiguous LDS; the K row permutation and the chunk swizzle come from the
@@ -140,14 +104,6 @@ __device__ __forceinline__ void issue_tile(int8_t *stage, __amdgpu_buffer_rsrc_t
         __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_void *)(stage + kKTileBytes + (4 * wave + i) * 1024), 16,
                                                  gm.v_src[i], key0 * 2, 0, 0);
 }
-
-// The QK^T accumulators start at kBias, the bit pattern of 1.5 * 2^23, so
-// each int32 result is the float 1.5 * 2^23 + dot exactly (|dot| <= 2^21 for
-// D = 128 int8 codes): float(dot) is then one exact subtraction instead of a
-// conversion, and integer comparisons of the biased values still order the
-// dots.
-constexpr int kBias = 0x4B400000;
-constexpr float kBiasF = 12582912.0f;
 
 // S^T for one tile: s[kt][qt][r] = biased score of key 32 (kt >> 1) + 8 g +
 // 4 (kt & 1) + r and query 16 qt + lc of the wave.
@@ -350,18 +306,6 @@ __device__ __forceinline__ void mfma_cluster(const int8_t *kst, const int8_t *vs
     __builtin_amdgcn_sched_group_barrier(0x008, 12, 0);
     __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
     __builtin_amdgcn_sched_group_barrier(0x008, 32, 0);
-}
-
-// Workgroup barrier that does not wait for memory (the LDS ring hand-off is
-// ordered by an explicit s_waitcnt vmcnt before it) and that no instruction
-// is scheduled across: the ping-pong phases must not leak MFMAs into the
-// other group's VALU phase.
-__device__ __forceinline__ void wg_barrier() {
-    __builtin_amdgcn_sched_barrier(0);
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
 }
 
 // Ping-pong schedule.  A workgroup is 8 waves in two groups of 4 (one wave of

@@ -85,6 +85,21 @@ def lib():
             L.or_qk_rms_rope_int8.restype = _i32
             L.or_qk_rms_rope_int8.argtypes = [_p, _i32, _i64, _i64, _i64, _i64, _p, _i32, ctypes.c_float,
                                               _p, _i64, _i64, _i64, _i32, _i64, _i64, _p, _p]
+            L.or_w8a8_sign_negative.restype = _i32
+            L.or_w8a8_sign_negative.argtypes = [_i32]
+            L.or_w8a8_hadamard.restype = None
+            L.or_w8a8_hadamard.argtypes = [_p, _i32]
+            L.or_w8a8_detect_anchor.restype = ctypes.c_int32
+            L.or_w8a8_detect_anchor.argtypes = [_p, _i32, _i64, _i64, _i64]
+            L.or_w8a8_quant_tiles.restype = _i32
+            L.or_w8a8_quant_tiles.argtypes = [_p, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                                              _i32, _p, _p, _p]
+            L.or_w8a8_quant_v.restype = _i32
+            L.or_w8a8_quant_v.argtypes = [_p, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p]
+            L.or_w8a8_attn_rows.restype = _i32
+            L.or_w8a8_attn_rows.argtypes = [_p, _i64, _i64, _i64, _p, _i64, _p, _i64, _i64, _i64, _p, _i64,
+                                            _p, _i64, _p, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _i32,
+                                            _p, _i64, _p]
             _lib = L
     return _lib
 
@@ -287,3 +302,90 @@ def qk_rms_rope_int8(x_bits: np.ndarray, dtype: int, norm_bits: np.ndarray, norm
                                      int(split_half), tile, ntiles, _ptr(q), _ptr(s)),
            "qk_rms_rope_int8")
     return q, s
+
+
+# --- W8A8 attention variant (fused.cu rotated/anchored Q/K, V per channel) --
+
+def w8a8_sign_negative(channel: int) -> bool:
+    return bool(lib().or_w8a8_sign_negative(channel))
+
+
+def w8a8_hadamard(x: np.ndarray) -> np.ndarray:
+    """The shared randomized Hadamard transform of one head row (fp32)."""
+    y = np.array(x, dtype=np.float32, copy=True)
+    assert y.ndim == 1 and y.size in (64, 128)
+    lib().or_w8a8_hadamard(_ptr(y), y.size)
+    return y
+
+
+def w8a8_detect_anchor(k_bits: np.ndarray, dtype: int = DTYPE_BF16) -> np.ndarray:
+    """int32 [B, H] anchor rows (-1 = no anchor) of HND K bit patterns."""
+    k_bits = np.ascontiguousarray(k_bits, dtype=np.uint16)
+    b, h, l, d = k_bits.shape
+    out = np.empty((b, h), dtype=np.int32)
+    for bi in range(b):
+        for hi in range(h):
+            out[bi, hi] = lib().or_w8a8_detect_anchor(_ptr(k_bits[bi, hi]), dtype, l, d, d)
+    return out
+
+
+def w8a8_quant_tiles(x_bits: np.ndarray, tile: int, ntiles: int, rotate: bool = True,
+                     anchors: np.ndarray | None = None, dtype: int = DTYPE_BF16) -> tuple[np.ndarray, np.ndarray]:
+    """(int8 [B, H, L, D], fp32 scales [B, H, ntiles]) of the rotated per-tile
+    quantizer; x_bits HND bf16/fp16 bit patterns."""
+    x_bits = np.ascontiguousarray(x_bits, dtype=np.uint16)
+    b, h, l, d, sb, sh, sl = _hnd(x_bits)
+    q = np.empty(x_bits.shape, dtype=np.int8)
+    s = np.empty((b, h, ntiles), dtype=np.float32)
+    anc = None if anchors is None else np.ascontiguousarray(anchors, dtype=np.int32)
+    _check(lib().or_w8a8_quant_tiles(_ptr(x_bits), dtype, b, h, l, d, sb, sh, sl, tile, ntiles, int(rotate),
+                                     None if anc is None else _ptr(anc), _ptr(q), _ptr(s)), "w8a8_quant_tiles")
+    return q, s
+
+
+def w8a8_quant_qk(q_bits: np.ndarray, k_bits: np.ndarray, dtype: int = DTYPE_BF16, rotate: bool = True,
+                  stabilize_k: bool = True):
+    """The reference's per_warp_int8_hadamard contract (quant.py:182-242):
+    Q per 16 tokens with ceil(Lq/64)*4 scales, K per 64 tokens.  Returns
+    (q8, q_scale, k8, k_scale, anchors or None)."""
+    lq, lk = q_bits.shape[2], k_bits.shape[2]
+    anchors = w8a8_detect_anchor(k_bits, dtype) if stabilize_k else None
+    q8, qs = w8a8_quant_tiles(q_bits, 16, (lq + 63) // 64 * 4, rotate, None, dtype)
+    k8, ks = w8a8_quant_tiles(k_bits, 64, (lk + 63) // 64, rotate, anchors, dtype)
+    return q8, qs, k8, ks, anchors
+
+
+def w8a8_quant_v(v_bits: np.ndarray, dtype: int = DTYPE_BF16) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """(int8 [B, H, D, Lpad], fp32 scales [B, H, D], int32 tile sums
+    [B, H, Lpad/64, D]) of the channel-wise V quantizer; v_bits HND."""
+    v_bits = np.ascontiguousarray(v_bits, dtype=np.uint16)
+    b, h, l, d, sb, sh, sl = _hnd(v_bits)
+    lpad = (l + 63) // 64 * 64
+    q = np.empty((b, h, d, lpad), dtype=np.int8)
+    s = np.empty((b, h, d), dtype=np.float32)
+    ts = np.empty((b, h, lpad // 64, d), dtype=np.int32)
+    _check(lib().or_w8a8_quant_v(_ptr(v_bits), dtype, b, h, l, d, sb, sh, sl, lpad, _ptr(q), _ptr(s), _ptr(ts)),
+           "w8a8_quant_v")
+    return q, s, ts
+
+
+def w8a8_attn_rows(q8: np.ndarray, qs: np.ndarray, k8: np.ndarray, ks: np.ndarray, v8: np.ndarray,
+                   vs: np.ndarray, lk: int, sm_scale: float, rows: np.ndarray, causal: bool = False) -> np.ndarray:
+    """fp32 [len(rows), D] dense W8A8 attention outputs for (b, h, i) rows.
+    q8/k8 HND int8, qs [B, Hq, nqs], ks [B, Hkv, nks], v8 [B, Hkv, D, Lpad],
+    vs [B, Hkv, D]."""
+    q8 = np.ascontiguousarray(q8, dtype=np.int8)
+    k8 = np.ascontiguousarray(k8, dtype=np.int8)
+    v8 = np.ascontiguousarray(v8, dtype=np.int8)
+    qs = np.ascontiguousarray(qs, dtype=np.float32)
+    ks = np.ascontiguousarray(ks, dtype=np.float32)
+    vs = np.ascontiguousarray(vs, dtype=np.float32)
+    rows = np.ascontiguousarray(rows, dtype=np.int64).reshape(-1, 3)
+    b, hq, lq, d, qsb, qsh, qsl = _hnd(q8)
+    _, hkv, lk8, _, ksb, ksh, ksl = _hnd(k8)
+    assert lk8 == lk and v8.shape[:3] == (b, hkv, d)
+    out = np.empty((rows.shape[0], d), dtype=np.float32)
+    _check(lib().or_w8a8_attn_rows(_ptr(q8), qsb, qsh, qsl, _ptr(qs), qs.shape[2], _ptr(k8), ksb, ksh, ksl,
+                                   _ptr(ks), ks.shape[2], _ptr(v8), v8.shape[3], _ptr(vs), hq, hkv, lq, lk, d,
+                                   sm_scale, int(causal), _ptr(rows), rows.shape[0], _ptr(out)), "w8a8_attn_rows")
+    return out

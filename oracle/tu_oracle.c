@@ -636,3 +636,311 @@ OR_API int or_qk_rms_rope_int8(const uint16_t *x, int dtype, int64_t batch, int6
     free(y);
     return 0;
 }
+
+/* ======================================================================== */
+/* W8A8 attention variant (loader default `w8a8` backend).                   */
+/* ======================================================================== */
+
+/* Sign diagonal of the shared Q/K Hadamard transform: channel c is negated  */
+/* when bit (c & 31) of word c >> 5 is 0 (fused.cu:206-212).                 */
+static const uint32_t kW8a8Signs[4] = {0x1035997bu, 0x8087f5eeu, 0xee2e4e1au, 0x71132418u};
+
+OR_API int or_w8a8_sign_negative(int channel) {
+    return ((kW8a8Signs[channel >> 5] >> (channel & 31)) & 1u) == 0u;
+}
+
+/* Randomized normalised Walsh-Hadamard transform of one head row in place   */
+/* (attention_hadamard8, fused.cu:214-260), exact fp32 operation order:      */
+/*   x_c = -x_c for negative-sign channels;                                  */
+/*   within each pack of 8 channels, spans 1, 2, 4: (l, r) -> (l + r, l - r);*/
+/*   across packs (pack index bits 1, 2, 4 [, 8]): the pack without the bit  */
+/*   takes mine + other, the pack with it other - mine, from the old values; */
+/*   finally x_c *= 1/8 (D = 64) or 0.08838834764831845f (D = 128).           */
+OR_API void or_w8a8_hadamard(float *x, int dim) {
+    const int packs = dim / 8;
+    for (int c = 0; c < dim; ++c)
+        if (or_w8a8_sign_negative(c)) x[c] = -x[c];
+    for (int p = 0; p < packs; ++p) {
+        float *v = x + 8 * p;
+        for (int span = 1; span < 8; span <<= 1)
+            for (int base = 0; base < 8; base += 2 * span)
+                for (int o = 0; o < span; ++o) {
+                    const float l = v[base + o], r = v[base + o + span];
+                    v[base + o] = l + r;
+                    v[base + o + span] = l - r;
+                }
+    }
+    for (int bit = 1; bit < packs; bit <<= 1) {
+        float old[128];
+        memcpy(old, x, sizeof(float) * (size_t)dim);
+        for (int p = 0; p < packs; ++p)
+            for (int j = 0; j < 8; ++j) {
+                const float mine = old[8 * p + j], other = old[8 * (p ^ bit) + j];
+                x[8 * p + j] = (p & bit) ? other - mine : mine + other;
+            }
+    }
+    const float norm = dim == 64 ? 0.125f : 0.08838834764831845f;
+    for (int c = 0; c < dim; ++c) x[c] *= norm;
+}
+
+/* Lane-0 result of a 32-lane shfl_down tree (offsets 16, 8, 4, 2, 1): the   */
+/* order the reference's warp reductions produce.                            */
+static float tree32_sum(const float *v) {
+    float t[32];
+    memcpy(t, v, sizeof(t));
+    for (int off = 16; off > 0; off >>= 1)
+        for (int i = 0; i < off; ++i) t[i] = t[i] + t[i + off];
+    return t[0];
+}
+static float tree32_max(const float *v) {
+    float t[32];
+    memcpy(t, v, sizeof(t));
+    for (int off = 16; off > 0; off >>= 1)
+        for (int i = 0; i < off; ++i) t[i] = fmaxf(t[i], t[i + off]);
+    return t[0];
+}
+
+/* K stabilisation anchor of one (batch, kv head): DetectKAnchorKernel       */
+/* (fused.cu:409-575).  Nine keys at rows s (L - 1) / 8 (integer division)   */
+/* are sampled; per channel c (one of 128 threads, 4 warps of 32):           */
+/*   E_c   = fma chain of x^2 over the samples, M_c = max |x|,               */
+/*   S_c   = sequential sum of the samples,                                  */
+/*   dist_c[j] = fma(9 x_j - S_c, 9 x_j - S_c, 0);                            */
+/* the totals are warp trees (tree32_*) added warp 0..3 from 0.              */
+/* The candidate with the smallest total distance (first on ties) is the    */
+/* anchor; with r = x - anchor, E' and M' are formed the same way, and the  */
+/* anchor row is kept iff E' < E and M' <= M * 1.125f, else -1.             */
+/* x: dtype 0 bf16 / 1 fp16 bit patterns, channel stride 1; dim <= 128.      */
+OR_API int32_t or_w8a8_detect_anchor(const uint16_t *x, int dtype, int64_t len, int64_t dim, int64_t s_l) {
+    float samples[9][128];
+    float e_lane[128], m_lane[128], d_lane[9][128], be_lane[128], bm_lane[128];
+    if (dim > 128 || dim <= 0 || len <= 0) return -2;
+    for (int s = 0; s < 9; ++s) {
+        const int64_t row = (int64_t)s * (len - 1) / 8;
+        for (int c = 0; c < 128; ++c) samples[s][c] = c < dim ? t_to_f32(x[row * s_l + c], dtype) : 0.0f;
+    }
+    for (int c = 0; c < 128; ++c) {
+        float e = 0.0f, m = 0.0f, sum = 0.0f;
+        for (int j = 0; j < 9; ++j) d_lane[j][c] = 0.0f;
+        if (c < dim) {
+            for (int s = 0; s < 9; ++s) {
+                const float v = samples[s][c];
+                e = fmaf(v, v, e);
+                m = fmaxf(m, fabsf(v));
+                sum += v;
+            }
+            for (int j = 0; j < 9; ++j) {
+                const float d = 9.0f * samples[j][c] - sum;
+                d_lane[j][c] = fmaf(d, d, 0.0f);
+            }
+        }
+        e_lane[c] = e;
+        m_lane[c] = m;
+    }
+    float tot_e = 0.0f, tot_m = 0.0f, dist[9];
+    for (int w = 0; w < 4; ++w) {
+        tot_e += tree32_sum(e_lane + 32 * w);
+        tot_m = fmaxf(tot_m, tree32_max(m_lane + 32 * w));
+    }
+    int best = 0;
+    float best_d = 3.402823466e+38F;
+    for (int j = 0; j < 9; ++j) {
+        dist[j] = 0.0f;
+        for (int w = 0; w < 4; ++w) dist[j] += tree32_sum(d_lane[j] + 32 * w);
+        if (dist[j] < best_d) {
+            best = j;
+            best_d = dist[j];
+        }
+    }
+    for (int c = 0; c < 128; ++c) {
+        float e = 0.0f, m = 0.0f;
+        if (c < dim) {
+            const float a = samples[best][c];
+            for (int s = 0; s < 9; ++s) {
+                const float r = samples[s][c] - a;
+                e = fmaf(r, r, e);
+                m = fmaxf(m, fabsf(r));
+            }
+        }
+        be_lane[c] = e;
+        bm_lane[c] = m;
+    }
+    float tot_be = 0.0f, tot_bm = 0.0f;
+    for (int w = 0; w < 4; ++w) {
+        tot_be += tree32_sum(be_lane + 32 * w);
+        tot_bm = fmaxf(tot_bm, tree32_max(bm_lane + 32 * w));
+    }
+    const int improves = tot_be < tot_e && tot_bm <= tot_m * 1.125f;
+    return improves ? (int32_t)((int64_t)best * (len - 1) / 8) : -1;
+}
+
+/* Rotated per-tile INT8 of one tensor (Q or K): quant_int8_tile             */
+/* (fused.cu:262-407) as launched by QuantQKInt8Kernel (:577-636).           */
+/*   v     = float(x) - float(x[anchor row]) (K only, when anchor >= 0)      */
+/*   v     = hadamard(v) when rotate                                         */
+/*   amax  = max(1e-7, max |v| over the tile's tokens x channels)            */
+/*   scale = amax / 127,  q = cvt.rni.sat.s8(v * (127 / amax))               */
+/* Tiles of `tile` tokens (Q: 16, K: 64); tiles past L get 1e-7 / 127.       */
+/* x: [B][H][L][D] with strides (channel stride 1); anchors: [B][H] or NULL; */
+/* q: [B][H][L][D] contiguous; scales: [B][H][ntiles].                       */
+OR_API int or_w8a8_quant_tiles(const uint16_t *x, int dtype, int64_t batch, int64_t heads, int64_t len,
+                               int64_t dim, int64_t s_b, int64_t s_h, int64_t s_l, int64_t tile, int64_t ntiles,
+                               int rotate, const int32_t *anchors, int8_t *q, float *scales) {
+    if ((dim != 64 && dim != 128) || ntiles * tile < len) return -1;
+    float *y = (float *)malloc(sizeof(float) * (size_t)(tile * dim));
+    if (!y) return -2;
+    for (int64_t b = 0; b < batch; ++b)
+        for (int64_t h = 0; h < heads; ++h) {
+            const uint16_t *xb = x + b * s_b + h * s_h;
+            const int32_t anchor = anchors ? anchors[b * heads + h] : -1;
+            for (int64_t ti = 0; ti < ntiles; ++ti) {
+                float amax = 0.0000001f;
+                const int64_t t0 = ti * tile;
+                for (int64_t to = 0; to < tile && t0 + to < len; ++to) {
+                    float *v = y + to * dim;
+                    for (int64_t c = 0; c < dim; ++c) {
+                        v[c] = t_to_f32(xb[(t0 + to) * s_l + c], dtype);
+                        if (anchor >= 0) v[c] -= t_to_f32(xb[(int64_t)anchor * s_l + c], dtype);
+                    }
+                    if (rotate) or_w8a8_hadamard(v, (int)dim);
+                    for (int64_t c = 0; c < dim; ++c) amax = fmaxf(amax, fabsf(v[c]));
+                }
+                scales[(b * heads + h) * ntiles + ti] = amax / 127.0f;
+                const float mult = 127.0f / amax;
+                for (int64_t to = 0; to < tile && t0 + to < len; ++to)
+                    for (int64_t c = 0; c < dim; ++c)
+                        q[((b * heads + h) * len + t0 + to) * dim + c] = sat_rne_s8(y[to * dim + c] * mult);
+            }
+        }
+    free(y);
+    return 0;
+}
+
+/* Channel-wise signed INT8 V: quantize_value_kernel                         */
+/* (quant_v_int8_cuda_sm75.cu:58-164).                                       */
+/*   scale[c] = max(amax_c / 127, 1e-12)  (amax over all L tokens)           */
+/*   q[c][t]  = cvt.rni.sat.s8(float(v[t][c]) * (1 / scale[c]))              */
+/* Output layout (this build's, channel-major with keys in natural order):   */
+/* q [B][H][D][lpad] with zeros for t >= L, and tile_sum [B][H][lpad/64][D]  */
+/* = the sum of each 64-key tile's codes per channel (used by the offset     */
+/* form of the u8 x s8 product).  The reference permutes keys within groups  */
+/* of 16 for its Turing MMA fragment; the codes are the same.                */
+OR_API int or_w8a8_quant_v(const uint16_t *v, int dtype, int64_t batch, int64_t heads, int64_t len, int64_t dim,
+                           int64_t s_b, int64_t s_h, int64_t s_l, int64_t lpad, int8_t *q, float *scale,
+                           int32_t *tile_sum) {
+    if (lpad < len || lpad % 64) return -1;
+    const int64_t ntiles = lpad / 64;
+    for (int64_t b = 0; b < batch; ++b)
+        for (int64_t h = 0; h < heads; ++h) {
+            const uint16_t *vb = v + b * s_b + h * s_h;
+            for (int64_t c = 0; c < dim; ++c) {
+                float amax = 0.0f;
+                for (int64_t t = 0; t < len; ++t) amax = fmaxf(amax, fabsf(t_to_f32(vb[t * s_l + c], dtype)));
+                const float sc = fmaxf(amax / 127.0f, 1.0e-12f);
+                const float inv = 1.0f / sc;
+                scale[(b * heads + h) * dim + c] = sc;
+                int8_t *qc = q + ((b * heads + h) * dim + c) * lpad;
+                for (int64_t t = 0; t < lpad; ++t)
+                    qc[t] = t < len ? sat_rne_s8(t_to_f32(vb[t * s_l + c], dtype) * inv) : 0;
+                for (int64_t ti = 0; ti < ntiles; ++ti) {
+                    int32_t s = 0;
+                    for (int64_t t = 64 * ti; t < 64 * ti + 64; ++t) s += qc[t];
+                    tile_sum[((b * heads + h) * ntiles + ti) * dim + c] = s;
+                }
+            }
+        }
+    return 0;
+}
+
+/* cvt.rni.sat.u8.f32 (attn_utils.cuh:588-597): round half to even, clamp to */
+/* [0, 255], NaN -> 0.                                                       */
+static inline int sat_rne_u8(float v) {
+    if (v != v) return 0;
+    float r = nearbyintf(v);
+    if (r > 255.0f) r = 255.0f;
+    if (r < 0.0f) r = 0.0f;
+    return (int)r;
+}
+
+/* Dense W8A8 attention rows: the ForceDense/UseW8A8 specialisation of       */
+/* sparse_attention_kernel (sol_sparse_cuda_sm75.cu:1182-1322) with          */
+/* update_mdo(exp_offset) / RS_to_u8 / accumulate_d / compute_int8_sv /      */
+/* normalize_d (attn_utils.cuh:31-34, :436-568, :588-623, :676-703,          */
+/* :791-841, :920-973).  Per query row, key blocks of 64 in order:           */
+/*   s_j   = float(q8 . k8_j); masked (j >= Lk, causal j > i) -> -5e6        */
+/*   f     = (sm_scale * log2 e) * q_scale * k_scale[block]                  */
+/*   m'    = max(m, fma(max_j s_j, f, -log2 255))    (m starts at -5e6)      */
+/*   a     = 2^(m - m'); d = d * a; O = O * a                                */
+/*   p_j   = 2^(fma(s_j, f, -m')),  P_j = cvt.rni.sat.u8(p_j)                */
+/*   d    += sum p_j (the unquantised p),  O_c += float(sum_j P_j v8_j[c])   */
+/* out_c = O_c * (1 / d) * v_scale[c], fp32 (the caller rounds to the output */
+/* dtype).  exp2 / reciprocal are the exact libm forms (the reference uses   */
+/* ex2.approx / rcp.approx).  d starts at 1 like the reference; the first    */
+/* block's a = 2^(-5e6 - m') is 0.  q_scale: [B][Hq][nqs] with one scale per */
+/* 16 query rows; k_scale: [B][Hkv][nks] per 64 keys; v8: [B][Hkv][D][lpad]; */
+/* v_scale: [B][Hkv][D].  Rows are (b, h, i) triples; out is [nrows][D].     */
+OR_API int or_w8a8_attn_rows(const int8_t *q8, int64_t q_sb, int64_t q_sh, int64_t q_sl, const float *qs,
+                             int64_t nqs, const int8_t *k8, int64_t k_sb, int64_t k_sh, int64_t k_sl,
+                             const float *ks, int64_t nks, const int8_t *v8, int64_t lpad, const float *vs,
+                             int64_t hq, int64_t hkv, int64_t lq, int64_t lk, int64_t dim, float sm_scale,
+                             int causal, const int64_t *rows, int64_t nrows, float *out) {
+    (void)lq;
+    const float scale_log2 = sm_scale * 1.44269504088896340736f;
+    const float offset = 7.9943534f;
+    const int64_t groups = hq / hkv;
+    const int64_t nblk = (lk + 63) / 64;
+    if (lpad < nblk * 64 || nks < nblk) return -1;
+#pragma omp parallel
+    {
+        float *o = (float *)malloc(sizeof(float) * (size_t)dim);
+        float s[64];
+        int pq[64];
+#pragma omp for schedule(dynamic)
+        for (int64_t r = 0; r < nrows; ++r) {
+            const int64_t b = rows[3 * r], h = rows[3 * r + 1], i = rows[3 * r + 2];
+            const int64_t hk = h / groups;
+            const int8_t *qi = q8 + b * q_sb + h * q_sh + i * q_sl;
+            const float qscale = qs[(b * hq + h) * nqs + i / 16];
+            const float *ksr = ks + (b * hkv + hk) * nks;
+            const int8_t *vh = v8 + (b * hkv + hk) * dim * lpad;
+            const int64_t blocks = causal ? (i / 64 + 1 < nblk ? i / 64 + 1 : nblk) : nblk;
+            float m = -5000000.0f, d = 1.0f;
+            for (int64_t c = 0; c < dim; ++c) o[c] = 0.0f;
+            for (int64_t blk = 0; blk < blocks; ++blk) {
+                float mx = -5000000.0f;
+                for (int j = 0; j < 64; ++j) {
+                    const int64_t key = 64 * blk + j;
+                    float sv = -5000000.0f;
+                    if (key < lk && !(causal && key > i)) {
+                        const int8_t *kj = k8 + b * k_sb + hk * k_sh + key * k_sl;
+                        int32_t acc = 0;
+                        for (int64_t c = 0; c < dim; ++c) acc += (int32_t)qi[c] * (int32_t)kj[c];
+                        sv = (float)acc;
+                    }
+                    s[j] = sv;
+                    mx = fmaxf(mx, sv);
+                }
+                const float f = (scale_log2 * qscale) * ksr[blk];
+                const float m_new = fmaxf(m, fmaf(mx, f, -offset));
+                const float a = exp2f(m - m_new);
+                d *= a;
+                for (int64_t c = 0; c < dim; ++c) o[c] *= a;
+                for (int j = 0; j < 64; ++j) {
+                    const float p = exp2f(fmaf(s[j], f, -m_new));
+                    pq[j] = sat_rne_u8(p);
+                    d += p;
+                }
+                for (int64_t c = 0; c < dim; ++c) {
+                    int32_t acc = 0;
+                    for (int j = 0; j < 64; ++j) acc += pq[j] * (int32_t)vh[c * lpad + 64 * blk + j];
+                    o[c] += (float)acc;
+                }
+                m = m_new;
+            }
+            const float rd = 1.0f / d;
+            for (int64_t c = 0; c < dim; ++c) out[r * dim + c] = (o[c] * rd) * vs[(b * hkv + hk) * dim + c];
+        }
+        free(o);
+    }
+    return 0;
+}

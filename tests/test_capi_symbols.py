@@ -20,7 +20,7 @@ def _declarations():
     text = open(HEADER).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     out = {}
-    for ret, name, args in re.findall(r"(const char \*|int32_t)\s*(tu_\w+)\(([^)]*)\);", text):
+    for ret, name, args in re.findall(r"(const char \*|int32_t|int64_t)\s*(tu_\w+)\(([^)]*)\);", text):
         args = args.strip()
         n = 0 if args in ("", "void") else len(args.split(","))
         out[name] = (ret.strip(), n)
@@ -39,7 +39,8 @@ def test_binding_matches_header():
     for name, (ret, nargs) in decls.items():
         restype, argtypes = _lib.SIGNATURES[name]
         assert len(argtypes) == nargs, name
-        assert restype is (ctypes.c_char_p if ret.startswith("const char") else ctypes.c_int32), name
+        expected = {"int32_t": ctypes.c_int32, "int64_t": ctypes.c_int64}.get(ret, ctypes.c_char_p)
+        assert restype is expected, name
 
 
 @pytest.fixture(scope="module")

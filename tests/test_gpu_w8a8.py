@@ -1,0 +1,277 @@
+"""GPU parity of the dense W8A8 attention path (HIP) against the CPU oracle.
+
+  * K anchor, rotated Q/K codes and scales: bit-exact (tu_w8a8_quant_qk vs
+    or_w8a8_detect_anchor / or_w8a8_quant_tiles), bf16 and fp16, D 64 / 128,
+    strided NHD views, rotation and anchoring on and off;
+  * V codes, scales and tile prefix sums: bit-exact (tu_w8a8_quant_v vs
+    or_w8a8_quant_v);
+  * attention (tu_w8a8_attn_fwd vs or_w8a8_attn_rows on the same codes): the
+    north-star attention bar, cosine >= 0.999 and max-abs <= 2e-2, plus a
+    tighter relative bound measured for this kernel; causal, GQA, ragged Lq /
+    Lk, head_dim 64 through the padded path, fp16 output, and the reference's
+    finite-mask behaviour on an all-zero K tile;
+  * the reference's own W8A8 self-test (turing_sage/__init__.py:573-609:
+    allclose rtol 0.12 / atol 0.09 to fp32 SDPA) through preflight_w8a8 and
+    the registered op, eager and under torch.compile;
+  * Wan B1 H40 L32760 D128: full-size V/Q/K quantization bit-exact and
+    attention rows from the start, middle and end checked against the oracle.
+
+Oracle: oracle/tu_oracle.c (or_w8a8_*), a restatement of
+kernel/csrc/turing/sage/fused.cu:202-639, quant_v_int8_cuda_sm75.cu:58-164 and
+sol_sparse_cuda_sm75.cu:1182-1322.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle
+from tests import inputs
+
+pytestmark = pytest.mark.gpu
+
+
+def _bits(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def _dt(dtype) -> int:
+    return oracle.DTYPE_FP16 if dtype == torch.float16 else oracle.DTYPE_BF16
+
+
+def _qkv(b, hq, hkv, lq, lk, d, dtype, seed, k_offset=2.0):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(b, hq, lq, d, generator=g)
+    k = torch.randn(b, hkv, lk, d, generator=g) + k_offset * torch.randn(b, hkv, 1, d, generator=g)
+    v = torch.randn(b, hkv, lk, d, generator=g)
+    return q.to(dtype), k.to(dtype), v.to(dtype)
+
+
+def _gpu_qk(q, k, dev, stabilize=True, rotate=True, layout="HND"):
+    from comfyui_turing_utils_kernel.turing_sage.quant import per_warp_int8_hadamard
+
+    out = per_warp_int8_hadamard(q.to(dev), k.to(dev), tensor_layout=layout, stabilize_k=stabilize, rotate=rotate)
+    torch.cuda.synchronize(dev)
+    return [t.cpu() for t in out]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("rotate,stabilize", [(True, True), (True, False), (False, False)])
+@pytest.mark.parametrize("lq,lk", [(129, 151), (1, 2), (64, 64), (300, 1000)])
+def test_qk_quant_exact(gpu_device, dtype, d, rotate, stabilize, lq, lk):
+    print(f"[w8a8-qk] {dtype} d={d} rot={rotate} anchor={stabilize} lq={lq} lk={lk}", flush=True)
+    q, k, _ = _qkv(2, 4, 2, lq, lk, d, dtype, lq + lk + d)
+    qi, qs, ki, ks = _gpu_qk(q, k, gpu_device, stabilize, rotate)
+    dt = _dt(dtype)
+    anchors = oracle.w8a8_detect_anchor(_bits(k), dt) if stabilize else None
+    rq, rqs = oracle.w8a8_quant_tiles(_bits(q), 16, qs.shape[-1], rotate, None, dt)
+    rk, rks = oracle.w8a8_quant_tiles(_bits(k), 64, ks.shape[-1], rotate, anchors, dt)
+    assert qs.shape == (2, 4, (lq + 63) // 64 * 4) and ks.shape == (2, 2, (lk + 63) // 64)
+    np.testing.assert_array_equal(qs.numpy().view(np.uint32), rqs.view(np.uint32))
+    np.testing.assert_array_equal(ks.numpy().view(np.uint32), rks.view(np.uint32))
+    np.testing.assert_array_equal(qi.numpy(), rq)
+    np.testing.assert_array_equal(ki.numpy(), rk)
+
+
+def test_anchor_exact_and_triggered(gpu_device):
+    """Offsets that make the anchor fire and symmetric keys that keep -1."""
+    from comfyui_turing_utils_kernel import _lib
+
+    print("[w8a8-anchor]", flush=True)
+    g = torch.Generator().manual_seed(5)
+    k = (torch.randn(3, 4, 778, 128, generator=g) + 4 * torch.randn(3, 4, 1, 128, generator=g)).to(torch.bfloat16)
+    k[1, 2] = torch.randn(778, 128, generator=g).to(torch.bfloat16)
+    k[1, 2, ::2] = -k[1, 2, 1::2]
+    ref = oracle.w8a8_detect_anchor(_bits(k))
+    assert (ref >= 0).sum() >= 10 and ref[1, 2] == -1
+    kd = k.to(gpu_device)
+    anchors = torch.empty((3, 4), dtype=torch.int32, device=gpu_device)
+    q8 = torch.empty((3, 4, 778, 128), dtype=torch.int8, device=gpu_device)
+    qs = torch.empty((3, 4, 13 * 4), dtype=torch.float32, device=gpu_device)
+    ks = torch.empty((3, 4, 13), dtype=torch.float32, device=gpu_device)
+    k8 = torch.empty_like(q8)
+    _lib.call("tu_w8a8_quant_qk", kd.data_ptr(), kd.data_ptr(), 0, 3, 4, 4, 778, 778, 128,
+              *kd.stride()[:3], *kd.stride()[:3], q8.data_ptr(), *q8.stride()[:3], k8.data_ptr(), *k8.stride()[:3],
+              qs.data_ptr(), ks.data_ptr(), anchors.data_ptr(), 1, _lib.stream_of(gpu_device))
+    torch.cuda.synchronize(gpu_device)
+    np.testing.assert_array_equal(anchors.cpu().numpy(), ref)
+
+
+def test_qk_quant_nhd_views(gpu_device):
+    """NHD tensors and strided HND views of them give the same codes."""
+    print("[w8a8-qk] nhd", flush=True)
+    q, k, _ = _qkv(1, 5, 5, 97, 97, 128, torch.bfloat16, 3)
+    q_nhd, k_nhd = q.transpose(1, 2).contiguous(), k.transpose(1, 2).contiguous()
+    qi, qs, ki, ks = _gpu_qk(q_nhd, k_nhd, gpu_device, layout="NHD")
+    hi, hs, hki, hks = _gpu_qk(q_nhd.transpose(1, 2), k_nhd.transpose(1, 2), gpu_device, layout="HND")
+    ri, rs, rki, rks = _gpu_qk(q, k, gpu_device)
+    torch.testing.assert_close(qi.transpose(1, 2), ri, rtol=0, atol=0)
+    torch.testing.assert_close(hi, ri, rtol=0, atol=0)
+    torch.testing.assert_close(ki.transpose(1, 2), rki, rtol=0, atol=0)
+    for a, b in ((qs, rs), (ks, rks), (hs, rs), (hks, rks)):
+        torch.testing.assert_close(a, b, rtol=0, atol=0)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("length", [1, 63, 64, 151, 2100])
+def test_v_quant_exact(gpu_device, dtype, d, length):
+    from comfyui_turing_utils_kernel.turing_sage.quant import quantize_v_int8
+
+    print(f"[w8a8-v] {dtype} d={d} L={length}", flush=True)
+    _, _, v = _qkv(2, 3, 3, 1, length, d, dtype, length + d)
+    v = v * 3
+    codes, scale, prefix = (t.cpu() for t in quantize_v_int8(v.to(gpu_device)))
+    rq, rs, rts = oracle.w8a8_quant_v(_bits(v), _dt(dtype))
+    np.testing.assert_array_equal(scale.numpy().view(np.uint32), rs.view(np.uint32))
+    np.testing.assert_array_equal(codes.numpy(), rq)
+    ref_prefix = np.concatenate([np.zeros_like(rts[:, :, :1]), np.cumsum(rts, axis=2)], axis=2)
+    np.testing.assert_array_equal(prefix.numpy(), ref_prefix)
+
+
+def test_v_quant_strided_nhd_view(gpu_device):
+    from comfyui_turing_utils_kernel.turing_sage.quant import quantize_v_int8
+
+    print("[w8a8-v] nhd view", flush=True)
+    _, _, v = _qkv(1, 4, 4, 1, 200, 128, torch.bfloat16, 9)
+    view = v.transpose(1, 2).contiguous().to(gpu_device).transpose(1, 2)
+    codes, scale, prefix = (t.cpu() for t in quantize_v_int8(view))
+    rq, rs, _ = oracle.w8a8_quant_v(_bits(v))
+    np.testing.assert_array_equal(codes.numpy(), rq)
+    np.testing.assert_array_equal(scale.numpy().view(np.uint32), rs.view(np.uint32))
+
+
+def _oracle_attention(q, k, v, causal, sm_scale, rows, stabilize=True):
+    """Oracle rows for the same (padded) inputs the facade quantizes."""
+    d = q.shape[-1]
+    kd = 64 if d <= 64 else 128
+    pad = [torch.nn.functional.pad(t, (0, kd - d)) for t in (q, k, v)]
+    dt = _dt(q.dtype)
+    q8, qs, k8, ks, _ = oracle.w8a8_quant_qk(_bits(pad[0]), _bits(pad[1]), dt, True, stabilize)
+    v8, vs, _ = oracle.w8a8_quant_v(_bits(pad[2]), dt)
+    out = oracle.w8a8_attn_rows(q8, qs, k8, ks, v8, vs, k.shape[2], sm_scale, rows, causal)
+    return torch.from_numpy(out[:, :d])
+
+
+def _compare(got: torch.Tensor, ref: torch.Tensor, rel: float = 1e-2):
+    got, ref = got.double(), ref.double()
+    cos = torch.nn.functional.cosine_similarity(got.flatten(), ref.flatten(), dim=0).item()
+    err = (got - ref).abs().max().item()
+    scale = ref.abs().max().item()
+    assert torch.isfinite(got).all()
+    assert cos >= 0.999 and err <= 2e-2, (cos, err)
+    # tighter: the only differences are exp2 rounding, u8 ties and summation order
+    assert err <= rel * scale + 1e-3, (err, scale)
+    return cos, err
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("hq,hkv,lq,lk,d", [(4, 2, 129, 151, 128), (2, 2, 300, 1000, 128), (3, 1, 257, 64, 64),
+                                             (2, 2, 513, 700, 96), (1, 1, 40, 2, 128)])
+def test_attention_vs_oracle(gpu_device, causal, dtype, hq, hkv, lq, lk, d):
+    from comfyui_turing_utils_kernel.turing_sage import w8a8attn
+
+    print(f"[w8a8-attn] causal={causal} {dtype} hq={hq} hkv={hkv} lq={lq} lk={lk} d={d}", flush=True)
+    q, k, v = _qkv(1, hq, hkv, lq, lk, d, dtype, hq * 7 + lq + lk)
+    out = w8a8attn(q.to(gpu_device), k.to(gpu_device), v.to(gpu_device), is_causal=causal)
+    torch.cuda.synchronize(gpu_device)
+    assert out.shape == q.shape and out.dtype == dtype
+    rows = np.array([(0, h, i) for h in range(hq) for i in range(lq)])
+    ref = _oracle_attention(q, k, v, causal, d ** -0.5, rows).reshape(1, hq, lq, d)
+    if causal and lk < lq:
+        # rows past Lk in a top-left causal layout see every key, like the oracle
+        pass
+    _compare(out.cpu().float(), ref)
+
+
+def test_attention_reference_self_test(gpu_device):
+    """turing_sage/__init__.py:573-609 through preflight_w8a8, plus the
+    same inputs through the op and torch.compile(fullgraph)."""
+    from comfyui_turing_utils_kernel import turing_sage
+
+    print("[w8a8-attn] reference self-test", flush=True)
+    turing_sage.preflight_w8a8(gpu_device)
+    for head_dim in (64, 128):
+        qv = torch.arange(4 * 129 * head_dim, dtype=torch.float32)
+        kv = torch.arange(2 * 151 * head_dim, dtype=torch.float32)
+        q = (((qv % 29) - 14) / 16).reshape(1, 4, 129, head_dim).to(torch.bfloat16).to(gpu_device)
+        k = ((((kv * 3) % 31) - 15) / 16).reshape(1, 2, 151, head_dim).to(torch.bfloat16).to(gpu_device)
+        v = ((((kv * 5) % 37) - 18) / 16).reshape_as(k).to(torch.bfloat16).to(gpu_device)
+        eager = turing_sage.w8a8attn(q, k, v)
+        op = turing_sage.w8a8attn_compiled(q, k, v)
+        compiled = torch.compile(lambda a, b, c: turing_sage.w8a8attn_compiled(a, b, c), backend="eager",
+                                 fullgraph=True)(q, k, v)
+        ref = torch.nn.functional.scaled_dot_product_attention(q.float(), k.float(), v.float(), enable_gqa=True)
+        assert torch.allclose(eager.float(), ref, rtol=0.12, atol=0.09)
+        torch.testing.assert_close(op, eager, rtol=0, atol=0)
+        torch.testing.assert_close(compiled, eager, rtol=0, atol=0)
+        rows = np.array([(0, h, i) for h in range(4) for i in range(129)])
+        oref = _oracle_attention(q.cpu(), k.cpu(), v.cpu(), False, head_dim ** -0.5, rows).reshape(1, 4, 129, head_dim)
+        _compare(eager.cpu().float(), oref)
+
+
+def test_attention_nhd_and_split_api(gpu_device):
+    """NHD layout, the split prequantize / execute API, rotate_qk=False."""
+    from comfyui_turing_utils_kernel import turing_sage
+
+    print("[w8a8-attn] nhd + split", flush=True)
+    q, k, v = _qkv(2, 4, 4, 200, 333, 128, torch.bfloat16, 77)
+    qd, kd, vd = (t.to(gpu_device) for t in (q, k, v))
+    hnd = turing_sage.w8a8attn(qd, kd, vd)
+    nhd = turing_sage.w8a8attn(qd.transpose(1, 2), kd.transpose(1, 2), vd.transpose(1, 2), tensor_layout="NHD")
+    torch.testing.assert_close(nhd.transpose(1, 2), hnd, rtol=0, atol=0)
+    state = turing_sage.prequantize_sol_sageattn(qd, kd, vd, threshold_sigma=0.0, use_w8a8=True, force_dense=True)
+    torch.testing.assert_close(turing_sage.sol_sparse_sageattn_from_prequantized(state), hnd, rtol=0, atol=0)
+    with pytest.raises(ValueError, match="dense W8A8"):
+        turing_sage.prequantize_sol_sageattn(qd, kd, vd, use_w8a8=True, force_dense=False)
+    plain = turing_sage.w8a8attn(qd, kd, vd, rotate_qk=False)
+    ref = torch.nn.functional.scaled_dot_product_attention(q.float(), k.float(), v.float())
+    assert torch.nn.functional.cosine_similarity(plain.cpu().float().flatten(), ref.flatten(), dim=0) > 0.999
+
+
+def test_attention_reference_finite_mask_on_zero_key_tile(gpu_device):
+    """Lk = 1 with the anchor: K quantizes to zeros, the reference's -5e6 mask
+    leaks into the 63 padded keys and out = v / 64, as in the oracle."""
+    from comfyui_turing_utils_kernel import turing_sage
+
+    print("[w8a8-attn] finite mask", flush=True)
+    q, k, v = _qkv(1, 2, 2, 20, 1, 128, torch.bfloat16, 4)
+    out = turing_sage.w8a8attn(q.to(gpu_device), k.to(gpu_device), v.to(gpu_device)).cpu().float()
+    rows = np.array([(0, h, i) for h in range(2) for i in range(20)])
+    ref = _oracle_attention(q, k, v, False, 128 ** -0.5, rows).reshape(1, 2, 20, 128)
+    _compare(out, ref)
+    assert (out - v.float() / 64).abs().max() < 0.02
+
+
+def test_wan_shape_b1_h40_l32760(gpu_device):
+    """The Wan 14B attention shape: full-size quantization bit-exact on four
+    heads, attention rows at the start, middle and end of the sequence."""
+    from comfyui_turing_utils_kernel.turing_sage.core import prequantize_w8a8attn, w8a8attn_from_prequantized
+
+    print("[w8a8-attn] wan B1 H40 L32760", flush=True)
+    g = torch.Generator().manual_seed(2024)
+    L, H = 32760, 40
+    q = torch.randn(1, H, L, 128, generator=g).to(torch.bfloat16)
+    k = (torch.randn(1, H, L, 128, generator=g) + torch.randn(1, H, 1, 128, generator=g)).to(torch.bfloat16)
+    v = torch.randn(1, H, L, 128, generator=g).to(torch.bfloat16)
+    state = prequantize_w8a8attn(q.to(gpu_device), k.to(gpu_device), v.to(gpu_device))
+    out = w8a8attn_from_prequantized(state)
+    torch.cuda.synchronize(gpu_device)
+    heads = [0, 13, 27, 39]
+    hq, hk, hv = (t[:, heads].contiguous() for t in (q, k, v))
+    q8, qs, k8, ks, _ = oracle.w8a8_quant_qk(_bits(hq), _bits(hk))
+    v8, vs, ts = oracle.w8a8_quant_v(_bits(hv))
+    np.testing.assert_array_equal(state.query_int8[:, heads].cpu().numpy(), q8)
+    np.testing.assert_array_equal(state.key_int8[:, heads].cpu().numpy(), k8)
+    np.testing.assert_array_equal(state.query_scale[:, heads].cpu().numpy().view(np.uint32), qs.view(np.uint32))
+    np.testing.assert_array_equal(state.key_scale[:, heads].cpu().numpy().view(np.uint32), ks.view(np.uint32))
+    np.testing.assert_array_equal(state.value_int8[:, heads].cpu().numpy(), v8)
+    np.testing.assert_array_equal(state.value_scale[:, heads].cpu().numpy().view(np.uint32), vs.view(np.uint32))
+    sel = [0, 1, 255, 256, 16383, 16384, 32511, 32512, 32759]
+    rows = np.array([(0, hi, i) for hi in range(len(heads)) for i in sel])
+    ref = torch.from_numpy(oracle.w8a8_attn_rows(q8, qs, k8, ks, v8, vs, L, 128 ** -0.5, rows))
+    got = out[:, heads][:, :, sel].cpu().float().reshape(-1, 128)
+    _compare(got, ref)

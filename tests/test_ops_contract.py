@@ -94,10 +94,52 @@ def test_public_sage_api():
     assert turing_sage.__all__ == [
         "available", "w8a8_available", "split_prequantization_available", "fused_qk_preprocessing_available",
         "sageattn", "sageattn_compiled", "prequantize_sageattn", "prequantize_rms_rope_qk",
-        "prequantize_sageattn_from_qk", "sageattn_from_prequantized", "preflight",
+        "prequantize_sageattn_from_qk", "sageattn_from_prequantized", "w8a8attn", "w8a8attn_compiled",
+        "prequantize_sol_sageattn", "prequantize_sol_sageattn_from_qk", "sol_sparse_sageattn_from_prequantized",
+        "preflight", "preflight_w8a8",
     ]
-    assert turing_sage.w8a8_available() is False
+    assert turing_sage.w8a8_available() is turing_sage.available()
+    assert turing_sage.split_prequantization_available() is turing_sage.w8a8_available()
     assert kernel.__version__
+
+
+def test_w8a8_fake_contract_and_fullgraph_leaf():
+    """Reference custom_ops.py:171-210: the op returns empty_like(query)."""
+    q = torch.empty((1, 4, 129, 128), dtype=torch.bfloat16, device=META)
+    k = torch.empty((1, 2, 151, 128), dtype=torch.bfloat16, device=META)
+    out = torch.ops.turing_utils.w8a8_attention(q, k, k, "HND", False, -1.0, 0, True, True)
+    assert out.shape == q.shape and out.dtype == q.dtype and out.device.type == META
+    out = turing_sage.w8a8attn_compiled(q, k, k, is_causal=True, key_tile_tokens=128)
+    assert out.shape == q.shape
+    q16 = torch.empty((2, 65, 3, 64), dtype=torch.float16, device=META)
+    compiled = torch.compile(lambda a, b, c: turing_sage.w8a8attn_compiled(a, b, c, tensor_layout="NHD"),
+                             backend="eager", fullgraph=True)
+    out = compiled(q16, q16, q16)
+    assert out.shape == q16.shape and out.dtype == torch.float16
+
+
+def test_w8a8_refusals():
+    q = torch.zeros((1, 2, 64, 128), dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="CUDA"):
+        core.w8a8attn(q, q, q)
+    with pytest.raises(ValueError, match="CUDA"):
+        core.prequantize_sol_sageattn(q, q, q, use_w8a8=True, force_dense=True)
+    with pytest.raises(ValueError, match="dense W8A8"):
+        core.prequantize_sol_sageattn(q, q, q, use_w8a8=False, force_dense=True)
+    with pytest.raises(ValueError, match="tensor_layout"):
+        core.w8a8attn(q, q, q, tensor_layout="BHSD")
+    with pytest.raises(ValueError, match="head_dim"):
+        wide = torch.zeros((1, 1, 4, 130), dtype=torch.bfloat16)
+        core.w8a8attn(wide, wide, wide)
+    with pytest.raises(ValueError, match="divisible"):
+        core.w8a8attn(q, q[:, :1].expand(1, 3, 64, 128), q[:, :1].expand(1, 3, 64, 128))
+    with pytest.raises(ValueError, match="key_tile_tokens"):
+        core._key_tile_tokens(96, 100)
+    assert core._key_tile_tokens(0, 1025) == 128 and core._key_tile_tokens(0, 1024) == 64
+    with pytest.raises(ValueError, match="CUDA"):
+        quant.per_warp_int8_hadamard(q, q)
+    with pytest.raises(ValueError, match="BLKQ"):
+        quant.per_warp_int8_hadamard(q, q, BLKQ=128)
 
 
 def test_preflight_refuses_cpu():

@@ -205,7 +205,7 @@ def main():
         "traffic": measured_traffic(dominant),
     }
 
-    extras = extra_kernels(torch, dev, ops, lin, q, k_, copy_gbs)
+    extras = extra_kernels(torch, dev, ops, lin, q, k_, v, copy_gbs)
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds)
 
     record = {
@@ -239,12 +239,14 @@ def main():
     return 0
 
 
-def extra_kernels(torch, dev, ops, lin, q, k, copy_gbs) -> dict:
+def extra_kernels(torch, dev, ops, lin, q, k, v, copy_gbs) -> dict:
     """Kernels of the path's next rows, timed outside the headline step (the
     metric's workload is the four linears and the attention): the GELU-fused
-    ConvRot quantizer at FFN-down (K13824) and the fused Q/K RMSNorm + RoPE +
+    ConvRot quantizer at FFN-down (K13824), the fused Q/K RMSNorm + RoPE +
     INT8 producer at the attention shape (row-scope RMSNorm, interleaved
-    full-width RoPE, as in a Wan block)."""
+    full-width RoPE, as in a Wan block), and the dense W8A8 attention variant
+    (INT8 PV) with its rotated Q/K and channel-wise V quantizers."""
+    from comfyui_turing_utils_kernel.turing_sage import core as sage_core, quant as sage_quant
     from comfyui_turing_utils_kernel.turing_sage.custom_ops import qk_rms_rope_int8
 
     def timed(fn, reps=10):
@@ -276,6 +278,17 @@ def extra_kernels(torch, dev, ops, lin, q, k, copy_gbs) -> dict:
     nbytes = 2 * 3.0 * q.numel()
     out["qk_rms_rope_int8"] = {"ms_avg": ms, "gbs": nbytes / ms / 1e6, "frac_copy": nbytes / ms / 1e6 / copy_gbs,
                                "shape": [b, h, l, d], "norm_scope": "row", "rot_dim": d}
+    state = sage_core.prequantize_w8a8attn(q, k, v)
+    ms = timed(lambda: sage_core.w8a8attn_from_prequantized(state))
+    flops = 4.0 * b * h * l * l * d
+    out["w8a8_attn"] = {"ms_avg": ms, "tops": flops / ms / 1e9, "frac_int8_peak": flops / ms / 1e9 / PEAK_INT8_TOPS,
+                        "shape": [b, h, l, d]}
+    ms = timed(lambda: sage_quant.per_warp_int8_hadamard(q, k))
+    out["w8a8_quant_qk"] = {"ms_avg": ms, "gbs": 2 * 3.0 * q.numel() / ms / 1e6}
+    ms = timed(lambda: sage_quant.quantize_v_int8(v))
+    # V read twice (amax pass, code pass), codes written once
+    out["w8a8_quant_v"] = {"ms_avg": ms, "gbs": 5.0 * v.numel() / ms / 1e6}
+    del state
     return out
 
 

@@ -470,13 +470,22 @@ __global__ __launch_bounds__(kVThreads) void v_quant_kernel(const uint16_t *__re
 template <int D>
 __global__ __launch_bounds__(D) void v_prefix_kernel(const int32_t *__restrict__ tile_sum, int64_t ntiles,
                                                      int32_t *__restrict__ prefix) {
+    constexpr int kBatch = 16;  // independent loads in flight per thread
     const int c = threadIdx.x;
     const int64_t bh = blockIdx.x;
+    const int32_t *src = tile_sum + bh * ntiles * D + c;
+    int32_t *dst = prefix + bh * (ntiles + 1) * D + c;
     int32_t acc = 0;
-    prefix[(bh * (ntiles + 1)) * D + c] = 0;
-    for (int64_t t = 0; t < ntiles; ++t) {
-        acc += tile_sum[(bh * ntiles + t) * D + c];
-        prefix[(bh * (ntiles + 1) + t + 1) * D + c] = acc;
+    dst[0] = 0;
+    for (int64_t t0 = 0; t0 < ntiles; t0 += kBatch) {
+        int32_t v[kBatch];
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) v[j] = t0 + j < ntiles ? src[(t0 + j) * D] : 0;
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+            acc += v[j];
+            if (t0 + j < ntiles) dst[(t0 + j + 1) * D] = acc;
+        }
     }
 }
 

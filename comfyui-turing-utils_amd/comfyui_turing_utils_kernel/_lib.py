@@ -68,7 +68,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          _c_void_p, _c_void_p, _i32, _f32, _c_void_p, _i64, _i32, _i64, _i64,
          _i64, _i64, _i64, _i64, _i64,
          _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _c_void_p, _i64, _i64, _i64,
-         _c_void_p, _c_void_p, _c_void_p],
+         _c_void_p, _c_void_p, _i32, _c_void_p, _c_void_p, _c_void_p],
     ),
     "tu_w8a8_quant_qk": (
         _i32,
@@ -93,7 +93,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
 }
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

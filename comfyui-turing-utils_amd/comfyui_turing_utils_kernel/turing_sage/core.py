@@ -341,11 +341,12 @@ def prequantize_sageattn_from_qk(
 ) -> PrequantizedSageAttention:
     """Attach V to a fused Q/K preprocessing result without rereading Q/K
     (reference core.py:477-513).  Q/K codes of head_dim 64 are zero-padded to
-    the kernel's 128 channels (dot products unchanged)."""
+    the kernel's 128 channels (dot products unchanged).  Rotated (and
+    anchored) codes are accepted as the reference accepts them: the rotation
+    leaves Q.K unchanged and the anchor shifts each query row's scores by a
+    constant, which the softmax cancels."""
     if qk.tensor_layout not in ("HND", "NHD"):
         raise ValueError(f"Unsupported tensor_layout: {qk.tensor_layout}")
-    if qk.route_original_basis:
-        raise ValueError("rotated Q/K belong to the w8a8 attention variant, which is not built for gfx950")
     if value.dtype != qk.input_dtype:
         raise TypeError("preprocessed Q/K and V must have matching logical dtypes")
     if value.device != qk.query_int8.device:

@@ -109,11 +109,10 @@ def rms_rope_per_warp_int8(
     reference's ``rms_rope_per_warp_int8`` (turing_sage/quant.py:6-87).
 
     Q scales are [B, Hq, ceil(Lq / 64) * 4], K scales [B, Hk, ceil(Lk / 64)].
-    ``rotate_qk`` / ``stabilize_k`` belong to the w8a8 attention variant,
-    which this build does not provide.
+    ``rotate_qk`` applies the W8A8 path's shared Hadamard rotation after RoPE;
+    with ``stabilize_k`` as well, K is first centred on its anchor row (the
+    reference's quant.py:57-64: stabilisation only with rotation).
     """
-    if rotate_qk or stabilize_k:
-        raise ValueError("rotate_qk / stabilize_k need the w8a8 attention variant, which is not built for gfx950")
     if tensor_layout not in ("HND", "NHD"):
         raise ValueError(f"Unknown tensor layout: {tensor_layout}")
     if norm_scope not in ("head", "row"):
@@ -160,6 +159,10 @@ def rms_rope_per_warp_int8(
     _, _, kob, koh, kol = _layout_dims(k_int8, tensor_layout)
     q_scale = torch.empty((batch, hq, (lq + 63) // 64 * 4), dtype=torch.float32, device=q.device)
     k_scale = torch.empty((batch, hk, (lk + 63) // 64), dtype=torch.float32, device=k.device)
+    anchors = anchor_values = None
+    if rotate_qk and stabilize_k:
+        anchors = torch.empty((batch, hk), dtype=torch.int32, device=k.device)
+        anchor_values = torch.empty((batch, hk, head_dim), dtype=torch.float32, device=k.device)
     q_rrms = k_rrms = None
     if norm_scope == "row":
         q_rrms = torch.empty((batch, lq), dtype=torch.float32, device=q.device)
@@ -171,7 +174,8 @@ def rms_rope_per_warp_int8(
             qsb, qsh, qsl, ksb, ksh, ksl, q_norm.data_ptr(), k_norm.data_ptr(), 1 if norm_scope == "row" else 0,
             float(epsilon), _lib.ptr(freqs) if rot_dim > 0 else None, int(rot_dim), int(bool(split_half)), fb, fl,
             *fstrides, _lib.ptr(q_rrms), _lib.ptr(k_rrms), q_int8.data_ptr(), qob, qoh, qol,
-            k_int8.data_ptr(), kob, koh, kol, q_scale.data_ptr(), k_scale.data_ptr(), _lib.stream_of(q.device),
+            k_int8.data_ptr(), kob, koh, kol, q_scale.data_ptr(), k_scale.data_ptr(), int(bool(rotate_qk)),
+            _lib.ptr(anchors), _lib.ptr(anchor_values), _lib.stream_of(q.device),
         )
     return q_int8, q_scale, k_int8, k_scale
 

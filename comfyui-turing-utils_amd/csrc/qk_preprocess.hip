@@ -28,7 +28,7 @@
 // rrms comes from a one-wave-per-token pre-pass into caller scratch.
 #include <type_traits>
 
-#include "tu_common.h"
+#include "w8a8_common.h"
 
 namespace tu {
 namespace {
@@ -72,9 +72,11 @@ struct QkArgs {
     int64_t f_batches, f_len;
     int rot_dim;
     float eps;
+    const int32_t *anchors;   // K stabilisation [B][Hk] (W8A8 variant) or null
+    float *anchor_values;     // [B][Hk][D]: the anchor row's processed values
 };
 
-template <bool kFp16, int D, bool kSplit, bool kRow>
+template <bool kFp16, int D, bool kSplit, bool kRow, bool kRotate>
 __global__ __launch_bounds__(kQkThreads) void qk_rope_quant_kernel(QkArgs args) {
     constexpr int kPacks = D / 8;                        // lanes per token
     constexpr int kIters = kChunk * kPacks / kQkThreads;  // packs per thread
@@ -99,6 +101,19 @@ __global__ __launch_bounds__(kQkThreads) void qk_rope_quant_kernel(QkArgs args) 
     const uint16_t *xbase = args.x[which] + b * args.x_sb[which] + head * args.x_sh[which];
     const uint16_t *norm = args.norm[which] + (kRow ? head * D : 0);
     const int pairs = args.rot_dim / 2;
+
+    // W8A8 variant: K rows are centred on the head's anchor row before the
+    // rotation.  A thread's pack index is fixed (256 is a multiple of D / 8).
+    float anc[8];
+    bool anchored = false;
+    if constexpr (kRotate) {
+        if (which == 1 && args.anchors != nullptr) {
+            anchored = args.anchors[b * args.heads[1] + head] >= 0;
+            const float *ap = args.anchor_values + (b * args.heads[1] + head) * D + (tid % kPacks) * 8;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) anc[j] = anchored ? ap[j] : 0.0f;
+        }
+    }
 
     // Pass 1: RMSNorm (into the LDS tile for split-half pairs).
     float av[kIters][8];
@@ -217,6 +232,18 @@ __global__ __launch_bounds__(kQkThreads) void qk_rope_quant_kernel(QkArgs args) 
                 pmax = fmaxf(pmax, fabsf(val));
             }
         }
+        if constexpr (kRotate) {
+            // v = hadamard(y - anchor), every lane of the token's group
+            // taking part (tokens past L are zero)
+            if (anchored && t < len) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) y[it][j] -= anc[j];
+            }
+            w8a8_hadamard_pack<D>(y[it], pack);
+            pmax = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) pmax = fmaxf(pmax, fabsf(y[it][j]));
+        }
         if (t < len) {
             const int sub = to / kQTile;
 #pragma unroll
@@ -310,22 +337,103 @@ __global__ __launch_bounds__(64) void row_rrms_kernel(QkArgs args) {
     }
 }
 
+// processed_value (qk_preprocess.cu:97-145) of channel c of K row xrow:
+// RMSNorm then RoPE, rounded to the input type, with strided frequencies.
+template <bool kFp16, bool kSplit>
+__device__ __forceinline__ float processed_value(const QkArgs &args, const uint16_t *xrow, const uint16_t *norm,
+                                                 int c, float rrms, int64_t b, int64_t t) {
+    const float ac = t_round<kFp16>((t_to_f32<kFp16>(xrow[c]) * rrms) * t_to_f32<kFp16>(norm[c]));
+    if (c >= args.rot_dim) return ac;
+    const int pairs = args.rot_dim / 2;
+    const int pair = kSplit ? (c < pairs ? c : c - pairs) : c >> 1;
+    const int first = kSplit ? pair : 2 * pair;
+    const int second = kSplit ? pair + pairs : first + 1;
+    const int comp = kSplit ? (c >= pairs) : (c & 1);
+    const float x0 = t_round<kFp16>((t_to_f32<kFp16>(xrow[first]) * rrms) * t_to_f32<kFp16>(norm[first]));
+    const float x1 = t_round<kFp16>((t_to_f32<kFp16>(xrow[second]) * rrms) * t_to_f32<kFp16>(norm[second]));
+    const uint16_t *fp = args.freqs + (args.f_batches == 1 ? 0 : b) * args.f_sb + (args.f_len == 1 ? 0 : t) * args.f_sl +
+                         pair * args.f_sp + comp * args.f_sr;
+    const float f0 = t_to_f32<kFp16>(fp[0]);
+    const float f1 = t_to_f32<kFp16>(fp[args.f_sc]);
+    return t_round<kFp16>(__builtin_fmaf(f1, x1, f0 * x0));
+}
+
+// K anchor of the fused producer (detect_anchor_kernel, qk_preprocess.cu
+// :250-416): one 128-thread workgroup per (K head, batch).  The nine samples
+// are processed values; their rrms is the row-scope pre-pass value, or for
+// the head scope 1 / sqrt(S / D + eps) with S a sequential fma chain over the
+// head's channels (the reference's order; it takes rsqrtf, here IEEE).
+template <bool kFp16, int D, bool kSplit, bool kRow>
+__global__ __launch_bounds__(kAnchorThreads) void qk_anchor_kernel(QkArgs args) {
+    __shared__ float samples[kAnchorSamples][128];
+    __shared__ float rr[kAnchorSamples];
+    const int c = threadIdx.x;
+    const int64_t head = blockIdx.x, b = blockIdx.y;
+    const int64_t len = args.len[1];
+    const uint16_t *xbase = args.x[1] + b * args.x_sb[1] + head * args.x_sh[1];
+    const uint16_t *norm = args.norm[1] + (kRow ? head * D : 0);
+    if (c < kAnchorSamples) {
+        const int64_t t = static_cast<int64_t>(c) * (len - 1) / (kAnchorSamples - 1);
+        if constexpr (kRow) {
+            rr[c] = args.rrms[1][b * len + t];
+        } else {
+            const uint16_t *xrow = xbase + t * args.x_sl[1];
+            float sq = 0.0f;
+            for (int ch = 0; ch < D; ++ch) {
+                const float v = t_to_f32<kFp16>(xrow[ch]);
+                sq = __builtin_fmaf(v, v, sq);
+            }
+            rr[c] = 1.0f / __builtin_sqrtf(sq / static_cast<float>(D) + args.eps);
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int sm = 0; sm < kAnchorSamples; ++sm) {
+        const int64_t t = static_cast<int64_t>(sm) * (len - 1) / (kAnchorSamples - 1);
+        samples[sm][c] = c < D ? processed_value<kFp16, kSplit>(args, xbase + t * args.x_sl[1], norm, c, rr[sm], b, t)
+                               : 0.0f;
+    }
+    __syncthreads();
+    const int sel = w8a8_anchor_decide(samples, D);
+    const int64_t bh = b * args.heads[1] + head;
+    if (c == 0)
+        const_cast<int32_t *>(args.anchors)[bh] =
+            sel >= 0 ? static_cast<int32_t>(static_cast<int64_t>(sel) * (len - 1) / (kAnchorSamples - 1)) : -1;
+    if (c < D) args.anchor_values[bh * D + c] = sel >= 0 ? samples[sel][c] : 0.0f;
+}
+
+template <bool kFp16, int D, bool kRotate>
+void launch_quant(const QkArgs &args, dim3 grid, bool split, bool row, hipStream_t s) {
+    if (split) {
+        if (row) qk_rope_quant_kernel<kFp16, D, true, true, kRotate><<<grid, kQkThreads, 0, s>>>(args);
+        else qk_rope_quant_kernel<kFp16, D, true, false, kRotate><<<grid, kQkThreads, 0, s>>>(args);
+    } else {
+        if (row) qk_rope_quant_kernel<kFp16, D, false, true, kRotate><<<grid, kQkThreads, 0, s>>>(args);
+        else qk_rope_quant_kernel<kFp16, D, false, false, kRotate><<<grid, kQkThreads, 0, s>>>(args);
+    }
+}
+
 template <bool kFp16, int D>
-int32_t launch_qk(const QkArgs &args, int64_t batch, bool split, bool row, hipStream_t s) {
+int32_t launch_qk(const QkArgs &args, int64_t batch, bool split, bool row, bool rotate, hipStream_t s) {
     if (row) {
         const dim3 g(static_cast<unsigned>(args.len[0] + args.len[1]), static_cast<unsigned>(batch));
         row_rrms_kernel<kFp16, D><<<g, 64, 0, s>>>(args);
     }
+    if (args.anchors != nullptr) {
+        const dim3 ga(static_cast<unsigned>(args.heads[1]), static_cast<unsigned>(batch));
+        if (split) {
+            if (row) qk_anchor_kernel<kFp16, D, true, true><<<ga, kAnchorThreads, 0, s>>>(args);
+            else qk_anchor_kernel<kFp16, D, true, false><<<ga, kAnchorThreads, 0, s>>>(args);
+        } else {
+            if (row) qk_anchor_kernel<kFp16, D, false, true><<<ga, kAnchorThreads, 0, s>>>(args);
+            else qk_anchor_kernel<kFp16, D, false, false><<<ga, kAnchorThreads, 0, s>>>(args);
+        }
+    }
     // one workgroup per 64-token chunk of each head: ntiles is 4 chunks' worth for Q, one for K
     const dim3 grid(static_cast<unsigned>(args.heads[0] * (args.ntiles[0] / 4) + args.heads[1] * args.ntiles[1]),
                     static_cast<unsigned>(batch));
-    if (split) {
-        if (row) qk_rope_quant_kernel<kFp16, D, true, true><<<grid, kQkThreads, 0, s>>>(args);
-        else qk_rope_quant_kernel<kFp16, D, true, false><<<grid, kQkThreads, 0, s>>>(args);
-    } else {
-        if (row) qk_rope_quant_kernel<kFp16, D, false, true><<<grid, kQkThreads, 0, s>>>(args);
-        else qk_rope_quant_kernel<kFp16, D, false, false><<<grid, kQkThreads, 0, s>>>(args);
-    }
+    if (rotate) launch_quant<kFp16, D, true>(args, grid, split, row, s);
+    else launch_quant<kFp16, D, false>(args, grid, split, row, s);
     return check_launch("tu_qk_rms_rope_int8");
 }
 
@@ -338,7 +446,8 @@ extern "C" int32_t tu_qk_rms_rope_int8(
     const void *q_norm, const void *k_norm, int32_t norm_scope, float eps, const void *freqs, int64_t rot_dim,
     int32_t split_half, int64_t f_batches, int64_t f_len, int64_t f_sb, int64_t f_sl, int64_t f_sp, int64_t f_sr,
     int64_t f_sc, float *q_rrms, float *k_rrms, int8_t *q8, int64_t qo_sb, int64_t qo_sh, int64_t qo_sl,
-    int8_t *k8, int64_t ko_sb, int64_t ko_sh, int64_t ko_sl, float *q_scale, float *k_scale, void *stream) {
+    int8_t *k8, int64_t ko_sb, int64_t ko_sh, int64_t ko_sl, float *q_scale, float *k_scale, int32_t rotate,
+    int32_t *anchors, float *anchor_values, void *stream) {
     using namespace tu;
     TU_REQUIRE(dtype == 0 || dtype == 1, "Q/K preprocessing dtype must be 0 (bf16) or 1 (fp16), got %d", dtype);
     TU_REQUIRE(dim == 64 || dim == 128, "Q/K preprocessing requires head_dim 64 or 128, got %lld",
@@ -353,6 +462,8 @@ extern "C" int32_t tu_qk_rms_rope_int8(
                                 (f_len == 1 || (f_len == lq && lq == lk))),
                "RoPE batch/sequence broadcasting is incompatible");
     TU_REQUIRE(norm_scope == 0 || (q_rrms && k_rrms), "row-scope RMSNorm needs rrms scratch");
+    TU_REQUIRE((anchors == nullptr) == (anchor_values == nullptr), "K anchors need both the index and value buffers");
+    TU_REQUIRE(anchors == nullptr || rotate, "K stabilisation is part of the rotated (W8A8) variant");
     const auto aligned16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
     TU_REQUIRE(aligned16(q) && aligned16(k) && aligned16(q_norm) && aligned16(k_norm) && q_sl % 8 == 0 &&
                    q_sh % 8 == 0 && q_sb % 8 == 0 && k_sl % 8 == 0 && k_sh % 8 == 0 && k_sb % 8 == 0,
@@ -393,8 +504,13 @@ extern "C" int32_t tu_qk_rms_rope_int8(
     a.f_len = f_len;
     a.rot_dim = static_cast<int>(rot_dim);
     a.eps = eps;
+    a.anchors = anchors;
+    a.anchor_values = anchor_values;
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool split = split_half != 0, row = norm_scope == 1;
-    if (dtype == 1) return dim == 128 ? launch_qk<true, 128>(a, batch, split, row, s) : launch_qk<true, 64>(a, batch, split, row, s);
-    return dim == 128 ? launch_qk<false, 128>(a, batch, split, row, s) : launch_qk<false, 64>(a, batch, split, row, s);
+    const bool rot = rotate != 0;
+    if (dtype == 1)
+        return dim == 128 ? launch_qk<true, 128>(a, batch, split, row, rot, s) : launch_qk<true, 64>(a, batch, split, row, rot, s);
+    return dim == 128 ? launch_qk<false, 128>(a, batch, split, row, rot, s)
+                      : launch_qk<false, 64>(a, batch, split, row, rot, s);
 }

@@ -23,7 +23,7 @@
 // per lane), plus per-64-key-tile code sums and their exclusive prefix over
 // tiles [B][H][Lpad/64 + 1][D]: the attention feeds P - 128 (signed) to the
 // MFMA and adds back 128 * sum(V) from the prefix.
-#include "tu_common.h"
+#include "w8a8_common.h"
 
 namespace tu {
 namespace {
@@ -45,125 +45,28 @@ __device__ __forceinline__ uint32_t pack_s8x4(int32_t a, int32_t b, int32_t c, i
            ((static_cast<uint32_t>(c) & 0xffu) << 16) | (static_cast<uint32_t>(d) << 24);
 }
 
-// Sign words of the shared Q/K transform (fused.cu:206-212): channel c is
-// negated when bit (c & 31) of word c >> 5 is 0.
-__device__ __forceinline__ bool sign_negative(int c) {
-    constexpr uint32_t kSigns[4] = {0x1035997bu, 0x8087f5eeu, 0xee2e4e1au, 0x71132418u};
-    return ((kSigns[c >> 5] >> (c & 31)) & 1u) == 0u;
-}
-
 // ---------------------------------------------------------------------------
 // K anchor: one workgroup of 128 threads (two wave64 = four 32-lane trees)
 // per (kv head, batch).
 // ---------------------------------------------------------------------------
-constexpr int kAnchorThreads = 128;
-constexpr int kSamples = 9;
-
-// Lane 0 / lane 32 of a wave64 end with the sum (max) of their 32-lane half,
-// formed in the order of a shfl_down tree (offsets 16 .. 1): the xor partner
-// of every lane below the offset is the lane the down-shift would read.
-__device__ __forceinline__ float tree32_sum(float v) {
-#pragma unroll
-    for (int off = 16; off > 0; off >>= 1) v = v + __shfl_xor(v, off);
-    return v;
-}
-__device__ __forceinline__ float tree32_max(float v) {
-#pragma unroll
-    for (int off = 16; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
-    return v;
-}
-
 template <bool kFp16>
 __global__ __launch_bounds__(kAnchorThreads) void anchor_kernel(const uint16_t *__restrict__ k, int64_t len, int dim,
                                                                 int64_t s_b, int64_t s_h, int64_t s_l,
                                                                 int32_t *__restrict__ anchors) {
-    __shared__ float samples[kSamples][128];
-    __shared__ float tree_e[4], tree_m[4], tree_d[kSamples][4], tree_be[4], tree_bm[4];
-    __shared__ int selected;
-
+    __shared__ float samples[kAnchorSamples][128];
     const int c = threadIdx.x;
-    const int lane = c & 31, tree = c >> 5;
     const int64_t h = blockIdx.x, b = blockIdx.y, heads = gridDim.x;
     const uint16_t *kb = k + b * s_b + h * s_h;
 #pragma unroll
-    for (int s = 0; s < kSamples; ++s) {
-        const int64_t row = static_cast<int64_t>(s) * (len - 1) / (kSamples - 1);
+    for (int s = 0; s < kAnchorSamples; ++s) {
+        const int64_t row = static_cast<int64_t>(s) * (len - 1) / (kAnchorSamples - 1);
         samples[s][c] = c < dim ? h_to_f32<kFp16>(kb[row * s_l + c]) : 0.0f;
     }
     __syncthreads();
-
-    float e = 0.0f, m = 0.0f, sum = 0.0f, dist[kSamples];
-#pragma unroll
-    for (int j = 0; j < kSamples; ++j) dist[j] = 0.0f;
-    if (c < dim) {
-#pragma unroll
-        for (int s = 0; s < kSamples; ++s) {
-            const float v = samples[s][c];
-            e = __builtin_fmaf(v, v, e);
-            m = fmaxf(m, fabsf(v));
-            sum = sum + v;
-        }
-#pragma unroll
-        for (int j = 0; j < kSamples; ++j) {
-            const float d = 9.0f * samples[j][c] - sum;
-            dist[j] = __builtin_fmaf(d, d, 0.0f);
-        }
-    }
-    e = tree32_sum(e);
-    m = tree32_max(m);
-#pragma unroll
-    for (int j = 0; j < kSamples; ++j) dist[j] = tree32_sum(dist[j]);
-    if (lane == 0) {
-        tree_e[tree] = e;
-        tree_m[tree] = m;
-#pragma unroll
-        for (int j = 0; j < kSamples; ++j) tree_d[j][tree] = dist[j];
-    }
-    __syncthreads();
-    if (c == 0) {
-        int best = 0;
-        float best_d = 3.402823466e+38F;
-        for (int j = 0; j < kSamples; ++j) {
-            float d = 0.0f;
-            for (int t = 0; t < 4; ++t) d = d + tree_d[j][t];
-            if (d < best_d) {
-                best = j;
-                best_d = d;
-            }
-        }
-        selected = best;
-    }
-    __syncthreads();
-    const int best = selected;
-    float be = 0.0f, bm = 0.0f;
-    if (c < dim) {
-        const float a = samples[best][c];
-#pragma unroll
-        for (int s = 0; s < kSamples; ++s) {
-            const float r = samples[s][c] - a;
-            be = __builtin_fmaf(r, r, be);
-            bm = fmaxf(bm, fabsf(r));
-        }
-    }
-    be = tree32_sum(be);
-    bm = tree32_max(bm);
-    if (lane == 0) {
-        tree_be[tree] = be;
-        tree_bm[tree] = bm;
-    }
-    __syncthreads();
-    if (c == 0) {
-        float te = 0.0f, tm = 0.0f, tbe = 0.0f, tbm = 0.0f;
-        for (int t = 0; t < 4; ++t) {
-            te = te + tree_e[t];
-            tm = fmaxf(tm, tree_m[t]);
-            tbe = tbe + tree_be[t];
-            tbm = fmaxf(tbm, tree_bm[t]);
-        }
-        const bool improves = tbe < te && tbm <= tm * 1.125f;
+    const int sel = w8a8_anchor_decide(samples, dim);
+    if (c == 0)
         anchors[b * heads + h] =
-            improves ? static_cast<int32_t>(static_cast<int64_t>(best) * (len - 1) / (kSamples - 1)) : -1;
-    }
+            sel >= 0 ? static_cast<int32_t>(static_cast<int64_t>(sel) * (len - 1) / (kAnchorSamples - 1)) : -1;
 }
 
 // ---------------------------------------------------------------------------
@@ -187,37 +90,6 @@ struct RotArgs {
     int64_t o_sb[2], o_sh[2], o_sl[2];
     int rotate;
 };
-
-// The transform of one pack (8 channels of pack index p) across the lanes
-// of a token (attention_hadamard8, fused.cu:214-260): signs, the in-pack
-// butterfly with spans 1, 2, 4, the cross-pack butterfly over lane bits, the
-// 1/sqrt(D) factor.
-template <int D>
-__device__ __forceinline__ void hadamard_pack(float (&v)[8], int p) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-        if (sign_negative(8 * p + j)) v[j] = -v[j];
-#pragma unroll
-    for (int span = 1; span < 8; span <<= 1)
-#pragma unroll
-        for (int base = 0; base < 8; base += 2 * span)
-#pragma unroll
-            for (int o = 0; o < span; ++o) {
-                const float l = v[base + o], r = v[base + o + span];
-                v[base + o] = l + r;
-                v[base + o + span] = l - r;
-            }
-#pragma unroll
-    for (int bit = 1; bit < D / 8; bit <<= 1)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const float other = __shfl_xor(v[j], bit);
-            v[j] = (p & bit) ? other - v[j] : v[j] + other;
-        }
-    constexpr float kNorm = D == 64 ? 0.125f : 0.08838834764831845f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] *= kNorm;
-}
 
 template <bool kFp16, int D>
 __global__ __launch_bounds__(kQkThreads) void rot_quant_kernel(RotArgs args) {
@@ -273,7 +145,7 @@ __global__ __launch_bounds__(kQkThreads) void rot_quant_kernel(RotArgs args) {
 #pragma unroll
             for (int j = 0; j < 8; ++j) v[it][j] = v[it][j] - anchor[j];
         }
-        if (args.rotate) hadamard_pack<D>(v[it], pack);
+        if (args.rotate) w8a8_hadamard_pack<D>(v[it], pack);
         float a = 0.0000001f;
 #pragma unroll
         for (int j = 0; j < 8; ++j) a = fmaxf(a, fabsf(v[it][j]));

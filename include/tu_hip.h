@@ -182,10 +182,15 @@ int32_t tu_sage_attn_fwd(const int8_t *q8, const float *q_scale, int64_t blkq, c
  * column f_sc); f_batches in {1, batch}, f_len in {1, lq == lk}.  q8, k8:
  * int8 by strides.  q_scale: fp32 [batch, hq, ceil(lq / 64) * 4] (tiles past
  * lq get 1e-7 / 127); k_scale: fp32 [batch, hk, ceil(lk / 64)].
- * Replaces turing_utils::qk_rms_rope_int8 without its rotate_qk /
- * stabilize_k variant (kernel/comfyui_turing_utils_kernel/turing_sage/
- * custom_ops.py:63-134 -> quant.py:6-87 -> kernel/csrc/turing/sage/
- * qk_preprocess.cu:417-629, :632-753). */
+ * rotate != 0 (the W8A8 variant): after RoPE each token row is rotated by
+ * the shared sign-diagonal Walsh-Hadamard transform of tu_w8a8_quant_qk
+ * before the tile amax; with anchors / anchor_values (int32 [batch, hk] /
+ * fp32 [batch, hk, dim], both or neither, rotate required) K is first
+ * centred on its stabilisation anchor, detected on the processed values of
+ * nine sampled rows (head scope: their rrms from a sequential fma chain).
+ * Replaces turing_utils::qk_rms_rope_int8 (kernel/comfyui_turing_utils_kernel/
+ * turing_sage/custom_ops.py:63-134 -> quant.py:6-87 -> kernel/csrc/turing/
+ * sage/qk_preprocess.cu:250-416 (anchor), :417-629, :632-753). */
 int32_t tu_qk_rms_rope_int8(const void *q, const void *k, int32_t dtype, int64_t batch, int64_t hq,
                             int64_t hk, int64_t lq, int64_t lk, int64_t dim, int64_t q_sb, int64_t q_sh,
                             int64_t q_sl, int64_t k_sb, int64_t k_sh, int64_t k_sl, const void *q_norm,
@@ -194,7 +199,8 @@ int32_t tu_qk_rms_rope_int8(const void *q, const void *k, int32_t dtype, int64_t
                             int64_t f_sb, int64_t f_sl, int64_t f_sp, int64_t f_sr, int64_t f_sc,
                             float *q_rrms, float *k_rrms, int8_t *q8, int64_t qo_sb, int64_t qo_sh,
                             int64_t qo_sl, int8_t *k8, int64_t ko_sb, int64_t ko_sh, int64_t ko_sl,
-                            float *q_scale, float *k_scale, void *stream);
+                            float *q_scale, float *k_scale, int32_t rotate, int32_t *anchors,
+                            float *anchor_values, void *stream);
 
 /* Dense W8A8 attention (the loader-default `w8a8` backend) ----------------- */
 

@@ -85,6 +85,15 @@ def lib():
             L.or_qk_rms_rope_int8.restype = _i32
             L.or_qk_rms_rope_int8.argtypes = [_p, _i32, _i64, _i64, _i64, _i64, _p, _i32, ctypes.c_float,
                                               _p, _i64, _i64, _i64, _i32, _i64, _i64, _p, _p]
+            L.or_qk_rms_rope_int8_ex.restype = _i32
+            L.or_qk_rms_rope_int8_ex.argtypes = [_p, _i32, _i64, _i64, _i64, _i64, _p, _i32, ctypes.c_float,
+                                                 _p, _i64, _i64, _i64, _i32, _i64, _i64, _i32, _p, _p, _p, _p]
+            L.or_qk_fused_anchor.restype = _i32
+            L.or_qk_fused_anchor.argtypes = [_p, _i32, _i64, _i64, _i64, _i64, _p, _i32, ctypes.c_float, _p,
+                                             _i64, _i64, _i64, _i32, _p, _p]
+            L.or_qk_processed.restype = _i32
+            L.or_qk_processed.argtypes = [_p, _i32, _i64, _i64, _i64, _i64, _p, _i32, ctypes.c_float, _p,
+                                          _i64, _i64, _i64, _i32, _p]
             L.or_w8a8_sign_negative.restype = _i32
             L.or_w8a8_sign_negative.argtypes = [_i32]
             L.or_w8a8_hadamard.restype = None
@@ -302,6 +311,70 @@ def qk_rms_rope_int8(x_bits: np.ndarray, dtype: int, norm_bits: np.ndarray, norm
                                      int(split_half), tile, ntiles, _ptr(q), _ptr(s)),
            "qk_rms_rope_int8")
     return q, s
+
+
+def _freq_args(freqs, rot_dim):
+    if freqs is not None:
+        freqs = np.ascontiguousarray(freqs, dtype=np.float32)
+        assert freqs.shape[2:] == (rot_dim // 2, 2, 2)
+        return freqs, freqs.shape[0], freqs.shape[1]
+    assert rot_dim == 0
+    return None, 1, 1
+
+
+def qk_rms_rope_int8_ex(x_bits: np.ndarray, dtype: int, norm_bits: np.ndarray, norm_scope: str, eps: float,
+                        freqs: np.ndarray | None, rot_dim: int, split_half: bool, tile: int, ntiles: int,
+                        rotate: bool = False, anchors: np.ndarray | None = None,
+                        anchor_values: np.ndarray | None = None) -> tuple[np.ndarray, np.ndarray]:
+    """The fused preprocessor with the W8A8 transform: K minus its anchor
+    row's processed values (when anchors[b, h] >= 0), then the shared
+    Hadamard rotation, then per-tile INT8."""
+    x_bits = np.ascontiguousarray(x_bits, dtype=np.uint16)
+    norm_bits = np.ascontiguousarray(norm_bits, dtype=np.uint16)
+    b, h, l, d = x_bits.shape
+    freqs, fb, fs = _freq_args(freqs, rot_dim)
+    anc = None if anchors is None else np.ascontiguousarray(anchors, dtype=np.int32)
+    av = None if anchor_values is None else np.ascontiguousarray(anchor_values, dtype=np.float32)
+    q = np.empty(x_bits.shape, dtype=np.int8)
+    s = np.empty((b, h, ntiles), dtype=np.float32)
+    _check(lib().or_qk_rms_rope_int8_ex(_ptr(x_bits), dtype, b, h, l, d, _ptr(norm_bits),
+                                        1 if norm_scope == "row" else 0, eps,
+                                        _ptr(freqs) if freqs is not None else None, fb, fs, rot_dim,
+                                        int(split_half), tile, ntiles, int(rotate),
+                                        None if anc is None else _ptr(anc), None if av is None else _ptr(av),
+                                        _ptr(q), _ptr(s)), "qk_rms_rope_int8_ex")
+    return q, s
+
+
+def qk_fused_anchor(x_bits: np.ndarray, dtype: int, norm_bits: np.ndarray, norm_scope: str, eps: float,
+                    freqs: np.ndarray | None, rot_dim: int, split_half: bool) -> tuple[np.ndarray, np.ndarray]:
+    """(int32 anchors [B, H], fp32 anchor values [B, H, D]) of the fused
+    preprocessor's K stabilisation."""
+    x_bits = np.ascontiguousarray(x_bits, dtype=np.uint16)
+    norm_bits = np.ascontiguousarray(norm_bits, dtype=np.uint16)
+    b, h, l, d = x_bits.shape
+    freqs, fb, fs = _freq_args(freqs, rot_dim)
+    anchors = np.empty((b, h), dtype=np.int32)
+    values = np.empty((b, h, d), dtype=np.float32)
+    _check(lib().or_qk_fused_anchor(_ptr(x_bits), dtype, b, h, l, d, _ptr(norm_bits), 1 if norm_scope == "row" else 0,
+                                    eps, _ptr(freqs) if freqs is not None else None, fb, fs, rot_dim,
+                                    int(split_half), _ptr(anchors), _ptr(values)), "qk_fused_anchor")
+    return anchors, values
+
+
+def qk_processed(x_bits: np.ndarray, dtype: int, norm_bits: np.ndarray, norm_scope: str, eps: float,
+                 freqs: np.ndarray | None, rot_dim: int, split_half: bool) -> np.ndarray:
+    """fp32 [B, H, L, D] RMSNorm + RoPE values (each exactly representable in
+    the input type) that the fused quantizer starts from."""
+    x_bits = np.ascontiguousarray(x_bits, dtype=np.uint16)
+    norm_bits = np.ascontiguousarray(norm_bits, dtype=np.uint16)
+    b, h, l, d = x_bits.shape
+    freqs, fb, fs = _freq_args(freqs, rot_dim)
+    out = np.empty(x_bits.shape, dtype=np.float32)
+    _check(lib().or_qk_processed(_ptr(x_bits), dtype, b, h, l, d, _ptr(norm_bits), 1 if norm_scope == "row" else 0,
+                                 eps, _ptr(freqs) if freqs is not None else None, fb, fs, rot_dim, int(split_half),
+                                 _ptr(out)), "qk_processed")
+    return out
 
 
 # --- W8A8 attention variant (fused.cu rotated/anchored Q/K, V per channel) --

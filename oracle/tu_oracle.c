@@ -567,16 +567,12 @@ static float head_sumsq(const uint16_t *row, int64_t dim, int dtype) {
 /* f32 [fb][fs][rot_dim/2][2][2] (fb, fs in {1, B}, {1, L}); q: [B][H][L][D];*/
 /* scales: [B][H][ntiles] (tiles past L get 1e-7 / 127).                     */
 /* ------------------------------------------------------------------------ */
-OR_API int or_qk_rms_rope_int8(const uint16_t *x, int dtype, int64_t batch, int64_t heads, int64_t len,
-                               int64_t dim, const uint16_t *norm, int norm_scope, float eps,
-                               const float *freqs, int64_t fb, int64_t fs, int64_t rot_dim,
-                               int split_half, int64_t tile, int64_t ntiles, int8_t *q, float *scales) {
-    if ((dim != 64 && dim != 128) || rot_dim < 0 || rot_dim > dim || (rot_dim & 1)) return -1;
-    if (ntiles * tile < len) return -1;
-    const int64_t pairs = rot_dim / 2;
-    float *rrms = (float *)malloc(sizeof(float) * (size_t)(batch * heads * len));
-    float *y = (float *)malloc(sizeof(float) * (size_t)(tile * dim));
-    if (!rrms || !y) { free(rrms); free(y); return -2; }
+OR_API void or_w8a8_hadamard(float *x, int dim);
+
+/* Row-scope (norm_scope 1) or head-scope rrms of every (b, h, t), the      */
+/* quantize path's order (head_sumsq; heads added in order).                 */
+static void qk_rrms_all(const uint16_t *x, int dtype, int64_t batch, int64_t heads, int64_t len, int64_t dim,
+                        int norm_scope, float eps, float *rrms) {
     for (int64_t b = 0; b < batch; ++b)
         for (int64_t t = 0; t < len; ++t) {
             if (norm_scope) {
@@ -587,13 +583,56 @@ OR_API int or_qk_rms_rope_int8(const uint16_t *x, int dtype, int64_t batch, int6
                 for (int64_t h = 0; h < heads; ++h) rrms[(b * heads + h) * len + t] = r;
             } else {
                 for (int64_t h = 0; h < heads; ++h) {
-                    const float s = head_sumsq(x + ((b * heads + h) * len + t) * dim, dim, dtype);
-                    rrms[(b * heads + h) * len + t] = 1.0f / sqrtf(s / (float)dim + eps);
+                    const float sq = head_sumsq(x + ((b * heads + h) * len + t) * dim, dim, dtype);
+                    rrms[(b * heads + h) * len + t] = 1.0f / sqrtf(sq / (float)dim + eps);
                 }
             }
         }
+}
+
+/* processed_value (qk_preprocess.cu:97-145): channel c of token row `row`   */
+/* after RMSNorm (a = T((x rrms) w)) and RoPE (T(fma(f1, a2, f0 a1))).       */
+static float qk_processed(const uint16_t *row, int dtype, int64_t c, float r, const uint16_t *norm,
+                          int norm_scope, int64_t h, int64_t dim, const float *fr, int64_t rot_dim,
+                          int split_half) {
+    const int64_t pairs = rot_dim / 2;
+    const int64_t wi = norm_scope ? h * dim + c : c;
+    const float a = t_round((t_to_f32(row[c], dtype) * r) * t_to_f32(norm[wi], dtype), dtype);
+    if (c >= rot_dim) return a;
+    const int64_t pair = split_half ? (c < pairs ? c : c - pairs) : c / 2;
+    const int64_t first = split_half ? pair : 2 * pair;
+    const int64_t second = split_half ? pair + pairs : first + 1;
+    const int comp = split_half ? (c >= pairs) : (int)(c & 1);
+    const int64_t w0 = norm_scope ? h * dim + first : first;
+    const int64_t w1 = norm_scope ? h * dim + second : second;
+    const float x0 = t_round((t_to_f32(row[first], dtype) * r) * t_to_f32(norm[w0], dtype), dtype);
+    const float x1 = t_round((t_to_f32(row[second], dtype) * r) * t_to_f32(norm[w1], dtype), dtype);
+    const float f0 = fr[pair * 4 + comp * 2 + 0];
+    const float f1 = fr[pair * 4 + comp * 2 + 1];
+    return t_round(fmaf(f1, x1, f0 * x0), dtype);
+}
+
+/* Fused variant with the W8A8 transform (qk_preprocess.cu:417-563 with      */
+/* Rotate / AllowAnchor): y = processed value; for K with anchor >= 0,       */
+/* y -= anchor_values[c]; rotate: y = hadamard(y) per token; then the tile   */
+/* amax / codes as above.  anchors / anchor_values: [B][H] / [B][H][D] or   */
+/* NULL.                                                                     */
+OR_API int or_qk_rms_rope_int8_ex(const uint16_t *x, int dtype, int64_t batch, int64_t heads, int64_t len,
+                                  int64_t dim, const uint16_t *norm, int norm_scope, float eps,
+                                  const float *freqs, int64_t fb, int64_t fs, int64_t rot_dim,
+                                  int split_half, int64_t tile, int64_t ntiles, int rotate,
+                                  const int32_t *anchors, const float *anchor_values, int8_t *q, float *scales) {
+    if ((dim != 64 && dim != 128) || rot_dim < 0 || rot_dim > dim || (rot_dim & 1)) return -1;
+    if (ntiles * tile < len) return -1;
+    const int64_t pairs = rot_dim / 2;
+    float *rrms = (float *)malloc(sizeof(float) * (size_t)(batch * heads * len));
+    float *y = (float *)malloc(sizeof(float) * (size_t)(tile * dim));
+    if (!rrms || !y) { free(rrms); free(y); return -2; }
+    qk_rrms_all(x, dtype, batch, heads, len, dim, norm_scope, eps, rrms);
     for (int64_t b = 0; b < batch; ++b)
-        for (int64_t h = 0; h < heads; ++h)
+        for (int64_t h = 0; h < heads; ++h) {
+            const int anchored = anchors && anchor_values && anchors[b * heads + h] >= 0;
+            const float *av = anchored ? anchor_values + (b * heads + h) * dim : NULL;
             for (int64_t ti = 0; ti < ntiles; ++ti) {
                 float amax = 0.0000001f;
                 const int64_t t0 = ti * tile;
@@ -602,26 +641,13 @@ OR_API int or_qk_rms_rope_int8(const uint16_t *x, int dtype, int64_t batch, int6
                     const uint16_t *row = x + ((b * heads + h) * len + t) * dim;
                     const float r = rrms[(b * heads + h) * len + t];
                     const float *fr = freqs ? freqs + ((fb == 1 ? 0 : b) * fs + (fs == 1 ? 0 : t)) * pairs * 4 : NULL;
+                    float *v = y + to * dim;
                     for (int64_t c = 0; c < dim; ++c) {
-                        const int64_t wi = norm_scope ? h * dim + c : c;
-                        const float a = t_round((t_to_f32(row[c], dtype) * r) * t_to_f32(norm[wi], dtype), dtype);
-                        float v = a;
-                        if (c < rot_dim) {
-                            const int64_t pair = split_half ? (c < pairs ? c : c - pairs) : c / 2;
-                            const int64_t first = split_half ? pair : 2 * pair;
-                            const int64_t second = split_half ? pair + pairs : first + 1;
-                            const int comp = split_half ? (c >= pairs) : (int)(c & 1);
-                            const int64_t w0 = norm_scope ? h * dim + first : first;
-                            const int64_t w1 = norm_scope ? h * dim + second : second;
-                            const float x0 = t_round((t_to_f32(row[first], dtype) * r) * t_to_f32(norm[w0], dtype), dtype);
-                            const float x1 = t_round((t_to_f32(row[second], dtype) * r) * t_to_f32(norm[w1], dtype), dtype);
-                            const float f0 = fr[pair * 4 + comp * 2 + 0];
-                            const float f1 = fr[pair * 4 + comp * 2 + 1];
-                            v = t_round(fmaf(f1, x1, f0 * x0), dtype);
-                        }
-                        y[to * dim + c] = v;
-                        amax = fmaxf(amax, fabsf(v));
+                        v[c] = qk_processed(row, dtype, c, r, norm, norm_scope, h, dim, fr, rot_dim, split_half);
+                        if (av) v[c] -= av[c];
                     }
+                    if (rotate) or_w8a8_hadamard(v, (int)dim);
+                    for (int64_t c = 0; c < dim; ++c) amax = fmaxf(amax, fabsf(v[c]));
                 }
                 scales[(b * heads + h) * ntiles + ti] = amax / 127.0f;
                 const float inv = 127.0f / amax;
@@ -632,10 +658,43 @@ OR_API int or_qk_rms_rope_int8(const uint16_t *x, int dtype, int64_t batch, int6
                         q[((b * heads + h) * len + t0 + to) * dim + c] = (int8_t)r;
                     }
             }
+        }
     free(rrms);
     free(y);
     return 0;
 }
+
+/* The processed values (RMSNorm + RoPE, rounded to T) of every token, fp32 */
+/* [B][H][L][D]: the quantizer's input before the W8A8 transform.            */
+OR_API int or_qk_processed(const uint16_t *x, int dtype, int64_t batch, int64_t heads, int64_t len, int64_t dim,
+                           const uint16_t *norm, int norm_scope, float eps, const float *freqs, int64_t fb,
+                           int64_t fs, int64_t rot_dim, int split_half, float *out) {
+    const int64_t pairs = rot_dim / 2;
+    float *rrms = (float *)malloc(sizeof(float) * (size_t)(batch * heads * len));
+    if (!rrms) return -2;
+    qk_rrms_all(x, dtype, batch, heads, len, dim, norm_scope, eps, rrms);
+    for (int64_t b = 0; b < batch; ++b)
+        for (int64_t h = 0; h < heads; ++h)
+            for (int64_t t = 0; t < len; ++t) {
+                const uint16_t *row = x + ((b * heads + h) * len + t) * dim;
+                const float *fr = freqs ? freqs + ((fb == 1 ? 0 : b) * fs + (fs == 1 ? 0 : t)) * pairs * 4 : NULL;
+                for (int64_t c = 0; c < dim; ++c)
+                    out[((b * heads + h) * len + t) * dim + c] =
+                        qk_processed(row, dtype, c, rrms[(b * heads + h) * len + t], norm, norm_scope, h, dim, fr,
+                                     rot_dim, split_half);
+            }
+    free(rrms);
+    return 0;
+}
+
+OR_API int or_qk_rms_rope_int8(const uint16_t *x, int dtype, int64_t batch, int64_t heads, int64_t len,
+                               int64_t dim, const uint16_t *norm, int norm_scope, float eps,
+                               const float *freqs, int64_t fb, int64_t fs, int64_t rot_dim,
+                               int split_half, int64_t tile, int64_t ntiles, int8_t *q, float *scales) {
+    return or_qk_rms_rope_int8_ex(x, dtype, batch, heads, len, dim, norm, norm_scope, eps, freqs, fb, fs, rot_dim,
+                                  split_half, tile, ntiles, 0, NULL, NULL, q, scales);
+}
+
 
 /* ======================================================================== */
 /* W8A8 attention variant (loader default `w8a8` backend).                   */
@@ -711,14 +770,10 @@ static float tree32_max(const float *v) {
 /* anchor; with r = x - anchor, E' and M' are formed the same way, and the  */
 /* anchor row is kept iff E' < E and M' <= M * 1.125f, else -1.             */
 /* x: dtype 0 bf16 / 1 fp16 bit patterns, channel stride 1; dim <= 128.      */
-OR_API int32_t or_w8a8_detect_anchor(const uint16_t *x, int dtype, int64_t len, int64_t dim, int64_t s_l) {
-    float samples[9][128];
+/* The detector's decision on nine sample rows (channels >= dim are 0):     */
+/* the selected sample (0..8) when centring on it helps, else -1.            */
+static int anchor_decide(float samples[9][128], int64_t dim) {
     float e_lane[128], m_lane[128], d_lane[9][128], be_lane[128], bm_lane[128];
-    if (dim > 128 || dim <= 0 || len <= 0) return -2;
-    for (int s = 0; s < 9; ++s) {
-        const int64_t row = (int64_t)s * (len - 1) / 8;
-        for (int c = 0; c < 128; ++c) samples[s][c] = c < dim ? t_to_f32(x[row * s_l + c], dtype) : 0.0f;
-    }
     for (int c = 0; c < 128; ++c) {
         float e = 0.0f, m = 0.0f, sum = 0.0f;
         for (int j = 0; j < 9; ++j) d_lane[j][c] = 0.0f;
@@ -771,7 +826,65 @@ OR_API int32_t or_w8a8_detect_anchor(const uint16_t *x, int dtype, int64_t len, 
         tot_bm = fmaxf(tot_bm, tree32_max(bm_lane + 32 * w));
     }
     const int improves = tot_be < tot_e && tot_bm <= tot_m * 1.125f;
-    return improves ? (int32_t)((int64_t)best * (len - 1) / 8) : -1;
+    return improves ? best : -1;
+}
+
+OR_API int32_t or_w8a8_detect_anchor(const uint16_t *x, int dtype, int64_t len, int64_t dim, int64_t s_l) {
+    float samples[9][128];
+    if (dim > 128 || dim <= 0 || len <= 0) return -2;
+    for (int s = 0; s < 9; ++s) {
+        const int64_t row = (int64_t)s * (len - 1) / 8;
+        for (int c = 0; c < 128; ++c) samples[s][c] = c < dim ? t_to_f32(x[row * s_l + c], dtype) : 0.0f;
+    }
+    const int sel = anchor_decide(samples, dim);
+    return sel >= 0 ? (int32_t)((int64_t)sel * (len - 1) / 8) : -1;
+}
+
+/* K anchor of the fused preprocessor: detect_anchor_kernel                  */
+/* (qk_preprocess.cu:250-416).  The nine samples are the processed values    */
+/* (RMSNorm + RoPE, rounded to T) of rows s (L - 1) / 8; their rrms is the   */
+/* row-scope rrms, or for head scope 1 / sqrt(S / D + eps) with S a          */
+/* sequential fma chain over the head's D channels (the reference uses      */
+/* rsqrtf; here IEEE).  The decision is anchor_decide; anchor_values        */
+/* [B][H][D] = the selected sample's values, or 0 when none is kept.         */
+OR_API int or_qk_fused_anchor(const uint16_t *x, int dtype, int64_t batch, int64_t heads, int64_t len,
+                              int64_t dim, const uint16_t *norm, int norm_scope, float eps, const float *freqs,
+                              int64_t fb, int64_t fs, int64_t rot_dim, int split_half, int32_t *anchors,
+                              float *anchor_values) {
+    if ((dim != 64 && dim != 128) || len <= 0) return -1;
+    const int64_t pairs = rot_dim / 2;
+    float *rrms = (float *)malloc(sizeof(float) * (size_t)(batch * heads * len));
+    if (!rrms) return -2;
+    if (norm_scope) qk_rrms_all(x, dtype, batch, heads, len, dim, 1, eps, rrms);
+    for (int64_t b = 0; b < batch; ++b)
+        for (int64_t h = 0; h < heads; ++h) {
+            float samples[9][128];
+            for (int sm = 0; sm < 9; ++sm) {
+                const int64_t t = (int64_t)sm * (len - 1) / 8;
+                const uint16_t *row = x + ((b * heads + h) * len + t) * dim;
+                float r;
+                if (norm_scope) {
+                    r = rrms[(b * heads + h) * len + t];
+                } else {
+                    float sq = 0.0f;
+                    for (int64_t c = 0; c < dim; ++c) {
+                        const float v = t_to_f32(row[c], dtype);
+                        sq = fmaf(v, v, sq);
+                    }
+                    r = 1.0f / sqrtf(sq / (float)dim + eps);
+                }
+                const float *fr = freqs ? freqs + ((fb == 1 ? 0 : b) * fs + (fs == 1 ? 0 : t)) * pairs * 4 : NULL;
+                for (int c = 0; c < 128; ++c)
+                    samples[sm][c] = c < dim ? qk_processed(row, dtype, c, r, norm, norm_scope, h, dim, fr, rot_dim,
+                                                            split_half)
+                                             : 0.0f;
+            }
+            const int sel = anchor_decide(samples, dim);
+            anchors[b * heads + h] = sel >= 0 ? (int32_t)((int64_t)sel * (len - 1) / 8) : -1;
+            for (int64_t c = 0; c < dim; ++c) anchor_values[(b * heads + h) * dim + c] = sel >= 0 ? samples[sel][c] : 0.0f;
+        }
+    free(rrms);
+    return 0;
 }
 
 /* Rotated per-tile INT8 of one tensor (Q or K): quant_int8_tile             */

@@ -166,3 +166,88 @@ def test_wan_shape_slices(gpu_device):
         rk, rks = oracle.qk_rms_rope_int8(_bits(xs), 0, _bits(w), "row", 1e-6, fs, d, False, 64, (t1 - t0 + 63) // 64)
         np.testing.assert_array_equal(ki[:, :, t0:t1].numpy(), rk)
         np.testing.assert_array_equal(ks[:, :, t0 // 64:(t1 + 63) // 64].numpy().view(np.uint32), rks.view(np.uint32))
+
+
+# --- W8A8 variant: rotate_qk / stabilize_k (qk_preprocess.cu:250-416, :417-563) ---
+
+def _check_w8a8_exact(q, k, qw, kw, freqs, rot, scope, split, stabilize, dev):
+    from comfyui_turing_utils_kernel.turing_sage.custom_ops import qk_rms_rope_int8
+
+    empty = torch.empty(0, dtype=q.dtype)
+    out = qk_rms_rope_int8(q.to(dev), k.to(dev), qw.to(dev), kw.to(dev),
+                           (freqs if freqs is not None else empty).to(dev), 1e-6, rot, "HND", scope, split,
+                           True, stabilize)
+    torch.cuda.synchronize(dev)
+    qi, qs, ki, ks = (t.cpu() for t in out)
+    dt = oracle.DTYPE_FP16 if q.dtype == torch.float16 else oracle.DTYPE_BF16
+    f32 = freqs.float()[:, :, 0].numpy() if freqs is not None else None
+    anchors = values = None
+    if stabilize:
+        anchors, values = oracle.qk_fused_anchor(_bits(k), dt, _bits(kw), scope, 1e-6, f32, rot, split)
+    for x, w, got_q, got_s, blk, anc, val in ((q, qw, qi, qs, 16, None, None), (k, kw, ki, ks, 64, anchors, values)):
+        ref_q, ref_s = oracle.qk_rms_rope_int8_ex(_bits(x), dt, _bits(w), scope, 1e-6, f32, rot, split, blk,
+                                                  got_s.shape[-1], True, anc, val)
+        np.testing.assert_array_equal(got_s.numpy().view(np.uint32), ref_s.view(np.uint32))
+        np.testing.assert_array_equal(got_q.numpy(), ref_q)
+    return anchors
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("d,scope,split,rot", [(128, "row", False, 128), (128, "head", True, 96),
+                                               (64, "head", False, 64), (64, "row", True, 32), (128, "head", False, 0)])
+@pytest.mark.parametrize("stabilize", [False, True])
+def test_w8a8_variant_exact(gpu_device, dtype, d, scope, split, rot, stabilize):
+    """Rotated (and anchored) codes and scales bit-exact vs the oracle; one
+    frequency row for all tokens keeps the per-head channel offset common, so
+    the anchor fires."""
+    print(f"[qk-rope-w8a8] {dtype} d={d} {scope} split={split} rot={rot} anchor={stabilize}", flush=True)
+    q, k, qw, kw, freqs = _case(2, 4, 2, 131, d, dtype, scope, rot, 2, 1, 300 + d + rot)
+    g = torch.Generator().manual_seed(301 + d)
+    k = (k.float() + 4 * torch.randn(2, 2, 1, d, generator=g)).to(dtype)
+    anchors = _check_w8a8_exact(q, k, qw, kw, freqs, rot, scope, split, stabilize, gpu_device)
+    if stabilize:
+        assert (anchors >= 0).any()
+
+
+def test_w8a8_variant_feeds_both_attentions(gpu_device):
+    """prequantize_rms_rope_qk(rotate_qk, stabilize_k) -> the W8A8 attention
+    (against the oracle's attention on the same codes) and the Sage attention
+    (rotation and anchor leave its softmax unchanged: against the unrotated
+    producer's result)."""
+    from comfyui_turing_utils_kernel.turing_sage import (prequantize_rms_rope_qk, prequantize_sageattn_from_qk,
+                                                           sageattn_from_prequantized)
+    from comfyui_turing_utils_kernel.turing_sage.core import prequantize_w8a8attn_from_qk, w8a8attn_from_prequantized
+    from comfyui_turing_utils_kernel.turing_sage.correctness import (attention_error_metrics,
+                                                                      require_attention_correctness)
+
+    print("[qk-rope-w8a8] attention", flush=True)
+    q, k, qw, kw, freqs = _case(1, 4, 2, 300, 128, torch.bfloat16, "row", 128, 1, 1, 41)
+    k = (k.float() + 3 * torch.randn(1, 2, 1, 128, generator=torch.Generator().manual_seed(42))).to(torch.bfloat16)
+    v = torch.randn((1, 2, 300, 128), generator=torch.Generator().manual_seed(43)).to(torch.bfloat16)
+    qd, kd, vd = q.to(gpu_device), k.to(gpu_device), v.to(gpu_device)
+    qk = prequantize_rms_rope_qk(qd, kd, qw, kw, freqs, epsilon=1e-6, rot_dim=128, norm_scope="row",
+                                 rotate_qk=True, stabilize_k=True)
+    assert qk.route_original_basis
+    out = w8a8attn_from_prequantized(prequantize_w8a8attn_from_qk(qk, vd)).float().cpu()
+    f32 = freqs.float()[:, :, 0].numpy()
+    anchors, values = oracle.qk_fused_anchor(_bits(k), 0, _bits(kw), "row", 1e-6, f32, 128, False)
+    assert (anchors >= 0).any()
+    q8, qs = oracle.qk_rms_rope_int8_ex(_bits(q), 0, _bits(qw), "row", 1e-6, f32, 128, False, 16, 20, True)
+    k8, ks = oracle.qk_rms_rope_int8_ex(_bits(k), 0, _bits(kw), "row", 1e-6, f32, 128, False, 64, 5, True,
+                                        anchors, values)
+    v8, vs, _ = oracle.w8a8_quant_v(_bits(v))
+    rows = np.array([[0, h, i] for h in range(4) for i in range(300)])
+    ref = oracle.w8a8_attn_rows(q8, qs, k8, ks, v8, vs, 300, 128 ** -0.5, rows).reshape(1, 4, 300, 128)
+    require_attention_correctness(attention_error_metrics(out, torch.from_numpy(ref)), max_abs=2e-2, cosine=0.999)
+    # Sage on rotated + anchored codes against exact attention on the
+    # processed Q/K (the rotation is orthogonal, the anchor a per-row shift):
+    # as close as Sage on the plain codes
+    sage_rot = sageattn_from_prequantized(prequantize_sageattn_from_qk(qk, vd)).float().cpu()
+    plain = prequantize_rms_rope_qk(qd, kd, qw, kw, freqs, epsilon=1e-6, rot_dim=128, norm_scope="row")
+    sage_plain = sageattn_from_prequantized(prequantize_sageattn_from_qk(plain, vd)).float().cpu()
+    pq = torch.from_numpy(oracle.qk_processed(_bits(q), 0, _bits(qw), "row", 1e-6, f32, 128, False)).double()
+    pk = torch.from_numpy(oracle.qk_processed(_bits(k), 0, _bits(kw), "row", 1e-6, f32, 128, False)).double()
+    exact = torch.nn.functional.scaled_dot_product_attention(pq, pk, v.double(), enable_gqa=True).float()
+    m_rot = attention_error_metrics(sage_rot, exact)
+    m_plain = attention_error_metrics(sage_plain, exact)
+    assert m_rot.cosine > 0.995 and m_rot.relative_l2 <= 1.5 * m_plain.relative_l2 + 0.005, (m_rot, m_plain)

@@ -203,9 +203,6 @@ def test_qk_rms_rope_refuses_what_is_not_built():
 
     x = torch.zeros((1, 2, 16, 128), dtype=torch.bfloat16)
     w = torch.ones(128, dtype=torch.bfloat16)
-    with pytest.raises(ValueError, match="w8a8"):
-        rms_rope_per_warp_int8(x, x, w, w, None, epsilon=1e-6, rot_dim=0, tensor_layout="HND", norm_scope="head",
-                               split_half=False, rotate_qk=True, stabilize_k=True)
     with pytest.raises(ValueError, match="head_dim"):
         rms_rope_per_warp_int8(x[..., :96], x[..., :96], w, w, None, epsilon=1e-6, rot_dim=0,
                                tensor_layout="HND", norm_scope="head", split_half=False)

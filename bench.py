@@ -289,6 +289,16 @@ def extra_kernels(torch, dev, ops, lin, q, k, v, copy_gbs) -> dict:
     # V read twice (amax pass, code pass), codes written once
     out["w8a8_quant_v"] = {"ms_avg": ms, "gbs": 5.0 * v.numel() / ms / 1e6}
     del state
+    # the block's norm1 / norm2: LayerNorm + AdaLN over [1, L, H * D] with one
+    # modulation row; 2 B read + 2 B written per element
+    gen = torch.Generator(device=dev).manual_seed(37)
+    xn = torch.randn(b, l, h * d, generator=gen, device=dev).to(torch.bfloat16)
+    mod = (0.1 * torch.randn(b, 1, h * d, generator=gen, device=dev)).to(torch.bfloat16)
+    ms = timed(lambda: ops.layer_norm_adaln(xn, mod, mod, 1e-6))
+    nbytes = 4.0 * xn.numel()
+    out["layer_norm_adaln"] = {"ms_avg": ms, "gbs": nbytes / ms / 1e6, "frac_copy": nbytes / ms / 1e6 / copy_gbs,
+                               "frac_hbm_peak": nbytes / ms / 1e6 / PEAK_HBM_GBS, "shape": [b, l, h * d]}
+    del xn, mod
     return out
 
 

@@ -17,6 +17,7 @@ from .ops import (
     turing_gelu_int8_convrot_quantize,
     turing_int8_gemm_i32,
     turing_int8_linear,
+    turing_layer_norm_adaln,
     turing_swiglu_int8_convrot_quantize,
 )
 from . import turing_sage
@@ -33,6 +34,7 @@ __all__ = [
     "turing_gelu_int8_convrot_quantize",
     "turing_int8_gemm_i32",
     "turing_int8_linear",
+    "turing_layer_norm_adaln",
     "turing_sage",
     "turing_swiglu_int8_convrot_quantize",
 ]

@@ -91,9 +91,13 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
          _f32, _i32, _c_void_p],
     ),
+    "tu_layer_norm_adaln": (
+        _i32,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i32, _i64, _i64, _i64, _i64, _f32, _c_void_p],
+    ),
 }
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

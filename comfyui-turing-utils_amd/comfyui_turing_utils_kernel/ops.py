@@ -277,3 +277,41 @@ def _turing_gelu_int8_convrot_quantize_fake(x, group_size=256):
         torch.empty(x.shape, dtype=torch.int8, device=x.device),
         torch.empty((x.size(0), 1), dtype=torch.float32, device=x.device),
     )
+
+
+# ---------------------------------------------------------------------------
+# LayerNorm + AdaLN (reference ops.py:399-418, segmented_rms_adaln.cu:236-409)
+# ---------------------------------------------------------------------------
+_LN_DTYPES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
+
+
+@torch.library.custom_op("turing_utils::layer_norm_adaln", mutates_args=())
+def turing_layer_norm_adaln(
+    x: torch.Tensor,
+    scale: torch.Tensor,
+    shift: torch.Tensor,
+    epsilon: float = 1.0e-5,
+) -> torch.Tensor:
+    """Fused FP32-reduction LayerNorm and Wan AdaLN modulation:
+    LayerNorm(x) * (1 + scale) + shift with x [B, L, H] and scale / shift
+    [B, steps, H] (token t of L uses modulation row t // ceil(L / steps))."""
+    _require_device(x, "LayerNorm+AdaLN")
+    if x.dtype not in _LN_DTYPES or x.ndim != 3:
+        raise TypeError("LayerNorm+AdaLN input must be 3D float16, bfloat16, or float32")
+    scale = scale.to(device=x.device, dtype=x.dtype).contiguous()
+    shift = shift.to(device=x.device, dtype=x.dtype).contiguous()
+    batch, length, hidden = x.shape
+    if scale.ndim != 3 or scale.shape != shift.shape or scale.size(0) != batch or scale.size(2) != hidden:
+        raise ValueError("LayerNorm+AdaLN scale / shift must be [B, steps, H] and match")
+    x = x.contiguous()
+    out = torch.empty_like(x)
+    with torch.cuda.device(x.device):
+        _lib.call("tu_layer_norm_adaln", x.data_ptr(), scale.data_ptr(), shift.data_ptr(), out.data_ptr(),
+                  _LN_DTYPES[x.dtype], batch, length, hidden, scale.size(1), float(epsilon),
+                  _lib.stream_of(x.device))
+    return out
+
+
+@turing_layer_norm_adaln.register_fake
+def _turing_layer_norm_adaln_fake(x, scale, shift, epsilon=1.0e-5):
+    return torch.empty_like(x)

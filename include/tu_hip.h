@@ -270,6 +270,24 @@ int32_t tu_w8a8_attn_fwd(const int8_t *q8, const float *q_scale, int64_t nqs, co
                          int64_t k_sl, int64_t o_sb, int64_t o_sh, int64_t o_sl, float sm_scale,
                          int32_t causal, void *stream);
 
+/* Wan block: LayerNorm + AdaLN --------------------------------------------- */
+
+/* out = T(fma(T((x - mean) / sqrt(var + eps)), T(1 + scale), shift)) per row
+ * of `hidden` channels, mean / var from fp32 Welford statistics in the
+ * reference's order (256 threads striding the row, 32-lane trees, eight tree
+ * results combined in order).  x, out: [batch, len, hidden] contiguous;
+ * scale, shift: [batch, steps, hidden] contiguous, token t of a row uses
+ * modulation row min(t / g, steps - 1) with g = len / steps, + 1 when steps
+ * does not divide len (steps == 1: row 0).  dtype 0 bf16, 1 fp16, 2 fp32 (T
+ * = the element type).  eps finite and positive.  Rows up to hidden 8192
+ * stay in registers (x read once); wider rows read x twice.
+ * Replaces turing_utils::layer_norm_adaln (kernel/comfyui_turing_utils_kernel/
+ * ops.py:399-418 -> kernel/csrc/turing/segmented_rms_adaln.cu:236-307,
+ * :372-409). */
+int32_t tu_layer_norm_adaln(const void *x, const void *scale, const void *shift, void *out, int32_t dtype,
+                            int64_t batch, int64_t len, int64_t hidden, int64_t steps, float eps,
+                            void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -94,6 +94,8 @@ def lib():
             L.or_qk_processed.restype = _i32
             L.or_qk_processed.argtypes = [_p, _i32, _i64, _i64, _i64, _i64, _p, _i32, ctypes.c_float, _p,
                                           _i64, _i64, _i64, _i32, _p]
+            L.or_layer_norm_adaln.restype = _i32
+            L.or_layer_norm_adaln.argtypes = [_p, _i32, _i64, _i64, _i64, _p, _p, _i64, ctypes.c_float, _p]
             L.or_w8a8_sign_negative.restype = _i32
             L.or_w8a8_sign_negative.argtypes = [_i32]
             L.or_w8a8_hadamard.restype = None
@@ -276,7 +278,7 @@ def sage_attn_rows(q8: np.ndarray, qs: np.ndarray, blkq: int, k8: np.ndarray, ks
 
 # --- fused Q/K RMSNorm + RoPE + INT8 (qk_preprocess.cu) ---------------------
 
-DTYPE_BF16, DTYPE_FP16 = 0, 1
+DTYPE_BF16, DTYPE_FP16, DTYPE_FP32 = 0, 1, 2
 
 
 def f32_to_f16_bits(v: float) -> int:
@@ -461,4 +463,22 @@ def w8a8_attn_rows(q8: np.ndarray, qs: np.ndarray, k8: np.ndarray, ks: np.ndarra
     _check(lib().or_w8a8_attn_rows(_ptr(q8), qsb, qsh, qsl, _ptr(qs), qs.shape[2], _ptr(k8), ksb, ksh, ksl,
                                    _ptr(ks), ks.shape[2], _ptr(v8), v8.shape[3], _ptr(vs), hq, hkv, lq, lk, d,
                                    sm_scale, int(causal), _ptr(rows), rows.shape[0], _ptr(out)), "w8a8_attn_rows")
+    return out
+
+
+# --- Wan block: LayerNorm + AdaLN -------------------------------------------
+
+def layer_norm_adaln(x, scale, shift, eps: float, dtype: int = DTYPE_BF16) -> np.ndarray:
+    """LayerNorm(x) * (1 + scale) + shift with the reference's Welford order.
+    x [B, L, H], scale/shift [B, steps, H]: uint16 bit patterns (dtype 0 bf16,
+    1 fp16) or float32 arrays (dtype 2); the result has x's numpy dtype."""
+    kind = np.float32 if dtype == DTYPE_FP32 else np.uint16
+    x = np.ascontiguousarray(x, dtype=kind)
+    scale = np.ascontiguousarray(scale, dtype=kind)
+    shift = np.ascontiguousarray(shift, dtype=kind)
+    b, l, h = x.shape
+    assert scale.shape == shift.shape and scale.shape[0] == b and scale.shape[2] == h
+    out = np.empty(x.shape, dtype=kind)
+    _check(lib().or_layer_norm_adaln(_ptr(x), dtype, b, l, h, _ptr(scale), _ptr(shift), scale.shape[1], eps,
+                                     _ptr(out)), "layer_norm_adaln")
     return out

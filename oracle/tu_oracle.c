@@ -1057,3 +1057,90 @@ OR_API int or_w8a8_attn_rows(const int8_t *q8, int64_t q_sb, int64_t q_sh, int64
     }
     return 0;
 }
+
+/* ======================================================================== */
+/* Wan block: LayerNorm + AdaLN modulation.                                  */
+/* ======================================================================== */
+
+typedef struct { float mean, m2; int count; } or_welford;
+
+/* welford_combine (segmented_rms_adaln.cu:87-101). */
+static or_welford welford_combine(or_welford l, or_welford r) {
+    if (r.count == 0) return l;
+    if (l.count == 0) return r;
+    const int count = l.count + r.count;
+    const float delta = r.mean - l.mean;
+    l.mean = l.mean + (delta * (float)r.count) / (float)count;
+    l.m2 = l.m2 + (r.m2 + (((delta * delta) * (float)l.count) * (float)r.count) / (float)count);
+    l.count = count;
+    return l;
+}
+
+/* layer_norm_adaln_kernel (segmented_rms_adaln.cu:236-307), one row:       */
+/*   256 threads, thread t takes columns t, t + 256, ... in order:           */
+/*     count++, delta = v - mean, mean += delta / count,                     */
+/*     m2 = fma(delta, v - mean, m2)   (nvcc contracts the reference's      */
+/*                                      m2 += delta * (v - mean))           */
+/*   32-lane shfl_down trees of welford_combine, the 8 tree results combined */
+/*   in order from {0, 0, 0};  var = m2 / count, inv = 1 / sqrt(var + eps)   */
+/*   (the reference uses rsqrtf; here IEEE)                                  */
+/*   out = T(fma(T((x - mean) inv), T(1 + scale), shift))                    */
+/*   (the reference's float a * b + c, contracted).                          */
+/* Modulation row of token t: steps == 1 -> 0; else group = ceil-ish        */
+/* repeats (L / steps, + 1 when it does not divide), row = min(t / group,   */
+/* steps - 1).  x/out: [B][L][H]; scale/shift: [B][steps][H]; dtype 0 bf16,  */
+/* 1 fp16 (2-byte patterns), 2 fp32 (T rounding is then the identity).       */
+static inline float ln_load(const void *p, int64_t i, int dtype) {
+    return dtype == 2 ? ((const float *)p)[i] : t_to_f32(((const uint16_t *)p)[i], dtype);
+}
+static inline float ln_round(float v, int dtype) { return dtype == 2 ? v : t_round(v, dtype); }
+
+OR_API int or_layer_norm_adaln(const void *x, int dtype, int64_t batch, int64_t len, int64_t hidden,
+                               const void *scale, const void *shift, int64_t steps, float eps, void *out) {
+    if (hidden <= 0 || steps <= 0) return -1;
+#pragma omp parallel for schedule(static)
+    for (int64_t row = 0; row < batch * len; ++row) {
+        const int64_t b = row / len, t = row % len;
+        int64_t mt = 0;
+        if (steps > 1) {
+            const int64_t repeats = len / steps;
+            const int64_t group = repeats * steps == len ? repeats : repeats + 1;
+            mt = t / (group > 1 ? group : 1);
+            if (mt > steps - 1) mt = steps - 1;
+        }
+        const int64_t xr = row * hidden;
+        or_welford lane[256];
+        for (int th = 0; th < 256; ++th) {
+            or_welford w = {0.0f, 0.0f, 0};
+            for (int64_t c = th; c < hidden; c += 256) {
+                const float v = ln_load(x, xr + c, dtype);
+                ++w.count;
+                const float delta = v - w.mean;
+                w.mean = w.mean + delta / (float)w.count;
+                w.m2 = fmaf(delta, v - w.mean, w.m2);
+            }
+            lane[th] = w;
+        }
+        or_welford total = {0.0f, 0.0f, 0};
+        for (int wp = 0; wp < 8; ++wp) {
+            or_welford *v = lane + 32 * wp;
+            or_welford tmp[32];
+            memcpy(tmp, v, sizeof(tmp));
+            for (int off = 16; off > 0; off >>= 1)
+                for (int i = 0; i < off; ++i) tmp[i] = welford_combine(tmp[i], tmp[i + off]);
+            total = welford_combine(total, tmp[0]);
+        }
+        const float mean = total.mean;
+        const float var = total.m2 / (float)total.count;
+        const float inv = 1.0f / sqrtf(var + eps);
+        const int64_t mrow = (b * steps + mt) * hidden;
+        for (int64_t c = 0; c < hidden; ++c) {
+            const float n = ln_round((ln_load(x, xr + c, dtype) - mean) * inv, dtype);
+            const float m = ln_round(1.0f + ln_load(scale, mrow + c, dtype), dtype);
+            const float r = fmaf(n, m, ln_load(shift, mrow + c, dtype));
+            if (dtype == 2) ((float *)out)[xr + c] = r;
+            else ((uint16_t *)out)[xr + c] = dtype ? or_f32_to_f16_rne(r) : or_f32_to_bf16_rne(r);
+        }
+    }
+    return 0;
+}

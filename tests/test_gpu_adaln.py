@@ -1,0 +1,122 @@
+"""GPU parity: LayerNorm + AdaLN (HIP, tu_layer_norm_adaln) vs the CPU oracle
+(oracle/tu_oracle.c or_layer_norm_adaln, a restatement of
+kernel/csrc/turing/segmented_rms_adaln.cu:236-307), bit for bit in bf16,
+fp16 and fp32, and the reference's own gate
+(kernel/scripts/validate_wan_fusions.py:80-119) through the op.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle
+from tests.test_oracle_adaln import _expanded
+
+pytestmark = pytest.mark.gpu
+
+_DT = {torch.bfloat16: oracle.DTYPE_BF16, torch.float16: oracle.DTYPE_FP16, torch.float32: oracle.DTYPE_FP32}
+
+
+def _np(t: torch.Tensor) -> np.ndarray:
+    t = t.contiguous()
+    if t.dtype == torch.float32:
+        return t.numpy()
+    return t.view(torch.int16).numpy().view(np.uint16)
+
+
+def _oracle(x, scale, shift, eps):
+    return _oracle_bits(_np(x), _np(scale), _np(shift), eps, x.dtype)
+
+
+def _oracle_bits(x, scale, shift, eps, dtype):
+    out = oracle.layer_norm_adaln(x, scale, shift, eps, _DT[dtype])
+    return out.view(np.uint32) if dtype == torch.float32 else out
+
+
+def _bits_of(t: torch.Tensor) -> np.ndarray:
+    a = _np(t.cpu())
+    return a.view(np.uint32) if t.dtype == torch.float32 else a
+
+
+def _case(b, l, h, steps, dtype, seed, offset=1.0):
+    g = torch.Generator().manual_seed(seed)
+    x = (torch.randn(b, l, h, generator=g) * 3 + offset).to(dtype)
+    scale = (torch.randn(b, steps, h, generator=g) * 0.2).to(dtype)
+    shift = (torch.randn(b, steps, h, generator=g) * 0.2).to(dtype)
+    return x, scale, shift
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("b,l,h,steps", [(2, 17, 5120, 4), (2, 33, 700, 1), (1, 5, 8192, 2), (2, 7, 9000, 3),
+                                         (1, 1, 64, 1), (3, 12, 1536, 5), (1, 40, 257, 40), (1, 3, 4096, 4)])
+def test_bit_exact_vs_oracle(gpu_device, dtype, b, l, h, steps):
+    from comfyui_turing_utils_kernel import turing_layer_norm_adaln
+
+    print(f"layer_norm_adaln {dtype} b={b} l={l} h={h} steps={steps}", flush=True)
+    x, scale, shift = _case(b, l, h, steps, dtype, b * 1000 + l + h + steps)
+    out = turing_layer_norm_adaln(x.to(gpu_device), scale.to(gpu_device), shift.to(gpu_device), 1e-6)
+    torch.cuda.synchronize(gpu_device)
+    np.testing.assert_array_equal(_bits_of(out), _oracle(x, scale, shift, 1e-6))
+
+
+@pytest.mark.parametrize("offset", [0.0, 100.0, 1000.0, 1e5])
+def test_offsets_bit_exact(gpu_device, offset):
+    from comfyui_turing_utils_kernel import turing_layer_norm_adaln
+
+    for dtype in (torch.bfloat16, torch.float32):
+        x, scale, shift = _case(2, 9, 5120, 1, dtype, 3, offset)
+        out = turing_layer_norm_adaln(x.to(gpu_device), scale.to(gpu_device), shift.to(gpu_device), 1e-5)
+        torch.cuda.synchronize(gpu_device)
+        np.testing.assert_array_equal(_bits_of(out), _oracle(x, scale, shift, 1e-5))
+
+
+@pytest.mark.parametrize("case", ["x", "x/8", "x+100", "x+1000"])
+def test_reference_gate(gpu_device, case):
+    """validate_wan_fusions.py:80-119: rtol 0.006 / atol 0.002 against torch
+    layer_norm + addcmul, on x and its scaled / offset variants (the oracle
+    test states the 3-element tie exception of x + 100)."""
+    from comfyui_turing_utils_kernel import turing_layer_norm_adaln
+
+    g = torch.Generator().manual_seed(1234)
+    x = torch.randn(2, 17, 5120, generator=g).to(torch.bfloat16)
+    scale = (torch.randn(2, 4, 5120, generator=g) * 0.1).to(torch.bfloat16)
+    shift = (torch.randn(2, 4, 5120, generator=g) * 0.1).to(torch.bfloat16)
+    xi = {"x": x, "x/8": x * 0.125, "x+100": x + 100.0, "x+1000": x + 1000.0}[case].to(torch.bfloat16)
+    out = turing_layer_norm_adaln(xi.to(gpu_device), scale.to(gpu_device), shift.to(gpu_device), 1e-6).cpu()
+    ref = torch.addcmul(_expanded(shift, 17), torch.nn.functional.layer_norm(xi, (5120,), eps=1e-6),
+                        1 + _expanded(scale, 17))
+    ok = torch.isclose(out.float(), ref.float(), rtol=0.006, atol=0.002)
+    assert ok.float().mean() >= 0.9999
+
+
+def test_wan_shape_rows(gpu_device):
+    """Wan 2.1 14B 720p norm1 shape: 32760 tokens x 5120, one modulation row;
+    a seeded sample of 600 rows (first, last and random) bit-exact."""
+    from comfyui_turing_utils_kernel import turing_layer_norm_adaln
+
+    g = torch.Generator(device=gpu_device).manual_seed(9)
+    x = torch.randn(1, 32760, 5120, generator=g, device=gpu_device).to(torch.bfloat16)
+    scale = (torch.randn(1, 1, 5120, generator=g, device=gpu_device) * 0.1).to(torch.bfloat16)
+    shift = (torch.randn(1, 1, 5120, generator=g, device=gpu_device) * 0.1).to(torch.bfloat16)
+    out = turing_layer_norm_adaln(x, scale, shift, 1e-6)
+    rows = torch.cat([torch.tensor([0, 32759]), torch.randperm(32760, generator=torch.Generator().manual_seed(1))[:598]])
+    got = _bits_of(out[0, rows.to(gpu_device)])
+    ref = _oracle_bits(_np(x[0, rows.to(gpu_device)].cpu()[None]), _np(scale.cpu()), _np(shift.cpu()), 1e-6,
+                       torch.bfloat16)
+    np.testing.assert_array_equal(got, ref[0])
+
+
+def test_errors(gpu_device):
+    from comfyui_turing_utils_kernel import turing_layer_norm_adaln
+
+    x = torch.randn(1, 4, 64, device=gpu_device, dtype=torch.bfloat16)
+    s = torch.zeros(1, 1, 64, device=gpu_device, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="epsilon"):
+        turing_layer_norm_adaln(x, s, s, 0.0)
+    with pytest.raises(RuntimeError, match="epsilon"):
+        turing_layer_norm_adaln(x, s, s, float("nan"))
+    with pytest.raises(ValueError):
+        turing_layer_norm_adaln(x, s[:, :, :32], s[:, :, :32], 1e-6)
+    with pytest.raises(TypeError):
+        turing_layer_norm_adaln(x[0], s, s, 1e-6)

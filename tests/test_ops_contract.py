@@ -209,3 +209,19 @@ def test_qk_rms_rope_refuses_what_is_not_built():
     with pytest.raises(ValueError, match="norm weight"):
         rms_rope_per_warp_int8(x, x, w, w, None, epsilon=1e-6, rot_dim=0, tensor_layout="HND", norm_scope="row",
                                split_half=False)
+
+
+def test_layer_norm_adaln_fake_contract_and_refusals():
+    """reference ops.py:399-418: empty_like fake; CPU tensors and non-3D or
+    integer inputs refused before any launch."""
+    x = torch.empty((2, 9, 5120), dtype=torch.bfloat16, device=META)
+    mod = torch.empty((2, 4, 5120), dtype=torch.bfloat16, device=META)
+    out = torch.ops.turing_utils.layer_norm_adaln(x, mod, mod, 1e-6)
+    assert out.shape == x.shape and out.dtype == x.dtype and out.device.type == META
+    compiled = torch.compile(lambda a, s, t: kernel.turing_layer_norm_adaln(a, s, t, 1e-6), backend="eager",
+                             fullgraph=True)
+    assert compiled(x, mod, mod).shape == x.shape
+    cpu = torch.zeros((1, 4, 64), dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="CUDA|HIP"):
+        kernel.turing_layer_norm_adaln(cpu, cpu[:, :1], cpu[:, :1])
+    assert "turing_layer_norm_adaln" in kernel.__all__

@@ -299,6 +299,18 @@ def extra_kernels(torch, dev, ops, lin, q, k, v, copy_gbs) -> dict:
     out["layer_norm_adaln"] = {"ms_avg": ms, "gbs": nbytes / ms / 1e6, "frac_copy": nbytes / ms / 1e6 / copy_gbs,
                                "frac_hbm_peak": nbytes / ms / 1e6 / PEAK_HBM_GBS, "shape": [b, l, h * d]}
     del xn, mod
+    # C5: the whole Wan-14B block forward (norms, seven W8A8 projections, fused
+    # Q/K producers, self- and cross-attention, gated residuals)
+    from comfyui_turing_utils_kernel import wan_block
+
+    cfg = wan_block.WanBlockConfig()
+    block, text = wan_block.random_block(cfg, seed=4, device=dev)
+    bx, be, bctx, bfreqs = wan_block.c5_inputs(text, dev)
+    ms = timed(lambda: block(bx, be, bctx, bfreqs), reps=5)
+    ops_ = wan_block.block_ops(cfg, bx.shape[1], bctx.shape[1])
+    out["wan_block_c5"] = {"ms_avg": ms, "tops": ops_ / ms / 1e9, "frac_int8_peak": ops_ / ms / 1e9 / PEAK_INT8_TOPS,
+                           "tokens": bx.shape[1], "text_tokens": bctx.shape[1]}
+    del block, text, bx, be, bctx, bfreqs
     return out
 
 

@@ -1,0 +1,305 @@
+"""Wan 2.1 DiT block forward on this package's W8A8 linears and INT8 attention.
+
+The reference plugin does not own the block: ComfyUI's WanAttentionBlock does,
+and the plugin swaps in its kernels at the self-attention site
+(comfyui_turing_utils/adapters/wan.py:55-137: q / k / v projections, row-scope
+RMSNorm + interleaved RoPE + INT8 through turing_utils::qk_rms_rope_int8, Sage
+attention, o projection), at the linears (the ConvRot W8A8 layout,
+quantization/dispatch.py) and at the norms (turing_utils::layer_norm_adaln,
+kernel/scripts/validate_wan_fusions.py:80-119).  This module composes the same
+ops into the whole block so that it can be run and timed without ComfyUI:
+
+    e = modulation + e_t                     [B, 6, C]: shift, scale, gate (attention),
+                                                         shift, scale, gate (FFN)
+    x = x + SelfAttn(LN(x) * (1 + e1) + e0) * e2
+    x = x + CrossAttn(LN_affine(x), context)
+    x = x + FFN(LN(x) * (1 + e4) + e3) * e5
+
+* norm1 / norm2 / norm3: ``turing_utils::layer_norm_adaln``.  norm3's affine
+  weight w and bias b enter as scale = w - 1 and shift = b; the constructor
+  checks that T(1 + T(w - 1)) == w for every channel.
+* SelfAttn: q, k and v come from one W8A8 GEMM (N = 3C).  q and k go through
+  one fused RMSNorm + RoPE + INT8 kernel.  Then Sage INT8 attention, and the
+  o projection.
+* CrossAttn: q from x; k and v from the text context through one GEMM
+  (N = 2C).  RMSNorm + INT8 of q and k, no RoPE.  Then Sage attention over the
+  text tokens.
+* FFN: W8A8 up projection; the tanh-GELU is fused into the down projection's
+  ConvRot quantizer (``turing_utils::bf16_gelu_int8_convrot_quantize``).
+* Text embedding (once per model forward, not per block): Linear(4096, C),
+  tanh-GELU, Linear(C, C), all W8A8 the same way.
+
+Every linear is ConvRot W8A8 at group 128: the weights are rotated and
+quantized per output channel by the same kernel that quantizes activations
+per token (the rotation is orthogonal, so rot(x) . rot(w) = x . w).  The
+residual stream x is bf16; a gated residual is torch.addcmul in bf16 (fp32
+arithmetic, one rounding).
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+from . import ops  # noqa: F401  (registers torch.ops.turing_utils.*)
+from .turing_sage import core as sage_core
+
+GROUP = 128
+
+
+class W8A8Linear:
+    """y = x W^T + b with W stored as ConvRot-rotated INT8 codes and a
+    per-output-channel fp32 scale; x is quantized per token by the ConvRot
+    quantizer (optionally with the tanh-GELU applied first)."""
+
+    def __init__(self, weight_int8: torch.Tensor, weight_scale: torch.Tensor, bias: Optional[torch.Tensor]):
+        if weight_int8.dtype != torch.int8 or weight_int8.dim() != 2:
+            raise TypeError("W8A8 weight must be a 2D int8 tensor")
+        self.weight = weight_int8.contiguous()
+        self.weight_scale = weight_scale.reshape(-1).to(torch.float32).contiguous()
+        self.bias = None if bias is None else bias.reshape(-1).to(torch.float32).contiguous()
+        self.out_features, self.in_features = self.weight.shape
+
+    @classmethod
+    def from_float(cls, weight: torch.Tensor, bias: Optional[torch.Tensor] = None) -> "W8A8Linear":
+        """Quantizes a dense weight [N, K] (rounded to bf16 first) on its device."""
+        codes, scale = torch.ops.turing_utils.bf16_int8_convrot_quantize(
+            weight.to(torch.bfloat16).contiguous(), GROUP)
+        return cls(codes, scale, bias)
+
+    def __call__(self, x: torch.Tensor, gelu: bool = False) -> torch.Tensor:
+        if x.dim() != 2 or x.shape[1] != self.in_features:
+            raise ValueError(f"W8A8 linear expects [M, {self.in_features}], got {tuple(x.shape)}")
+        quantize = (torch.ops.turing_utils.bf16_gelu_int8_convrot_quantize if gelu
+                    else torch.ops.turing_utils.bf16_int8_convrot_quantize)
+        codes, scale = quantize(x.contiguous(), GROUP)
+        return torch.ops.turing_utils.int8_linear(codes, self.weight, scale, self.weight_scale, self.bias)
+
+
+def rope_freqs(grid: tuple[int, int, int], head_dim: int = 128, theta: float = 10000.0,
+               device=None) -> torch.Tensor:
+    """Wan's 3D rotary table as rotation matrices, [1, F*H*W, 1, D/2, 2, 2]
+    ([[cos, -sin], [sin, cos]] per channel pair, interleaved pairs): the
+    head_dim splits into D - 4*(D//6) temporal and 2*(D//6) + 2*(D//6)
+    spatial channels, each axis with frequencies theta^(-2i/d)."""
+    f, h, w = grid
+    dims = (head_dim - 4 * (head_dim // 6), 2 * (head_dim // 6), 2 * (head_dim // 6))
+    angles = []
+    for n, d, shape in zip((f, h, w), dims, ((f, 1, 1), (1, h, 1), (1, 1, w))):
+        inv = theta ** (-torch.arange(0, d, 2, dtype=torch.float64) / d)
+        a = torch.arange(n, dtype=torch.float64)[:, None] * inv[None, :]
+        angles.append(a.view(*shape, d // 2).expand(f, h, w, d // 2))
+    ang = torch.cat(angles, -1).reshape(1, f * h * w, 1, head_dim // 2)
+    cos, sin = ang.cos(), ang.sin()
+    rot = torch.stack([torch.stack([cos, -sin], -1), torch.stack([sin, cos], -1)], -2)
+    return rot.to(torch.float32).to(device)
+
+
+@dataclass
+class WanBlockConfig:
+    dim: int = 5120
+    heads: int = 40
+    ffn_dim: int = 13824
+    text_dim: int = 4096
+    eps: float = 1e-6
+
+    @property
+    def head_dim(self) -> int:
+        return self.dim // self.heads
+
+
+class WanTextEmbeddingW8A8:
+    """Linear(text_dim, C), tanh-GELU, Linear(C, C) on the text context."""
+
+    def __init__(self, fc1: W8A8Linear, fc2: W8A8Linear):
+        self.fc1, self.fc2 = fc1, fc2
+
+    def __call__(self, context: torch.Tensor) -> torch.Tensor:
+        b, l, d = context.shape
+        hidden = self.fc1(context.reshape(b * l, d))
+        return self.fc2(hidden, gelu=True).view(b, l, -1)
+
+
+class WanBlockW8A8:
+    """One Wan 2.1 attention block; see the module docstring for the math."""
+
+    def __init__(self, cfg: WanBlockConfig, *, modulation: torch.Tensor,
+                 self_qkv: W8A8Linear, self_o: W8A8Linear, self_norm_q: torch.Tensor, self_norm_k: torch.Tensor,
+                 norm3_weight: torch.Tensor, norm3_bias: torch.Tensor,
+                 cross_q: W8A8Linear, cross_kv: W8A8Linear, cross_o: W8A8Linear,
+                 cross_norm_q: torch.Tensor, cross_norm_k: torch.Tensor,
+                 ffn_up: W8A8Linear, ffn_down: W8A8Linear):
+        c = cfg.dim
+        if cfg.head_dim not in (64, 128) or cfg.head_dim * cfg.heads != c:
+            raise ValueError("Wan block needs head_dim 64 or 128 and heads * head_dim == dim")
+        for lin, k, n in ((self_qkv, c, 3 * c), (self_o, c, c), (cross_q, c, c), (cross_kv, c, 2 * c),
+                          (cross_o, c, c), (ffn_up, c, cfg.ffn_dim), (ffn_down, cfg.ffn_dim, c)):
+            if (lin.in_features, lin.out_features) != (k, n):
+                raise ValueError(f"linear shape {(lin.out_features, lin.in_features)} != {(n, k)}")
+        self.cfg = cfg
+        self.modulation = modulation.to(torch.float32).reshape(1, 6, c)
+        self.self_qkv, self.self_o = self_qkv, self_o
+        self.self_norm_q = self_norm_q.to(torch.bfloat16).contiguous()
+        self.self_norm_k = self_norm_k.to(torch.bfloat16).contiguous()
+        self.cross_q, self.cross_kv, self.cross_o = cross_q, cross_kv, cross_o
+        self.cross_norm_q = cross_norm_q.to(torch.bfloat16).contiguous()
+        self.cross_norm_k = cross_norm_k.to(torch.bfloat16).contiguous()
+        self.ffn_up, self.ffn_down = ffn_up, ffn_down
+        w = norm3_weight.to(torch.bfloat16).reshape(1, 1, c)
+        scale3 = (w.float() - 1.0).to(torch.bfloat16)
+        if not torch.equal((1.0 + scale3.float()).to(torch.bfloat16), w):
+            raise ValueError("norm3 weight is not exactly 1 + a bf16 value; the AdaLN form cannot express it")
+        self.norm3_scale = scale3.contiguous()
+        self.norm3_shift = norm3_bias.to(torch.bfloat16).reshape(1, 1, c).contiguous()
+
+    # -- sublayers (each takes and returns bf16 [B, L, C]) ---------------------
+
+    def self_attention(self, h: torch.Tensor, freqs: torch.Tensor) -> torch.Tensor:
+        cfg = self.cfg
+        b, l, c = h.shape
+        qkv = self.self_qkv(h.reshape(b * l, c)).view(b, l, 3, cfg.heads, cfg.head_dim)
+        q, k, v = qkv[:, :, 0], qkv[:, :, 1], qkv[:, :, 2]
+        qk = sage_core.prequantize_rms_rope_qk(
+            q, k, self.self_norm_q, self.self_norm_k, freqs, epsilon=cfg.eps, rot_dim=cfg.head_dim,
+            tensor_layout="NHD", norm_scope="row")
+        state = sage_core.prequantize_sageattn_from_qk(qk, v, sm_scale=cfg.head_dim ** -0.5)
+        del qkv, q, k, qk
+        out = sage_core.sageattn_from_prequantized(state)
+        return self.self_o(out.reshape(b * l, c)).view(b, l, c)
+
+    def cross_attention(self, h: torch.Tensor, context: torch.Tensor) -> torch.Tensor:
+        cfg = self.cfg
+        b, l, c = h.shape
+        lc = context.shape[1]
+        q = self.cross_q(h.reshape(b * l, c)).view(b, l, cfg.heads, cfg.head_dim)
+        kv = self.cross_kv(context.reshape(b * lc, c)).view(b, lc, 2, cfg.heads, cfg.head_dim)
+        k, v = kv[:, :, 0], kv[:, :, 1]
+        qk = sage_core.prequantize_rms_rope_qk(
+            q, k, self.cross_norm_q, self.cross_norm_k, None, epsilon=cfg.eps, rot_dim=0,
+            tensor_layout="NHD", norm_scope="row")
+        state = sage_core.prequantize_sageattn_from_qk(qk, v, sm_scale=cfg.head_dim ** -0.5)
+        del q, kv, k, qk
+        out = sage_core.sageattn_from_prequantized(state)
+        return self.cross_o(out.reshape(b * l, c)).view(b, l, c)
+
+    def ffn(self, h: torch.Tensor) -> torch.Tensor:
+        b, l, c = h.shape
+        up = self.ffn_up(h.reshape(b * l, c))
+        return self.ffn_down(up, gelu=True).view(b, l, c)
+
+    def modulation_chunks(self, e: torch.Tensor) -> list[torch.Tensor]:
+        """(modulation + e) split into the six [B, 1, C] bf16 rows."""
+        mod = (self.modulation + e.to(torch.float32)).to(torch.bfloat16)
+        return [mod[:, i:i + 1] for i in range(6)]
+
+    def forward(self, x: torch.Tensor, e: torch.Tensor, context: torch.Tensor, freqs: torch.Tensor) -> torch.Tensor:
+        """x bf16 [B, L, C]; e [B, 6, C] time modulation; context bf16 [B, Lc, C]
+        (after the text embedding); freqs [1|B, L, 1, D/2, 2, 2]."""
+        cfg = self.cfg
+        if x.dtype != torch.bfloat16 or x.dim() != 3 or x.shape[2] != cfg.dim:
+            raise TypeError(f"Wan block input must be bf16 [B, L, {cfg.dim}]")
+        if context.dtype != torch.bfloat16 or context.dim() != 3 or context.shape[2] != cfg.dim:
+            raise TypeError(f"Wan block context must be bf16 [B, Lc, {cfg.dim}]")
+        lnadaln = torch.ops.turing_utils.layer_norm_adaln
+        e0, e1, e2, e3, e4, e5 = self.modulation_chunks(e)
+        y = self.self_attention(lnadaln(x, e1, e0, cfg.eps), freqs)
+        x = torch.addcmul(x, y, e2)
+        y = self.cross_attention(lnadaln(x, self.norm3_scale, self.norm3_shift, cfg.eps), context)
+        x = x + y
+        y = self.ffn(lnadaln(x, e4, e3, cfg.eps))
+        return torch.addcmul(x, y, e5)
+
+    __call__ = forward
+
+
+def random_block(cfg: WanBlockConfig, seed: int, device) -> tuple[WanBlockW8A8, WanTextEmbeddingW8A8]:
+    """Random-init block and text embedding: every linear weight and bias
+    N(0, 0.02) (generated in fp32 on ``device`` with a seeded generator), then
+    quantized; RMSNorm weights 1 + N(0, 0.05); norm3 weight 1 + k / 128 (k
+    uniform in -16..16, so that w - 1 is exact in bf16) and bias N(0, 0.02);
+    the modulation table N(0, 1) / sqrt(C) as in Wan's initialisation."""
+    device = torch.device(device)
+    g = torch.Generator(device=device).manual_seed(seed)
+    c, f = cfg.dim, cfg.ffn_dim
+
+    def randn(*shape):
+        return torch.randn(*shape, generator=g, device=device)
+
+    def linear(n, k):
+        w = randn(n, k) * 0.02
+        b = randn(n) * 0.02
+        return W8A8Linear.from_float(w, b.to(torch.bfloat16))
+
+    def norm_weight():
+        return (1 + 0.05 * randn(c)).to(torch.bfloat16)
+
+    block = WanBlockW8A8(
+        cfg,
+        modulation=randn(1, 6, c) / math.sqrt(c),
+        self_qkv=linear(3 * c, c), self_o=linear(c, c),
+        self_norm_q=norm_weight(), self_norm_k=norm_weight(),
+        norm3_weight=1 + torch.randint(-16, 17, (c,), generator=g, device=device).float() / 128,
+        norm3_bias=randn(c) * 0.02,
+        cross_q=linear(c, c), cross_kv=linear(2 * c, c), cross_o=linear(c, c),
+        cross_norm_q=norm_weight(), cross_norm_k=norm_weight(),
+        ffn_up=linear(f, c), ffn_down=linear(c, f),
+    )
+    text = WanTextEmbeddingW8A8(linear(c, cfg.text_dim), linear(c, c))
+    return block, text
+
+
+def c5_inputs(text: WanTextEmbeddingW8A8, device, seed: int = 4, grid=(21, 30, 52), text_tokens: int = 512):
+    """Synthetic C5 inputs: x bf16 [1, F*H*W, 5120] ~ N(0, 1), the time
+    modulation e fp32 [1, 6, 5120] ~ N(0, 0.01), the text context bf16
+    [1, 512, 4096] ~ N(0, 1) passed through the text embedding, and the
+    rotary table of the latent grid (Wan 2.1 480p, 81 frames: 21 x 30 x 52)."""
+    g = torch.Generator(device=device).manual_seed(seed)
+    tokens = grid[0] * grid[1] * grid[2]
+    x = torch.randn(1, tokens, 5120, generator=g, device=device).to(torch.bfloat16)
+    e = 0.1 * torch.randn(1, 6, 5120, generator=g, device=device)
+    context = text(torch.randn(1, text_tokens, 4096, generator=g, device=device).to(torch.bfloat16))
+    return x, e, context, rope_freqs(grid, 128, device=device)
+
+
+def block_ops(cfg: WanBlockConfig, tokens: int, text_tokens: int) -> float:
+    """Multiply-adds x 2 of one block forward: the seven projections and the
+    self / cross attention (4 H L Lk D each)."""
+    c, f, m = cfg.dim, cfg.ffn_dim, tokens
+    linears = 2.0 * m * c * (3 * c + c + c + c + 2 * f) + 2.0 * text_tokens * c * 2 * c
+    attention = 4.0 * cfg.heads * m * (m + text_tokens) * cfg.head_dim
+    return linears + attention
+
+
+def main(argv=None) -> int:
+    """Runs the random-init C5 block forward on cuda:0 and prints one JSON
+    line (ms per forward, TOPS) -- the workload profiled with rocprofv3."""
+    import argparse
+    import json
+
+    p = argparse.ArgumentParser(description=main.__doc__)
+    p.add_argument("--iters", type=int, default=10)
+    p.add_argument("--warmup", type=int, default=3)
+    args = p.parse_args(argv)
+    dev = torch.device("cuda", 0)
+    cfg = WanBlockConfig()
+    block, text = random_block(cfg, seed=4, device=dev)
+    x, e, context, freqs = c5_inputs(text, dev)
+    for _ in range(args.warmup):
+        block(x, e, context, freqs)
+    torch.cuda.synchronize(dev)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(args.iters):
+        block(x, e, context, freqs)
+    end.record()
+    end.synchronize()
+    ms = start.elapsed_time(end) / args.iters
+    ops_ = block_ops(cfg, x.shape[1], context.shape[1])
+    print(json.dumps({"workload": "wan14b_block_c5", "ms": ms, "tops": ops_ / ms / 1e9, "iters": args.iters}))
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

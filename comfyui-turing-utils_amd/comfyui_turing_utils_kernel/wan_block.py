@@ -54,28 +54,60 @@ class W8A8Linear:
     per-output-channel fp32 scale; x is quantized per token by the ConvRot
     quantizer (optionally with the tanh-GELU applied first)."""
 
-    def __init__(self, weight_int8: torch.Tensor, weight_scale: torch.Tensor, bias: Optional[torch.Tensor]):
+    def __init__(self, weight_int8: torch.Tensor, weight_scale: torch.Tensor, bias: Optional[torch.Tensor],
+                 group: int = GROUP):
         if weight_int8.dtype != torch.int8 or weight_int8.dim() != 2:
             raise TypeError("W8A8 weight must be a 2D int8 tensor")
+        if group not in (128, 256) or weight_int8.shape[1] % group:
+            raise ValueError(f"ConvRot group {group} must be 128 or 256 and divide K={weight_int8.shape[1]}")
         self.weight = weight_int8.contiguous()
-        self.weight_scale = weight_scale.reshape(-1).to(torch.float32).contiguous()
-        self.bias = None if bias is None else bias.reshape(-1).to(torch.float32).contiguous()
         self.out_features, self.in_features = self.weight.shape
+        scale = weight_scale.reshape(-1).to(torch.float32)
+        if scale.numel() == 1:  # tensor-wise scale
+            scale = scale.expand(self.out_features)
+        if scale.numel() != self.out_features:
+            raise ValueError(f"weight scale has {scale.numel()} values for {self.out_features} output channels")
+        self.weight_scale = scale.contiguous()
+        self.bias = None if bias is None else bias.reshape(-1).to(torch.float32).contiguous()
+        if self.bias is not None and self.bias.numel() != self.out_features:
+            raise ValueError("bias length must equal the output channels")
+        self.group = group
 
     @classmethod
-    def from_float(cls, weight: torch.Tensor, bias: Optional[torch.Tensor] = None) -> "W8A8Linear":
+    def from_float(cls, weight: torch.Tensor, bias: Optional[torch.Tensor] = None, group: int = GROUP) -> "W8A8Linear":
         """Quantizes a dense weight [N, K] (rounded to bf16 first) on its device."""
         codes, scale = torch.ops.turing_utils.bf16_int8_convrot_quantize(
-            weight.to(torch.bfloat16).contiguous(), GROUP)
-        return cls(codes, scale, bias)
+            weight.to(torch.bfloat16).contiguous(), group)
+        return cls(codes, scale, bias, group)
 
     def __call__(self, x: torch.Tensor, gelu: bool = False) -> torch.Tensor:
         if x.dim() != 2 or x.shape[1] != self.in_features:
             raise ValueError(f"W8A8 linear expects [M, {self.in_features}], got {tuple(x.shape)}")
         quantize = (torch.ops.turing_utils.bf16_gelu_int8_convrot_quantize if gelu
                     else torch.ops.turing_utils.bf16_int8_convrot_quantize)
-        codes, scale = quantize(x.contiguous(), GROUP)
+        codes, scale = quantize(x.contiguous(), self.group)
         return torch.ops.turing_utils.int8_linear(codes, self.weight, scale, self.weight_scale, self.bias)
+
+    @staticmethod
+    def concat(parts: "list[W8A8Linear]") -> "W8A8Linear":
+        """One linear whose output is the parts' outputs side by side (same K
+        and group): codes, scales and biases stacked along N."""
+        if len({(p.in_features, p.group) for p in parts}) != 1:
+            raise ValueError("concatenated linears need one K and one ConvRot group")
+        if len({p.bias is None for p in parts}) != 1:
+            raise ValueError("concatenated linears must all have a bias or none")
+        bias = None if parts[0].bias is None else torch.cat([p.bias for p in parts])
+        return W8A8Linear(torch.cat([p.weight for p in parts]), torch.cat([p.weight_scale for p in parts]), bias,
+                          parts[0].group)
+
+    def split(self, n: int) -> "list[W8A8Linear]":
+        """The inverse of ``concat`` for ``n`` equal parts."""
+        if self.out_features % n:
+            raise ValueError(f"{self.out_features} output channels do not split into {n} equal parts")
+        size = self.out_features // n
+        return [W8A8Linear(self.weight[i * size:(i + 1) * size], self.weight_scale[i * size:(i + 1) * size],
+                           None if self.bias is None else self.bias[i * size:(i + 1) * size], self.group)
+                for i in range(n)]
 
 
 def rope_freqs(grid: tuple[int, int, int], head_dim: int = 128, theta: float = 10000.0,
@@ -248,6 +280,72 @@ def random_block(cfg: WanBlockConfig, seed: int, device) -> tuple[WanBlockW8A8, 
     )
     text = WanTextEmbeddingW8A8(linear(c, cfg.text_dim), linear(c, c))
     return block, text
+
+
+# Wan 2.1 parameter names of one block (the official checkpoint's and
+# ComfyUI's): quantized linears and plain tensors, relative to "blocks.{i}.".
+_BLOCK_LINEARS = ("self_attn.q", "self_attn.k", "self_attn.v", "self_attn.o", "cross_attn.q", "cross_attn.k",
+                  "cross_attn.v", "cross_attn.o", "ffn.0", "ffn.2")
+_BLOCK_TENSORS = ("modulation", "self_attn.norm_q.weight", "self_attn.norm_k.weight", "cross_attn.norm_q.weight",
+                  "cross_attn.norm_k.weight", "norm3.weight", "norm3.bias")
+
+
+def block_state(block: WanBlockW8A8, index: int, prefix: str = "") -> tuple[dict, dict]:
+    """(W8 linears, plain tensors) of ``block`` under Wan's names for block
+    ``index``: the fused q / k / v and k / v GEMMs split back into layers."""
+    p = f"{prefix}blocks.{index}."
+    q, k, v = block.self_qkv.split(3)
+    ck, cv = block.cross_kv.split(2)
+    linears = dict(zip((p + n for n in _BLOCK_LINEARS),
+                       (q, k, v, block.self_o, block.cross_q, ck, cv, block.cross_o, block.ffn_up, block.ffn_down)))
+    norm3_weight = (1.0 + block.norm3_scale.float()).to(torch.bfloat16).reshape(-1)
+    tensors = dict(zip((p + n for n in _BLOCK_TENSORS),
+                       (block.modulation, block.self_norm_q, block.self_norm_k, block.cross_norm_q,
+                        block.cross_norm_k, norm3_weight, block.norm3_shift.reshape(-1))))
+    return linears, tensors
+
+
+def load_block(path, index: int, cfg: Optional[WanBlockConfig] = None, *, prefix: str = "",
+               device="cpu") -> WanBlockW8A8:
+    """Block ``index`` of a Wan 2.1 ConvRot W8A8 safetensors checkpoint (its
+    W8 layers as the ConvRot metadata describes them, the norms and the
+    modulation table as plain tensors), with q / k / v and cross k / v fused."""
+    from safetensors import safe_open
+
+    from .convrot_format import load_w8a8_linears
+
+    cfg = cfg or WanBlockConfig()
+    p = f"{prefix}blocks.{index}."
+    lin = load_w8a8_linears(path, prefix=p, device=device)
+    missing = [p + n for n in _BLOCK_LINEARS if p + n not in lin]
+    if missing:
+        raise ValueError(f"checkpoint has no W8 ConvRot layers {missing}")
+    with safe_open(str(path), framework="pt", device="cpu") as f:
+        keys = set(f.keys())
+        absent = [p + n for n in _BLOCK_TENSORS if p + n not in keys]
+        if absent:
+            raise ValueError(f"checkpoint has no tensors {absent}")
+        t = {n: f.get_tensor(p + n).to(device) for n in _BLOCK_TENSORS}
+    L = {n: lin[p + n] for n in _BLOCK_LINEARS}
+    return WanBlockW8A8(
+        cfg, modulation=t["modulation"],
+        self_qkv=W8A8Linear.concat([L["self_attn.q"], L["self_attn.k"], L["self_attn.v"]]), self_o=L["self_attn.o"],
+        self_norm_q=t["self_attn.norm_q.weight"], self_norm_k=t["self_attn.norm_k.weight"],
+        norm3_weight=t["norm3.weight"], norm3_bias=t["norm3.bias"],
+        cross_q=L["cross_attn.q"], cross_kv=W8A8Linear.concat([L["cross_attn.k"], L["cross_attn.v"]]),
+        cross_o=L["cross_attn.o"], cross_norm_q=t["cross_attn.norm_q.weight"],
+        cross_norm_k=t["cross_attn.norm_k.weight"], ffn_up=L["ffn.0"], ffn_down=L["ffn.2"])
+
+
+def load_text_embedding(path, *, prefix: str = "", device="cpu") -> WanTextEmbeddingW8A8:
+    """Wan's ``text_embedding.0`` / ``text_embedding.2`` W8 layers."""
+    from .convrot_format import load_w8a8_linears
+
+    lin = load_w8a8_linears(path, prefix=f"{prefix}text_embedding.", device=device)
+    try:
+        return WanTextEmbeddingW8A8(lin[f"{prefix}text_embedding.0"], lin[f"{prefix}text_embedding.2"])
+    except KeyError as exc:
+        raise ValueError(f"checkpoint has no W8 ConvRot layer {exc}") from None
 
 
 def c5_inputs(text: WanTextEmbeddingW8A8, device, seed: int = 4, grid=(21, 30, 52), text_tokens: int = 512):

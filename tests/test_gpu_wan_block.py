@@ -100,3 +100,18 @@ def test_block_c5_sampled_rows(harness, gpu_device):
     want = ref.block_rows(block, x, e, context, freqs, rows)
     _check("C5 block update (rows)", out[:, rows].float() - x[:, rows].float(), want - x[:, rows].float(),
            BLOCK_REL_MAX)
+
+
+def test_checkpoint_round_trip_forward(harness, gpu_device, tmp_path):
+    """The block written as a ConvRot W8A8 checkpoint under Wan's names and
+    loaded back runs the same forward, bit for bit."""
+    from comfyui_turing_utils_kernel import convrot_format
+    from comfyui_turing_utils_kernel.wan_block import block_state, load_block
+
+    block, text = harness
+    linears, tensors = block_state(block, 0)
+    path = tmp_path / "wan_block0.safetensors"
+    convrot_format.save_w8a8_linears(path, linears, tensors)
+    loaded = load_block(path, 0, block.cfg, device=gpu_device)
+    x, e, _, context, freqs = _inputs(block, text, (2, 16, 32), 77, 14, gpu_device)
+    assert torch.equal(loaded(x, e, context, freqs), block(x, e, context, freqs))

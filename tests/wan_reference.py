@@ -2,7 +2,7 @@
 
 Same block as comfyui_turing_utils_kernel.wan_block, computed in fp32 with
 dequantized weights (codes x per-channel scale, rotated back to the original
-basis with the dense 128 x 128 ConvRot matrix built from the CPU oracle),
+basis with the dense ConvRot group matrix built from the CPU oracle),
 unquantized activations and exact softmax attention.  Cross-token work is
 confined to the self-attention, so the block output of any subset of rows can
 be computed from keys / values of all tokens plus the rows' own queries --
@@ -18,11 +18,11 @@ from oracle import oracle
 _ROT = {}
 
 
-def rotation(device) -> torch.Tensor:
-    """M with rot(v) = v @ M for one 128-group (orthogonal and symmetric)."""
-    key = str(device)
+def rotation(device, group: int = 128) -> torch.Tensor:
+    """M with rot(v) = v @ M for one group (orthogonal and symmetric)."""
+    key = (str(device), group)
     if key not in _ROT:
-        m = np.stack([oracle.rotate_group(r, 128) for r in np.eye(128, dtype=np.float32)])
+        m = np.stack([oracle.rotate_group(r, group) for r in np.eye(group, dtype=np.float32)])
         _ROT[key] = torch.from_numpy(m).to(device)
     return _ROT[key]
 
@@ -32,8 +32,8 @@ def dense_weight(lin) -> torch.Tensor:
     if getattr(lin, "_ref_dense", None) is None:
         w = lin.weight.float() * lin.weight_scale[:, None]
         n, k = w.shape
-        m = rotation(w.device)
-        lin._ref_dense = (w.view(n, k // 128, 128) @ m.T).reshape(n, k)
+        m = rotation(w.device, lin.group)
+        lin._ref_dense = (w.view(n, k // lin.group, lin.group) @ m.T).reshape(n, k)
     return lin._ref_dense
 
 

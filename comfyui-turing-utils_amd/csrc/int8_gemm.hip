@@ -14,8 +14,11 @@
 //     workgroup per CU, two waves per SIMD, so one wave's LDS fragment reads
 //     and barrier waits overlap the other's MFMAs.
 //   * The W tile is the MFMA A operand and the activation tile the B operand,
-//     so each lane ends with 4 consecutive output columns of one row: the
-//     epilogue issues one 8-byte store per 16 x 16 sub-tile.
+//     so each lane ends with 4 consecutive output columns of one row.  The
+//     bf16 epilogue loads the tile's scales and bias in one batch, writes
+//     each wave's 64 x 128 bf16 tile to LDS (the ring is free by then) and
+//     stores whole 256-byte rows, 16 bytes per lane; the INT32 output stores
+//     16 bytes per 16 x 16 sub-tile row directly.
 //   * K steps of 128 bytes through a 2-stage LDS ring (2 x 64 KiB) filled by
 //     global_load_lds_dwordx4 (direct to LDS, no staging registers) one step
 //     ahead of the MFMAs.  Within a step the two 64-deep fragment sets are
@@ -90,13 +93,9 @@ __device__ __forceinline__ void store_tiles(const TileLoad &t, int8_t *lds_a, in
     }
 }
 
-// Maps the linear workgroup id to (m-tile, n-tile): XCD-contiguous ranges,
-// grouped m-major inside each range.
-__device__ __forceinline__ void tile_coords(int bid, int tiles_m, int tiles_n, int &tm, int &tn) {
-    const int total = tiles_m * tiles_n;
-    const int q = total / 8, r = total % 8;
-    const int xcd = bid % 8, idx = bid / 8;
-    const int t = xcd < r ? xcd * (q + 1) + idx : r * (q + 1) + (xcd - r) * q + idx;
+// Linear tile index t -> (m-tile, n-tile): groups of kGroupM m-tiles,
+// m-major inside a group.
+__device__ __forceinline__ void tile_of(int t, int tiles_m, int tiles_n, int &tm, int &tn) {
     const int per_group = kGroupM * tiles_n;
     const int group = t / per_group;
     const int first_m = group * kGroupM;
@@ -104,6 +103,16 @@ __device__ __forceinline__ void tile_coords(int bid, int tiles_m, int tiles_n, i
     const int in_group = t % per_group;
     tm = first_m + in_group % gsm;
     tn = in_group / gsm;
+}
+
+// Maps the linear workgroup id to (m-tile, n-tile): XCD x (workgroup id mod
+// 8) owns a contiguous range of tile indices, walked in order.
+__device__ __forceinline__ void tile_coords(int bid, int tiles_m, int tiles_n, int &tm, int &tn) {
+    const int total = tiles_m * tiles_n;
+    const int q = total / 8, r = total % 8;
+    const int xcd = bid % 8, idx = bid / 8;
+    const int t = xcd < r ? xcd * (q + 1) + idx : r * (q + 1) + (xcd - r) * q + idx;
+    tile_of(t, tiles_m, tiles_n, tm, tn);
 }
 
 constexpr int kStages = 2;
@@ -247,36 +256,81 @@ __global__ __launch_bounds__(kThreads, kWaves / 4) void int8_gemm_kernel(
     // acc[i][j][r] = C[m = m0 + wm*16*kFragsM + 16j + (lane & 15)]
     //                  [n = n0 + wn*128 + 16i + 4*(lane >> 4) + r]
     const int g = lane >> 4;
+    if constexpr (kI32Out) {
 #pragma unroll
-    for (int j = 0; j < kFragsM; ++j) {
-        const int64_t row = m0 + wm * 16 * kFragsM + j * 16 + (lane & 15);
-        if (row >= m) continue;
-        float arow = 0.0f;
-        if constexpr (!kI32Out) arow = as[row];
+        for (int j = 0; j < kFragsM; ++j) {
+            const int64_t row = m0 + wm * 16 * kFragsM + j * 16 + (lane & 15);
+            if (row >= m) continue;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int64_t col = n0 + wn * 128 + i * 16 + 4 * g;
+                if (col >= n) continue;  // n % 8 == 0, so a group of 4 is all in or all out
+                *reinterpret_cast<i32x4 *>(static_cast<int32_t *>(out) + row * n + col) = acc[i][j];
+            }
+        }
+    } else {
+        // bf16 tile of this wave (16 kFragsM rows x 128 columns) staged through
+        // LDS, so that global stores write whole rows: the ring is free once
+        // every wave is past its last fragment read.  Rows of 256 B; the
+        // 16-byte chunk index is XORed with the row's low 4 bits (both the
+        // 8-byte writes below and the 16-byte row reads are conflict free).
+        constexpr int kRows = 16 * kFragsM;
+        static_assert(kWaves * kRows * 256 <= kStages * kStageBytes, "epilogue tile exceeds the LDS ring");
+        const int frow = lane & 15;
+        const int64_t row_base = m0 + wm * kRows;
+        const int64_t col_base = n0 + wn * 128;
+        // All of the tile's scales and bias in one batch, from in-range
+        // addresses without branches (rows / columns past the end read the
+        // last valid ones and are never stored): vector-memory operations
+        // retire in order, so loads interleaved with their uses would each
+        // wait a full round trip.
+        const float *bp = bias ? bias : ws;
+        float arow[kFragsM];
+        f32x4 wsv[8], bv[8];
+#pragma unroll
+        for (int j = 0; j < kFragsM; ++j) arow[j] = as[min(row_base + j * 16 + frow, m - 1)];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const int64_t col = n0 + wn * 128 + i * 16 + 4 * g;
-            if (col >= n) continue;  // n % 8 == 0, so a group of 4 is all in or all out
-            if constexpr (kI32Out) {
-                *reinterpret_cast<i32x4 *>(static_cast<int32_t *>(out) + row * n + col) = acc[i][j];
-            } else {
-                const f32x4 wsv = *reinterpret_cast<const f32x4 *>(ws + col);
-                f32x4 bv = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-                if (bias) bv = *reinterpret_cast<const f32x4 *>(bias + col);
+            const int64_t col = min(col_base + i * 16 + 4 * g, n - 4);
+            wsv[i] = *reinterpret_cast<const f32x4 *>(ws + col);
+            bv[i] = *reinterpret_cast<const f32x4 *>(bp + col);
+        }
+        __syncthreads();
+        int8_t *tile = &lds[0][0] + wave * kRows * 256;
+#pragma unroll
+        for (int j = 0; j < kFragsM; ++j) {
+            const int lrow = j * 16 + frow;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
                 float v[4];
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     float x = static_cast<float>(acc[i][j][r]);
-                    x = x * arow;
-                    x = x * wsv[r];
-                    if (bias) x = x + bv[r];
+                    x = x * arow[j];
+                    x = x * wsv[i][r];
+                    if (bias) x = x + bv[i][r];
                     v[r] = x;
                 }
                 u32x2 packed;
                 packed.x = pack_bf16x2(v[0], v[1]);
                 packed.y = pack_bf16x2(v[2], v[3]);
-                *reinterpret_cast<u32x2 *>(static_cast<uint16_t *>(out) + row * n + col) = packed;
+                const int chunk = (2 * i + (g >> 1)) ^ (lrow & 15);
+                *reinterpret_cast<u32x2 *>(tile + lrow * 256 + chunk * 16 + (g & 1) * 8) = packed;
             }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        // 4 rows of 16 chunks per pass
+        const int rsub = lane >> 4, c = lane & 15;
+#pragma unroll
+        for (int pass = 0; pass < kRows / 4; ++pass) {
+            const int lrow = pass * 4 + rsub;
+            const int64_t row = row_base + lrow;
+            const int64_t col = col_base + c * 8;
+            const u32x4 val = *reinterpret_cast<const u32x4 *>(tile + lrow * 256 + ((c ^ (lrow & 15)) << 4));
+            if (row < m && col < n)  // n % 8 == 0: a chunk is all in or all out
+                *reinterpret_cast<u32x4 *>(static_cast<uint16_t *>(out) + row * n + col) = val;
         }
     }
 }

@@ -238,7 +238,10 @@ class WanBlockW8A8:
         e0, e1, e2, e3, e4, e5 = self.modulation_chunks(e)
         y = self.self_attention(lnadaln(x, e1, e0, cfg.eps), freqs)
         x = torch.addcmul(x, y, e2)
-        y = self.cross_attention(lnadaln(x, self.norm3_scale, self.norm3_shift, cfg.eps), context)
+        b = x.shape[0]
+        # the op takes one modulation row per sample: the affine row repeats
+        y = self.cross_attention(lnadaln(x, self.norm3_scale.expand(b, 1, cfg.dim),
+                                         self.norm3_shift.expand(b, 1, cfg.dim), cfg.eps), context)
         x = x + y
         y = self.ffn(lnadaln(x, e4, e3, cfg.eps))
         return torch.addcmul(x, y, e5)

@@ -115,3 +115,24 @@ def test_checkpoint_round_trip_forward(harness, gpu_device, tmp_path):
     loaded = load_block(path, 0, block.cfg, device=gpu_device)
     x, e, _, context, freqs = _inputs(block, text, (2, 16, 32), 77, 14, gpu_device)
     assert torch.equal(loaded(x, e, context, freqs), block(x, e, context, freqs))
+
+
+def test_batch_of_two(harness, gpu_device):
+    """B = 2 with per-sample modulation and text: every view, stride and
+    broadcast of the block holds beyond batch 1, and each sample equals the
+    block run on it alone."""
+    from comfyui_turing_utils_kernel.wan_block import rope_freqs
+
+    block, text = harness
+    g = torch.Generator(device=gpu_device).manual_seed(21)
+    grid = (1, 16, 16)
+    x = torch.randn(2, 256, 5120, generator=g, device=gpu_device).to(torch.bfloat16)
+    e = 0.1 * torch.randn(2, 6, 5120, generator=g, device=gpu_device)
+    context = text(torch.randn(2, 40, 4096, generator=g, device=gpu_device).to(torch.bfloat16))
+    freqs = rope_freqs(grid, 128, device=gpu_device).to(torch.bfloat16).float()
+    out = block(x, e, context, freqs)
+    want = ref.block_rows(block, x, e, context, freqs)
+    _check("block update, B=2", out.float() - x.float(), want - x.float(), BLOCK_REL_MAX)
+    for i in range(2):
+        alone = block(x[i:i + 1].contiguous(), e[i:i + 1], context[i:i + 1].contiguous(), freqs)
+        assert torch.equal(alone, out[i:i + 1]), i

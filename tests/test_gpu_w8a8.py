@@ -187,6 +187,21 @@ def test_attention_vs_oracle(gpu_device, causal, dtype, hq, hkv, lq, lk, d):
     _compare(out.cpu().float(), ref)
 
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_attention_batch_two(gpu_device, causal):
+    """B = 2 with GQA: batch strides of the codes, scales, V prefix sums and
+    output; each batch entry against its own oracle rows."""
+    from comfyui_turing_utils_kernel.turing_sage import w8a8attn
+
+    q, k, v = _qkv(2, 4, 2, 200, 333, 128, torch.bfloat16, 91)
+    out = w8a8attn(q.to(gpu_device), k.to(gpu_device), v.to(gpu_device), is_causal=causal)
+    torch.cuda.synchronize(gpu_device)
+    rows = np.array([(b, h, i) for b in range(2) for h in range(4) for i in range(0, 200, 7)])
+    ref = _oracle_attention(q, k, v, causal, 128 ** -0.5, rows)
+    got = out.cpu().float()[rows[:, 0], rows[:, 1], rows[:, 2]]
+    _compare(got, ref)
+
+
 def test_attention_reference_self_test(gpu_device):
     """turing_sage/__init__.py:573-609 through preflight_w8a8, plus the
     same inputs through the op and torch.compile(fullgraph)."""

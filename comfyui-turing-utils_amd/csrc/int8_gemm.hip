@@ -18,7 +18,10 @@
 //     bf16 epilogue loads the tile's scales and bias in one batch, writes
 //     each wave's 64 x 128 bf16 tile to LDS (the ring is free by then) and
 //     stores whole 256-byte rows, 16 bytes per lane; the INT32 output stores
-//     16 bytes per 16 x 16 sub-tile row directly.
+//     16 bytes per 16 x 16 sub-tile row directly.  Output stores are
+//     non-temporal: written once and never re-read here, they would otherwise
+//     evict the activation and weight panels that neighbouring tiles re-read
+//     from L2 (measured: 15 % at qkv and ffn-up).
 //   * K steps of 128 bytes through a 2-stage LDS ring (2 x 64 KiB) filled by
 //     global_load_lds_dwordx4 (direct to LDS, no staging registers) one step
 //     ahead of the MFMAs.  Within a step the two 64-deep fragment sets are
@@ -265,7 +268,7 @@ __global__ __launch_bounds__(kThreads, kWaves / 4) void int8_gemm_kernel(
             for (int i = 0; i < 8; ++i) {
                 const int64_t col = n0 + wn * 128 + i * 16 + 4 * g;
                 if (col >= n) continue;  // n % 8 == 0, so a group of 4 is all in or all out
-                *reinterpret_cast<i32x4 *>(static_cast<int32_t *>(out) + row * n + col) = acc[i][j];
+                __builtin_nontemporal_store(acc[i][j], reinterpret_cast<i32x4 *>(static_cast<int32_t *>(out) + row * n + col));
             }
         }
     } else {
@@ -330,7 +333,7 @@ __global__ __launch_bounds__(kThreads, kWaves / 4) void int8_gemm_kernel(
             const int64_t col = col_base + c * 8;
             const u32x4 val = *reinterpret_cast<const u32x4 *>(tile + lrow * 256 + ((c ^ (lrow & 15)) << 4));
             if (row < m && col < n)  // n % 8 == 0: a chunk is all in or all out
-                *reinterpret_cast<u32x4 *>(static_cast<uint16_t *>(out) + row * n + col) = val;
+                __builtin_nontemporal_store(val, reinterpret_cast<u32x4 *>(static_cast<uint16_t *>(out) + row * n + col));
         }
     }
 }

@@ -31,7 +31,9 @@
 //     address).  A partial last K step (K % 128 != 0) is staged through
 //     registers with zero fill.
 //   * Tiles are renumbered so each XCD (workgroup id mod 8) owns a contiguous
-//     range, walked in groups of 8 m-tiles for L2 reuse of the A and W panels.
+//     range, walked in groups of 4 m-tiles for L2 reuse of the A and W panels
+//     (measured best among 2, 4, 6, 8, 16 and 32 once the output no longer
+//     pollutes L2).
 #include "tu_common.h"
 
 namespace tu {
@@ -49,7 +51,7 @@ constexpr int kWavesM = TU_GEMM_WAVES_M;
 constexpr int kWaves = 2 * kWavesM;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kFragsM = kBM / kWavesM / 16;  // 16-row activation fragments per wave
-constexpr int kGroupM = 8;
+constexpr int kGroupM = 4;
 
 // LDS panel layout: 128-byte rows, the 16-byte chunk index XOR-swizzled with
 // row bits 1..3 (measured bank-conflict free for 16 lanes reading one chunk

@@ -259,6 +259,10 @@ __device__ __forceinline__ void pv_tile(const int8_t *stage, const LaneGeom &gm,
 __device__ __forceinline__ void mfma_cluster(const int8_t *kst, const int8_t *vst, const LaneGeom &gm,
                                              const i32x4 (&qf)[kQT][2], i32x4 (&s)[4][kQT],
                                              const bf16x8 (&p)[2][kQT], SoftmaxState &st, const bf16x8 &ones) {
+    // This wave's MFMA cluster is the critical phase of the ping-pong: raise its
+    // issue priority over the other group's softmax VALU on the same SIMD
+    // (measured about 1 % faster; raising the softmax phase instead was slower).
+    __builtin_amdgcn_s_setprio(3);
     i32x4 kf[4][2];
     bf16x8 va[8], vb[8];
     // first-slice K fragments first: the first QK^T MFMAs only need those
@@ -306,6 +310,7 @@ __device__ __forceinline__ void mfma_cluster(const int8_t *kst, const int8_t *vs
     __builtin_amdgcn_sched_group_barrier(0x008, 12, 0);
     __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
     __builtin_amdgcn_sched_group_barrier(0x008, 32, 0);
+    __builtin_amdgcn_s_setprio(0);
 }
 
 // Ping-pong schedule.  A workgroup is 8 waves in two groups of 4 (one wave of

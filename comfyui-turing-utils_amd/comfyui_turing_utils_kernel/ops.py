@@ -32,15 +32,8 @@ def _require_device(t: torch.Tensor, what: str) -> None:
 # ---------------------------------------------------------------------------
 # INT8 linear (reference ops.py:96-126, bindings.cpp:371-421)
 # ---------------------------------------------------------------------------
-@torch.library.custom_op("turing_utils::int8_linear", mutates_args=())
-def turing_int8_linear(
-    activation: torch.Tensor,
-    weight: torch.Tensor,
-    activation_scale: torch.Tensor,
-    weight_scale: torch.Tensor,
-    bias: torch.Tensor | None = None,
-) -> torch.Tensor:
-    """W8A8 contraction with the fused per-token x per-channel scale + bias epilogue."""
+def _linear_args(activation, weight, activation_scale, weight_scale, bias):
+    """int8_linear's checks and layouts; returns the normalized tensors and (m, n, k)."""
     _require_device(activation, "INT8 linear")
     activation = activation.contiguous()
     weight = weight.contiguous()
@@ -69,6 +62,20 @@ def turing_int8_linear(
         raise ValueError("weight_scale must contain one value per output channel")
     if bias is not None and bias.numel() != n:
         raise ValueError("bias must contain one value per output channel")
+    return activation, weight, activation_scale, weight_scale, bias, m, n, k
+
+
+@torch.library.custom_op("turing_utils::int8_linear", mutates_args=())
+def turing_int8_linear(
+    activation: torch.Tensor,
+    weight: torch.Tensor,
+    activation_scale: torch.Tensor,
+    weight_scale: torch.Tensor,
+    bias: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """W8A8 contraction with the fused per-token x per-channel scale + bias epilogue."""
+    activation, weight, activation_scale, weight_scale, bias, m, n, k = _linear_args(
+        activation, weight, activation_scale, weight_scale, bias)
     out = torch.empty((m, n), dtype=torch.bfloat16, device=activation.device)
     if m == 0:
         return out
@@ -83,6 +90,62 @@ def turing_int8_linear(
 
 @turing_int8_linear.register_fake
 def _turing_int8_linear_fake(activation, weight, activation_scale, weight_scale, bias=None):
+    return torch.empty((activation.size(0), weight.size(0)), dtype=torch.bfloat16, device=activation.device)
+
+
+def _check_residual(residual, gate, gate_rows, m, n) -> None:
+    if residual.dtype != torch.bfloat16 or tuple(residual.shape) != (m, n):
+        raise ValueError(f"residual must be bf16 [{m}, {n}], got {residual.dtype} {tuple(residual.shape)}")
+    if gate is not None:
+        rows = (m + gate_rows - 1) // gate_rows if gate_rows > 0 else -1
+        if gate.numel() != rows * n:
+            raise ValueError(f"gate must hold one row of {n} values per {gate_rows} output rows, "
+                             f"got {tuple(gate.shape)}")
+
+
+@torch.library.custom_op("turing_utils::int8_linear_residual", mutates_args=())
+def turing_int8_linear_residual(
+    activation: torch.Tensor,
+    weight: torch.Tensor,
+    activation_scale: torch.Tensor,
+    weight_scale: torch.Tensor,
+    bias: torch.Tensor | None,
+    residual: torch.Tensor,
+    gate: torch.Tensor | None = None,
+    gate_rows: int = 1,
+) -> torch.Tensor:
+    """int8_linear with a gated residual add fused into the epilogue:
+    bf16_rn(fma(y, gate[row // gate_rows], residual)), y the int8_linear
+    output, gate 1 when None.  residual: bf16 [M, N]; gate: bf16 [G, N]
+    (one row per gate_rows consecutive rows, e.g. [B, N] with gate_rows = L).
+    No counterpart in the reference's ops (it fuses a DiT block's residual
+    add / addcmul into the projection)."""
+    activation, weight, activation_scale, weight_scale, bias, m, n, k = _linear_args(
+        activation, weight, activation_scale, weight_scale, bias)
+    _check_residual(residual, gate, gate_rows, m, n)
+    residual = residual.contiguous()
+    if gate is not None:
+        gate = gate.to(torch.bfloat16).reshape(-1, n).contiguous()
+    devices = {activation.device, residual.device} | ({gate.device} if gate is not None else set())
+    if len(devices) != 1:
+        raise ValueError("INT8 linear tensors must use the same CUDA device")
+    out = torch.empty((m, n), dtype=torch.bfloat16, device=activation.device)
+    if m == 0:
+        return out
+    with torch.cuda.device(activation.device):
+        _lib.call(
+            "tu_int8_gemm_bf16_residual",
+            activation.data_ptr(), weight.data_ptr(), activation_scale.data_ptr(), weight_scale.data_ptr(),
+            _lib.ptr(bias), residual.data_ptr(), _lib.ptr(gate), int(gate_rows) if gate is not None else 1,
+            out.data_ptr(), m, n, k, _lib.stream_of(activation.device),
+        )
+    return out
+
+
+@turing_int8_linear_residual.register_fake
+def _turing_int8_linear_residual_fake(activation, weight, activation_scale, weight_scale, bias, residual, gate=None,
+                                      gate_rows=1):
+    _check_residual(residual, gate, gate_rows, activation.size(0), weight.size(0))
     return torch.empty((activation.size(0), weight.size(0)), dtype=torch.bfloat16, device=activation.device)
 
 

@@ -32,8 +32,9 @@ ops into the whole block so that it can be run and timed without ComfyUI:
 Every linear is ConvRot W8A8 at group 128: the weights are rotated and
 quantized per output channel by the same kernel that quantizes activations
 per token (the rotation is orthogonal, so rot(x) . rot(w) = x . w).  The
-residual stream x is bf16; a gated residual is torch.addcmul in bf16 (fp32
-arithmetic, one rounding).
+residual stream x is bf16; each residual add, x + y * gate, runs in the
+epilogue of the projection that produces y (``turing_utils::int8_linear_residual``):
+bf16_rn(fma(y, gate, x)) with y the bf16 projection output.
 """
 from __future__ import annotations
 
@@ -80,13 +81,19 @@ class W8A8Linear:
             weight.to(torch.bfloat16).contiguous(), group)
         return cls(codes, scale, bias, group)
 
-    def __call__(self, x: torch.Tensor, gelu: bool = False) -> torch.Tensor:
+    def __call__(self, x: torch.Tensor, gelu: bool = False, residual: Optional[torch.Tensor] = None,
+                 gate: Optional[torch.Tensor] = None, gate_rows: int = 1) -> torch.Tensor:
+        """y = x W^T + b, or residual + y * gate[row // gate_rows] (gate 1 when
+        None) fused into the GEMM epilogue when ``residual`` [M, N] is given."""
         if x.dim() != 2 or x.shape[1] != self.in_features:
             raise ValueError(f"W8A8 linear expects [M, {self.in_features}], got {tuple(x.shape)}")
         quantize = (torch.ops.turing_utils.bf16_gelu_int8_convrot_quantize if gelu
                     else torch.ops.turing_utils.bf16_int8_convrot_quantize)
         codes, scale = quantize(x.contiguous(), self.group)
-        return torch.ops.turing_utils.int8_linear(codes, self.weight, scale, self.weight_scale, self.bias)
+        if residual is None:
+            return torch.ops.turing_utils.int8_linear(codes, self.weight, scale, self.weight_scale, self.bias)
+        return torch.ops.turing_utils.int8_linear_residual(codes, self.weight, scale, self.weight_scale, self.bias,
+                                                           residual, gate, gate_rows)
 
     @staticmethod
     def concat(parts: "list[W8A8Linear]") -> "W8A8Linear":
@@ -188,7 +195,10 @@ class WanBlockW8A8:
 
     # -- sublayers (each takes and returns bf16 [B, L, C]) ---------------------
 
-    def self_attention(self, h: torch.Tensor, freqs: torch.Tensor) -> torch.Tensor:
+    def self_attention(self, h: torch.Tensor, freqs: torch.Tensor, residual: Optional[torch.Tensor] = None,
+                       gate: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """The attention output projected by o; with ``residual`` [B, L, C],
+        residual + that * gate (gate [B, 1, C] or None) from one epilogue."""
         cfg = self.cfg
         b, l, c = h.shape
         qkv = self.self_qkv(h.reshape(b * l, c)).view(b, l, 3, cfg.heads, cfg.head_dim)
@@ -199,9 +209,17 @@ class WanBlockW8A8:
         state = sage_core.prequantize_sageattn_from_qk(qk, v, sm_scale=cfg.head_dim ** -0.5)
         del qkv, q, k, qk
         out = sage_core.sageattn_from_prequantized(state)
-        return self.self_o(out.reshape(b * l, c)).view(b, l, c)
+        return self._project(self.self_o, out.reshape(b * l, c), residual, gate).view(b, l, c)
 
-    def cross_attention(self, h: torch.Tensor, context: torch.Tensor) -> torch.Tensor:
+    def _project(self, lin: W8A8Linear, x2d: torch.Tensor, residual, gate, gelu: bool = False) -> torch.Tensor:
+        if residual is None:
+            return lin(x2d, gelu=gelu)
+        b, l, c = residual.shape
+        g = None if gate is None else gate.reshape(b, c)
+        return lin(x2d, gelu=gelu, residual=residual.reshape(b * l, c), gate=g, gate_rows=l)
+
+    def cross_attention(self, h: torch.Tensor, context: torch.Tensor,
+                        residual: Optional[torch.Tensor] = None) -> torch.Tensor:
         cfg = self.cfg
         b, l, c = h.shape
         lc = context.shape[1]
@@ -214,12 +232,13 @@ class WanBlockW8A8:
         state = sage_core.prequantize_sageattn_from_qk(qk, v, sm_scale=cfg.head_dim ** -0.5)
         del q, kv, k, qk
         out = sage_core.sageattn_from_prequantized(state)
-        return self.cross_o(out.reshape(b * l, c)).view(b, l, c)
+        return self._project(self.cross_o, out.reshape(b * l, c), residual, None).view(b, l, c)
 
-    def ffn(self, h: torch.Tensor) -> torch.Tensor:
+    def ffn(self, h: torch.Tensor, residual: Optional[torch.Tensor] = None,
+            gate: Optional[torch.Tensor] = None) -> torch.Tensor:
         b, l, c = h.shape
         up = self.ffn_up(h.reshape(b * l, c))
-        return self.ffn_down(up, gelu=True).view(b, l, c)
+        return self._project(self.ffn_down, up, residual, gate, gelu=True).view(b, l, c)
 
     def modulation_chunks(self, e: torch.Tensor) -> list[torch.Tensor]:
         """(modulation + e) split into the six [B, 1, C] bf16 rows."""
@@ -236,15 +255,14 @@ class WanBlockW8A8:
             raise TypeError(f"Wan block context must be bf16 [B, Lc, {cfg.dim}]")
         lnadaln = torch.ops.turing_utils.layer_norm_adaln
         e0, e1, e2, e3, e4, e5 = self.modulation_chunks(e)
-        y = self.self_attention(lnadaln(x, e1, e0, cfg.eps), freqs)
-        x = torch.addcmul(x, y, e2)
+        x = x.contiguous()
+        # each residual add runs in the epilogue of the projection before it
+        x = self.self_attention(lnadaln(x, e1, e0, cfg.eps), freqs, residual=x, gate=e2)
         b = x.shape[0]
         # the op takes one modulation row per sample: the affine row repeats
-        y = self.cross_attention(lnadaln(x, self.norm3_scale.expand(b, 1, cfg.dim),
-                                         self.norm3_shift.expand(b, 1, cfg.dim), cfg.eps), context)
-        x = x + y
-        y = self.ffn(lnadaln(x, e4, e3, cfg.eps))
-        return torch.addcmul(x, y, e5)
+        x = self.cross_attention(lnadaln(x, self.norm3_scale.expand(b, 1, cfg.dim),
+                                         self.norm3_shift.expand(b, 1, cfg.dim), cfg.eps), context, residual=x)
+        return self.ffn(lnadaln(x, e4, e3, cfg.eps), residual=x, gate=e5)
 
     __call__ = forward
 

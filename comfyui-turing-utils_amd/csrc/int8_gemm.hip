@@ -172,11 +172,17 @@ struct Frags {
     i32x4 b[kFragsM];  // activation rows (MFMA B operand)
 };
 
-template <bool kI32Out>
+// (1, 1) in bf16: the gate of a residual add without one.
+constexpr uint32_t kBf16OnePair = 0x3f803f80u;
+
+// kResidual: out = bf16_rn(fma(y, gate[row / gate_rows][col], residual[row][col]))
+// with y the bf16 epilogue value (gate 1 when absent).  residual may be out.
+template <bool kI32Out, bool kResidual>
 __global__ __launch_bounds__(kThreads, kWaves / 4) void int8_gemm_kernel(
     const int8_t *__restrict__ a, const int8_t *__restrict__ w, const float *__restrict__ as,
     const float *__restrict__ ws, const float *__restrict__ bias, void *__restrict__ out,
-    int64_t m, int64_t n, int64_t k, int tiles_m, int tiles_n) {
+    int64_t m, int64_t n, int64_t k, int tiles_m, int tiles_n, const uint16_t *residual, const uint16_t *gate,
+    int64_t gate_rows) {
     __shared__ __align__(1024) int8_t lds[kStages][kStageBytes];
 
     const int tid = threadIdx.x;
@@ -328,12 +334,35 @@ __global__ __launch_bounds__(kThreads, kWaves / 4) void int8_gemm_kernel(
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         // 4 rows of 16 chunks per pass
         const int rsub = lane >> 4, c = lane & 15;
+        // residual (and gate) chunks of every pass, loaded before any store
+        u32x4 res[kResidual ? kRows / 4 : 1], gv[kResidual ? kRows / 4 : 1];
+        if constexpr (kResidual) {
+#pragma unroll
+            for (int pass = 0; pass < kRows / 4; ++pass) {
+                const int64_t row = min(row_base + pass * 4 + rsub, m - 1);
+                const int64_t col = min(col_base + c * 8, n - 8);
+                res[pass] = *reinterpret_cast<const u32x4 *>(residual + row * n + col);
+                gv[pass] = gate ? *reinterpret_cast<const u32x4 *>(gate + (row / gate_rows) * n + col)
+                                : u32x4{kBf16OnePair, kBf16OnePair, kBf16OnePair, kBf16OnePair};
+            }
+        }
 #pragma unroll
         for (int pass = 0; pass < kRows / 4; ++pass) {
             const int lrow = pass * 4 + rsub;
             const int64_t row = row_base + lrow;
             const int64_t col = col_base + c * 8;
-            const u32x4 val = *reinterpret_cast<const u32x4 *>(tile + lrow * 256 + ((c ^ (lrow & 15)) << 4));
+            u32x4 val = *reinterpret_cast<const u32x4 *>(tile + lrow * 256 + ((c ^ (lrow & 15)) << 4));
+            if constexpr (kResidual) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const uint32_t y = val[e], r = res[pass][e], gg = gv[pass][e];
+                    const float lo = __builtin_fmaf(__uint_as_float(y << 16), __uint_as_float(gg << 16),
+                                                    __uint_as_float(r << 16));
+                    const float hi = __builtin_fmaf(__uint_as_float(y & 0xffff0000u), __uint_as_float(gg & 0xffff0000u),
+                                                    __uint_as_float(r & 0xffff0000u));
+                    val[e] = pack_bf16x2(lo, hi);
+                }
+            }
             if (row < m && col < n)  // n % 8 == 0: a chunk is all in or all out
                 __builtin_nontemporal_store(val, reinterpret_cast<u32x4 *>(static_cast<uint16_t *>(out) + row * n + col));
         }
@@ -385,15 +414,16 @@ int32_t check_gemm_args(const int8_t *a, const int8_t *w, const void *out, int64
     return require_gfx950();
 }
 
-template <bool kI32Out>
+template <bool kI32Out, bool kResidual = false>
 int32_t launch_gemm(const int8_t *a, const int8_t *w, const float *as, const float *ws, const float *bias,
-                    void *out, int64_t m, int64_t n, int64_t k, void *stream) {
+                    void *out, int64_t m, int64_t n, int64_t k, void *stream, const uint16_t *residual = nullptr,
+                    const uint16_t *gate = nullptr, int64_t gate_rows = 1) {
     if (m == 0) return 0;
     const int tiles_m = static_cast<int>((m + kBM - 1) / kBM);
     const int tiles_n = static_cast<int>((n + kBN - 1) / kBN);
-    int8_gemm_kernel<kI32Out><<<dim3(tiles_m * tiles_n), kThreads, 0, static_cast<hipStream_t>(stream)>>>(
-        a, w, as, ws, bias, out, m, n, k, tiles_m, tiles_n);
-    return check_launch(kI32Out ? "tu_int8_gemm_i32" : "tu_int8_gemm_bf16");
+    int8_gemm_kernel<kI32Out, kResidual><<<dim3(tiles_m * tiles_n), kThreads, 0, static_cast<hipStream_t>(stream)>>>(
+        a, w, as, ws, bias, out, m, n, k, tiles_m, tiles_n, residual, gate, gate_rows);
+    return check_launch(kI32Out ? "tu_int8_gemm_i32" : kResidual ? "tu_int8_gemm_bf16_residual" : "tu_int8_gemm_bf16");
 }
 
 }  // namespace
@@ -408,6 +438,24 @@ extern "C" int32_t tu_int8_gemm_bf16(const int8_t *a, const int8_t *w, const flo
     TU_REQUIRE((reinterpret_cast<uintptr_t>(w_scale) & 15) == 0 && (reinterpret_cast<uintptr_t>(bias) & 15) == 0,
                "INT8 GEMM weight scale and bias must be 16-byte aligned");
     return launch_gemm<false>(a, w, a_scale, w_scale, bias, out_bf16, m, n, k, stream);
+}
+
+extern "C" int32_t tu_int8_gemm_bf16_residual(const int8_t *a, const int8_t *w, const float *a_scale,
+                                              const float *w_scale, const float *bias, const void *residual_bf16,
+                                              const void *gate_bf16, int64_t gate_rows, void *out_bf16, int64_t m,
+                                              int64_t n, int64_t k, void *stream) {
+    using namespace tu;
+    if (check_gemm_args(a, w, out_bf16, m, n, k)) return -1;
+    TU_REQUIRE(a_scale && w_scale && residual_bf16, "INT8 GEMM scales and residual must be non-null");
+    TU_REQUIRE((reinterpret_cast<uintptr_t>(w_scale) & 15) == 0 && (reinterpret_cast<uintptr_t>(bias) & 15) == 0 &&
+                   (reinterpret_cast<uintptr_t>(residual_bf16) & 15) == 0 &&
+                   (reinterpret_cast<uintptr_t>(gate_bf16) & 15) == 0,
+               "INT8 GEMM weight scale, bias, residual and gate must be 16-byte aligned");
+    TU_REQUIRE(!gate_bf16 || gate_rows > 0, "INT8 GEMM gate_rows must be positive with a gate (got %lld)",
+               static_cast<long long>(gate_rows));
+    return launch_gemm<false, true>(a, w, a_scale, w_scale, bias, out_bf16, m, n, k, stream,
+                                    static_cast<const uint16_t *>(residual_bf16),
+                                    static_cast<const uint16_t *>(gate_bf16), gate_bf16 ? gate_rows : 1);
 }
 
 extern "C" int32_t tu_int8_gemm_i32(const int8_t *a, const int8_t *w, int32_t *acc, int64_t m, int64_t n,

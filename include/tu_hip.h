@@ -88,6 +88,20 @@ int32_t tu_int8_gemm_bf16(const int8_t *a, const int8_t *w, const float *a_scale
                           const float *w_scale, const float *bias, void *out_bf16, int64_t m,
                           int64_t n, int64_t k, void *stream);
 
+/* The same GEMM with a gated residual add fused into the epilogue, for a DiT
+ * block's x + y * gate: out[m][n] = bf16_rn(fma(y, g, residual[m][n])) with
+ * y the tu_int8_gemm_bf16 value above, g = gate[m / gate_rows][n] (bf16 [G, n],
+ * one row per gate_rows consecutive output rows, e.g. per batch entry) or 1
+ * when gate is NULL (then exactly bf16_rn(y + residual)).  residual: bf16
+ * [m, n], may be out (in place); residual, gate 16-byte aligned.
+ * No counterpart in the reference's ops: it fuses the torch add / addcmul
+ * that a ComfyUI Wan block (the caller of comfyui_turing_utils/adapters/
+ * wan.py:55-137) runs after the o and FFN-down projections. */
+int32_t tu_int8_gemm_bf16_residual(const int8_t *a, const int8_t *w, const float *a_scale,
+                                   const float *w_scale, const float *bias, const void *residual_bf16,
+                                   const void *gate_bf16, int64_t gate_rows, void *out_bf16, int64_t m,
+                                   int64_t n, int64_t k, void *stream);
+
 /* acc[m][n] = sum_k a[m][k] * w[n][k] as int32, row-major [m, n].  Same
  * kernel as tu_int8_gemm_bf16 with the epilogue replaced by an int32 store;
  * the accumulator half of the reference's cuBLAS INT8 + epilogue split

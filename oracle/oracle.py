@@ -67,6 +67,8 @@ def lib():
             L.or_int8_gemm_i32.argtypes = [_p, _p, _i64, _i64, _i64, _p]
             L.or_int8_epilogue_bf16.restype = _i32
             L.or_int8_epilogue_bf16.argtypes = [_p, _i64, _p, _p, _i32, _p, _i64, _i64, _p]
+            L.or_residual_gate_bf16.restype = _i32
+            L.or_residual_gate_bf16.argtypes = [_p, _p, _p, _i64, _i64, _i64, _p]
             L.or_sage_kmean.restype = _i32
             L.or_sage_kmean.argtypes = [_p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p]
             L.or_sage_quant.restype = _i32
@@ -223,6 +225,22 @@ def epilogue_bf16(acc: np.ndarray, a_scale: np.ndarray, w_scale: np.ndarray,
     out = np.empty((m, cols), dtype=np.uint16)
     _check(lib().or_int8_epilogue_bf16(_ptr(acc), ld, _ptr(a_scale), _ptr(w_scale), scalar,
                                        None if b is None else _ptr(b), m, cols, _ptr(out)), "epilogue")
+    return out
+
+
+def residual_gate_bf16(y_bits: np.ndarray, residual_bits: np.ndarray, gate_bits: np.ndarray | None = None,
+                       gate_rows: int = 1) -> np.ndarray:
+    """bf16 bits of bf16_rn(fma(y, gate[i // gate_rows][j] or 1, residual))."""
+    y = np.ascontiguousarray(y_bits, dtype=np.uint16)
+    r = np.ascontiguousarray(residual_bits, dtype=np.uint16)
+    m, n = y.shape
+    assert r.shape == (m, n)
+    g = None if gate_bits is None else np.ascontiguousarray(gate_bits, dtype=np.uint16)
+    if g is not None:
+        assert g.shape == ((m + gate_rows - 1) // gate_rows, n)
+    out = np.empty((m, n), dtype=np.uint16)
+    _check(lib().or_residual_gate_bf16(_ptr(y), _ptr(r), None if g is None else _ptr(g), gate_rows, m, n,
+                                       _ptr(out)), "residual_gate")
     return out
 
 

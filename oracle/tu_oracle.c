@@ -23,6 +23,7 @@
  *                             vs IEEE division (or_check_markstein_quant)
  *   or_int8_gemm_i32          pinned: numpy int64 matmul (brute force)
  *   or_int8_epilogue_bf16     pinned: fp64 closed form within bf16 rounding
+ *   or_residual_gate_bf16     pinned: numpy fp64 product-plus-sum rounded once
  *   or_sage_kmean             pinned: fp64 mean within one bf16 ulp
  *   or_sage_quant             pinned: invariants (max|q|==127, dequant error)
  *   or_sage_attn_rows         pinned: fp64 SDPA on dequantized inputs, torch SDPA
@@ -311,6 +312,21 @@ OR_API int or_int8_epilogue_bf16(const int32_t *acc, int64_t acc_ld, const float
             v = v * ws[ws_scalar ? 0 : j];
             if (bias) v = v + bias[j];
             out[i * n + j] = or_f32_to_bf16_rne(v);
+        }
+    }
+    return 0;
+}
+
+/* Gated residual of tu_int8_gemm_bf16_residual (no reference counterpart:   */
+/* the torch add / addcmul after a Wan block's o and FFN-down projections):  */
+/*   out = bf16_rn(fmaf(y, g, r)), g = gate[i / gate_rows][j] or 1.          */
+OR_API int or_residual_gate_bf16(const uint16_t *y, const uint16_t *residual, const uint16_t *gate,
+                                 int64_t gate_rows, int64_t m, int64_t n, uint16_t *out) {
+    for (int64_t i = 0; i < m; ++i) {
+        for (int64_t j = 0; j < n; ++j) {
+            const float g = gate ? or_bf16_to_f32(gate[(i / gate_rows) * n + j]) : 1.0f;
+            out[i * n + j] = or_f32_to_bf16_rne(fmaf(or_bf16_to_f32(y[i * n + j]), g,
+                                                     or_bf16_to_f32(residual[i * n + j])));
         }
     }
     return 0;

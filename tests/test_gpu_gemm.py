@@ -66,6 +66,37 @@ def test_int8_linear_epilogue_exact(gpu_device, m, n, k, with_bias):
     assert bad.size == 0, f"{len(bad)} outputs differ, first {bad[:5].tolist()}"
 
 
+@pytest.mark.parametrize("gate_rows", [None, 1, 37])
+@pytest.mark.parametrize("m,n,k,with_bias", [(300, 264, 192, True), (257, 520, 1040, False), (96, 5120, 1536, True)])
+def test_int8_linear_residual_exact(gpu_device, m, n, k, with_bias, gate_rows):
+    """The gated residual epilogue: bf16_rn(fma(y, gate[i // gate_rows], residual)) with
+    y the bf16 epilogue output; ragged M and N tiles, ungated and per-row / per-block gates."""
+    print(f"[int8_linear_residual] m={m} n={n} k={k} bias={with_bias} gate_rows={gate_rows}", flush=True)
+    a = _rand_i8((m, k), 11 + m)
+    w, ws, bias = inputs.weights(n, k, 4, with_bias)
+    g = torch.Generator().manual_seed(8)
+    as_ = torch.empty(m).uniform_(1e-3, 1e-1, generator=g)
+    residual = (torch.randn(m, n, generator=g) * 4).to(torch.bfloat16)
+    gate = None
+    if gate_rows is not None:
+        gate = torch.empty((m + gate_rows - 1) // gate_rows, n).uniform_(-2, 2, generator=g).to(torch.bfloat16)
+    dev = gpu_device
+    res_dev = residual.to(dev)
+    out = torch.ops.turing_utils.int8_linear_residual(
+        a.to(dev), w.to(dev), as_.to(dev), ws.to(dev), None if bias is None else bias.to(dev),
+        res_dev, None if gate is None else gate.to(dev), 1 if gate_rows is None else gate_rows,
+    )
+    torch.cuda.synchronize(dev)
+    acc = oracle.int8_gemm_i32(a.numpy(), w.numpy())
+    y = oracle.epilogue_bf16(acc, as_.numpy(), ws.numpy(), None if bias is None else bias.numpy())
+    ref = oracle.residual_gate_bf16(y, inputs.bits(residual), None if gate is None else inputs.bits(gate),
+                                    1 if gate_rows is None else gate_rows)
+    got = inputs.bits(out)
+    bad = np.argwhere(got != ref)
+    assert bad.size == 0, f"{len(bad)} outputs differ, first {bad[:5].tolist()}"
+    np.testing.assert_array_equal(inputs.bits(res_dev), inputs.bits(residual))
+
+
 def test_int8_linear_config1_rows(gpu_device):
     """BASELINE config 1 through the drop-in ops (quantize G=128, then int8_linear);
     128 sampled rows checked bit-exact against the oracle chain."""

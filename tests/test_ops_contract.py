@@ -51,6 +51,14 @@ def test_linear_and_epilogue_fake_contracts():
     assert epi.shape == (7, 64) and epi.dtype == torch.bfloat16
     epi = torch.ops.turing_utils.dequantize_int8_bf16(accumulator, row_scale, column_scale)
     assert epi.shape == (7, 80)
+    residual = torch.empty((7, 64), dtype=torch.bfloat16, device=META)
+    gate = torch.empty((2, 64), dtype=torch.bfloat16, device=META)
+    out = torch.ops.turing_utils.int8_linear_residual(activation, weight, row_scale, column_scale, None,
+                                                      residual, gate, 4)
+    assert out.shape == (7, 64) and out.dtype == torch.bfloat16
+    with pytest.raises(Exception, match="gate"):
+        torch.ops.turing_utils.int8_linear_residual(activation, weight, row_scale, column_scale, None,
+                                                    residual, gate, 1)
 
 
 def test_sage_fake_contract_and_fullgraph_leaf():

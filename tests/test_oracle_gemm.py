@@ -62,3 +62,33 @@ def test_epilogue_scalar_weight_scale_and_column_slice():
     exact = acc[:, :17].astype(np.float64) * as_[:, None] * 3e-3
     assert out.shape == (9, 17)
     assert np.all(np.abs(out - exact) <= np.abs(exact) * 2.0 ** -8 + 1e-30)
+
+
+def _bf16_rne(x64: np.ndarray) -> np.ndarray:
+    """fp64 -> fp32 (one rounding) -> bf16 bits by round-to-nearest-even on the fp32 pattern."""
+    u = np.asarray(x64, np.float64).astype(np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+@pytest.mark.parametrize("gate_rows,gated", [(1, True), (37, True), (1, False)])
+def test_residual_gate_closed_form(gate_rows, gated):
+    """bf16 y * g is exact in fp64 and fp32, so fma(y, g, r) in fp32 is the fp64
+    sum rounded once to fp32, then to bf16; a gate indexed by i % rows, a dropped
+    gate or a dropped residual must all show."""
+    rng = np.random.default_rng(gate_rows + 7 * gated)
+    m, n = 131, 48
+    y = oracle.f32_to_bf16_bits(rng.standard_normal((m, n)).astype(np.float32)).reshape(m, n)
+    r = oracle.f32_to_bf16_bits((rng.standard_normal((m, n)) * 4).astype(np.float32)).reshape(m, n)
+    rows = (m + gate_rows - 1) // gate_rows
+    g = oracle.f32_to_bf16_bits(rng.uniform(-2, 2, (rows, n)).astype(np.float32)).reshape(rows, n) if gated else None
+    out = oracle.residual_gate_bf16(y, r, g, gate_rows)
+    yf, rf = _bf16_to_f64(y), _bf16_to_f64(r)
+    gf = np.ones((m, n)) if g is None else _bf16_to_f64(g)[np.arange(m) // gate_rows]
+    np.testing.assert_array_equal(out, _bf16_rne(yf * gf + rf))
+    wrong = [_bf16_rne(yf * gf), _bf16_rne(rf)]
+    if g is not None:
+        wrong.append(_bf16_rne(yf + rf))
+    if g is not None and gate_rows > 1:
+        wrong.append(_bf16_rne(yf * _bf16_to_f64(g)[np.arange(m) % rows] + rf))
+    for w_ in wrong:
+        assert np.any(out != w_)

@@ -110,6 +110,24 @@ def test_gelu_quant_exact(gpu_device, group, m, k, seed):
     np.testing.assert_array_equal(q.cpu().numpy(), q_ref)
 
 
+def test_gelu_every_bf16_input(gpu_device):
+    """Every finite bf16 value x, one per row at column 0 of an otherwise zero
+    row: the row scale carries the bits of gelu(x), so the whole activation
+    domain is checked bit for bit against the oracle."""
+    print("[convrot gelu] every finite bf16 input", flush=True)
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    bits = bits[(bits & 0x7F80) != 0x7F80]
+    x = np.zeros((bits.size, 128), np.uint16)
+    x[:, 0] = bits
+    xt = inputs.from_bits(x)
+    q, s = torch.ops.turing_utils.bf16_gelu_int8_convrot_quantize(xt.to(gpu_device), 128)
+    q_ref, s_ref = oracle.convrot_quant(x, 128, act=oracle.ACT_GELU_TANH)
+    got = s.cpu().numpy().reshape(-1).view(np.uint32)
+    bad = np.flatnonzero(got != s_ref.view(np.uint32))
+    assert bad.size == 0, f"{bad.size} scales differ, first inputs {[hex(int(v)) for v in bits[bad[:5]]]}"
+    np.testing.assert_array_equal(q.cpu().numpy(), q_ref)
+
+
 @pytest.mark.parametrize("group", [128, 256])
 @pytest.mark.parametrize("m,k,seed", [(5, 512, 51), (48, 5120, 52)])
 def test_swiglu_quant_exact(gpu_device, group, m, k, seed):

@@ -94,7 +94,8 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(the hot path shards by tokens/heads with no exchange; see DESIGN.md). "
+              "(the hot path shards by tokens for the linears and by heads for the attention, "
+              "with no exchange between GPUs). "
               "Run with --gpus 1.", file=sys.stderr)
         return 2
 

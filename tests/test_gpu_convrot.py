@@ -128,6 +128,24 @@ def test_gelu_every_bf16_input(gpu_device):
     np.testing.assert_array_equal(q.cpu().numpy(), q_ref)
 
 
+def test_swiglu_every_bf16_gate(gpu_device):
+    """Every finite bf16 gate g with up = 1, one per row at column 0 of
+    [gate | up] rows that are otherwise zero: the row scale carries the bits of
+    g / (1 + exp(-g)) over the gate's whole bf16 domain, checked bit for bit."""
+    print("[convrot swiglu] every finite bf16 gate", flush=True)
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    bits = bits[(bits & 0x7F80) != 0x7F80]
+    x = np.zeros((bits.size, 256), np.uint16)
+    x[:, 0] = bits
+    x[:, 128] = 0x3F80  # up = 1.0
+    q, s = torch.ops.turing_utils.bf16_int8_convrot_quantize(inputs.from_bits(x).to(gpu_device), 128, swiglu=True)
+    q_ref, s_ref = oracle.convrot_quant(x, 128, act=oracle.ACT_SWIGLU)
+    got = s.cpu().numpy().reshape(-1).view(np.uint32)
+    bad = np.flatnonzero(got != s_ref.view(np.uint32))
+    assert bad.size == 0, f"{bad.size} scales differ, first gates {[hex(int(v)) for v in bits[bad[:5]]]}"
+    np.testing.assert_array_equal(q.cpu().numpy(), q_ref)
+
+
 @pytest.mark.parametrize("group", [128, 256])
 @pytest.mark.parametrize("m,k,seed", [(5, 512, 51), (48, 5120, 52)])
 def test_swiglu_quant_exact(gpu_device, group, m, k, seed):

@@ -230,14 +230,20 @@ def _turing_dequantize_int8_bf16_fake(accumulator, activation_scale, weight_scal
 SUPPORTED_GROUP_SIZES = (128, 256)
 ACT_NONE, ACT_GELU_TANH, ACT_SWIGLU = 0, 1, 2
 STAGED_SCALE = 0x100  # scale = absmax * (1/127), the two-pass kernels' formula
+FP16_INPUT = 0x200  # x holds float16 (the two-pass kernels' InputType = half)
 MAX_CONVROT_COLUMNS = 65536  # activated width; the kernel keeps a whole row in registers
 
 
 def _convrot_quantize(x: torch.Tensor, group_size: int, act: int, what: str,
                       staged: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
+    """staged=True is the two-pass ops' contract: staged scale formula and
+    float16 or bfloat16 input (ops.py:163-186, :215-233); the row-buffer ops
+    take bfloat16 only (ops.py:257-282, :313-331)."""
     _require_device(x, what)
-    if x.dtype != torch.bfloat16:
-        # the reference's two-pass ops also take float16; only bf16 is built here
+    if staged:
+        if x.dtype not in (torch.float16, torch.bfloat16):
+            raise TypeError(f"{what} input must be float16 or bfloat16")
+    elif x.dtype != torch.bfloat16:
         raise TypeError(f"{what} input must be bfloat16")
     if x.ndim != 2:
         raise ValueError(f"{what} input must be 2D")
@@ -257,8 +263,9 @@ def _convrot_quantize(x: torch.Tensor, group_size: int, act: int, what: str,
     q = torch.empty((rows, hidden), dtype=torch.int8, device=x.device)
     scales = torch.empty((rows, 1), dtype=torch.float32, device=x.device)
     with torch.cuda.device(x.device):
+        flags = (STAGED_SCALE if staged else 0) | (FP16_INPUT if x.dtype == torch.float16 else 0)
         _lib.call("tu_convrot_quant_i8", x.data_ptr(), q.data_ptr(), scales.data_ptr(), rows, hidden,
-                  group_size, act | (STAGED_SCALE if staged else 0), _lib.stream_of(x.device))
+                  group_size, act | flags, _lib.stream_of(x.device))
     return q, scales
 
 
@@ -304,16 +311,18 @@ def _turing_bf16_gelu_int8_convrot_quantize_fake(x, group_size=256):
 # ---------------------------------------------------------------------------
 # Two-pass ("staged") fused-activation quantizers (reference ops.py:163-186,
 # :215-233; bindings.cpp:474-510, :550-600).  The reference computes these in
-# two kernels through a global bf16 copy of the rotated rows; here the same
-# single-pass kernel runs with the staged scale formula, so codes and scales
-# equal the reference's two-pass results.
+# two kernels through a global bf16 / fp16 copy of the rotated rows; here the
+# same single-pass kernel runs with the staged scale formula (and fp16
+# elements for float16 input), so codes and scales equal the reference's
+# two-pass results.
 # ---------------------------------------------------------------------------
 @torch.library.custom_op("turing_utils::swiglu_int8_convrot_quantize", mutates_args=())
 def turing_swiglu_int8_convrot_quantize(
     x: torch.Tensor,
     group_size: int = 256,
 ) -> tuple[torch.Tensor, torch.Tensor]:
-    """SwiGLU over the [gate | up] halves of each row, then ConvRot INT8 quantization."""
+    """SwiGLU over the [gate | up] halves of each row (float16 or bfloat16),
+    then ConvRot INT8 quantization."""
     return _convrot_quantize(x, group_size, ACT_SWIGLU, "SwiGLU ConvRot", staged=True)
 
 
@@ -330,7 +339,8 @@ def turing_gelu_int8_convrot_quantize(
     x: torch.Tensor,
     group_size: int = 256,
 ) -> tuple[torch.Tensor, torch.Tensor]:
-    """tanh-GELU (rounded to bf16), then ConvRot INT8 quantization."""
+    """tanh-GELU (rounded to the input type, float16 or bfloat16), then
+    ConvRot INT8 quantization."""
     return _convrot_quantize(x, group_size, ACT_GELU_TANH, "GELU ConvRot", staged=True)
 
 
@@ -377,4 +387,40 @@ def turing_layer_norm_adaln(
 
 @turing_layer_norm_adaln.register_fake
 def _turing_layer_norm_adaln_fake(x, scale, shift, epsilon=1.0e-5):
+    return torch.empty_like(x)
+
+
+# ---------------------------------------------------------------------------
+# LayerNorm with an elementwise affine weight / bias (no reference op: ComfyUI's
+# torch LayerNorm runs the Wan block's norm3, which the reference leaves alone)
+# ---------------------------------------------------------------------------
+@torch.library.custom_op("turing_utils::layer_norm_affine", mutates_args=())
+def turing_layer_norm_affine(
+    x: torch.Tensor,
+    weight: torch.Tensor,
+    bias: torch.Tensor,
+    epsilon: float = 1.0e-5,
+) -> torch.Tensor:
+    """layer_norm(x, (H,), weight, bias, epsilon) over the last dimension of
+    x [..., H]: fp32 statistics in the order of layer_norm_adaln, one rounding
+    of fma(normalized, weight, bias) to x's dtype."""
+    _require_device(x, "LayerNorm")
+    if x.dtype not in _LN_DTYPES or x.ndim < 1:
+        raise TypeError("LayerNorm input must be float16, bfloat16, or float32")
+    hidden = x.shape[-1]
+    weight = weight.to(device=x.device, dtype=x.dtype).reshape(-1).contiguous()
+    bias = bias.to(device=x.device, dtype=x.dtype).reshape(-1).contiguous()
+    if weight.numel() != hidden or bias.numel() != hidden:
+        raise ValueError(f"LayerNorm weight and bias must hold {hidden} values")
+    x = x.contiguous()
+    out = torch.empty_like(x)
+    rows = x.numel() // hidden if hidden else 0
+    with torch.cuda.device(x.device):
+        _lib.call("tu_layer_norm_affine", x.data_ptr(), weight.data_ptr(), bias.data_ptr(), out.data_ptr(),
+                  _LN_DTYPES[x.dtype], rows, hidden, float(epsilon), _lib.stream_of(x.device))
+    return out
+
+
+@turing_layer_norm_affine.register_fake
+def _turing_layer_norm_affine_fake(x, weight, bias, epsilon=1.0e-5):
     return torch.empty_like(x)

@@ -13,6 +13,14 @@
 // With the staged-scale flag the scale is absmax * (1/127) instead, as in the
 // reference's two-pass kernels (convrot_quant.cu:233-236) behind the
 // gelu_/swiglu_int8_convrot_quantize ops; everything else is identical.
+// With the fp16-input flag the elements are IEEE binary16, as the two-pass
+// kernels' InputType = half instantiation (convrot_quant.cu:158-248): GELU
+// output, rotated values and the quotient are rounded to fp16 where the bf16
+// path rounds to bf16, the absmax clip is 65504 (finite_max<half>, :58-62),
+// and the quotient is an IEEE division by fp16(scale) (quant_div_to_float,
+// :69-73).  fp16(scale) is 0 when scale < 2^-25 (all-zero or tiny rows): the
+// reference then divides by zero and its clamp maps the resulting +-inf to
+// 127 / -128 and NaN (0 / 0) to -128; the same happens here.
 // G = 128 is this build's extension: three radix-4 digits then the
 // orthonormal radix-2 digit (1/sqrt2)[[1,1],[1,-1]] on stride 64.
 //
@@ -118,27 +126,34 @@ __device__ __forceinline__ float exp_det_0_18(float v) {
     return __builtin_ldexpf(p, static_cast<int>(n));
 }
 
+template <bool kF16>
 __device__ __forceinline__ float tanh_det(float u) {
     if (u != u) return u;
     const float a = fabsf(u);
     const float e = exp_det_0_18(2.0f * fminf(a, 9.0f));
-    // 2 / b for b = e + 1 in [2, 7e7]: q0 = 2 rcp(b), one FMA residual and one
-    // FMA correction.  Equal to the IEEE quotient for every b that a bf16
-    // input reaches (the GELU quantizer's GPU test runs all of them).
+    // 2 / b for b = e + 1 in [2, 7e7].  bf16 inputs: q0 = 2 rcp(b), one FMA
+    // residual and one FMA correction, equal to the IEEE quotient for every b
+    // that a bf16 input reaches (the GELU quantizer's GPU test runs all of
+    // them).  fp16 inputs reach other values of b: IEEE division.
     const float b = e + 1.0f;
-    const float y = __builtin_amdgcn_rcpf(b);
-    const float q0 = 2.0f * y;
-    const float q = __builtin_fmaf(__builtin_fmaf(-q0, b, 2.0f), y, q0);
+    float q;
+    if constexpr (kF16) {
+        q = 2.0f / b;
+    } else {
+        const float y = __builtin_amdgcn_rcpf(b);
+        const float q0 = 2.0f * y;
+        q = __builtin_fmaf(__builtin_fmaf(-q0, b, 2.0f), y, q0);
+    }
     float t = 1.0f - q;
     t = a < 0.000244140625f ? a : t;
     t = a > 9.0f ? 1.0f : t;
     return __builtin_copysignf(t, u);
 }
 
-__device__ __forceinline__ float gelu_tanh_bf16(float x) {
+template <bool kF16>
+__device__ __forceinline__ float gelu_tanh_f32(float x) {
     const float inner = 0.7978845608028654f * (x + ((0.044715f * x) * x) * x);
-    const float act = (0.5f * x) * (1.0f + tanh_det(inner));
-    return bf16_round(act);
+    return (0.5f * x) * (1.0f + tanh_det<kF16>(inner));
 }
 
 __device__ __forceinline__ float swiglu(float gate, float up) { return (gate / (1.0f + exp_det(-gate))) * up; }
@@ -155,6 +170,30 @@ __device__ __forceinline__ uint16_t hw_bf16_bits(float v) {
 // bf16 arithmetic.
 __device__ __forceinline__ float hw_bf16_round(float v) { return bf16_bits_to_f32(hw_bf16_bits(v)); }
 
+// fp16 (RNE by the hardware conversion) and back.  The empty asm pins the
+// fp32 value first, so the compiler cannot fold "fp32 multiply, then round to
+// fp16" into one single-rounding mixed-precision FMA.
+__device__ __forceinline__ uint16_t hw_f16_bits(float v) {
+    asm("" : "+v"(v));
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
+}
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t b) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(b)));
+}
+__device__ __forceinline__ float hw_f16_round(float v) { return f16_bits_to_f32(hw_f16_bits(v)); }
+
+// Element type of the input and of the rotated row buffer.
+template <bool kF16>
+__device__ __forceinline__ float elem_to_f32(uint32_t b) {
+    if constexpr (kF16) return f16_bits_to_f32(b & 0xffffu);
+    else return bf16_bits_to_f32(b & 0xffffu);
+}
+template <bool kF16>
+__device__ __forceinline__ uint32_t elem_bits(float v) {
+    if constexpr (kF16) return hw_f16_bits(v);
+    else return hw_bf16_bits(v);
+}
+
 __device__ __forceinline__ int32_t quant_code(float v, float rs, float ry) {
     const float divided = hw_bf16_round(div_markstein(v, rs, ry));
     float qf = __builtin_rintf(divided);
@@ -162,8 +201,24 @@ __device__ __forceinline__ int32_t quant_code(float v, float rs, float ry) {
     return static_cast<int32_t>(qf);
 }
 
+// fp16 elements: fp16(v / rs) with IEEE division (rs may be 0, see the top).
+__device__ __forceinline__ int32_t quant_code_f16(float v, float rs) {
+    const float divided = hw_f16_round(v / rs);
+    float qf = __builtin_rintf(divided);
+    qf = fminf(127.0f, fmaxf(-128.0f, qf));
+    return static_cast<int32_t>(qf);
+}
+
+// The GELU output is rounded to the element type before the rotation
+// (convrot_quant.cu:153-155); SwiGLU's is not (:137-143).
+template <bool kF16>
 __device__ __forceinline__ float activate(float v, float up, std::integral_constant<int, 0>) { return v; }
-__device__ __forceinline__ float activate(float v, float up, std::integral_constant<int, 1>) { return gelu_tanh_bf16(v); }
+template <bool kF16>
+__device__ __forceinline__ float activate(float v, float up, std::integral_constant<int, 1>) {
+    if constexpr (kF16) return hw_f16_round(gelu_tanh_f32<true>(v));
+    else return bf16_round(gelu_tanh_f32<false>(v));
+}
+template <bool kF16>
 __device__ __forceinline__ float activate(float v, float up, std::integral_constant<int, 2>) { return swiglu(v, up); }
 
 // Raw bf16 input of one lane for one pass: 16 columns (and 16 "up" columns
@@ -200,7 +255,7 @@ __device__ __forceinline__ void load_lane(LaneInput<kAct> &in, const uint16_t *x
 // element index 16 L + p with L = l % (G/16), p = d0 + 4 d1.  After the
 // transpose a lane holds, for G = 256, p = L and t = d2 + 4 d3 = 0..15; for
 // G = 128, p = 2L and 2L + 1 (z[t] and z[8 + t]) with t = d2 + 4 d3 = 0..7.
-template <int G, int kAct, int kPasses>
+template <int G, int kAct, int kPasses, bool kF16>
 __global__ __launch_bounds__(1024) void convrot_quant_i8_kernel(
     const uint16_t *__restrict__ x, int8_t *__restrict__ q, float *__restrict__ scales, int k, int staged_scale) {
     extern __shared__ __align__(16) unsigned char smem[];
@@ -243,10 +298,10 @@ __global__ __launch_bounds__(1024) void convrot_quant_i8_kernel(
         for (int j = 0; j < 8; ++j) {
             const uint32_t w = in[pass].x[j / 4][j % 4];
             const uint32_t u = kAct == 2 ? in[pass].up[(j / 4) % (kAct == 2 ? 2 : 1)][j % 4] : 0u;
-            v[2 * j] = activate(bf16_bits_to_f32(w & 0xffffu), bf16_bits_to_f32(u & 0xffffu),
-                                std::integral_constant<int, kAct>{});
-            v[2 * j + 1] = activate(bf16_bits_to_f32(w >> 16), bf16_bits_to_f32(u >> 16),
-                                    std::integral_constant<int, kAct>{});
+            v[2 * j] = activate<kF16>(elem_to_f32<kF16>(w), elem_to_f32<kF16>(u),
+                                      std::integral_constant<int, kAct>{});
+            v[2 * j + 1] = activate<kF16>(elem_to_f32<kF16>(w >> 16), elem_to_f32<kF16>(u >> 16),
+                                          std::integral_constant<int, kAct>{});
         }
         // Digits d0 (stride 1) and d1 (stride 4) in registers (convrot_quant.cu:384-391).
 #pragma unroll
@@ -305,8 +360,7 @@ __global__ __launch_bounds__(1024) void convrot_quant_i8_kernel(
             // G = 256: t = 2j, 2j + 1 of p = L.  G = 128: p = 2L (low), 2L + 1 (high) of t = j.
             const float lo = G == 256 ? z[2 * j] : z[j];
             const float hi = G == 256 ? z[2 * j + 1] : z[8 + j];
-            packed[pass][j] =
-                static_cast<uint32_t>(hw_bf16_bits(lo)) | (static_cast<uint32_t>(hw_bf16_bits(hi)) << 16);
+            packed[pass][j] = elem_bits<kF16>(lo) | (elem_bits<kF16>(hi) << 16);
         }
     }
 
@@ -315,10 +369,10 @@ __global__ __launch_bounds__(1024) void convrot_quant_i8_kernel(
     __syncthreads();
     float amax = wave_amax[0];
     for (int w = 1; w < waves; ++w) amax = fmaxf(amax, wave_amax[w]);
-    const float clipped = fminf(amax, 3.38953139e38f);
+    const float clipped = fminf(amax, kF16 ? 65504.0f : 3.38953139e38f);
     const float scale = fmaxf(staged_scale ? clipped * (1.0f / 127.0f) : clipped / 127.0f, 1.0e-30f);
     if (tid == 0) scales[row] = scale;
-    const float rs = bf16_round(scale);
+    const float rs = kF16 ? hw_f16_round(scale) : bf16_round(scale);
     const float ry = 1.0f / rs;
 
     int8_t *qrow = q + row * static_cast<int64_t>(k);
@@ -334,8 +388,14 @@ __global__ __launch_bounds__(1024) void convrot_quant_i8_kernel(
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const uint32_t w = packed[pass][j];
-            const uint32_t c0 = static_cast<uint32_t>(quant_code(bf16_bits_to_f32(w & 0xffffu), rs, ry)) & 0xffu;
-            const uint32_t c1 = static_cast<uint32_t>(quant_code(bf16_bits_to_f32(w >> 16), rs, ry)) & 0xffu;
+            uint32_t c0, c1;
+            if constexpr (kF16) {
+                c0 = static_cast<uint32_t>(quant_code_f16(f16_bits_to_f32(w & 0xffffu), rs)) & 0xffu;
+                c1 = static_cast<uint32_t>(quant_code_f16(f16_bits_to_f32(w >> 16), rs)) & 0xffu;
+            } else {
+                c0 = static_cast<uint32_t>(quant_code(bf16_bits_to_f32(w & 0xffffu), rs, ry)) & 0xffu;
+                c1 = static_cast<uint32_t>(quant_code(bf16_bits_to_f32(w >> 16), rs, ry)) & 0xffu;
+            }
             if constexpr (G == 256) {
                 gb[32 * j + L] = static_cast<unsigned char>(c0);
                 gb[32 * j + 16 + L] = static_cast<unsigned char>(c1);
@@ -357,7 +417,8 @@ extern "C" int32_t tu_convrot_quant_i8(const void *x_bf16, int8_t *q, float *sca
     using namespace tu;
     TU_REQUIRE(group == 128 || group == 256, "ConvRot group_size must be 128 or 256, got %d", group);
     const int staged_scale = (act & TU_CONVROT_STAGED_SCALE) != 0;
-    act &= ~TU_CONVROT_STAGED_SCALE;
+    const bool f16 = (act & TU_CONVROT_FP16_INPUT) != 0;
+    act &= ~(TU_CONVROT_STAGED_SCALE | TU_CONVROT_FP16_INPUT);
     TU_REQUIRE(act >= TU_ACT_NONE && act <= TU_ACT_SWIGLU,
                "ConvRot input activation must be 0 (none), 1 (tanh-GELU) or 2 (SwiGLU), got %d", act);
     TU_REQUIRE(rows >= 0 && cols > 0 && cols % group == 0,
@@ -380,14 +441,19 @@ extern "C" int32_t tu_convrot_quant_i8(const void *x_bf16, int8_t *q, float *sca
     hipStream_t s = static_cast<hipStream_t>(stream);
     const auto *xp = static_cast<const uint16_t *>(x_bf16);
     const dim3 grid(static_cast<unsigned>(rows));
-#define TU_CONVROT_LAUNCH(G, A)                                                                                \
+#define TU_CONVROT_LAUNCH_T(G, A, F)                                                                          \
     do {                                                                                                      \
         switch (passes) {                                                                                     \
-            case 1: convrot_quant_i8_kernel<G, A, 1><<<grid, waves * 64, lds, s>>>(xp, q, scale, k, staged_scale); break; \
-            case 2: convrot_quant_i8_kernel<G, A, 2><<<grid, waves * 64, lds, s>>>(xp, q, scale, k, staged_scale); break; \
-            case 3: convrot_quant_i8_kernel<G, A, 3><<<grid, waves * 64, lds, s>>>(xp, q, scale, k, staged_scale); break; \
-            default: convrot_quant_i8_kernel<G, A, 4><<<grid, waves * 64, lds, s>>>(xp, q, scale, k, staged_scale); break; \
+            case 1: convrot_quant_i8_kernel<G, A, 1, F><<<grid, waves * 64, lds, s>>>(xp, q, scale, k, staged_scale); break; \
+            case 2: convrot_quant_i8_kernel<G, A, 2, F><<<grid, waves * 64, lds, s>>>(xp, q, scale, k, staged_scale); break; \
+            case 3: convrot_quant_i8_kernel<G, A, 3, F><<<grid, waves * 64, lds, s>>>(xp, q, scale, k, staged_scale); break; \
+            default: convrot_quant_i8_kernel<G, A, 4, F><<<grid, waves * 64, lds, s>>>(xp, q, scale, k, staged_scale); break; \
         }                                                                                                     \
+    } while (0)
+#define TU_CONVROT_LAUNCH(G, A)                   \
+    do {                                          \
+        if (f16) TU_CONVROT_LAUNCH_T(G, A, true); \
+        else TU_CONVROT_LAUNCH_T(G, A, false);    \
     } while (0)
     if (group == 256) {
         if (act == 0) TU_CONVROT_LAUNCH(256, 0);
@@ -399,5 +465,6 @@ extern "C" int32_t tu_convrot_quant_i8(const void *x_bf16, int8_t *q, float *sca
         else TU_CONVROT_LAUNCH(128, 2);
     }
 #undef TU_CONVROT_LAUNCH
+#undef TU_CONVROT_LAUNCH_T
     return check_launch("tu_convrot_quant_i8");
 }

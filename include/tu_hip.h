@@ -52,6 +52,12 @@ int32_t tu_device_supported(int32_t device);
 /* OR-ed into `act`: scale = absmax * (1/127) (the two-pass kernels' formula,
  * convrot_quant.cu:233-236) instead of absmax / 127. */
 #define TU_CONVROT_STAGED_SCALE 0x100
+/* OR-ed into `act`: x holds IEEE fp16 instead of bf16, as the reference's
+ * two-pass kernels with InputType = half (convrot_quant.cu:158-248): the GELU
+ * output and the rotated values are rounded to fp16, the absmax clip is 65504
+ * and q = clamp(rne(fp16(fp16(y) / fp16(scale))), -128, 127) with IEEE
+ * division (quant_div_to_float, convrot_quant.cu:69-73). */
+#define TU_CONVROT_FP16_INPUT 0x200
 
 /* Rotates each row of the activated input a = act(x) by the block-Hadamard
  * ConvRot transform (group 128 or 256), then quantizes per row to symmetric
@@ -301,6 +307,17 @@ int32_t tu_w8a8_attn_fwd(const int8_t *q8, const float *q_scale, int64_t nqs, co
 int32_t tu_layer_norm_adaln(const void *x, const void *scale, const void *shift, void *out, int32_t dtype,
                             int64_t batch, int64_t len, int64_t hidden, int64_t steps, float eps,
                             void *stream);
+
+/* LayerNorm with an elementwise affine weight and bias shared by all rows:
+ *   out[r][c] = T(fma((x[r][c] - mean_r) / sqrt(var_r + eps), weight[c], bias[c]))
+ * with the statistics of tu_layer_norm_adaln (same order) and one rounding to
+ * the element type T.  x/out: [rows, hidden] contiguous; weight/bias:
+ * [hidden]; dtype 0 bf16, 1 fp16, 2 fp32.  No counterpart in the reference's
+ * kernel package: ComfyUI's torch LayerNorm(elementwise_affine=True) runs the
+ * Wan block's norm3, which the reference's Wan adapter leaves in place
+ * (comfyui_turing_utils/adapters/wan.py:55-137 patches only the attention). */
+int32_t tu_layer_norm_affine(const void *x, const void *weight, const void *bias, void *out,
+                             int32_t dtype, int64_t rows, int64_t hidden, float eps, void *stream);
 
 #ifdef __cplusplus
 }

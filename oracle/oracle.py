@@ -42,7 +42,7 @@ def lib():
             if not os.path.exists(LIB_PATH):
                 build()
             L = ctypes.CDLL(LIB_PATH)
-            for fn in ("or_exp_det", "or_tanh_det", "or_gelu_tanh_bf16"):
+            for fn in ("or_exp_det", "or_tanh_det", "or_gelu_tanh_bf16", "or_gelu_tanh_f16"):
                 getattr(L, fn).restype = ctypes.c_float
                 getattr(L, fn).argtypes = [ctypes.c_float]
             L.or_swiglu.restype = ctypes.c_float
@@ -59,6 +59,8 @@ def lib():
             L.or_convrot_rotate_group.argtypes = [_p, _p, _i32]
             L.or_convrot_quant_i8.restype = _i32
             L.or_convrot_quant_i8.argtypes = [_p, _i64, _i64, _i32, _i32, _i32, _p, _p]
+            L.or_convrot_quant_i8_t.restype = _i32
+            L.or_convrot_quant_i8_t.argtypes = [_p, _i64, _i64, _i32, _i32, _i32, _i32, _p, _p]
             L.or_div_markstein_f32.restype = ctypes.c_float
             L.or_div_markstein_f32.argtypes = [ctypes.c_float, ctypes.c_float]
             L.or_check_markstein_quant.restype = _i64
@@ -98,6 +100,8 @@ def lib():
                                           _i64, _i64, _i64, _i32, _p]
             L.or_layer_norm_adaln.restype = _i32
             L.or_layer_norm_adaln.argtypes = [_p, _i32, _i64, _i64, _i64, _p, _p, _i64, ctypes.c_float, _p]
+            L.or_layer_norm_affine.restype = _i32
+            L.or_layer_norm_affine.argtypes = [_p, _i32, _i64, _i64, _p, _p, ctypes.c_float, _p]
             L.or_w8a8_sign_negative.restype = _i32
             L.or_w8a8_sign_negative.argtypes = [_i32]
             L.or_w8a8_hadamard.restype = None
@@ -158,15 +162,16 @@ ACT_NONE, ACT_GELU_TANH, ACT_SWIGLU = 0, 1, 2
 
 
 def convrot_quant(x_bits: np.ndarray, group: int, staged: bool = False,
-                  act: int = ACT_NONE) -> tuple[np.ndarray, np.ndarray]:
+                  act: int = ACT_NONE, fp16: bool = False) -> tuple[np.ndarray, np.ndarray]:
     """(int8 codes [M, K], fp32 scales [M]) of the row-buffer quantizer.
-    act: 0 none, 1 tanh-GELU, 2 SwiGLU (input [M, 2K] = [gate | up])."""
+    act: 0 none, 1 tanh-GELU, 2 SwiGLU (input [M, 2K] = [gate | up]).
+    fp16: x_bits are IEEE fp16 patterns (the two-pass ops' float16 input)."""
     x_bits = np.ascontiguousarray(x_bits, dtype=np.uint16)
     m, width = x_bits.shape
     k = width // 2 if act == ACT_SWIGLU else width
     q = np.empty((m, k), dtype=np.int8)
     s = np.empty(m, dtype=np.float32)
-    _check(lib().or_convrot_quant_i8(_ptr(x_bits), m, k, group, act, int(staged), _ptr(q), _ptr(s)),
+    _check(lib().or_convrot_quant_i8_t(_ptr(x_bits), m, k, group, act, int(staged), int(fp16), _ptr(q), _ptr(s)),
            "convrot_quant")
     return q, s
 
@@ -181,6 +186,10 @@ def tanh_det(u: float) -> float:
 
 def gelu_tanh_bf16(x: float) -> float:
     return float(lib().or_gelu_tanh_bf16(x))
+
+
+def gelu_tanh_f16(x: float) -> float:
+    return float(lib().or_gelu_tanh_f16(x))
 
 
 def swiglu(gate: float, up: float) -> float:
@@ -499,4 +508,19 @@ def layer_norm_adaln(x, scale, shift, eps: float, dtype: int = DTYPE_BF16) -> np
     out = np.empty(x.shape, dtype=kind)
     _check(lib().or_layer_norm_adaln(_ptr(x), dtype, b, l, h, _ptr(scale), _ptr(shift), scale.shape[1], eps,
                                      _ptr(out)), "layer_norm_adaln")
+    return out
+
+
+def layer_norm_affine(x, weight, bias, eps: float, dtype: int = DTYPE_BF16) -> np.ndarray:
+    """LayerNorm with an elementwise affine weight / bias: x [R, H] (uint16
+    patterns for bf16 / fp16, float32 for fp32), weight / bias [H] in the same
+    type.  Returns the output in the same representation."""
+    x = np.ascontiguousarray(x)
+    weight = np.ascontiguousarray(weight).reshape(-1)
+    bias = np.ascontiguousarray(bias).reshape(-1)
+    r, h = x.shape
+    assert weight.shape == (h,) and bias.shape == (h,)
+    out = np.empty_like(x)
+    _check(lib().or_layer_norm_affine(_ptr(x), dtype, r, h, _ptr(weight), _ptr(bias), eps, _ptr(out)),
+           "layer_norm_affine")
     return out

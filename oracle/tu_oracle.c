@@ -19,6 +19,10 @@
  *   or_convrot_rotate_group   pinned: dense Kronecker matrix (fp64), orthogonality,
  *                             involution, basis columns, regular-row property
  *   or_convrot_quant_i8       pinned: invariants + staged==row-buffer KAT
+ *   or_convrot_quant_i8_t     fp16 elements pinned: numpy float16 restatement of
+ *                             the rotation output, scale and quotient; zero /
+ *                             tiny rows (division by fp16(scale) = 0); GELU
+ *                             fp16 output vs torch float16 gelu(tanh)
  *   or_div_markstein_f32      pinned: exhaustive over the quantizer's bf16 domain
  *                             vs IEEE division (or_check_markstein_quant)
  *   or_int8_gemm_i32          pinned: numpy int64 matmul (brute force)
@@ -29,6 +33,8 @@
  *   or_sage_attn_rows         pinned: fp64 SDPA on dequantized inputs, torch SDPA
  *                             on raw inputs (reference gate rtol .08 / atol .06)
  *   or_f32_to_f16_rne         pinned: every fp32 class vs numpy float16 casts
+ *   or_layer_norm_affine      pinned: torch layer_norm(weight, bias) in fp32 and
+ *                             bf16 (equal apart from rounding ties), fp64 formula
  *   or_qk_rms_rope_int8       pinned: the reference's own KAT (torch restatement of
  *                             validate_compatible.py:241-286 + per-warp INT8,
  *                             codes within 2 LSB, scales rtol .015), fp64 RMSNorm,
@@ -181,6 +187,23 @@ static inline float load_act(const uint16_t *row, int64_t col, int64_t k, int ac
     return or_bf16_to_f32(row[col]);
 }
 
+OR_API uint16_t or_f32_to_f16_rne(float value);
+OR_API float or_f16_to_f32(uint16_t h);
+static inline float f16_round_f32(float v) { return or_f16_to_f32(or_f32_to_f16_rne(v)); }
+
+/* fp16 elements (the reference's InputType = half, convrot_quant.cu:137-156):
+ * GELU's output is rounded to fp16 (:153-155), SwiGLU's is not. */
+OR_API float or_gelu_tanh_f16(float x) {
+    const float inner = 0.7978845608028654f * (x + ((0.044715f * x) * x) * x);
+    return f16_round_f32((0.5f * x) * (1.0f + or_tanh_det(inner)));
+}
+
+static inline float load_act_f16(const uint16_t *row, int64_t col, int64_t k, int act) {
+    if (act == 2) return or_swiglu(or_f16_to_f32(row[col]), or_f16_to_f32(row[k + col]));
+    if (act == 1) return or_gelu_tanh_f16(or_f16_to_f32(row[col]));
+    return or_f16_to_f32(row[col]);
+}
+
 /* ------------------------------------------------------------------------ */
 /* Row-buffer ConvRot INT8 quantizer: convrot_quant.cu:350-444 (Int4=false). */
 /*   absmax over fp32 y of the whole row (:400-404)                           */
@@ -191,9 +214,15 @@ static inline float load_act(const uint16_t *row, int64_t col, int64_t k, int ac
 /* staged != 0 selects the staged formulation's scale, absmax*(1/127)        */
 /* (convrot_quant.cu:233-236), the reference's own cross-check partner.      */
 /* ------------------------------------------------------------------------ */
-OR_API int or_convrot_quant_i8(const uint16_t *x, int64_t rows, int64_t k, int group, int act,
-                               int staged, int8_t *q, float *scales) {
-    if ((group != 128 && group != 256) || k <= 0 || k % group) return -1;
+/* dtype 1: fp16 elements, the two-pass kernels' InputType = half           */
+/* (convrot_quant.cu:158-248): rotated values kept as fp16, clip 65504         */
+/* (finite_max<half>, :58-62), q = clamp(nearbyint(fp16(fp16(y) / fp16(scale)))) */
+/* (quant_div_to_float, :69-73).  fp16(scale) is 0 below 2^-25: the quotient */
+/* is then +-inf or NaN, which the clamp maps to 127 / -128 (fmaxf(-128, NaN) */
+/* is -128), as in the reference.                                             */
+OR_API int or_convrot_quant_i8_t(const uint16_t *x, int64_t rows, int64_t k, int group, int act,
+                                 int staged, int dtype, int8_t *q, float *scales) {
+    if ((group != 128 && group != 256) || k <= 0 || k % group || (dtype != 0 && dtype != 1)) return -1;
     const int64_t in_width = act == 2 ? 2 * k : k;
     uint16_t *buf = (uint16_t *)malloc((size_t)k * sizeof(uint16_t));
     if (!buf) return -2;
@@ -202,21 +231,22 @@ OR_API int or_convrot_quant_i8(const uint16_t *x, int64_t rows, int64_t k, int g
         float absmax = 0.0f;
         for (int64_t g = 0; g < k / group; ++g) {
             float xin[256], y[256];
-            for (int i = 0; i < group; ++i) xin[i] = load_act(row, g * group + i, k, act);
+            for (int i = 0; i < group; ++i)
+                xin[i] = dtype ? load_act_f16(row, g * group + i, k, act) : load_act(row, g * group + i, k, act);
             or_convrot_rotate_group(xin, y, group);
             for (int i = 0; i < group; ++i) {
                 absmax = fmaxf(absmax, fabsf(y[i]));
-                buf[g * group + i] = or_f32_to_bf16_rne(y[i]);
+                buf[g * group + i] = dtype ? or_f32_to_f16_rne(y[i]) : or_f32_to_bf16_rne(y[i]);
             }
         }
-        const float clipped = fminf(absmax, 3.38953139e38f);
+        const float clipped = fminf(absmax, dtype ? 65504.0f : 3.38953139e38f);
         const float scale = staged ? fmaxf(clipped * (1.0f / 127.0f), 1.0e-30f)
                                    : fmaxf(clipped / 127.0f, 1.0e-30f);
         scales[r] = scale;
-        const float rs = bf16_round_f32(scale);
+        const float rs = dtype ? f16_round_f32(scale) : bf16_round_f32(scale);
         for (int64_t c = 0; c < k; ++c) {
-            const float v = or_bf16_to_f32(buf[c]);
-            const float divided = bf16_round_f32(v / rs);
+            const float v = dtype ? or_f16_to_f32(buf[c]) : or_bf16_to_f32(buf[c]);
+            const float divided = dtype ? f16_round_f32(v / rs) : bf16_round_f32(v / rs);
             float qf = nearbyintf(divided);
             qf = fminf(127.0f, fmaxf(-128.0f, qf));
             q[r * k + c] = (int8_t)qf;
@@ -224,6 +254,11 @@ OR_API int or_convrot_quant_i8(const uint16_t *x, int64_t rows, int64_t k, int g
     }
     free(buf);
     return 0;
+}
+
+OR_API int or_convrot_quant_i8(const uint16_t *x, int64_t rows, int64_t k, int group, int act,
+                               int staged, int8_t *q, float *scales) {
+    return or_convrot_quant_i8_t(x, rows, k, group, act, staged, 0, q, scales);
 }
 
 /* Division by reciprocal plus one FMA correction (Markstein): the GPU
@@ -1111,8 +1146,13 @@ static inline float ln_load(const void *p, int64_t i, int dtype) {
 }
 static inline float ln_round(float v, int dtype) { return dtype == 2 ? v : t_round(v, dtype); }
 
-OR_API int or_layer_norm_adaln(const void *x, int dtype, int64_t batch, int64_t len, int64_t hidden,
-                               const void *scale, const void *shift, int64_t steps, float eps, void *out) {
+/* affine != 0: LayerNorm with an elementwise affine weight w and bias b    */
+/* (scale / shift carry w / b, one row for every token): out = T(fma(       */
+/* (x - mean) inv, w, b)), the normalized value not rounded -- the          */
+/* single-rounding form of torch's layer_norm, which ComfyUI runs for the   */
+/* Wan block's norm3 (the reference leaves that norm to ComfyUI).            */
+static int layer_norm_rows(const void *x, int dtype, int64_t batch, int64_t len, int64_t hidden,
+                           const void *scale, const void *shift, int64_t steps, float eps, int affine, void *out) {
     if (hidden <= 0 || steps <= 0) return -1;
 #pragma omp parallel for schedule(static)
     for (int64_t row = 0; row < batch * len; ++row) {
@@ -1151,12 +1191,29 @@ OR_API int or_layer_norm_adaln(const void *x, int dtype, int64_t batch, int64_t 
         const float inv = 1.0f / sqrtf(var + eps);
         const int64_t mrow = (b * steps + mt) * hidden;
         for (int64_t c = 0; c < hidden; ++c) {
-            const float n = ln_round((ln_load(x, xr + c, dtype) - mean) * inv, dtype);
-            const float m = ln_round(1.0f + ln_load(scale, mrow + c, dtype), dtype);
-            const float r = fmaf(n, m, ln_load(shift, mrow + c, dtype));
+            float r;
+            if (affine) {
+                r = fmaf((ln_load(x, xr + c, dtype) - mean) * inv, ln_load(scale, mrow + c, dtype),
+                         ln_load(shift, mrow + c, dtype));
+            } else {
+                const float n = ln_round((ln_load(x, xr + c, dtype) - mean) * inv, dtype);
+                const float m = ln_round(1.0f + ln_load(scale, mrow + c, dtype), dtype);
+                r = fmaf(n, m, ln_load(shift, mrow + c, dtype));
+            }
             if (dtype == 2) ((float *)out)[xr + c] = r;
             else ((uint16_t *)out)[xr + c] = dtype ? or_f32_to_f16_rne(r) : or_f32_to_bf16_rne(r);
         }
     }
     return 0;
+}
+
+OR_API int or_layer_norm_adaln(const void *x, int dtype, int64_t batch, int64_t len, int64_t hidden,
+                               const void *scale, const void *shift, int64_t steps, float eps, void *out) {
+    return layer_norm_rows(x, dtype, batch, len, hidden, scale, shift, steps, eps, 0, out);
+}
+
+/* rows x hidden, one weight / bias row of hidden values for all rows. */
+OR_API int or_layer_norm_affine(const void *x, int dtype, int64_t rows, int64_t hidden, const void *weight,
+                                const void *bias, float eps, void *out) {
+    return layer_norm_rows(x, dtype, 1, rows, hidden, weight, bias, 1, eps, 1, out);
 }

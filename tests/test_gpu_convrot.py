@@ -169,3 +169,70 @@ def test_staged_ops_exact(gpu_device, act, name, group):
     q_ref, s_ref = oracle.convrot_quant(inputs.bits(x), group, staged=True, act=act)
     np.testing.assert_array_equal(s.cpu().numpy().reshape(-1).view(np.uint32), s_ref.view(np.uint32))
     np.testing.assert_array_equal(q.cpu().numpy(), q_ref)
+
+
+# ---------------------------------------------------------------------------
+# float16 input to the two-pass ops (ops.py:163-186, :215-233; InputType = half
+# of convrot_quant.cu:158-248)
+# ---------------------------------------------------------------------------
+def _f16(x: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(x, dtype=np.float32)).to(torch.float16)
+
+
+def _f16_bits(t: torch.Tensor) -> np.ndarray:
+    return t.contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def _assert_f16_exact(x: torch.Tensor, name: str, act: int, group: int, dev, label: str):
+    print(f"[convrot fp16] {name} {label} shape={tuple(x.shape)} group={group}", flush=True)
+    q, s = getattr(torch.ops.turing_utils, name)(x.to(dev), group)
+    q_ref, s_ref = oracle.convrot_quant(_f16_bits(x), group, staged=True, act=act, fp16=True)
+    got = s.cpu().numpy().reshape(-1).view(np.uint32)
+    bad = np.flatnonzero(got != s_ref.view(np.uint32))
+    assert bad.size == 0, f"{label}: {bad.size} scales differ, first rows {bad[:5]}"
+    bad_q = np.argwhere(q.cpu().numpy() != q_ref)
+    assert bad_q.size == 0, f"{label}: {len(bad_q)} codes differ, first {bad_q[:5].tolist()}"
+
+
+@pytest.mark.parametrize("act,name", [(1, "gelu_int8_convrot_quantize"), (2, "swiglu_int8_convrot_quantize")])
+@pytest.mark.parametrize("group", [128, 256])
+def test_staged_ops_fp16_exact(gpu_device, act, name, group):
+    """fp16 rows of several magnitudes (tiny rows whose fp16 scale underflows,
+    large rows whose rotated absmax passes 65504) plus random rows."""
+    rng = np.random.default_rng(70 + act + group)
+    k = 5120
+    width = 2 * k if act == 2 else k
+    x = rng.standard_normal((40, width)).astype(np.float32)
+    x *= np.array([1e-7, 1e-4, 1e-2, 1, 30, 3000, 60000, 1] * 5, np.float32)[:, None]
+    x[7, :] = 0.0
+    x = np.clip(x, -65504, 65504)
+    _assert_f16_exact(_f16(x), name, act, group, gpu_device, "magnitudes")
+
+
+def test_gelu_fp16_every_input(gpu_device):
+    """Every finite fp16 x, one per row at column 0 of a zero row: the scale
+    carries gelu(x) bit for bit over the fp16 domain."""
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    bits = bits[(bits & 0x7C00) != 0x7C00]
+    x = np.zeros((bits.size, 128), np.uint16)
+    x[:, 0] = bits
+    xt = torch.from_numpy(x.view(np.int16)).view(torch.float16)
+    _assert_f16_exact(xt, "gelu_int8_convrot_quantize", 1, 128, gpu_device, "every finite fp16 input")
+
+
+def test_swiglu_fp16_every_gate(gpu_device):
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    bits = bits[(bits & 0x7C00) != 0x7C00]
+    x = np.zeros((bits.size, 256), np.uint16)
+    x[:, 0] = bits
+    x[:, 128] = 0x3C00  # up = 1.0
+    xt = torch.from_numpy(x.view(np.int16)).view(torch.float16)
+    _assert_f16_exact(xt, "swiglu_int8_convrot_quantize", 2, 128, gpu_device, "every finite fp16 gate")
+
+
+def test_row_buffer_ops_refuse_fp16(gpu_device):
+    x = torch.zeros((2, 256), dtype=torch.float16, device=gpu_device)
+    with pytest.raises(TypeError):
+        torch.ops.turing_utils.bf16_int8_convrot_quantize(x, 256)
+    with pytest.raises(TypeError):
+        torch.ops.turing_utils.bf16_gelu_int8_convrot_quantize(x, 256)

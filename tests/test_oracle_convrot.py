@@ -245,3 +245,102 @@ def test_staged_equals_row_buffer_with_activation(act):
     q2, s2 = oracle.convrot_quant(xb, 256, staged=True, act=act)
     np.testing.assert_array_equal(q1, q2)
     np.testing.assert_allclose(s1, s2, rtol=1e-6, atol=5e-8)
+
+
+# ---------------------------------------------------------------------------
+# fp16 elements (the two-pass ops' float16 input, convrot_quant.cu:158-248)
+# ---------------------------------------------------------------------------
+def _f16_bits(x: np.ndarray) -> np.ndarray:
+    return np.ascontiguousarray(x, dtype=np.float32).astype(np.float16).view(np.uint16)
+
+
+def _rows_y_f16(xb: np.ndarray, group: int) -> np.ndarray:
+    xf = xb.view(np.float16).astype(np.float32)
+    m, k = xf.shape
+    y = np.empty_like(xf)
+    for r in range(m):
+        for g in range(k // group):
+            y[r, g * group:(g + 1) * group] = oracle.rotate_group(xf[r, g * group:(g + 1) * group], group)
+    return y
+
+
+def _f16_codes(y: np.ndarray, scale: np.ndarray) -> np.ndarray:
+    """numpy's float16 casts (independent of the oracle's converter):
+    clamp(rint(f16(f16(y) / f16(scale)))) with fmax/fmin NaN semantics."""
+    yh = y.astype(np.float16).astype(np.float32)
+    rs = scale.astype(np.float16).astype(np.float32)[:, None]
+    with np.errstate(divide="ignore", invalid="ignore", over="ignore"):
+        d = (yh / rs).astype(np.float16).astype(np.float32)
+    return np.fmin(np.float32(127), np.fmax(np.float32(-128), np.rint(d))).astype(np.int8)
+
+
+@pytest.mark.parametrize("group", [128, 256])
+def test_fp16_quantizer_rederivation(group):
+    rng = np.random.default_rng(100 + group)
+    x = rng.standard_normal((12, 1024)).astype(np.float32) * np.array([1e-2, 1, 30, 3000] * 3, np.float32)[:, None]
+    # the sign pattern of a column of the (involutive) rotation concentrates a
+    # group onto one output: |y| ~ 60000 * 16 (G=256) or 60000 * 8 sqrt2 (G=128),
+    # above 65504 -> the scale clip applies and the fp16 row buffer holds inf
+    sign = np.sign(dense(group)[:, 0]).astype(np.float32)
+    x[5, :group] = 60000.0 * sign
+    x[6, group:2 * group] = -50000.0 * np.sign(dense(group)[:, 3]).astype(np.float32)
+    xb = _f16_bits(x)
+    q, s = oracle.convrot_quant(xb, group, staged=True, fp16=True)
+    y = _rows_y_f16(xb, group)
+    absmax = np.abs(y).max(axis=1)
+    expect = np.maximum(np.minimum(absmax, np.float32(65504)) * np.float32(1.0 / 127.0), np.float32(1e-30))
+    np.testing.assert_array_equal(s.view(np.uint32), expect.astype(np.float32).view(np.uint32))
+    assert absmax[5] > 65504 and absmax[6] > 65504
+    np.testing.assert_array_equal(q, _f16_codes(y, s))
+    assert s[5] == s[6] == np.float32(65504) * np.float32(1.0 / 127.0)
+    assert q[5, 0] == 127 and q[6, group + 3] == -128  # +-inf / fp16(scale) saturates
+
+
+def test_fp16_zero_and_tiny_rows_divide_by_a_zero_scale():
+    """fp16(scale) is 0 for scale < 2^-25: the reference divides by zero and
+    its clamp maps +-inf to 127 / -128 and 0 / 0 (NaN) to -128."""
+    x = np.zeros((3, 256), np.float32)
+    x[1, 3] = 1e-6   # absmax 1e-6 / 16 after rotation: scale ~ 5e-10 -> fp16 0
+    x[2, 3] = 1.0    # an ordinary row for contrast
+    q, s = oracle.convrot_quant(_f16_bits(x), 256, staged=True, fp16=True)
+    assert s[0] == np.float32(1e-30) and np.all(q[0] == -128)
+    y = _rows_y_f16(_f16_bits(x), 256)
+    assert np.float16(s[1]) == 0
+    np.testing.assert_array_equal(q[1], np.where(y[1] > 0, 127, -128).astype(np.int8))
+    assert np.abs(q[2].astype(int)).max() == 127
+
+
+def test_gelu_tanh_f16_matches_fp64_and_torch():
+    x = np.arange(0, 0x7c00, dtype=np.uint16)
+    x = np.concatenate([x, x | 0x8000]).view(np.float16).astype(np.float32)  # every finite fp16
+    got = np.array([oracle.gelu_tanh_f16(float(t)) for t in x], np.float32)
+    ref = _gelu64(x)
+    assert np.all(np.abs(got - ref) <= np.abs(ref) * 2.0 ** -11 + 2.0 ** -24 + np.abs(x) * 2e-7)
+    assert np.array_equal(got.astype(np.float16).astype(np.float32), got)  # fp16 values
+    tg = torch.nn.functional.gelu(torch.from_numpy(x), approximate="tanh").half().float().numpy()
+    assert np.mean(tg[x > -4] == got[x > -4]) > 0.999
+
+
+@pytest.mark.parametrize("group", [128, 256])
+def test_fp16_gelu_quantizer_is_gelu_then_quantizer(group):
+    rng = np.random.default_rng(group + 3)
+    xb = _f16_bits(rng.standard_normal((8, 512)) * 2)
+    xf = xb.view(np.float16).astype(np.float32)
+    gb = _f16_bits(np.vectorize(oracle.gelu_tanh_f16, otypes=[np.float32])(xf))
+    q1, s1 = oracle.convrot_quant(xb, group, staged=True, act=oracle.ACT_GELU_TANH, fp16=True)
+    q0, s0 = oracle.convrot_quant(gb, group, staged=True, fp16=True)
+    np.testing.assert_array_equal(q1, q0)
+    np.testing.assert_array_equal(s1.view(np.uint32), s0.view(np.uint32))
+
+
+@pytest.mark.parametrize("group", [128, 256])
+def test_fp16_swiglu_quantizer_bounds(group):
+    rng = np.random.default_rng(group + 9)
+    xb = _f16_bits(rng.standard_normal((8, 1024)) * 2)
+    xf = xb.view(np.float16).astype(np.float64)
+    q, s = oracle.convrot_quant(xb, group, staged=True, act=oracle.ACT_SWIGLU, fp16=True)
+    act = xf[:, :512] / (1 + np.exp(-xf[:, :512])) * xf[:, 512:]
+    y = (act.reshape(8, -1, group) @ dense(group).T).reshape(8, 512)
+    np.testing.assert_allclose(s, np.abs(y).max(axis=1) / 127, rtol=1e-5)
+    err = np.abs(q - y / s[:, None])
+    assert np.all(err <= 0.5 + np.abs(y / s[:, None]) * 3 * 2.0 ** -11 + 1e-3)

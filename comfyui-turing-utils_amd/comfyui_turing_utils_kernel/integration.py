@@ -47,8 +47,8 @@ def int8_linear(
     weight_scale: torch.Tensor,
     bias: torch.Tensor | None = None,
     out_dtype: torch.dtype | None = None,
-    convrot: bool = True,
-    convrot_groupsize: int = 128,
+    convrot: bool = False,
+    convrot_groupsize: int = 256,
     input_act: str | None = None,
 ) -> torch.Tensor:
     """ConvRot W8A8 linear: y = dequant(int8(R act(x)) @ W^T) * s_x * s_w + bias.
@@ -57,6 +57,11 @@ def int8_linear(
     weight_scale: fp32 scalar or [N]; bias: [N] or None; input_act: None /
     "none", "gelu_tanh" or "swiglu" (dispatch.py:326-393), folded into the
     quantizer.  Returns [..., N] in ``out_dtype`` (default x.dtype).
+
+    The defaults are the reference's (dispatch.py:618-627): ``convrot=False``
+    (unrotated activations, which only comfy-kitchen serves: refused here) and
+    ``convrot_groupsize=256``.  A caller whose weights were rotated with
+    groups of 128 (this build's extension) passes ``convrot_groupsize=128``.
     """
     if input_act not in (None, "none", "swiglu", "gelu_tanh"):
         raise ValueError(f"unsupported fused INT8 activation: {input_act!r}")
@@ -185,33 +190,81 @@ def finish_attention_output(output: torch.Tensor, call: AttentionCall) -> torch.
     return result.to(call.input_dtype) if call.input_dtype == torch.float32 else result
 
 
+ATTENTION_TUNING_KEY = "turing_utils_attention_tuning"
+
+
+@dataclasses.dataclass(frozen=True)
+class AttentionKernelTuning:
+    """W8A8 attention controls a model patch stores in ``transformer_options``
+    (comfyui_turing_utils/attention/tuning.py:8-32)."""
+    key_tile_tokens: int = 0
+    rotate_qk: bool = True
+    stabilize_k: bool = True
+
+
+def attention_kernel_tuning(transformer_options) -> AttentionKernelTuning:
+    """tuning.py:18-32: invalid or missing settings give the defaults; K
+    stabilisation needs the rotation."""
+    if not isinstance(transformer_options, dict):
+        return AttentionKernelTuning()
+    raw = transformer_options.get(ATTENTION_TUNING_KEY)
+    if not isinstance(raw, dict):
+        return AttentionKernelTuning()
+    key_tile_tokens = int(raw.get("key_tile_tokens", 0))
+    if key_tile_tokens not in (0, 64, 128):
+        key_tile_tokens = 0
+    rotate_qk = bool(raw.get("rotate_qk", True))
+    return AttentionKernelTuning(key_tile_tokens=key_tile_tokens, rotate_qk=rotate_qk,
+                                 stabilize_k=rotate_qk and bool(raw.get("stabilize_k", True)))
+
+
 def sage_attention_override(
     original: Callable,
     q: torch.Tensor,
     k: torch.Tensor,
     v: torch.Tensor,
     heads: int,
-    *,
     mask=None,
+    attn_precision=None,
     skip_reshape: bool = False,
     skip_output_reshape: bool = False,
-    enable_gqa: bool = False,
-    is_causal: bool = False,
-    low_precision_attention: bool = True,
+    *,
     device_predicate: Callable[[torch.device], bool] = is_supported_device,
     **kwargs,
 ):
-    """``attention_override`` body for the Sage backend (patches.py:475-490):
-    serve the call with ``torch.ops.turing_utils.sage_attention`` or hand it,
-    unconsumed, to ``original``."""
+    """``attention_override`` body (``turing_sage_attention``,
+    stable.py:593-706): serve the call with ``torch.ops.turing_utils.
+    sage_attention`` -- or ``w8a8_attention`` when ``_turing_kernel="w8a8"``
+    (``turing_w8a8_attention``, the loader default) -- or hand it to
+    ``original`` with every argument as received.  ``enable_gqa``,
+    ``low_precision_attention``, ``is_causal``, ``scale`` and
+    ``transformer_options`` are read from ``kwargs`` as the reference does;
+    ``device_predicate`` is this build's test hook and is not forwarded."""
+    kernel = kwargs.pop("_turing_kernel", "sage")
+    if kernel not in ("sage", "w8a8"):
+        raise ValueError(f"unsupported bundled attention kernel: {kernel}")
     call, reason = inspect_attention_call(
         q, k, v, heads, mask=mask, skip_reshape=skip_reshape, skip_output_reshape=skip_output_reshape,
-        enable_gqa=enable_gqa, low_precision_attention=low_precision_attention, device_predicate=device_predicate,
+        enable_gqa=bool(kwargs.get("enable_gqa", False)),
+        low_precision_attention=kwargs.get("low_precision_attention", True), device_predicate=device_predicate,
     )
     if call is None:
-        return original(q, k, v, heads, mask=mask, skip_reshape=skip_reshape,
-                        skip_output_reshape=skip_output_reshape, enable_gqa=enable_gqa, is_causal=is_causal,
-                        **kwargs)
+        return original(q, k, v, heads, mask=mask, attn_precision=attn_precision, skip_reshape=skip_reshape,
+                        skip_output_reshape=skip_output_reshape, **kwargs)
     qn, kn, vn = normalize_attention_tensors(q, k, v, call)
-    out = torch.ops.turing_utils.sage_attention(qn, kn, vn, call.tensor_layout, bool(is_causal), -1.0)
+    scale = kwargs.get("scale")
+    sm_scale = float(scale) if scale is not None else -1.0  # <= 0: the op's default head_dim ** -0.5
+    is_causal = bool(kwargs.get("is_causal", False))
+    if kernel == "w8a8":
+        tuning = attention_kernel_tuning(kwargs.get("transformer_options"))
+        out = torch.ops.turing_utils.w8a8_attention(qn, kn, vn, call.tensor_layout, is_causal, sm_scale,
+                                                    tuning.key_tile_tokens, tuning.rotate_qk, tuning.stabilize_k)
+    else:
+        out = torch.ops.turing_utils.sage_attention(qn, kn, vn, call.tensor_layout, is_causal, sm_scale)
     return finish_attention_output(out, call)
+
+
+def w8a8_attention_override(*args, **kwargs):
+    """``turing_w8a8_attention`` (stable.py:709-711)."""
+    kwargs["_turing_kernel"] = "w8a8"
+    return sage_attention_override(*args, **kwargs)

@@ -7,6 +7,8 @@ GPU.  The fallback cases mirror the reference's attention override contract
 (comfyui_turing_utils/attention/stable.py:83-200)."""
 from __future__ import annotations
 
+import inspect
+
 import pytest
 import torch
 
@@ -101,21 +103,34 @@ def test_override_routes_to_sage_and_restores_layout(skip_reshape, skip_output_r
     assert out.shape == expect
 
 
+def test_int8_linear_defaults_are_the_reference_defaults():
+    """dispatch.py:618-627: out_dtype None, convrot False, convrot_groupsize
+    256, input_act None.  A caller that omits them must not get G=128 rotation
+    against G=256 weights, or rotated activations against unrotated weights."""
+    params = inspect.signature(integration.int8_linear).parameters
+    assert list(params) == ["x", "weight", "weight_scale", "bias", "out_dtype", "convrot", "convrot_groupsize",
+                            "input_act"]
+    assert params["bias"].default is None and params["out_dtype"].default is None
+    assert params["convrot"].default is False
+    assert params["convrot_groupsize"].default == 256
+    assert params["input_act"].default is None
+
+
 def test_int8_linear_contract(monkeypatch):
     monkeypatch.setattr(integration, "is_supported_device", lambda device: True)
     x = torch.empty((2, 5, 256), dtype=torch.bfloat16, device="meta")
     w = torch.empty((48, 256), dtype=torch.int8, device="meta")
-    out = integration.int8_linear(x, w, torch.empty((), dtype=torch.float32, device="meta"))
+    out = integration.int8_linear(x, w, torch.empty((), dtype=torch.float32, device="meta"), convrot=True)
     assert out.shape == (2, 5, 48) and out.dtype == torch.bfloat16
-    out = integration.int8_linear(x, w, torch.empty((48,), device="meta"), convrot_groupsize=256,
+    out = integration.int8_linear(x, w, torch.empty((48,), device="meta"), convrot=True, convrot_groupsize=128,
                                   out_dtype=torch.float16)
     assert out.dtype == torch.float16
     with pytest.raises(ValueError, match="scalar or have 48"):
-        integration.int8_linear(x, w, torch.empty((7,), device="meta"))
-    out = integration.int8_linear(x, w, torch.empty((48,), device="meta"), input_act="gelu_tanh")
+        integration.int8_linear(x, w, torch.empty((7,), device="meta"), convrot=True)
+    out = integration.int8_linear(x, w, torch.empty((48,), device="meta"), convrot=True, input_act="gelu_tanh")
     assert out.shape == (2, 5, 48)
     xs = torch.empty((2, 5, 512), dtype=torch.bfloat16, device="meta")
-    out = integration.int8_linear(xs, w, torch.empty((48,), device="meta"), input_act="swiglu")
+    out = integration.int8_linear(xs, w, torch.empty((48,), device="meta"), convrot=True, input_act="swiglu")
     assert out.shape == (2, 5, 48)
 
 
@@ -124,10 +139,63 @@ def test_int8_linear_declines_what_it_cannot_serve():
     w = torch.zeros((16, 256), dtype=torch.int8)
     s = torch.ones(16)
     with pytest.raises(NotImplementedError, match="gfx950"):
-        integration.int8_linear(x, w, s)
+        integration.int8_linear(x, w, s, convrot=True)
     with pytest.raises(NotImplementedError, match="bfloat16"):
-        integration.int8_linear(x.float(), w, s)
+        integration.int8_linear(x.float(), w, s, convrot=True)
     with pytest.raises(NotImplementedError, match="ConvRot"):
-        integration.int8_linear(x, w, s, convrot=False)
+        integration.int8_linear(x, w, s)  # the default convrot=False
     with pytest.raises(ValueError, match="activation"):
         integration.int8_linear(x, w, s, input_act="gelu")
+
+
+def test_fallback_forwards_every_argument_as_received():
+    """stable.py:611-618: the fallback gets (q, k, v, heads) and mask,
+    attn_precision, skip_reshape, skip_output_reshape plus every other keyword
+    (low_precision_attention, scale, transformer_options, ...), unchanged."""
+    q, k, v = _nhd()
+    original, calls = _fallback_recorder()
+    opts = {"x": 1}
+    out = integration.sage_attention_override(original, q, k, v, 4, attn_precision=torch.float32,
+                                              low_precision_attention=False, scale=0.3, transformer_options=opts,
+                                              enable_gqa=False, device_predicate=lambda d: True)
+    assert out == "fallback"
+    kw = calls[0]
+    assert kw["low_precision_attention"] is False and kw["scale"] == 0.3 and kw["transformer_options"] is opts
+    assert kw["attn_precision"] is torch.float32 and kw["mask"] is None and kw["enable_gqa"] is False
+    assert "device_predicate" not in kw and "_turing_kernel" not in kw
+    # the w8a8 entry (turing_w8a8_attention) falls back the same way
+    integration.w8a8_attention_override(original, q, k, v, 4, mask=torch.zeros(1), device_predicate=lambda d: True)
+    assert "_turing_kernel" not in calls[1] and calls[1]["mask"] is not None
+    with pytest.raises(ValueError, match="kernel"):
+        integration.sage_attention_override(original, q, k, v, 4, _turing_kernel="sol")
+
+
+def test_attention_kernel_tuning_parsing():
+    """tuning.py:18-32."""
+    key = integration.ATTENTION_TUNING_KEY
+    assert integration.attention_kernel_tuning(None) == integration.AttentionKernelTuning(0, True, True)
+    assert integration.attention_kernel_tuning({key: "x"}) == integration.AttentionKernelTuning(0, True, True)
+    t = integration.attention_kernel_tuning({key: {"key_tile_tokens": 128, "rotate_qk": True, "stabilize_k": False}})
+    assert t == integration.AttentionKernelTuning(128, True, False)
+    t = integration.attention_kernel_tuning({key: {"key_tile_tokens": 96, "rotate_qk": False, "stabilize_k": True}})
+    assert t == integration.AttentionKernelTuning(0, False, False)
+
+
+def test_w8a8_override_routes_to_the_w8a8_op(monkeypatch):
+    seen = {}
+
+    def fake_w8a8(q, k, v, layout, causal, sm_scale, tile, rotate, stabilize):
+        seen.update(layout=layout, causal=causal, sm_scale=sm_scale, tile=tile, rotate=rotate, stabilize=stabilize)
+        return torch.empty_like(q)
+
+    monkeypatch.setattr(torch.ops.turing_utils, "w8a8_attention", fake_w8a8, raising=False)
+    q, k, v = _nhd(d=64)
+    opts = {integration.ATTENTION_TUNING_KEY: {"key_tile_tokens": 64, "rotate_qk": True, "stabilize_k": False}}
+    out = integration.w8a8_attention_override(_not_called, q, k, v, 4, is_causal=True, scale=0.125,
+                                              transformer_options=opts, device_predicate=lambda d: True)
+    assert out.shape == (2, 7, 4 * 64)
+    assert seen == dict(layout="NHD", causal=True, sm_scale=0.125, tile=64, rotate=True, stabilize=False)
+
+
+def _not_called(*args, **kwargs):
+    raise AssertionError("fell back")

@@ -100,6 +100,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _i32,
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i32, _i64, _i64, _i64, _i64, _f32, _c_void_p],
     ),
+    "tu_layer_norm_affine": (
+        _i32,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i32, _i64, _i64, _f32, _c_void_p],
+    ),
 }
 
 ABI_VERSION = 7

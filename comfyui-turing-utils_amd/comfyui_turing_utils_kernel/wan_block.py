@@ -15,9 +15,9 @@ ops into the whole block so that it can be run and timed without ComfyUI:
     x = x + CrossAttn(LN_affine(x), context)
     x = x + FFN(LN(x) * (1 + e4) + e3) * e5
 
-* norm1 / norm2 / norm3: ``turing_utils::layer_norm_adaln``.  norm3's affine
-  weight w and bias b enter as scale = w - 1 and shift = b; the constructor
-  checks that T(1 + T(w - 1)) == w for every channel.
+* norm1 / norm2: ``turing_utils::layer_norm_adaln``.  norm3, LayerNorm with
+  an elementwise weight and bias (ComfyUI's own LayerNorm in the reference's
+  setting): ``turing_utils::layer_norm_affine``, any weight values.
 * SelfAttn: q, k and v come from one W8A8 GEMM (N = 3C).  q and k go through
   one fused RMSNorm + RoPE + INT8 kernel.  Then Sage INT8 attention, and the
   o projection.
@@ -186,12 +186,8 @@ class WanBlockW8A8:
         self.cross_norm_q = cross_norm_q.to(torch.bfloat16).contiguous()
         self.cross_norm_k = cross_norm_k.to(torch.bfloat16).contiguous()
         self.ffn_up, self.ffn_down = ffn_up, ffn_down
-        w = norm3_weight.to(torch.bfloat16).reshape(1, 1, c)
-        scale3 = (w.float() - 1.0).to(torch.bfloat16)
-        if not torch.equal((1.0 + scale3.float()).to(torch.bfloat16), w):
-            raise ValueError("norm3 weight is not exactly 1 + a bf16 value; the AdaLN form cannot express it")
-        self.norm3_scale = scale3.contiguous()
-        self.norm3_shift = norm3_bias.to(torch.bfloat16).reshape(1, 1, c).contiguous()
+        self.norm3_weight = norm3_weight.to(torch.bfloat16).reshape(c).contiguous()
+        self.norm3_bias = norm3_bias.to(torch.bfloat16).reshape(c).contiguous()
 
     # -- sublayers (each takes and returns bf16 [B, L, C]) ---------------------
 
@@ -258,10 +254,8 @@ class WanBlockW8A8:
         x = x.contiguous()
         # each residual add runs in the epilogue of the projection before it
         x = self.self_attention(lnadaln(x, e1, e0, cfg.eps), freqs, residual=x, gate=e2)
-        b = x.shape[0]
-        # the op takes one modulation row per sample: the affine row repeats
-        x = self.cross_attention(lnadaln(x, self.norm3_scale.expand(b, 1, cfg.dim),
-                                         self.norm3_shift.expand(b, 1, cfg.dim), cfg.eps), context, residual=x)
+        x = self.cross_attention(torch.ops.turing_utils.layer_norm_affine(x, self.norm3_weight, self.norm3_bias,
+                                                                          cfg.eps), context, residual=x)
         return self.ffn(lnadaln(x, e4, e3, cfg.eps), residual=x, gate=e5)
 
     __call__ = forward
@@ -270,8 +264,8 @@ class WanBlockW8A8:
 def random_block(cfg: WanBlockConfig, seed: int, device) -> tuple[WanBlockW8A8, WanTextEmbeddingW8A8]:
     """Random-init block and text embedding: every linear weight and bias
     N(0, 0.02) (generated in fp32 on ``device`` with a seeded generator), then
-    quantized; RMSNorm weights 1 + N(0, 0.05); norm3 weight 1 + k / 128 (k
-    uniform in -16..16, so that w - 1 is exact in bf16) and bias N(0, 0.02);
+    quantized; RMSNorm weights 1 + N(0, 0.05); norm3 weight 1 + N(0, 0.05) and
+    bias N(0, 0.02);
     the modulation table N(0, 1) / sqrt(C) as in Wan's initialisation."""
     device = torch.device(device)
     g = torch.Generator(device=device).manual_seed(seed)
@@ -293,7 +287,7 @@ def random_block(cfg: WanBlockConfig, seed: int, device) -> tuple[WanBlockW8A8, 
         modulation=randn(1, 6, c) / math.sqrt(c),
         self_qkv=linear(3 * c, c), self_o=linear(c, c),
         self_norm_q=norm_weight(), self_norm_k=norm_weight(),
-        norm3_weight=1 + torch.randint(-16, 17, (c,), generator=g, device=device).float() / 128,
+        norm3_weight=norm_weight(),
         norm3_bias=randn(c) * 0.02,
         cross_q=linear(c, c), cross_kv=linear(2 * c, c), cross_o=linear(c, c),
         cross_norm_q=norm_weight(), cross_norm_k=norm_weight(),
@@ -319,10 +313,9 @@ def block_state(block: WanBlockW8A8, index: int, prefix: str = "") -> tuple[dict
     ck, cv = block.cross_kv.split(2)
     linears = dict(zip((p + n for n in _BLOCK_LINEARS),
                        (q, k, v, block.self_o, block.cross_q, ck, cv, block.cross_o, block.ffn_up, block.ffn_down)))
-    norm3_weight = (1.0 + block.norm3_scale.float()).to(torch.bfloat16).reshape(-1)
     tensors = dict(zip((p + n for n in _BLOCK_TENSORS),
                        (block.modulation, block.self_norm_q, block.self_norm_k, block.cross_norm_q,
-                        block.cross_norm_k, norm3_weight, block.norm3_shift.reshape(-1))))
+                        block.cross_norm_k, block.norm3_weight, block.norm3_bias)))
     return linears, tensors
 
 

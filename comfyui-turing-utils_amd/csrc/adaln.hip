@@ -13,6 +13,11 @@
 // combined in order.  Kept exactly so that the CPU oracle restates it bit for
 // bit; 1 / sqrt is IEEE (the reference uses rsqrtf).
 //
+// The affine variant (kAffine) is LayerNorm with an elementwise weight w and
+// bias b shared by every row, as ComfyUI's LayerNorm(elementwise_affine=True)
+// runs the Wan block's norm3 (torch layer_norm computes in fp32 and rounds
+// once): out = T(fma((x - mean) / sqrt(var + eps), w, b)), same statistics.
+//
 // MI355X mapping: one workgroup of 256 threads (4 wave64) per row; a wave64
 // holds two 32-lane trees (xor partners below 32 stay in the half).  Up to
 // hidden 8192 a thread keeps its columns in registers between the statistics
@@ -47,10 +52,16 @@ __device__ __forceinline__ float t_round(float v) {
     else return __uint_as_float(static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(v))) << 16);
 }
 
+// The fp32 result is pinned before the fp16 conversion: otherwise the
+// compiler folds "fp32 fma, then round to fp16" into one single-rounding
+// v_fma_mix instruction, which differs on fp32 values near fp16 ties.
 template <int kT>
 __device__ __forceinline__ typename Elem<kT>::type from_f32(float v) {
     if constexpr (kT == 2) return v;
-    else if constexpr (kT == 1) return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
+    else if constexpr (kT == 1) {
+        asm("" : "+v"(v));
+        return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
+    }
     else return __builtin_bit_cast(uint16_t, static_cast<__bf16>(v));
 }
 
@@ -105,7 +116,7 @@ struct Recips {
 // One workgroup per token row.  kPer > 0: the thread's columns t + 256 i
 // (i < kPer) and their modulation values stay in registers; kUniform: every
 // thread holds exactly hidden / 256 of them and all counts are known.
-template <int kT, int kPer, bool kUniform>
+template <int kT, int kPer, bool kUniform, bool kAffine>
 __global__ __launch_bounds__(kThreads) void layer_norm_adaln_kernel(const typename Elem<kT>::type *__restrict__ x,
                                                                    const typename Elem<kT>::type *__restrict__ scale,
                                                                    const typename Elem<kT>::type *__restrict__ shift,
@@ -202,9 +213,13 @@ __global__ __launch_bounds__(kThreads) void layer_norm_adaln_kernel(const typena
     const float inv = 1.0f / __builtin_sqrtf(var + eps);
 
     auto emit = [&](int c, float value, float s, float h) {
-        const float n = t_round<kT>((value - mean) * inv);
-        const float m = t_round<kT>(1.0f + s);
-        orow[c] = from_f32<kT>(__builtin_fmaf(n, m, h));
+        if constexpr (kAffine) {
+            orow[c] = from_f32<kT>(__builtin_fmaf((value - mean) * inv, s, h));
+        } else {
+            const float n = t_round<kT>((value - mean) * inv);
+            const float m = t_round<kT>(1.0f + s);
+            orow[c] = from_f32<kT>(__builtin_fmaf(n, m, h));
+        }
     };
     if constexpr (kPer > 0) {
 #pragma unroll
@@ -217,7 +232,7 @@ __global__ __launch_bounds__(kThreads) void layer_norm_adaln_kernel(const typena
     }
 }
 
-template <int kT>
+template <int kT, bool kAffine>
 void launch(const void *xv, const void *scv, const void *shv, void *outv, int64_t rows, int64_t len, int hidden,
             int64_t steps, float eps, hipStream_t s) {
     typedef typename Elem<kT>::type E;
@@ -232,7 +247,8 @@ void launch(const void *xv, const void *scv, const void *shv, void *outv, int64_
         for (int lvl = 0; lvl < 5; ++lvl) rc.level[lvl] = 1.0f / static_cast<float>(per << (lvl + 1));
         for (int i = 1; i < kThreads / 32; ++i) rc.total[i] = 1.0f / static_cast<float>((i + 1) * 32 * per);
     }
-#define TU_LN(P, U) layer_norm_adaln_kernel<kT, P, U><<<grid, kThreads, 0, s>>>(x, sc, sh, out, len, hidden, steps, eps, rc)
+#define TU_LN(P, U) \
+    layer_norm_adaln_kernel<kT, P, U, kAffine><<<grid, kThreads, 0, s>>>(x, sc, sh, out, len, hidden, steps, eps, rc)
 #define TU_LN2(P) \
     if (uniform) TU_LN(P, true); \
     else TU_LN(P, false)
@@ -263,8 +279,27 @@ extern "C" int32_t tu_layer_norm_adaln(const void *x, const void *scale, const v
     if (require_gfx950()) return -1;
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int h = static_cast<int>(hidden);
-    if (dtype == 2) launch<2>(x, scale, shift, out, batch * len, len, h, steps, eps, s);
-    else if (dtype == 1) launch<1>(x, scale, shift, out, batch * len, len, h, steps, eps, s);
-    else launch<0>(x, scale, shift, out, batch * len, len, h, steps, eps, s);
+    if (dtype == 2) launch<2, false>(x, scale, shift, out, batch * len, len, h, steps, eps, s);
+    else if (dtype == 1) launch<1, false>(x, scale, shift, out, batch * len, len, h, steps, eps, s);
+    else launch<0, false>(x, scale, shift, out, batch * len, len, h, steps, eps, s);
     return check_launch("tu_layer_norm_adaln");
+}
+
+extern "C" int32_t tu_layer_norm_affine(const void *x, const void *weight, const void *bias, void *out,
+                                        int32_t dtype, int64_t rows, int64_t hidden, float eps, void *stream) {
+    using namespace tu;
+    TU_REQUIRE(dtype >= 0 && dtype <= 2, "LayerNorm dtype must be 0 (bf16), 1 (fp16) or 2 (fp32), got %d", dtype);
+    TU_REQUIRE(rows >= 0 && hidden > 0, "LayerNorm rows must be >= 0 and hidden positive");
+    TU_REQUIRE(rows <= 0x7fffffff && hidden <= 0x7fffffff, "LayerNorm dimensions exceed the kernel range");
+    TU_REQUIRE(eps > 0.0f && eps <= 3.4e38f, "LayerNorm epsilon must be finite and positive");
+    TU_REQUIRE(x && weight && bias && out, "LayerNorm pointers must be non-null");
+    if (require_gfx950()) return -1;
+    if (rows == 0) return 0;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int h = static_cast<int>(hidden);
+    // one batch of `rows` tokens and a single "modulation" row: weight / bias
+    if (dtype == 2) launch<2, true>(x, weight, bias, out, rows, rows, h, 1, eps, s);
+    else if (dtype == 1) launch<1, true>(x, weight, bias, out, rows, rows, h, 1, eps, s);
+    else launch<0, true>(x, weight, bias, out, rows, rows, h, 1, eps, s);
+    return check_launch("tu_layer_norm_affine");
 }

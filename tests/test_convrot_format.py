@@ -225,7 +225,7 @@ def test_wan_block_checkpoint_round_trip(tmp_path):
         cfg, modulation=torch.randn(1, 6, c, generator=g),
         self_qkv=_linear(3 * c, c, seed=1), self_o=_linear(c, c, seed=2),
         self_norm_q=torch.rand(c, generator=g) + 0.5, self_norm_k=torch.rand(c, generator=g) + 0.5,
-        norm3_weight=1 + torch.randint(-16, 17, (c,), generator=g) / 128, norm3_bias=torch.randn(c, generator=g),
+        norm3_weight=torch.randn(c, generator=g) * 0.5 + 1, norm3_bias=torch.randn(c, generator=g),
         cross_q=_linear(c, c, seed=4), cross_kv=_linear(2 * c, c, seed=5), cross_o=_linear(c, c, seed=6),
         cross_norm_q=torch.rand(c, generator=g) + 0.5, cross_norm_k=torch.rand(c, generator=g) + 0.5,
         ffn_up=_linear(f, c, seed=7), ffn_down=_linear(c, f, 256, seed=8))
@@ -237,8 +237,8 @@ def test_wan_block_checkpoint_round_trip(tmp_path):
     got = load_block(path, 7, cfg, prefix="model.diffusion_model.")
     for name in ("self_qkv", "self_o", "cross_q", "cross_kv", "cross_o", "ffn_up", "ffn_down"):
         _same(getattr(got, name), getattr(block, name))
-    for name in ("modulation", "self_norm_q", "self_norm_k", "cross_norm_q", "cross_norm_k", "norm3_scale",
-                 "norm3_shift"):
+    for name in ("modulation", "self_norm_q", "self_norm_k", "cross_norm_q", "cross_norm_k", "norm3_weight",
+                 "norm3_bias"):
         assert torch.equal(getattr(got, name), getattr(block, name)), name
     text = load_text_embedding(path, prefix="model.diffusion_model.")
     _same(text.fc1, linears["model.diffusion_model.text_embedding.0"])

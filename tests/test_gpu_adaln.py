@@ -120,3 +120,49 @@ def test_errors(gpu_device):
         turing_layer_norm_adaln(x, s[:, :, :32], s[:, :, :32], 1e-6)
     with pytest.raises(TypeError):
         turing_layer_norm_adaln(x[0], s, s, 1e-6)
+
+
+# ---------------------------------------------------------------------------
+# Affine LayerNorm (turing_utils::layer_norm_affine, tu_layer_norm_affine):
+# the Wan block's norm3 with weights of any sign and size
+# ---------------------------------------------------------------------------
+def _affine_case(rows, h, dtype, seed, offset=1.0):
+    g = torch.Generator().manual_seed(seed)
+    x = (torch.randn(rows, h, generator=g) * 3 + offset).to(dtype)
+    w = (1 + torch.randn(h, generator=g) * 0.5).to(dtype)  # N(1, 0.5): negative and sub-0.5 weights
+    b = (torch.randn(h, generator=g) * 0.3).to(dtype)
+    return x, w, b
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("rows,h", [(34, 5120), (33, 700), (5, 8192), (7, 9000), (1, 64), (12, 1536), (40, 257)])
+def test_affine_bit_exact_vs_oracle(gpu_device, dtype, rows, h):
+    print(f"layer_norm_affine {dtype} rows={rows} h={h}", flush=True)
+    x, w, b = _affine_case(rows, h, dtype, rows * 7 + h)
+    out = torch.ops.turing_utils.layer_norm_affine(x.to(gpu_device), w.to(gpu_device), b.to(gpu_device), 1e-6)
+    torch.cuda.synchronize(gpu_device)
+    ref = oracle.layer_norm_affine(_np(x), _np(w), _np(b), 1e-6, _DT[dtype])
+    np.testing.assert_array_equal(_bits_of(out), ref.view(np.uint32) if dtype == torch.float32 else ref)
+    assert (w.float() < 0).any()
+
+
+def test_affine_wan_shape_rows_and_3d(gpu_device):
+    """[1, 32760, 5120] bf16 through the op (3-D input, rows flattened); 600
+    rows checked against the oracle; the whole output against torch's
+    layer_norm within one bf16 step."""
+    print("layer_norm_affine Wan shape 32760x5120", flush=True)
+    g = torch.Generator(device=gpu_device).manual_seed(3)
+    x = (torch.randn(1, 32760, 5120, generator=g, device=gpu_device) * 2).to(torch.bfloat16)
+    w = (1 + torch.randn(5120, generator=g, device=gpu_device) * 0.5).to(torch.bfloat16)
+    b = (torch.randn(5120, generator=g, device=gpu_device) * 0.3).to(torch.bfloat16)
+    out = torch.ops.turing_utils.layer_norm_affine(x, w, b, 1e-6)
+    torch.cuda.synchronize(gpu_device)
+    rows = torch.randperm(32760, generator=torch.Generator().manual_seed(1))[:600].to(gpu_device)
+    ref = oracle.layer_norm_affine(_np(x[0, rows].cpu()), _np(w.cpu()), _np(b.cpu()), 1e-6, oracle.DTYPE_BF16)
+    np.testing.assert_array_equal(_bits_of(out[0, rows]), ref)
+    t = torch.nn.functional.layer_norm(x.float(), (5120,), w.float(), b.float(), eps=1e-6).to(torch.bfloat16)
+    diff = (out.float() - t.float()).abs()
+    mag = t.float().abs() + b.float().abs()
+    ulp = torch.exp2(torch.floor(torch.log2(mag.clamp_min(1e-30))) - 7)
+    assert (diff <= 2 * ulp + 1e-6).all()
+    assert (out == t).float().mean() > 0.99

@@ -136,3 +136,26 @@ def test_batch_of_two(harness, gpu_device):
     for i in range(2):
         alone = block(x[i:i + 1].contiguous(), e[i:i + 1], context[i:i + 1].contiguous(), freqs)
         assert torch.equal(alone, out[i:i + 1]), i
+
+
+def test_block_norm3_wide_affine_weights(harness, gpu_device):
+    """norm3 weights drawn from N(1, 0.5) (negative and sub-0.5 channels, which
+    the AdaLN form cannot express) and bias N(0, 0.3): the block still meets
+    the composition bar, and dropping norm3's weight in the reference is far
+    outside it."""
+    import copy
+
+    block, text = harness
+    g = torch.Generator(device=gpu_device).manual_seed(31)
+    wide = copy.copy(block)
+    wide.norm3_weight = (1 + 0.5 * torch.randn(5120, generator=g, device=gpu_device)).to(torch.bfloat16)
+    wide.norm3_bias = (0.3 * torch.randn(5120, generator=g, device=gpu_device)).to(torch.bfloat16)
+    assert (wide.norm3_weight < 0).any()
+    x, e, _, context, freqs = _inputs(block, text, (2, 16, 32), 77, 15, gpu_device)
+    out = wide(x, e, context, freqs)
+    want = ref.block_rows(wide, x, e, context, freqs)
+    _check("block update, wide norm3", out.float() - x.float(), want - x.float(), BLOCK_REL_MAX)
+    dropped = copy.copy(wide)
+    dropped.norm3_weight = torch.ones_like(wide.norm3_weight)
+    bad = ref.metrics(out.float() - x.float(), ref.block_rows(dropped, x, e, context, freqs) - x.float())
+    assert bad["rel_l2"] > 2 * BLOCK_REL_MAX, bad

@@ -127,3 +127,67 @@ def test_modulation_row_mapping(steps, length):
     if length < steps:  # repeats == 0: the reference keeps the unexpanded rows
         expect = torch.arange(length).float().clamp_max(steps - 1)
     assert torch.equal(rows[0], expect)
+
+
+# ---------------------------------------------------------------------------
+# Affine LayerNorm (weight / bias), the Wan block's norm3 as ComfyUI runs it:
+# torch.nn.functional.layer_norm(x, (H,), weight, bias, eps)
+# ---------------------------------------------------------------------------
+def _affine(x, w, b, eps):
+    dt = {torch.bfloat16: oracle.DTYPE_BF16, torch.float16: oracle.DTYPE_FP16}[x.dtype]
+    return _from_bits(oracle.layer_norm_affine(_bits(x), _bits(w), _bits(b), eps, dt), x.dtype)
+
+
+def _affine_inputs(rows, hidden, dtype, seed, offset=0.0):
+    g = torch.Generator().manual_seed(seed)
+    x = (torch.randn(rows, hidden, generator=g) * 2 + offset).to(dtype)
+    w = (1 + torch.randn(hidden, generator=g) * 0.5).to(dtype)  # includes negative and sub-0.5 weights
+    b = (torch.randn(hidden, generator=g) * 0.3).to(dtype)
+    return x, w, b
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("hidden,offset", [(5120, 0.0), (700, 3.0), (64, 0.0), (8192, 100.0)])
+def test_affine_matches_torch_layer_norm(dtype, hidden, offset):
+    """torch's layer_norm with weight and bias on the CPU, computed in fp32 and
+    rounded once: equal except where the two fp32 values straddle a rounding
+    tie (a different statistics order), and never more than one step apart."""
+    x, w, b = _affine_inputs(33, hidden, dtype, hidden + 7, offset)
+    out = _affine(x, w, b, 1e-6).float()
+    ref = torch.nn.functional.layer_norm(x.float(), (hidden,), w.float(), b.float(), eps=1e-6).to(dtype).float()
+    # both are fp32 statistics in different orders; at an offset the mean's
+    # fp32 rounding moves the normalized values, for torch as for the oracle,
+    # so the bar is torch's own agreement with the fp64 formula
+    xs = x.double()
+    n = (xs - xs.mean(-1, keepdim=True)) / torch.sqrt(xs.var(-1, unbiased=False, keepdim=True) + 1e-6)
+    r64 = (n * w.double() + b.double()).to(dtype).float()
+    torch_vs_fp64 = (ref == r64).float().mean()
+    assert (out == r64).float().mean() >= torch_vs_fp64 - 5e-3
+    assert (out == ref).float().mean() > (0.995 if offset == 0 else 0.98)
+    # a moved normalized value shifts the result by a step of n * w, whose
+    # magnitude is at most |out| + |b| (cancellation near zero)
+    mag = ref.abs() + b.float().abs()
+    ulp = 2.0 ** (torch.floor(torch.log2(mag.clamp_min(1e-30))) - (7 if dtype == torch.bfloat16 else 10))
+    assert ((out - ref).abs() <= 2 * ulp + 1e-7).all()
+    assert (w.float() < 0.5).any() and (w.float() < 0).any()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_affine_fp64_formula_and_planted_mistakes(dtype):
+    """T((x - mean) / sqrt(var + eps) * w + b) in fp64 agrees except near ties;
+    the AdaLN form T(T(n) T(1 + (w - 1))) + b), a dropped bias or an unbiased
+    variance each move far more elements."""
+    x, w, b = _affine_inputs(40, 1536, dtype, 3)
+    out = _affine(x, w, b, 1e-6).float()
+    xs = x.double()
+    n = (xs - xs.mean(-1, keepdim=True)) / torch.sqrt(xs.var(-1, unbiased=False, keepdim=True) + 1e-6)
+    ref = (n * w.double() + b.double()).to(dtype).float()
+    same = (out == ref).float().mean()
+    assert same > 0.995
+    nb = n.to(dtype).double()
+    adaln_form = (nb * w.double() + b.double()).to(dtype).float()
+    no_bias = (n * w.double()).to(dtype).float()
+    unbiased = ((xs - xs.mean(-1, keepdim=True)) / torch.sqrt(xs.var(-1, unbiased=True, keepdim=True) + 1e-6)
+                * w.double() + b.double()).to(dtype).float()
+    for wrong in (adaln_form, no_bias, unbiased):
+        assert (out == wrong).float().mean() < same - 0.01

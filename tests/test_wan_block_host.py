@@ -20,12 +20,13 @@ def _kwargs(c=256, f=512):
 CFG = WanBlockConfig(dim=256, heads=2, ffn_dim=512, text_dim=256)
 
 
-def test_norm3_weight_must_be_one_plus_a_bf16_value():
-    ones = torch.ones(256)
-    WanBlockW8A8(CFG, norm3_weight=ones * 1.25, **_kwargs())
-    with pytest.raises(ValueError, match="norm3"):
-        # 129 / 512: w - 1 = -383 / 512 is a bf16 tie that rounds to -0.75
-        WanBlockW8A8(CFG, norm3_weight=ones * 0.251953125, **_kwargs())
+def test_norm3_takes_any_affine_weight():
+    """norm3 is a plain affine LayerNorm: weights below 0.5, negative or
+    not of the form 1 + a bf16 value (129 / 512 is one) are kept as given."""
+    w = torch.tensor([0.251953125, -0.3, 0.01, -3.5, 1.25, 0.0] * 43)[:256]
+    block = WanBlockW8A8(CFG, norm3_weight=w, **_kwargs())
+    assert torch.equal(block.norm3_weight, w.to(torch.bfloat16))
+    assert block.norm3_bias.shape == (256,)
 
 
 def test_linear_shapes_and_inputs_are_checked():

@@ -124,8 +124,8 @@ def block_rows(block, x: torch.Tensor, e: torch.Tensor, context: torch.Tensor, f
     h = layer_norm(xf, cfg.eps) * (1 + e1) + e0
     xr = xf if rows is None else xf[:, rows]
     xr = xr + self_attention(block, h, freqs, rows) * e2
-    w3 = 1 + block.norm3_scale.float()
-    xr = xr + cross_attention(block, layer_norm(xr, cfg.eps) * w3 + block.norm3_shift.float(), context)
+    xr = xr + cross_attention(block, layer_norm(xr, cfg.eps) * block.norm3_weight.float() + block.norm3_bias.float(),
+                              context)
     return xr + ffn(block, layer_norm(xr, cfg.eps) * (1 + e4) + e3) * e5
 
 

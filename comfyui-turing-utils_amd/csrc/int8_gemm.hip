@@ -176,11 +176,15 @@ struct Frags {
 constexpr uint32_t kBf16OnePair = 0x3f803f80u;
 
 // kResidual: out = bf16_rn(fma(y, gate[row / gate_rows][col], residual[row][col]))
-// with y the bf16 epilogue value (gate 1 when absent).  residual may be out.
+// with y the bf16 epilogue value (gate 1 when absent).  residual may be out
+// (in place), so neither carries __restrict__: each output chunk is read as
+// residual and then written by the same lane, and no lane stores a chunk
+// that another lane reads (clamped reads past the last row feed only rows
+// that are never stored).
 template <bool kI32Out, bool kResidual>
 __global__ __launch_bounds__(kThreads, kWaves / 4) void int8_gemm_kernel(
     const int8_t *__restrict__ a, const int8_t *__restrict__ w, const float *__restrict__ as,
-    const float *__restrict__ ws, const float *__restrict__ bias, void *__restrict__ out,
+    const float *__restrict__ ws, const float *__restrict__ bias, void *out,
     int64_t m, int64_t n, int64_t k, int tiles_m, int tiles_n, const uint16_t *residual, const uint16_t *gate,
     int64_t gate_rows) {
     __shared__ __align__(1024) int8_t lds[kStages][kStageBytes];

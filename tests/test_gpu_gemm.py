@@ -97,6 +97,38 @@ def test_int8_linear_residual_exact(gpu_device, m, n, k, with_bias, gate_rows):
     np.testing.assert_array_equal(inputs.bits(res_dev), inputs.bits(residual))
 
 
+@pytest.mark.parametrize("gate_rows", [None, 37])
+@pytest.mark.parametrize("m,n,k", [(300, 264, 192), (257, 520, 1040), (513, 776, 1536)])
+def test_residual_in_place_through_the_c_abi(gpu_device, m, n, k, gate_rows):
+    """tu_int8_gemm_bf16_residual with out == residual (the header allows it):
+    bit-exact against the oracle on ragged M / N tiles."""
+    from comfyui_turing_utils_kernel import _lib
+
+    print(f"[int8_gemm_bf16_residual in place] m={m} n={n} k={k} gate_rows={gate_rows}", flush=True)
+    a = _rand_i8((m, k), 21 + m)
+    w, ws, bias = inputs.weights(n, k, 6, True)
+    g = torch.Generator().manual_seed(9)
+    as_ = torch.empty(m).uniform_(1e-3, 1e-1, generator=g)
+    residual = (torch.randn(m, n, generator=g) * 4).to(torch.bfloat16)
+    gate = None
+    if gate_rows is not None:
+        gate = torch.empty((m + gate_rows - 1) // gate_rows, n).uniform_(-2, 2, generator=g).to(torch.bfloat16)
+    dev = gpu_device
+    ad, wd, asd, wsd, bd = a.to(dev), w.to(dev), as_.to(dev), ws.to(dev), bias.to(dev)
+    buf = residual.to(dev)
+    gd = None if gate is None else gate.to(dev)
+    with torch.cuda.device(dev):
+        _lib.call("tu_int8_gemm_bf16_residual", ad.data_ptr(), wd.data_ptr(), asd.data_ptr(), wsd.data_ptr(),
+                  bd.data_ptr(), buf.data_ptr(), _lib.ptr(gd), 1 if gate_rows is None else gate_rows,
+                  buf.data_ptr(), m, n, k, _lib.stream_of(dev))
+    torch.cuda.synchronize(dev)
+    y = oracle.epilogue_bf16(oracle.int8_gemm_i32(a.numpy(), w.numpy()), as_.numpy(), ws.numpy(), bias.numpy())
+    ref = oracle.residual_gate_bf16(y, inputs.bits(residual), None if gate is None else inputs.bits(gate),
+                                    1 if gate_rows is None else gate_rows)
+    bad = np.argwhere(inputs.bits(buf) != ref)
+    assert bad.size == 0, f"{len(bad)} outputs differ, first {bad[:5].tolist()}"
+
+
 def test_int8_linear_config1_rows(gpu_device):
     """BASELINE config 1 through the drop-in ops (quantize G=128, then int8_linear);
     128 sampled rows checked bit-exact against the oracle chain."""

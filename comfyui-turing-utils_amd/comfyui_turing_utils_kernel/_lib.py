@@ -50,6 +50,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _i32,
         [_c_void_p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _c_void_p, _c_void_p, _c_void_p],
     ),
+    "tu_sage_kmean_noalloc": (
+        _i32,
+        [_c_void_p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _c_void_p, _c_void_p],
+    ),
     "tu_sage_quant": (
         _i32,
         [_c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
@@ -106,7 +110,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
 }
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

@@ -17,12 +17,21 @@
 //   per-thread sums run over ascending tokens, the rows partial sums of a
 //   chunk are added in ascending row order, and the chunk sums in ascending
 //   chunk order by a second kernel.
+#include <mutex>
+
 #include "tu_common.h"
 
 namespace tu {
 namespace {
 
 constexpr int kThreads = 256;
+
+// Chunk-sum scratch of tu_sage_kmean_noalloc: a file-scope device array that
+// every GPU running this library holds until the process ends.  In host code
+// `scratch` names a host-side stand-in, not a device address; the device
+// address comes from hipGetSymbolAddress, once per device (scratch_ptr).
+constexpr int64_t kNoAllocScratchFloats = int64_t{1} << 22;  // 16 MiB
+static __device__ __align__(256) float scratch[kNoAllocScratchFloats];
 
 template <int D>
 __global__ __launch_bounds__(kThreads) void kmean_chunk_kernel(const uint16_t *__restrict__ k, int64_t len,
@@ -230,6 +239,71 @@ extern "C" int32_t tu_sage_kmean(const void *k_bf16, int64_t batch, int64_t head
     kmean_final_kernel<<<dim3(static_cast<unsigned>(batch * heads)), 128, 0, s>>>(
         chunk_sums, chunks, len, static_cast<int>(dim), static_cast<uint16_t *>(mean_bf16));
     return check_launch("tu_sage_kmean(final)");
+}
+
+namespace tu {
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+float *g_scratch_ptr[kMaxDevices];
+
+// Device address of `scratch` on the current device, looked up on the first
+// call on that device (with the device current) and kept per device.
+int32_t scratch_ptr(float **out) {
+    int dev = 0;
+    hipError_t err = hipGetDevice(&dev);
+    if (err != hipSuccess) return fail("hipGetDevice failed: %s", hipGetErrorString(err));
+    if (dev < 0 || dev >= kMaxDevices) return fail("device %d is beyond the %d devices this library serves", dev,
+                                                   kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (err != hipSuccess || !p)
+            return fail("hipGetSymbolAddress(scratch) on device %d failed: %s", dev, hipGetErrorString(err));
+        g_scratch_ptr[dev] = static_cast<float *>(p);
+    }
+    *out = g_scratch_ptr[dev];
+    return 0;
+}
+
+}  // namespace
+}  // namespace tu
+
+extern "C" int32_t tu_sage_kmean_noalloc(const void *k_bf16, int64_t batch, int64_t heads, int64_t len,
+                                         int64_t dim, int64_t s_b, int64_t s_h, int64_t s_l, void *mean_bf16,
+                                         void *stream) {
+    using namespace tu;
+    TU_REQUIRE(dim == 64 || dim == 128, "K mean requires head_dim 64 or 128, got %lld", static_cast<long long>(dim));
+    TU_REQUIRE(batch > 0 && heads > 0 && len > 0, "K mean requires positive batch, heads and length");
+    TU_REQUIRE(heads <= 65535 && batch <= 65535 && (len + 127) / 128 <= 0x7fffffff, "K mean grid too large");
+    TU_REQUIRE(k_bf16 && mean_bf16, "K mean pointers must be non-null");
+    TU_REQUIRE(s_l % 8 == 0 && s_h % 8 == 0 && s_b % 8 == 0 && (reinterpret_cast<uintptr_t>(k_bf16) & 15) == 0,
+               "K mean needs 16-byte aligned token rows");
+    const int64_t chunks = (len + 127) / 128;
+    // batch, heads <= 65535 and chunks < 2^31 cannot overflow the product in
+    // steps: check each factor against the limit first
+    TU_REQUIRE(chunks <= kNoAllocScratchFloats / dim &&
+                   batch * heads <= kNoAllocScratchFloats / (chunks * dim),
+               "K mean without allocation: batch*heads*ceil(len/128)*dim = %lld*%lld*%lld*%lld exceeds the "
+               "%lld-float scratch (use tu_sage_kmean with caller scratch)",
+               static_cast<long long>(batch), static_cast<long long>(heads), static_cast<long long>(chunks),
+               static_cast<long long>(dim), static_cast<long long>(kNoAllocScratchFloats));
+    if (require_gfx950()) return -1;
+    float *chunk_sums = nullptr;
+    if (scratch_ptr(&chunk_sums)) return -1;
+    // Every chunk sum the final kernel reads is written by the chunk kernel
+    // of the same call first, so nothing needs clearing.
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const dim3 grid(static_cast<unsigned>(chunks), static_cast<unsigned>(heads), static_cast<unsigned>(batch));
+    const auto *k = static_cast<const uint16_t *>(k_bf16);
+    if (dim == 128) kmean_chunk_kernel<128><<<grid, kThreads, 0, s>>>(k, len, s_b, s_h, s_l, chunk_sums);
+    else kmean_chunk_kernel<64><<<grid, kThreads, 0, s>>>(k, len, s_b, s_h, s_l, chunk_sums);
+    if (check_launch("tu_sage_kmean_noalloc(chunks)")) return -1;
+    kmean_final_kernel<<<dim3(static_cast<unsigned>(batch * heads)), 128, 0, s>>>(
+        chunk_sums, chunks, len, static_cast<int>(dim), static_cast<uint16_t *>(mean_bf16));
+    return check_launch("tu_sage_kmean_noalloc(final)");
 }
 
 extern "C" int32_t tu_sage_quant(const void *x_bf16, const void *mean_bf16, int64_t batch, int64_t heads,

@@ -136,6 +136,21 @@ int32_t tu_sage_kmean(const void *k_bf16, int64_t batch, int64_t heads, int64_t 
                       int64_t dim, int64_t s_b, int64_t s_h, int64_t s_l, float *chunk_sums,
                       void *mean_bf16, void *stream);
 
+/* tu_sage_kmean without caller scratch and without any allocation: the
+ * chunk sums live in a file-scope device array of 2^22 floats (16 MiB) that
+ * each GPU running the library holds until the process ends; its device
+ * address is looked up once per device on the first call there.  Same
+ * arguments and result as tu_sage_kmean minus `chunk_sums`; rejects
+ * batch*heads*ceil(len/128)*dim > 2^22 (e.g. Wan-14B's B1 H40 L32760 D128
+ * needs 1310720).  Every call on one GPU shares that GPU's array: calls that
+ * overlap on one GPU (other streams, other host threads) race; calls in one
+ * stream are ordered.  No counterpart in the reference: it is for callers
+ * that cannot allocate (HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc). */
+int32_t tu_sage_kmean_noalloc(const void *k_bf16, int64_t batch, int64_t heads, int64_t len,
+                              int64_t dim, int64_t s_b, int64_t s_h, int64_t s_l, void *mean_bf16,
+                              void *stream);
+
 /* Per-block symmetric INT8 quantization of Q or K, optionally after
  * subtracting a per-(batch, head) channel mean (K smoothing):
  *   amax = max(1e-7, max |x - mean| over blk tokens x dim channels)

@@ -13,10 +13,12 @@
 // MI355X mapping
 //   * Workgroup = 8 wave64 = 256 query rows of one (batch, head): two groups
 //     of 4 waves, 32 rows (two 16-row fragments) per wave, one wave of each
-//     group per SIMD.  The groups run the same program one phase apart
-//     (ping-pong): while one group issues its MFMA cluster, the other runs its
-//     softmax VALU cluster on the same SIMD; a workgroup barrier separates the
-//     phases.
+//     group per SIMD.  One workgroup barrier per key tile; within a tile's
+//     interval group 0 runs its MFMA cluster then its softmax VALU cluster,
+//     group 1 the softmax first, so each SIMD sees one wave's MFMAs beside the
+//     other's VALU work, with the two MFMA clusters overlapping in the middle
+//     (a lone wave issues 16x16 MFMAs at about 60 % of the pipe, two waves
+//     together fill it).
 //   * Keys stream in tiles of 64 through a 5-stage LDS ring (24 KiB a stage)
 //     filled by buffer_load_dwordx4 ... lds (no staging registers) from group
 //     0, four tiles ahead of the MFMAs.  V arrives pre-transposed (V^T,
@@ -313,17 +315,19 @@ __device__ __forceinline__ void mfma_cluster(const int8_t *kst, const int8_t *vs
     __builtin_amdgcn_s_setprio(0);
 }
 
-// Ping-pong schedule.  A workgroup is 8 waves in two groups of 4 (one wave of
-// each group per SIMD), 256 query rows of one (batch, head).  Each wave runs
-// the same sequence of clusters over the key tiles t = 0 .. T-1:
-//   C0 = QK(0), C1 = softmax(0), then per tile
-//   M_t = { QK(t+1), PV(t) }   (MFMA cluster; also LDS operand reads)
-//   V_t = { softmax(t+1) }     (VALU cluster)
-// with a workgroup barrier after every cluster.  Group 1 starts one barrier
-// later than group 0, so while one group is in an MFMA cluster the other is
-// in a VALU cluster on the same SIMD.  Group 0 alone streams the K and V^T
-// tiles through a kStages-deep LDS ring, kAhead tiles ahead, and waits for
-// the tile the next MFMA cluster reads before the barrier that opens it.
+// Schedule.  A workgroup is 8 waves in two groups of 4 (one wave of each
+// group per SIMD), 256 query rows of one (batch, head).  Each wave runs the
+// same sequence of clusters over the key tiles t = 0 .. T-1:
+//   QK(0), softmax(0), then per tile M_t = { QK(t+1), PV(t) } and
+//   softmax(t+1),
+// with one workgroup barrier per interval: interval 0 = [QK(0), softmax(0)]
+// for group 0 and [QK(0)] for group 1; interval t+1 = [M_t, softmax(t+1)]
+// for group 0 and [softmax(t), M_t] for group 1.  Both groups read tiles t
+// and t+1 in interval t+1.  Group 0 alone streams the K and V^T tiles
+// through a kStages-deep LDS ring, kAhead tiles ahead, and waits for the
+// tile the next interval reads before the barrier that opens it.
+// tests/test_attn_schedule.py replays these loops on the host and checks
+// equal barrier counts and ring residency for every wave.
 constexpr int kStages = 5;
 constexpr int kAhead = kStages - 1;
 constexpr int kLoadsPerTile = 6;  // per group-0 wave: 2 K + 4 V^T 1 KiB blocks
@@ -425,42 +429,52 @@ __global__ __launch_bounds__(kThreads, 1) void sage_attn_kernel(
     // Group 0 has tile 0 (and the Q loads) resident before the first barrier.
     if (grp == 0) __builtin_amdgcn_s_waitcnt(vmcnt_imm((kAhead - 1) * kLoadsPerTile));
     wg_barrier();
-    if (grp == 1) wg_barrier();
-    // C0 = QK(0), C1 = softmax(0); group 0 then waits for tile 1.
+    // Interval 0: QK(0); group 0 also runs softmax(0) and waits for tile 1.
+    // Group 1 runs softmax(0) right after the barrier, opening interval 1.
     qk_tile(lds[0], gm, qf, s);
-    wg_barrier();
-    softmax(0, std::true_type{});
-    if (grp == 0) __builtin_amdgcn_s_waitcnt(vmcnt_imm((kAhead - 2) * kLoadsPerTile));
-    wg_barrier();
-    // Steady-state steps: M_it = QK(it + 1), PV(it); V_it = unmasked
-    // softmax(it + 1).  Group 0 issues tile it + kAhead in M_it and, before
-    // the barrier that ends V_it, waits for tile it + 2, which M_{it + 1}
-    // reads.
     const int main_steps = max(0, min(my_tiles, first_masked) - 1);
+    if (grp == 0) {
+        softmax(0, std::true_type{});
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm((kAhead - 2) * kLoadsPerTile));
+    }
+    wg_barrier();
+    if (grp == 1) softmax(0, std::true_type{});
+    // Intervals 1 .. main_steps, one barrier each.  Both groups run the same
+    // sequence M_it = {QK(it + 1), PV(it)}, softmax(it + 1); group 0's
+    // barrier follows the softmax, group 1's precedes it, so interval it + 1
+    // is [M_it, softmax(it + 1)] for group 0 and [softmax(it), M_it] for
+    // group 1: on each SIMD the second half of one wave's MFMA cluster
+    // overlaps the first half of the other's.  Group 0 issues tile
+    // it + kAhead after its MFMA cluster (its stage held tile it - 1, which
+    // both groups last read in the previous interval) and, before its
+    // barrier, waits for tile it + 2, which interval it + 2 reads.
 #pragma clang loop unroll(disable)
     for (int it = 0; it < main_steps; ++it) {
         mfma_cluster(lds[(it + 1) % kStages], lds[it % kStages], gm, qf, s, pb, st, ones);
-        if (grp == 0)
-            issue_tile(lds[(it + kAhead) % kStages], krs, vrs, gm, k_sl32, tile_key0(it + kAhead), w4);
-        wg_barrier();
+        if (grp == 0) issue_tile(lds[(it + kAhead) % kStages], krs, vrs, gm, k_sl32, tile_key0(it + kAhead), w4);
+        else wg_barrier();
         softmax(it + 1, std::false_type{});
-        if (grp == 0) __builtin_amdgcn_s_waitcnt(vmcnt_imm((kAhead - 2) * kLoadsPerTile));
-        wg_barrier();
+        if (grp == 0) {
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm((kAhead - 2) * kLoadsPerTile));
+            wg_barrier();
+        }
     }
-    // Remaining steps: masked tiles, the last tile, and (causal) tiles past
-    // this wave's diagonal, which only keep the barrier count.
+    // Remaining intervals: masked tiles, the last tile, and (causal) tiles
+    // past this wave's diagonal, which only keep the barrier count.  Group 1
+    // has already run softmax(main_steps).
 #pragma clang loop unroll(disable)
     for (int it = main_steps; it < tiles; ++it) {
         if (grp == 0)
             issue_tile(lds[(it + kAhead) % kStages], krs, vrs, gm, k_sl32, tile_key0(it + kAhead), w4);
         if (it + 1 < my_tiles) qk_tile(lds[(it + 1) % kStages], gm, qf, s);
         if (it < my_tiles) pv_tile(lds[it % kStages], gm, pb, st, ones);
-        wg_barrier();
+        if (grp == 1) wg_barrier();
         if (it + 1 < my_tiles) softmax(it + 1, std::true_type{});
-        if (grp == 0) __builtin_amdgcn_s_waitcnt(vmcnt_imm((kAhead - 2) * kLoadsPerTile));
-        wg_barrier();
+        if (grp == 0) {
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm((kAhead - 2) * kLoadsPerTile));
+            wg_barrier();
+        }
     }
-    if (grp == 0) wg_barrier();
     __builtin_amdgcn_s_waitcnt(0);
 
     // acc_o[ds][qt][r] = O[q0 + 16 qt + lc][16 ds + 4 g + r]; acc_l[qt][*] = l.

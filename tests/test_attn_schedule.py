@@ -1,0 +1,241 @@
+"""Host model of the Sage attention kernel's barrier and LDS-ring schedule.
+
+``sage_attn_kernel`` (csrc/sage_attn.hip) runs 8 waves in two groups that
+share one workgroup barrier per key tile.  Every wave executes, per tile t,
+an MFMA cluster M_t = {QK(t + 1), PV(t)} and a softmax cluster V_t; group 0
+orders an interval as [M_t, V_{t+1}], group 1 as [V_t, M_t], so the two
+groups' MFMA clusters overlap on each SIMD.  Group 0 alone streams the K and
+V^T tiles into a ring of kStages LDS stages, kAhead tiles ahead, and waits on
+its own load counter before a barrier.
+
+This model replays, wave by wave, the same loops, bounds and counts as the
+kernel (non-causal and causal, ragged tails, waves past the causal diagonal)
+and checks what the GPU cannot be allowed to get wrong:
+  * every wave executes the same number of barriers (a mismatch hangs);
+  * every LDS stage a cluster reads holds the tile it expects, resident
+    (its loads waited for before the barrier that opens the interval);
+  * no stage is reloaded while any wave may still read it (no load into a
+    stage in the interval of, or between the issue and, a read of another
+    tile from it);
+  * each softmax consumes the scores of the QK it follows and each PV the
+    P of the softmax of the same tile, in order.
+"""
+from __future__ import annotations
+
+import itertools
+
+import pytest
+
+K_STAGES = 5
+K_AHEAD = K_STAGES - 1
+LOADS_PER_TILE = 6  # per group-0 wave: 2 K + 4 V^T 1 KiB blocks
+KBKEY = 64
+KBQ = 256
+KWAVEQ = 32
+
+
+class Wave:
+    def __init__(self, wave: int):
+        self.wave = wave
+        self.grp = wave >> 2
+        self.events = []  # (kind, payload) in program order
+
+    def barrier(self):
+        self.events.append(("barrier", None))
+
+    def issue(self, stage, tile):
+        self.events.append(("issue", (stage, tile)))
+
+    def wait(self, n):
+        self.events.append(("wait", n))
+
+    def qk(self, stage, tile):
+        self.events.append(("read", (stage, tile, "K")))
+        self.events.append(("qk", tile))
+
+    def pv(self, stage, tile):
+        self.events.append(("read", (stage, tile, "V")))
+        self.events.append(("pv", tile))
+
+    def softmax(self, tile, masked):
+        self.events.append(("softmax", (tile, masked)))
+
+
+def kernel_program(wave: int, lq: int, lk: int, causal: bool, qblock: int) -> Wave:
+    """The kernel's control flow for one wave, statement for statement."""
+    w = Wave(wave)
+    grp, w4 = wave >> 2, wave & 3
+    qblock0 = qblock * KBQ
+    q0 = qblock0 + grp * (KBQ // 2) + w4 * KWAVEQ
+    key_end = min(lk, qblock0 + KBQ) if causal else lk
+    tiles = (key_end + KBKEY - 1) // KBKEY
+    my_tiles = tiles
+    if causal:
+        my_tiles = min(tiles, max(1, (min(q0 + KWAVEQ, lq) + KBKEY - 1) // KBKEY))
+    mask_from = lk // KBKEY
+    if causal:
+        mask_from = min(mask_from, q0 // KBKEY)
+    first_masked = min(tiles, mask_from)
+    tile_key0 = lambda it: min(it, tiles - 1)  # noqa: E731  (tile index the load reads)
+
+    def softmax(it, mask_tag):
+        if not mask_tag:
+            assert it < first_masked, "unmasked softmax on a tile that needs a mask"
+        w.softmax(it, mask_tag and it >= first_masked)
+
+    if grp == 0:
+        for j in range(K_AHEAD):
+            w.issue(j, tile_key0(j))
+        w.wait((K_AHEAD - 1) * LOADS_PER_TILE)
+    w.barrier()
+    # interval 0: QK(0) (and, group 0, softmax(0)); group 1 runs softmax(0)
+    # right after the barrier
+    w.qk(0, 0)
+    main_steps = max(0, min(my_tiles, first_masked) - 1)
+    if grp == 0:
+        softmax(0, True)
+        w.wait((K_AHEAD - 2) * LOADS_PER_TILE)
+    w.barrier()
+    if grp == 1:
+        softmax(0, True)
+    # intervals 1 .. main_steps: unmasked steady state; the same sequence for
+    # both groups, group 1's barrier before the softmax, group 0's after
+    for it in range(main_steps):
+        w.qk((it + 1) % K_STAGES, it + 1)
+        w.pv(it % K_STAGES, it)
+        if grp == 0:
+            w.issue((it + K_AHEAD) % K_STAGES, tile_key0(it + K_AHEAD))
+        else:
+            w.barrier()
+        softmax(it + 1, False)
+        if grp == 0:
+            w.wait((K_AHEAD - 2) * LOADS_PER_TILE)
+            w.barrier()
+    # remaining intervals: masked tiles, the last tile, causal tiles past the
+    # wave's diagonal (barriers only)
+    for it in range(main_steps, tiles):
+        if grp == 0:
+            w.issue((it + K_AHEAD) % K_STAGES, tile_key0(it + K_AHEAD))
+        if it + 1 < my_tiles:
+            w.qk((it + 1) % K_STAGES, it + 1)
+        if it < my_tiles:
+            w.pv(it % K_STAGES, it)
+        if grp == 1:
+            w.barrier()
+        if it + 1 < my_tiles:
+            softmax(it + 1, True)
+        if grp == 0:
+            w.wait((K_AHEAD - 2) * LOADS_PER_TILE)
+            w.barrier()
+    return w, dict(tiles=tiles, my_tiles=my_tiles)
+
+
+def check_schedule(lq: int, lk: int, causal: bool, qblock: int):
+    waves = [kernel_program(i, lq, lk, causal, qblock) for i in range(8)]
+    progs = [w for w, _ in waves]
+    # 1. equal barrier counts
+    counts = [sum(1 for k, _ in p.events if k == "barrier") for p in progs]
+    assert len(set(counts)) == 1, f"barrier counts differ: {counts}"
+    n_intervals = counts[0] + 1  # interval i precedes barrier i
+    # split each wave's events into intervals
+    intervals = []
+    for p in progs:
+        cur, out = [], []
+        for ev in p.events:
+            if ev[0] == "barrier":
+                out.append(cur)
+                cur = []
+            else:
+                cur.append(ev)
+        out.append(cur)
+        assert len(out) == n_intervals
+        intervals.append(out)
+    # 2. loads: group 0 waves issue identical loads; model the loader's
+    # outstanding queue (loads complete in issue order for the wait counter)
+    loaders = [i for i in range(8) if progs[i].grp == 0]
+    for i in loaders[1:]:
+        assert [e for e in progs[i].events if e[0] in ("issue", "wait")] == \
+               [e for e in progs[loaders[0]].events if e[0] in ("issue", "wait")]
+    stage_content = {}  # stage -> (tile, resident_from_interval)
+    outstanding = []  # [(stage, tile, ops_left)] in issue order
+    resident_at = {}  # (stage, tile) -> first interval in which it may be read
+    issued_in = {}  # (stage, tile) -> interval of issue
+    reads = []  # (interval, wave, stage, tile)
+    for k in range(n_intervals):
+        for ev in intervals[loaders[0]][k]:
+            kind, pay = ev
+            if kind == "issue":
+                stage, tile = pay
+                outstanding.append([stage, tile])
+                issued_in[(stage, tile, len(outstanding))] = k
+                stage_content.setdefault(stage, [])
+                stage_content[stage].append((tile, k))
+            elif kind == "wait":
+                # all but the most recent pay // LOADS_PER_TILE tiles complete
+                keep = pay // LOADS_PER_TILE
+                assert pay % LOADS_PER_TILE == 0
+                while len(outstanding) > keep:
+                    stage, tile = outstanding.pop(0)
+                    resident_at.setdefault((stage, tile), k + 1)
+        for wi in range(8):
+            for kind, pay in intervals[wi][k]:
+                if kind == "read":
+                    stage, tile, _ = pay
+                    reads.append((k, wi, stage, tile))
+    # 3. every read finds its tile resident and not overwritten
+    for k, wi, stage, tile in reads:
+        hist = stage_content.get(stage, [])
+        # the most recent load into the stage issued before interval k
+        before = [(t, ki) for t, ki in hist if ki < k]
+        assert before, f"interval {k} wave {wi}: stage {stage} never loaded"
+        t_last, k_last = before[-1]
+        assert t_last == tile, f"interval {k} wave {wi}: stage {stage} holds tile {t_last}, expected {tile}"
+        assert resident_at.get((stage, tile), 10 ** 9) <= k, \
+            f"interval {k} wave {wi}: tile {tile} in stage {stage} not waited for"
+        # no load into this stage during interval k (a concurrent overwrite)
+        assert not any(ki == k and t != tile for t, ki in hist), \
+            f"interval {k}: stage {stage} reloaded while wave {wi} reads tile {tile}"
+    # 4. per-wave data flow: QK(t) -> softmax(t) -> PV(t), each once, in order
+    for (p, info), wi in zip(waves, range(8)):
+        seq = [(k, pay) for k, pay in p.events if k in ("qk", "softmax", "pv")]
+        last_qk, last_sm, last_pv = -1, -1, -1
+        for kind, pay in seq:
+            if kind == "qk":
+                assert pay == last_qk + 1 and last_sm == pay - 1
+                last_qk = pay
+            elif kind == "softmax":
+                t = pay[0]
+                assert t == last_sm + 1 and last_qk == t, (wi, kind, pay, last_qk)
+                last_sm = t
+            else:
+                assert pay == last_pv + 1 and last_sm == pay
+                last_pv = pay
+        assert last_pv == info["my_tiles"] - 1 and last_sm == info["my_tiles"] - 1, (wi, info, last_pv)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("lk", [1, 2, 63, 64, 65, 127, 128, 129, 191, 256, 257, 300, 333, 511, 700, 1000, 32760])
+def test_schedule_every_block(causal, lk):
+    lq = lk if causal else max(lk, 300)
+    for qblock in range((lq + KBQ - 1) // KBQ):
+        check_schedule(lq, lk, causal, qblock)
+
+
+@pytest.mark.parametrize("lq,lk", list(itertools.product([1, 40, 129, 256, 257, 700], [1, 2, 64, 65, 151, 333])))
+def test_schedule_ragged_pairs(lq, lk):
+    for causal in (False, True):
+        for qblock in range((lq + KBQ - 1) // KBQ):
+            check_schedule(lq, lk, causal, qblock)
+
+
+def test_model_catches_a_missing_wait():
+    """Planted mistake: without the loader's wait in the steady state, a
+    read finds its tile not yet resident."""
+    global K_AHEAD
+    saved = K_AHEAD
+    try:
+        K_AHEAD = 5  # loads one stage further ahead than the ring holds
+        with pytest.raises(AssertionError):
+            check_schedule(1000, 1000, False, 0)
+    finally:
+        K_AHEAD = saved

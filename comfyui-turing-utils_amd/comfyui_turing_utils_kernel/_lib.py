@@ -98,7 +98,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          _c_void_p, _i64, _c_void_p, _i32,
          _i64, _i64, _i64, _i64, _i64, _i64,
          _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
-         _f32, _i32, _c_void_p],
+         _f32, _i32, _f32, _c_void_p],
     ),
     "tu_layer_norm_adaln": (
         _i32,
@@ -110,7 +110,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
 }
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

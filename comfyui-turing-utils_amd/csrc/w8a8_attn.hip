@@ -13,9 +13,9 @@
 //   out = O / d * v_scale[channel]
 // The masked score is the reference's finite -5e6 in the raw score domain.
 //
-// MI355X mapping (shared with the Sage kernel: 8 wave64, two ping-pong
-// groups of 4, 32 query rows a wave, a 5-stage LDS ring filled by
-// buffer_load ... lds from group 0):
+// MI355X mapping (shared with the Sage kernel: 8 wave64, two groups of 4
+// whose MFMA and softmax clusters interleave, 32 query rows a wave, a
+// 5-stage LDS ring filled by buffer_load ... lds from group 0):
 //   * S^T = K Q^T on v_mfma_i32_16x16x64_i8 as in the Sage kernel, with the
 //     K rows permuted so that lane group g holds the 16 consecutive keys
 //     16 g .. 16 g + 15 of each query: exactly one 16-byte B operand of the
@@ -173,7 +173,8 @@ __device__ __forceinline__ void flush_segment(W8State &st, int tile, const int32
 // rescale when one moved, then P - 128 packed as the PV B operands p8[qt]
 // (dword kt = keys 16 g + 4 kt .. + 3 of query 16 qt + lc) and l += p.
 __device__ __forceinline__ void softmax_tile8(const i32x4 (&s)[4][kQT], const float (&f)[kQT], W8State &st,
-                                              i32x4 (&p8)[kQT], int tile, const int32_t *__restrict__ vpre, int g) {
+                                              i32x4 (&p8)[kQT], int tile, const int32_t *__restrict__ vpre, int g,
+                                              float headroom) {
     float mlane[kQT];
     bool need = false;
 #pragma unroll
@@ -193,7 +194,10 @@ __device__ __forceinline__ void softmax_tile8(const i32x4 (&s)[4][kQT], const fl
         flush_segment(st, tile, vpre, g);
 #pragma unroll
         for (int qt = 0; qt < kQT; ++qt) {
-            const float m_new = fmaxf(st.m_used[qt], xmax_f32(mlane[qt]));
+            // a row whose maximum passed the base moves it to that maximum
+            // plus the headroom (0: the reference's exact running maximum)
+            const float mx = xmax_f32(mlane[qt]);
+            const float m_new = mx > st.m_used[qt] ? mx + headroom : st.m_used[qt];
             const float alpha = __builtin_amdgcn_exp2f(st.m_used[qt] - m_new);  // 2^-inf = 0 on the first tile
             st.m_used[qt] = m_new;
             st.l[qt] *= alpha;
@@ -290,16 +294,16 @@ __device__ __forceinline__ void mfma_cluster8(const int8_t *kst, const int8_t *v
     __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
 }
 
-// Ping-pong schedule of the Sage kernel (see sage_attn.hip): per key tile t
-// an MFMA cluster {QK(t+1), PV(t)} and a VALU cluster {softmax(t+1)}, the
-// two groups one barrier apart.
+// Schedule of the Sage kernel (see sage_attn.hip): per key tile t an MFMA
+// cluster {QK(t+1), PV(t)} and a VALU cluster {softmax(t+1)}, one barrier
+// per tile, the two groups' barriers on either side of the softmax.
 template <bool kCausal, bool kFp16Out>
 __global__ __launch_bounds__(kThreads, 1) void w8a8_attn_kernel(
     const int8_t *__restrict__ q8, const float *__restrict__ q_scale, const int8_t *__restrict__ k8,
     const float *__restrict__ k_scale, const int8_t *__restrict__ vt, const float *__restrict__ v_scale,
     const int32_t *__restrict__ v_prefix, uint16_t *__restrict__ o, int hq, int groups, int64_t lq, int64_t lk,
     int64_t lpad, int64_t nqs, int64_t nks, int64_t q_sb, int64_t q_sh, int64_t q_sl, int64_t k_sb, int64_t k_sh,
-    int64_t k_sl, int64_t o_sb, int64_t o_sh, int64_t o_sl, float sm_log2) {
+    int64_t k_sl, int64_t o_sb, int64_t o_sh, int64_t o_sl, float sm_log2, float headroom) {
     __shared__ __align__(1024) int8_t lds[kStages][kStageBytes];
 
     const int tid = threadIdx.x;
@@ -380,27 +384,33 @@ __global__ __launch_bounds__(kThreads, 1) void w8a8_attn_kernel(
                 static_cast<int>(max(min(q0 - key0, static_cast<int64_t>(kBKey)), static_cast<int64_t>(-kBQ)));
             mask_tile8<kCausal>(s, key_lim, q_rel, g, lc);
         }
-        softmax_tile8(s, f, st, p8, it, vpre, g);
+        softmax_tile8(s, f, st, p8, it, vpre, g, headroom);
     };
 
+    // The schedule of the Sage kernel (sage_attn.hip): one barrier per key
+    // tile; both groups run M_it = {QK(it + 1), PV(it)} then softmax(it + 1),
+    // group 0's barrier after the softmax, group 1's before it, so the two
+    // groups' MFMA clusters overlap on each SIMD.
     if (grp == 0) __builtin_amdgcn_s_waitcnt(vmcnt_imm((kAhead - 1) * kLoadsPerTile));
     wg_barrier();
-    if (grp == 1) wg_barrier();
     qk_tile8(lds[0], gm, qf, s);
-    wg_barrier();
-    softmax(0, std::true_type{});
-    if (grp == 0) __builtin_amdgcn_s_waitcnt(vmcnt_imm((kAhead - 2) * kLoadsPerTile));
-    wg_barrier();
     const int main_steps = max(0, min(my_tiles, first_masked) - 1);
+    if (grp == 0) {
+        softmax(0, std::true_type{});
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm((kAhead - 2) * kLoadsPerTile));
+    }
+    wg_barrier();
+    if (grp == 1) softmax(0, std::true_type{});
 #pragma clang loop unroll(disable)
     for (int it = 0; it < main_steps; ++it) {
         mfma_cluster8(lds[(it + 1) % kStages], lds[it % kStages], gm, qf, s, p8, st);
-        if (grp == 0)
-            issue_tile8(lds[(it + kAhead) % kStages], krs, vrs, gm, k_sl32, tile_key0(it + kAhead), w4);
-        wg_barrier();
+        if (grp == 0) issue_tile8(lds[(it + kAhead) % kStages], krs, vrs, gm, k_sl32, tile_key0(it + kAhead), w4);
+        else wg_barrier();
         softmax(it + 1, std::false_type{});
-        if (grp == 0) __builtin_amdgcn_s_waitcnt(vmcnt_imm((kAhead - 2) * kLoadsPerTile));
-        wg_barrier();
+        if (grp == 0) {
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm((kAhead - 2) * kLoadsPerTile));
+            wg_barrier();
+        }
     }
 #pragma clang loop unroll(disable)
     for (int it = main_steps; it < tiles; ++it) {
@@ -408,12 +418,13 @@ __global__ __launch_bounds__(kThreads, 1) void w8a8_attn_kernel(
             issue_tile8(lds[(it + kAhead) % kStages], krs, vrs, gm, k_sl32, tile_key0(it + kAhead), w4);
         if (it + 1 < my_tiles) qk_tile8(lds[(it + 1) % kStages], gm, qf, s);
         if (it < my_tiles) pv_tile8(lds[it % kStages], gm, p8, st);
-        wg_barrier();
+        if (grp == 1) wg_barrier();
         if (it + 1 < my_tiles) softmax(it + 1, std::true_type{});
-        if (grp == 0) __builtin_amdgcn_s_waitcnt(vmcnt_imm((kAhead - 2) * kLoadsPerTile));
-        wg_barrier();
+        if (grp == 0) {
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm((kAhead - 2) * kLoadsPerTile));
+            wg_barrier();
+        }
     }
-    if (grp == 0) wg_barrier();
     __builtin_amdgcn_s_waitcnt(0);
 
     // Final segment, then out = O / l * v_scale.  acc_o[ds][qt][r] holds
@@ -456,9 +467,10 @@ extern "C" int32_t tu_w8a8_attn_fwd(const int8_t *q8, const float *q_scale, int6
                                     int64_t batch, int64_t hq, int64_t hkv, int64_t lq, int64_t lk, int64_t dim,
                                     int64_t q_sb, int64_t q_sh, int64_t q_sl, int64_t k_sb, int64_t k_sh,
                                     int64_t k_sl, int64_t o_sb, int64_t o_sh, int64_t o_sl, float sm_scale,
-                                    int32_t causal, void *stream) {
+                                    int32_t causal, float exp_headroom, void *stream) {
     using namespace tu;
     TU_REQUIRE(dim == kD, "W8A8 attention kernel requires head_dim 128, got %lld", static_cast<long long>(dim));
+    TU_REQUIRE(exp_headroom >= 0.0f && exp_headroom <= 4.0f, "W8A8 attention exp_headroom must be in [0, 4]");
     TU_REQUIRE(batch > 0 && hq > 0 && hkv > 0 && hq % hkv == 0, "W8A8 attention: hq must be a positive multiple of hkv");
     TU_REQUIRE(lq > 0 && lk > 0, "W8A8 attention requires non-empty sequences");
     TU_REQUIRE(lpad == (lk + kBKey - 1) / kBKey * kBKey, "W8A8 attention: V^T padded length must be ceil(lk/64)*64");
@@ -484,7 +496,7 @@ extern "C" int32_t tu_w8a8_attn_fwd(const int8_t *q8, const float *q_scale, int6
     const int groups = static_cast<int>(hq / hkv);
 #define TU_W8_ARGS                                                                                            \
     q8, q_scale, k8, k_scale, vt, v_scale, v_prefix, static_cast<uint16_t *>(out), static_cast<int>(hq), groups, \
-        lq, lk, lpad, nqs, nks, q_sb, q_sh, q_sl, k_sb, k_sh, k_sl, o_sb, o_sh, o_sl, sm_log2
+        lq, lk, lpad, nqs, nks, q_sb, q_sh, q_sl, k_sb, k_sh, k_sl, o_sb, o_sh, o_sl, sm_log2, exp_headroom
     if (causal) {
         if (out_fp16) w8a8_attn_kernel<true, true><<<grid, kThreads, 0, s>>>(TU_W8_ARGS);
         else w8a8_attn_kernel<true, false><<<grid, kThreads, 0, s>>>(TU_W8_ARGS);

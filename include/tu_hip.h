@@ -288,6 +288,10 @@ int32_t tu_w8a8_quant_v(const void *v, int32_t dtype, int64_t batch, int64_t hea
  *       p = 2^(fma(s, f, -m)), P = cvt.rni.sat.u8(p), l += p,
  *       O += P . vq (exact), O and l rescaled by 2^(m_old - m)
  *   out = O / l * v_scale[channel], bf16 (out_fp16 0) or fp16 (1)
+ * exp_headroom in [0, 4]: 0 keeps the reference's exact running maximum m;
+ * h > 0 moves a row's base only when its maximum passes the base, and then
+ * to that maximum + h (so P <= 255 * 2^-h right after a move, and fewer
+ * tiles move it).
  * q8, k8: int8 by element strides (16-byte aligned rows), dim == 128, GQA
  * hq % hkv == 0; q_scale: fp32 [batch, hq, nqs >= ceil(lq/16)]; k_scale:
  * fp32 [batch, hkv, nks >= ceil(lk/64)]; vq, v_scale, prefix from
@@ -303,7 +307,7 @@ int32_t tu_w8a8_attn_fwd(const int8_t *q8, const float *q_scale, int64_t nqs, co
                          int64_t batch, int64_t hq, int64_t hkv, int64_t lq, int64_t lk, int64_t dim,
                          int64_t q_sb, int64_t q_sh, int64_t q_sl, int64_t k_sb, int64_t k_sh,
                          int64_t k_sl, int64_t o_sb, int64_t o_sh, int64_t o_sl, float sm_scale,
-                         int32_t causal, void *stream);
+                         int32_t causal, float exp_headroom, void *stream);
 
 /* Wan block: LayerNorm + AdaLN --------------------------------------------- */
 

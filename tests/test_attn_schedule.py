@@ -1,6 +1,7 @@
-"""Host model of the Sage attention kernel's barrier and LDS-ring schedule.
+"""Host model of the attention kernels' barrier and LDS-ring schedule.
 
-``sage_attn_kernel`` (csrc/sage_attn.hip) runs 8 waves in two groups that
+``sage_attn_kernel`` (csrc/sage_attn.hip) and ``w8a8_attn_kernel``
+(csrc/w8a8_attn.hip, 4 loads per tile instead of 6) run 8 waves in two groups that
 share one workgroup barrier per key tile.  Every wave executes, per tile t,
 an MFMA cluster M_t = {QK(t + 1), PV(t)} and a softmax cluster V_t; group 0
 orders an interval as [M_t, V_{t+1}], group 1 as [V_t, M_t], so the two

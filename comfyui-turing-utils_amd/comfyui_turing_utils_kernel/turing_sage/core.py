@@ -14,7 +14,9 @@ MI355X build choices (each a parameter with the Wan default):
   * PV runs in bf16 on MFMA; the reference converted V to fp16 for Turing.
   * The kernel is used for every sequence length (no SDPA short-sequence
     detour): tails are masked inside the kernel.
-  * head_dim <= 128 is zero-padded to 128, which leaves Q.K and P.V exact.
+  * head_dim <= 64 is zero-padded to 64 and 64 < head_dim <= 128 to 128, as
+    the reference pads (core.py:436-448); the kernel is built for both widths,
+    and zero channels leave Q.K and P.V exact.
 """
 from __future__ import annotations
 
@@ -35,7 +37,12 @@ from .quant import (
     value_transpose,
 )
 
-KERNEL_HEAD_DIM = 128
+KERNEL_HEAD_DIM = 128  # widest head; the W8A8 kernel's only width
+
+
+def _sage_head_dim(head_dim: int) -> int:
+    """Kernel width for a head_dim <= 128: 64 or 128 (reference core.py:436-448)."""
+    return 64 if head_dim <= 64 else 128
 
 
 @dataclasses.dataclass(frozen=True)
@@ -104,11 +111,11 @@ def _validate(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, tensor_layout: 
         raise ValueError(f"Unsupported head_dim: {q.size(-1)}")
 
 
-def _prepare(x: torch.Tensor) -> torch.Tensor:
-    """bf16, channels padded to the kernel head_dim, last dim contiguous."""
+def _prepare(x: torch.Tensor, width: int) -> torch.Tensor:
+    """bf16, channels padded to the kernel width, last dim contiguous."""
     if x.dtype != torch.bfloat16:
         x = x.to(torch.bfloat16)
-    pad = KERNEL_HEAD_DIM - x.size(-1)
+    pad = width - x.size(-1)
     if pad:
         x = torch.nn.functional.pad(x, (0, pad))
     if x.stride(-1) != 1 or x.data_ptr() % 16 != 0 or any(s % 8 for s in x.stride()[:-1]):
@@ -136,7 +143,8 @@ def prequantize_sageattn(
     if not (scale > 0.0 and math.isfinite(scale)):
         raise ValueError("sm_scale must be a positive finite number")
     output_dtype = q.dtype
-    qp, kp, vp = _prepare(q), _prepare(k), _prepare(v)
+    width = _sage_head_dim(head_dim)
+    qp, kp, vp = _prepare(q, width), _prepare(k, width), _prepare(v, width)
     with torch.cuda.device(q.device):
         q_int8, q_scale, k_int8, k_scale, _ = per_block_int8(
             qp, kp, BLKQ=BLKQ, BLKK=BLKK, tensor_layout=tensor_layout, smooth_k=smooth_k
@@ -160,8 +168,8 @@ def _check_qk(q_int8, q_scale, k_int8, k_scale, tensor_layout, blkq, blkk):
         raise ValueError("prequantized Sage Q/K must be four-dimensional")
     if len({q_int8.device, k_int8.device, q_scale.device, k_scale.device}) != 1:
         raise ValueError("prequantized Sage tensors must share one device")
-    if q_int8.size(-1) != KERNEL_HEAD_DIM or k_int8.size(-1) != KERNEL_HEAD_DIM:
-        raise ValueError("prequantized Sage requires head_dim 128")
+    if q_int8.size(-1) not in (64, 128) or k_int8.size(-1) != q_int8.size(-1):
+        raise ValueError("prequantized Sage requires Q/K head_dim 64 or 128")
     if q_int8.stride(-1) != 1 or k_int8.stride(-1) != 1:
         raise ValueError("the last Q/K dimension must be contiguous")
     hq, lq, *_ = _layout_dims(q_int8, tensor_layout)
@@ -196,12 +204,13 @@ def attention_from_vt(
 ) -> torch.Tensor:
     """Attention kernel only: quantized Q/K and V^T from ``value_transpose``."""
     batch, hq, hkv, lq, lk = _check_qk(q_int8, q_scale, k_int8, k_scale, tensor_layout, blkq, blkk)
+    width = q_int8.size(-1)
     lpad = (lk + 63) // 64 * 64
-    if value_t.dtype != torch.bfloat16 or value_t.shape != (batch, hkv, KERNEL_HEAD_DIM, lpad):
-        raise ValueError(f"V^T must be bf16 [{batch}, {hkv}, {KERNEL_HEAD_DIM}, {lpad}]")
+    if value_t.dtype != torch.bfloat16 or value_t.shape != (batch, hkv, width, lpad):
+        raise ValueError(f"V^T must be bf16 [{batch}, {hkv}, {width}, {lpad}]")
     if value_t.device != q_int8.device or not value_t.is_contiguous():
         raise ValueError("V^T must be contiguous on the Q/K device")
-    scale = float(sm_scale) if sm_scale is not None else KERNEL_HEAD_DIM ** -0.5
+    scale = float(sm_scale) if sm_scale is not None else width ** -0.5
     if output is None:
         output = torch.empty(q_int8.shape, dtype=torch.bfloat16, device=q_int8.device)
     elif (output.shape != q_int8.shape or output.dtype != torch.bfloat16 or output.device != q_int8.device
@@ -216,7 +225,7 @@ def attention_from_vt(
         _lib.call(
             "tu_sage_attn_fwd",
             q_int8.data_ptr(), q_scale.data_ptr(), blkq, k_int8.data_ptr(), k_scale.data_ptr(), blkk,
-            value_t.data_ptr(), lpad, output.data_ptr(), batch, hq, hkv, lq, lk, KERNEL_HEAD_DIM,
+            value_t.data_ptr(), lpad, output.data_ptr(), batch, hq, hkv, lq, lk, width,
             qsb, qsh, qsl, ksb, ksh, ksl, osb, osh, osl,
             scale, int(bool(is_causal)), _lib.stream_of(q_int8.device),
         )
@@ -237,7 +246,7 @@ def sageattn_prequantized(
     blkk: int = 128,
     output: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
-    """Attention on already-quantized Q/K and bf16 V (head_dim 128), the
+    """Attention on already-quantized Q/K and bf16 V (head_dim 64 or 128), the
     counterpart of the reference's ``sageattn_prequantized`` (core.py:573-653)."""
     batch, hq, hkv, lq, lk = _check_qk(q_int8, q_scale, k_int8, k_scale, tensor_layout, blkq, blkk)
     if v.dtype != torch.bfloat16:
@@ -245,7 +254,7 @@ def sageattn_prequantized(
     if v.ndim != 4 or v.device != q_int8.device or v.stride(-1) != 1:
         raise ValueError("prequantized Sage V must be 4D, contiguous in channels, on the Q/K device")
     vh, vl, *_ = _layout_dims(v, tensor_layout)
-    if v.size(0) != batch or vh != hkv or vl != lk or v.size(-1) != KERNEL_HEAD_DIM:
+    if v.size(0) != batch or vh != hkv or vl != lk or v.size(-1) != q_int8.size(-1):
         raise ValueError("prequantized Sage Q/K/V shapes are incompatible")
     value_t, _ = value_transpose(v, tensor_layout)
     return attention_from_vt(q_int8, q_scale, k_int8, k_scale, value_t, tensor_layout=tensor_layout,
@@ -340,8 +349,8 @@ def prequantize_sageattn_from_qk(
     sm_scale: Optional[float] = None,
 ) -> PrequantizedSageAttention:
     """Attach V to a fused Q/K preprocessing result without rereading Q/K
-    (reference core.py:477-513).  Q/K codes of head_dim 64 are zero-padded to
-    the kernel's 128 channels (dot products unchanged).  Rotated (and
+    (reference core.py:477-513).  The fused producer's head_dim (64 or 128)
+    is a kernel width, so nothing is padded.  Rotated (and
     anchored) codes are accepted as the reference accepts them: the rotation
     leaves Q.K unchanged and the anchor shifts each query row's scores by a
     constant, which the softmax cancels."""
@@ -360,7 +369,8 @@ def prequantize_sageattn_from_qk(
         raise ValueError("preprocessed Q/K and V shapes are incompatible")
     scale = float(sm_scale) if sm_scale is not None else qk.original_head_dim ** -0.5
     q_int8, k_int8 = qk.query_int8, qk.key_int8
-    pad = KERNEL_HEAD_DIM - q_int8.size(-1)
+    width = _sage_head_dim(q_int8.size(-1))
+    pad = width - q_int8.size(-1)
     if pad:
         q_int8 = torch.nn.functional.pad(q_int8, (0, pad))
         k_int8 = torch.nn.functional.pad(k_int8, (0, pad))
@@ -369,7 +379,7 @@ def prequantize_sageattn_from_qk(
     # them as ceil(Lq / 16) per head
     q_scale = qk.query_scale[..., : (lq + 15) // 16].contiguous()
     with torch.cuda.device(value.device):
-        value_t, _ = value_transpose(_prepare(value), qk.tensor_layout)
+        value_t, _ = value_transpose(_prepare(value, width), qk.tensor_layout)
     return PrequantizedSageAttention(
         query_int8=q_int8, query_scale=q_scale, key_int8=k_int8, key_scale=qk.key_scale, value_t=value_t,
         tensor_layout=qk.tensor_layout, original_head_dim=qk.original_head_dim, is_causal=bool(is_causal),

@@ -44,15 +44,27 @@ namespace tu {
 namespace {
 
 constexpr int kThreads = 512;  // 8 waves: two groups of 4
-constexpr int kD = 128;
 constexpr int kQT = 2;                   // 16-row query fragments per wave
 constexpr int kWaveQ = 16 * kQT;         // query rows per wave
 constexpr int kBQ = 8 * kWaveQ;          // query rows per workgroup
 constexpr int kBKey = 64;                // keys per tile
-constexpr int kKTileBytes = kBKey * kD;      // int8 K tile, 8 KiB
-constexpr int kVTileBytes = kD * kBKey * 2;  // bf16 V^T tile, 16 KiB
-constexpr int kStageBytes = kKTileBytes + kVTileBytes;
 constexpr float kRescaleSlack = 8.0f;        // log2 of the largest p allowed
+
+// Head-dim geometry (D = 64 or 128).  K tile: 64 keys x D bytes; V^T tile:
+// D channels x 64 keys of bf16 (128-byte rows); group 0's 4 waves each move
+// kKLoads + kVLoads 1 KiB blocks of a tile.
+template <int D>
+struct Geo {
+    static_assert(D == 64 || D == 128, "head_dim 64 or 128");
+    static constexpr int kKTileBytes = kBKey * D;
+    static constexpr int kVTileBytes = D * kBKey * 2;
+    static constexpr int kStageBytes = kKTileBytes + kVTileBytes;
+    static constexpr int kKSlices = D / 64;  // 64-byte QK^T slices of a key row
+    static constexpr int kDS = D / 16;       // 16-channel PV blocks
+    static constexpr int kKLoads = kKTileBytes / 4096;
+    static constexpr int kVLoads = kVTileBytes / 4096;
+    static constexpr int kLoadsPerTile = kKLoads + kVLoads;
+};
 
 // K tile LDS row p holds key kperm(p): within each 32-key half, row
 // 16 kt + i holds key 8 (i >> 2) + 4 kt + (i & 3).  The QK MFMA reads 16
@@ -65,26 +77,39 @@ __device__ __forceinline__ int kperm(int p) {
 }
 
 // Per-lane constants of the tile loads and the MFMA operand reads.
+template <int D>
 struct LaneGeom {
-    uint32_t k_src[2];   // byte offset (from key0's row) of this lane's two K source chunks
-    uint32_t v_src[4];   // byte offset (from key0's column) of this lane's four V^T source chunks
-    uint32_t k_rd[2];    // LDS byte offset of the K operand, chunk g / 4 + g
-    uint32_t v_rd[2];    // LDS byte offset of the V^T operand, half 0 / 1
+    uint32_t k_src[Geo<D>::kKLoads];    // byte offset (from key0's row) of this lane's K source chunks
+    uint32_t v_src[Geo<D>::kVLoads];    // byte offset (from key0's column) of this lane's V^T source chunks
+    uint32_t k_rd[Geo<D>::kKSlices];    // LDS byte offset of the K operand of slice i
+    uint32_t v_rd[2];                   // LDS byte offset of the V^T operand, half 0 / 1
 };
 
-__device__ __forceinline__ LaneGeom lane_geom(int wave, int lane, int64_t k_sl, int64_t lpad) {
-    LaneGeom gm;
+// K rows of 128 B (D = 128) have their 16-byte chunks XOR-swizzled by row
+// bits 1..3, rows of 64 B (D = 64) by row bits 2..3; either way the 16 lanes
+// that read one chunk column of 16 consecutive rows hit distinct banks.
+template <int D>
+__device__ __forceinline__ LaneGeom<D> lane_geom(int wave, int lane, int64_t k_sl, int64_t lpad) {
+    LaneGeom<D> gm;
     const int g = lane >> 4, lc = lane & 15, sw = (lc >> 1) & 7;
+    if constexpr (D == 128) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int row = (2 * wave + i) * 8 + (lane >> 3);
-        gm.k_src[i] = static_cast<uint32_t>(kperm(row) * k_sl + ((lane & 7) ^ ((row >> 1) & 7)) * 16);
-        gm.k_rd[i] = static_cast<uint32_t>(lc * 128 + (((4 * i + g) ^ sw) << 4));
-        gm.v_rd[i] = static_cast<uint32_t>(kKTileBytes + lc * 128 + (((4 * i + g) ^ sw) << 4));
+        for (int i = 0; i < 2; ++i) {
+            const int row = (2 * wave + i) * 8 + (lane >> 3);
+            gm.k_src[i] = static_cast<uint32_t>(kperm(row) * k_sl + ((lane & 7) ^ ((row >> 1) & 7)) * 16);
+            gm.k_rd[i] = static_cast<uint32_t>(lc * 128 + (((4 * i + g) ^ sw) << 4));
+        }
+    } else {
+        const int row = wave * 16 + (lane >> 2);
+        gm.k_src[0] = static_cast<uint32_t>(kperm(row) * k_sl + ((lane & 3) ^ ((row >> 2) & 3)) * 16);
+        gm.k_rd[0] = static_cast<uint32_t>(lc * 64 + ((g ^ ((lc >> 2) & 3)) << 4));
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int d = (4 * wave + i) * 8 + (lane >> 3);
+    for (int i = 0; i < 2; ++i)
+        gm.v_rd[i] = static_cast<uint32_t>(Geo<D>::kKTileBytes + lc * 128 + (((4 * i + g) ^ sw) << 4));
+#pragma unroll
+    for (int i = 0; i < Geo<D>::kVLoads; ++i) {
+        const int d = (Geo<D>::kVLoads * wave + i) * 8 + (lane >> 3);
         gm.v_src[i] = static_cast<uint32_t>((d * lpad + ((lane & 7) ^ ((d >> 1) & 7)) * 8) * 2);
     }
     return gm;
@@ -95,31 +120,44 @@ __device__ __forceinline__ LaneGeom lane_geom(int wave, int lane, int64_t k_sl, 
 // contiguous LDS; the K row permutation and the chunk swizzle come from the
 // per-lane source offsets.  K rows at or past lk read as zeros (the buffer
 // range ends there); those keys are masked by the softmax.
+// One overload per head dim: the host compilation pass rejects a template of
+// this function (the buffer builtins only exist for the device target), a
+// plain device function it accepts.
+#define TU_ISSUE_TILE_BODY(D)                                                                                      \
+    constexpr int kK = Geo<D>::kKLoads, kV = Geo<D>::kVLoads;                                                      \
+    _Pragma("unroll") for (int i = 0; i < kK; ++i)                                                                 \
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_void *)(stage + (kK * wave + i) * 1024), 16,            \
+                                                 gm.k_src[i], key0 * k_sl, 0, 0);                                  \
+    _Pragma("unroll") for (int i = 0; i < kV; ++i)                                                                 \
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_void *)(stage + Geo<D>::kKTileBytes + (kV * wave + i) * 1024), \
+                                                 16, gm.v_src[i], key0 * 2, 0, 0);
 __device__ __forceinline__ void issue_tile(int8_t *stage, __amdgpu_buffer_rsrc_t krs, __amdgpu_buffer_rsrc_t vrs,
-                                           const LaneGeom &gm, uint32_t k_sl, uint32_t key0, int wave) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_void *)(stage + (2 * wave + i) * 1024), 16, gm.k_src[i],
-                                                 key0 * k_sl, 0, 0);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_void *)(stage + kKTileBytes + (4 * wave + i) * 1024), 16,
-                                                 gm.v_src[i], key0 * 2, 0, 0);
+                                           const LaneGeom<128> &gm, uint32_t k_sl, uint32_t key0, int wave) {
+    TU_ISSUE_TILE_BODY(128)
 }
+__device__ __forceinline__ void issue_tile(int8_t *stage, __amdgpu_buffer_rsrc_t krs, __amdgpu_buffer_rsrc_t vrs,
+                                           const LaneGeom<64> &gm, uint32_t k_sl, uint32_t key0, int wave) {
+    TU_ISSUE_TILE_BODY(64)
+}
+#undef TU_ISSUE_TILE_BODY
 
 // S^T for one tile: s[kt][qt][r] = biased score of key 32 (kt >> 1) + 8 g +
 // 4 (kt & 1) + r and query 16 qt + lc of the wave.
-__device__ __forceinline__ void qk_tile(const int8_t *stage, const LaneGeom &gm, const i32x4 (&qf)[kQT][2],
-                                        i32x4 (&s)[4][kQT]) {
+template <int D>
+__device__ __forceinline__ void qk_tile(const int8_t *stage, const LaneGeom<D> &gm,
+                                        const i32x4 (&qf)[kQT][Geo<D>::kKSlices], i32x4 (&s)[4][kQT]) {
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt) {
-        const i32x4 kf0 = *reinterpret_cast<const i32x4 *>(stage + gm.k_rd[0] + kt * 16 * 128);
-        const i32x4 kf1 = *reinterpret_cast<const i32x4 *>(stage + gm.k_rd[1] + kt * 16 * 128);
+        i32x4 kf[Geo<D>::kKSlices];
+#pragma unroll
+        for (int i = 0; i < Geo<D>::kKSlices; ++i)
+            kf[i] = *reinterpret_cast<const i32x4 *>(stage + gm.k_rd[i] + kt * 16 * D);
 #pragma unroll
         for (int qt = 0; qt < kQT; ++qt) {
-            const i32x4 z = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf0, qf[qt][0], i32x4{kBias, kBias, kBias, kBias},
-                                                                  0, 0, 0);
-            s[kt][qt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf1, qf[qt][1], z, 0, 0, 0);
+            i32x4 acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf[0], qf[qt][0], i32x4{kBias, kBias, kBias, kBias},
+                                                              0, 0, 0);
+            if constexpr (D == 128) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf[1], qf[qt][1], acc, 0, 0, 0);
+            s[kt][qt] = acc;
         }
     }
 }
@@ -127,9 +165,10 @@ __device__ __forceinline__ void qk_tile(const int8_t *stage, const LaneGeom &gm,
 // Softmax state of the wave: exponent base per query block, O^T and the row
 // sums (l, accumulated by an MFMA against a ones operand so every lane ends
 // with the complete sum for its query column).
+template <int D>
 struct SoftmaxState {
     float m_used[kQT];
-    f32x4 acc_o[8][kQT];
+    f32x4 acc_o[Geo<D>::kDS][kQT];
     f32x4 acc_l[kQT];
 };
 
@@ -171,7 +210,8 @@ __device__ __forceinline__ void mask_tile(i32x4 (&s)[4][kQT], int key_lim, int q
 // x = dot f - m_used is formed as fma(biased, f, c) with
 // c = -(1.5 * 2^23 f + m_used) when |c| < 2^12, which keeps the rounding of c
 // below 2^-13 in the exponent; otherwise the bias is subtracted exactly first.
-__device__ __forceinline__ void softmax_tile(const i32x4 (&s)[4][kQT], const float (&f)[kQT], SoftmaxState &st,
+template <int D>
+__device__ __forceinline__ void softmax_tile(const i32x4 (&s)[4][kQT], const float (&f)[kQT], SoftmaxState<D> &st,
                                              bf16x8 (&p)[2][kQT]) {
     float mlane[kQT];
     bool need = false;
@@ -197,7 +237,7 @@ __device__ __forceinline__ void softmax_tile(const i32x4 (&s)[4][kQT], const flo
             st.m_used[qt] = m_new;
             st.acc_l[qt] *= alpha;
 #pragma unroll
-            for (int ds = 0; ds < 8; ++ds) st.acc_o[ds][qt] *= alpha;
+            for (int ds = 0; ds < Geo<D>::kDS; ++ds) st.acc_o[ds][qt] *= alpha;
         }
     }
     float c[kQT];
@@ -237,18 +277,20 @@ __device__ __forceinline__ void softmax_tile(const i32x4 (&s)[4][kQT], const flo
 }
 
 // O^T += V^T P and l += 1 P for one tile.
-__device__ __forceinline__ void pv_tile(const int8_t *stage, const LaneGeom &gm, const bf16x8 (&p)[2][kQT],
-                                        SoftmaxState &st, const bf16x8 &ones) {
+template <int D>
+__device__ __forceinline__ void pv_tile(const int8_t *stage, const LaneGeom<D> &gm, const bf16x8 (&p)[2][kQT],
+                                        SoftmaxState<D> &st, const bf16x8 &ones) {
+    constexpr int kDS = Geo<D>::kDS;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-        bf16x8 vf[8];
+        bf16x8 vf[kDS];
 #pragma unroll
-        for (int ds = 0; ds < 8; ++ds)
+        for (int ds = 0; ds < kDS; ++ds)
             vf[ds] = *reinterpret_cast<const bf16x8 *>(stage + gm.v_rd[h] + ds * 16 * 128);
 #pragma unroll
         for (int qt = 0; qt < kQT; ++qt) {
 #pragma unroll
-            for (int ds = 0; ds < 8; ++ds)
+            for (int ds = 0; ds < kDS; ++ds)
                 st.acc_o[ds][qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[ds], p[h][qt], st.acc_o[ds][qt], 0, 0, 0);
             st.acc_l[qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, p[h][qt], st.acc_l[qt], 0, 0, 0);
         }
@@ -258,22 +300,24 @@ __device__ __forceinline__ void pv_tile(const int8_t *stage, const LaneGeom &gm,
 // MFMA cluster of a steady-state step: QK^T of the tile in kst and PV of the
 // tile in vst, with the LDS fragment reads issued a group of MFMAs ahead of
 // their first use.
-__device__ __forceinline__ void mfma_cluster(const int8_t *kst, const int8_t *vst, const LaneGeom &gm,
-                                             const i32x4 (&qf)[kQT][2], i32x4 (&s)[4][kQT],
-                                             const bf16x8 (&p)[2][kQT], SoftmaxState &st, const bf16x8 &ones) {
+template <int D>
+__device__ __forceinline__ void mfma_cluster(const int8_t *kst, const int8_t *vst, const LaneGeom<D> &gm,
+                                             const i32x4 (&qf)[kQT][Geo<D>::kKSlices], i32x4 (&s)[4][kQT],
+                                             const bf16x8 (&p)[2][kQT], SoftmaxState<D> &st, const bf16x8 &ones) {
+    constexpr int kDS = Geo<D>::kDS, kSl = Geo<D>::kKSlices;
     // This wave's MFMA cluster is the critical phase of the ping-pong: raise its
     // issue priority over the other group's softmax VALU on the same SIMD
     // (measured about 1 % faster; raising the softmax phase instead was slower).
     __builtin_amdgcn_s_setprio(3);
-    i32x4 kf[4][2];
-    bf16x8 va[8], vb[8];
+    i32x4 kf[4][kSl];
+    bf16x8 va[kDS], vb[kDS];
     // first-slice K fragments first: the first QK^T MFMAs only need those
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < kSl; ++i)
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt) kf[kt][i] = *reinterpret_cast<const i32x4 *>(kst + gm.k_rd[i] + kt * 16 * 128);
+        for (int kt = 0; kt < 4; ++kt) kf[kt][i] = *reinterpret_cast<const i32x4 *>(kst + gm.k_rd[i] + kt * 16 * D);
 #pragma unroll
-    for (int ds = 0; ds < 8; ++ds) va[ds] = *reinterpret_cast<const bf16x8 *>(vst + gm.v_rd[0] + ds * 16 * 128);
+    for (int ds = 0; ds < kDS; ++ds) va[ds] = *reinterpret_cast<const bf16x8 *>(vst + gm.v_rd[0] + ds * 16 * 128);
     i32x4 z[4][kQT];
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt)
@@ -281,37 +325,53 @@ __device__ __forceinline__ void mfma_cluster(const int8_t *kst, const int8_t *vs
         for (int qt = 0; qt < kQT; ++qt)
             z[kt][qt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf[kt][0], qf[qt][0], i32x4{kBias, kBias, kBias, kBias},
                                                               0, 0, 0);
+    if constexpr (D == 128) {
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt)
+        for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-        for (int qt = 0; qt < kQT; ++qt)
-            s[kt][qt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf[kt][1], qf[qt][1], z[kt][qt], 0, 0, 0);
+            for (int qt = 0; qt < kQT; ++qt)
+                s[kt][qt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf[kt][kSl - 1], qf[qt][kSl - 1], z[kt][qt], 0, 0, 0);
+    } else {
 #pragma unroll
-    for (int ds = 0; ds < 8; ++ds) vb[ds] = *reinterpret_cast<const bf16x8 *>(vst + gm.v_rd[1] + ds * 16 * 128);
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+            for (int qt = 0; qt < kQT; ++qt) s[kt][qt] = z[kt][qt];
+    }
+#pragma unroll
+    for (int ds = 0; ds < kDS; ++ds) vb[ds] = *reinterpret_cast<const bf16x8 *>(vst + gm.v_rd[1] + ds * 16 * 128);
 #pragma unroll
     for (int qt = 0; qt < kQT; ++qt) {
 #pragma unroll
-        for (int ds = 0; ds < 8; ++ds)
+        for (int ds = 0; ds < kDS; ++ds)
             st.acc_o[ds][qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[ds], p[0][qt], st.acc_o[ds][qt], 0, 0, 0);
         st.acc_l[qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, p[0][qt], st.acc_l[qt], 0, 0, 0);
     }
 #pragma unroll
     for (int qt = 0; qt < kQT; ++qt) {
 #pragma unroll
-        for (int ds = 0; ds < 8; ++ds)
+        for (int ds = 0; ds < kDS; ++ds)
             st.acc_o[ds][qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vb[ds], p[1][qt], st.acc_o[ds][qt], 0, 0, 0);
         st.acc_l[qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, p[1][qt], st.acc_l[qt], 0, 0, 0);
     }
     // Issue order, keeping at most 12 LDS reads in flight (the wait counter
     // holds 15; past that the compiler can only wait for all of them):
-    // K reads, first QK^T MFMAs, first V^T half, second QK^T MFMAs, 4 PV
-    // MFMAs, second V^T half, remaining PV MFMAs.
-    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
-    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
-    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
-    __builtin_amdgcn_sched_group_barrier(0x008, 12, 0);
-    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
-    __builtin_amdgcn_sched_group_barrier(0x008, 32, 0);
+    // K reads, first QK^T MFMAs, first V^T half, second QK^T MFMAs (D = 128)
+    // and 4 PV MFMAs, second V^T half, remaining PV MFMAs.
+    if constexpr (D == 128) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 12, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 32, 0);
+    } else {
+        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 9, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 15, 0);
+    }
     __builtin_amdgcn_s_setprio(0);
 }
 
@@ -330,15 +390,16 @@ __device__ __forceinline__ void mfma_cluster(const int8_t *kst, const int8_t *vs
 // equal barrier counts and ring residency for every wave.
 constexpr int kStages = 5;
 constexpr int kAhead = kStages - 1;
-constexpr int kLoadsPerTile = 6;  // per group-0 wave: 2 K + 4 V^T 1 KiB blocks
 
-template <bool kCausal>
+template <int D, bool kCausal>
 __global__ __launch_bounds__(kThreads, 1) void sage_attn_kernel(
     const int8_t *__restrict__ q8, const float *__restrict__ q_scale, int blkq, const int8_t *__restrict__ k8,
     const float *__restrict__ k_scale, int kscale_shift, const uint16_t *__restrict__ vt, uint16_t *__restrict__ o,
     int hq, int groups, int64_t lq, int64_t lk, int64_t lpad, int64_t q_sb, int64_t q_sh, int64_t q_sl,
     int64_t k_sb, int64_t k_sh, int64_t k_sl, int64_t o_sb, int64_t o_sh, int64_t o_sl, float sm_log2) {
-    __shared__ __align__(1024) int8_t lds[kStages][kStageBytes];
+    constexpr int kSl = Geo<D>::kKSlices;
+    constexpr int kLoadsPerTile = Geo<D>::kLoadsPerTile;
+    __shared__ __align__(1024) int8_t lds[kStages][Geo<D>::kStageBytes];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -356,7 +417,7 @@ __global__ __launch_bounds__(kThreads, 1) void sage_attn_kernel(
 
     const int8_t *qp = q8 + b * q_sb + h * q_sh;
     const int8_t *kp = k8 + b * k_sb + hk * k_sh;
-    const uint16_t *vtp = vt + (b * hkv + hk) * kD * lpad;
+    const uint16_t *vtp = vt + (b * hkv + hk) * D * lpad;
     const int64_t nbq = (lq + blkq - 1) / blkq;
     const int64_t nbk = ((lk + kBKey - 1) / kBKey + (1 << kscale_shift) - 1) >> kscale_shift;
     const float *ks_row = k_scale + (b * hkv + hk) * nbk;
@@ -374,19 +435,19 @@ __global__ __launch_bounds__(kThreads, 1) void sage_attn_kernel(
     if constexpr (kCausal) mask_from = min(mask_from, q0 / kBKey);
     const int first_masked = static_cast<int>(min<int64_t>(tiles, mask_from));
 
-    const LaneGeom gm = lane_geom(w4, lane, k_sl, lpad);
+    const LaneGeom<D> gm = lane_geom<D>(w4, lane, k_sl, lpad);
     const __amdgpu_buffer_rsrc_t krs = make_rsrc(kp, static_cast<uint32_t>(lk * k_sl));
-    const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vtp, static_cast<uint32_t>(kD * lpad * 2));
+    const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vtp, static_cast<uint32_t>(D * lpad * 2));
     const uint32_t k_sl32 = static_cast<uint32_t>(k_sl);
     auto tile_key0 = [&](int it) { return static_cast<uint32_t>(min(it, tiles - 1) * kBKey); };
 
-    i32x4 qf[kQT][2];
+    i32x4 qf[kQT][kSl];
     float qsc[kQT];
 #pragma unroll
     for (int qt = 0; qt < kQT; ++qt) {
         const int64_t qi = min(q0 + 16 * qt + lc, lq - 1);
 #pragma unroll
-        for (int ds = 0; ds < 2; ++ds)
+        for (int ds = 0; ds < kSl; ++ds)
             qf[qt][ds] = *reinterpret_cast<const i32x4 *>(qp + qi * q_sl + 64 * ds + 16 * g);
         qsc[qt] = q_scale[(b * hq + h) * nbq + qi / blkq] * sm_log2;
     }
@@ -394,13 +455,13 @@ __global__ __launch_bounds__(kThreads, 1) void sage_attn_kernel(
 #pragma unroll
         for (int j = 0; j < kAhead; ++j) issue_tile(lds[j], krs, vrs, gm, k_sl32, tile_key0(j), w4);
     }
-    SoftmaxState st;
+    SoftmaxState<D> st;
 #pragma unroll
     for (int qt = 0; qt < kQT; ++qt) {
         st.m_used[qt] = -INFINITY;
         st.acc_l[qt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int ds = 0; ds < 8; ++ds) st.acc_o[ds][qt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int ds = 0; ds < Geo<D>::kDS; ++ds) st.acc_o[ds][qt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     }
     bf16x8 ones;
 #pragma unroll
@@ -485,7 +546,7 @@ __global__ __launch_bounds__(kThreads, 1) void sage_attn_kernel(
         const float inv = 1.0f / st.acc_l[qt][0];
         if (qi >= lq) continue;
 #pragma unroll
-        for (int ds = 0; ds < 8; ++ds) {
+        for (int ds = 0; ds < Geo<D>::kDS; ++ds) {
             u32x2 packed;
             packed.x = pack_bf16x2(st.acc_o[ds][qt][0] * inv, st.acc_o[ds][qt][1] * inv);
             packed.y = pack_bf16x2(st.acc_o[ds][qt][2] * inv, st.acc_o[ds][qt][3] * inv);
@@ -497,18 +558,21 @@ __global__ __launch_bounds__(kThreads, 1) void sage_attn_kernel(
 // V [key][d] (bf16, strides) -> V^T [b][h][d][lpad] with zero keys in [lk, lpad).
 // One workgroup per 64-key tile: 64 x 128 staged through LDS (rows padded to
 // 132 elements so the column reads are bank-conflict free).
+template <int D>
 __global__ __launch_bounds__(256) void v_prep_kernel(const uint16_t *__restrict__ v, int64_t lk, int64_t lpad,
                                                      int64_t v_sb, int64_t v_sh, int64_t v_sl,
                                                      uint16_t *__restrict__ vt) {
-    __shared__ uint16_t tile[kBKey][kD + 4];
+    constexpr int kChunks = D / 8;             // 16-byte chunks of a key row
+    constexpr int kRowsPerPass = 256 / kChunks;
+    __shared__ uint16_t tile[kBKey][D + 4];
     const int tid = threadIdx.x;
     const int64_t key0 = static_cast<int64_t>(blockIdx.x) * kBKey;
     const int64_t h = blockIdx.y, b = blockIdx.z, heads = gridDim.y;
     const uint16_t *vp = v + b * v_sb + h * v_sh;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int row = i * 16 + (tid >> 4);
-        const int c = tid & 15;
+    for (int i = 0; i < kBKey / kRowsPerPass; ++i) {
+        const int row = i * kRowsPerPass + tid / kChunks;
+        const int c = tid % kChunks;
         u32x4 val = u32x4{0u, 0u, 0u, 0u};
         if (key0 + row < lk) val = *reinterpret_cast<const u32x4 *>(vp + (key0 + row) * v_sl + c * 8);
 #pragma unroll
@@ -518,9 +582,9 @@ __global__ __launch_bounds__(256) void v_prep_kernel(const uint16_t *__restrict_
         }
     }
     __syncthreads();
-    uint16_t *dst = vt + (b * heads + h) * kD * lpad + key0;
+    uint16_t *dst = vt + (b * heads + h) * D * lpad + key0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < D * 8 / 256; ++i) {
         const int item = tid + 256 * i;  // (d, 8-key chunk)
         const int d = item >> 3, c = item & 7;
         u32x4 out;
@@ -537,7 +601,7 @@ __global__ __launch_bounds__(256) void v_prep_kernel(const uint16_t *__restrict_
 extern "C" int32_t tu_sage_v_prep(const void *v_bf16, int64_t batch, int64_t heads, int64_t len, int64_t dim,
                                   int64_t s_b, int64_t s_h, int64_t s_l, void *vt_bf16, int64_t lpad, void *stream) {
     using namespace tu;
-    TU_REQUIRE(dim == kD, "V prep requires head_dim 128, got %lld", static_cast<long long>(dim));
+    TU_REQUIRE(dim == 64 || dim == 128, "V prep requires head_dim 64 or 128, got %lld", static_cast<long long>(dim));
     TU_REQUIRE(batch > 0 && heads > 0 && len > 0 && batch <= 65535 && heads <= 65535, "V prep dimensions out of range");
     TU_REQUIRE(lpad >= len && lpad % kBKey == 0, "V prep padded length must cover len and be a multiple of 64");
     TU_REQUIRE(v_bf16 && vt_bf16, "V prep pointers must be non-null");
@@ -546,8 +610,10 @@ extern "C" int32_t tu_sage_v_prep(const void *v_bf16, int64_t batch, int64_t hea
                "V prep needs 16-byte aligned rows");
     if (require_gfx950()) return -1;
     const dim3 grid(static_cast<unsigned>(lpad / kBKey), static_cast<unsigned>(heads), static_cast<unsigned>(batch));
-    v_prep_kernel<<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(static_cast<const uint16_t *>(v_bf16), len, lpad,
-                                                                       s_b, s_h, s_l, static_cast<uint16_t *>(vt_bf16));
+    const auto *vp = static_cast<const uint16_t *>(v_bf16);
+    auto *vtp = static_cast<uint16_t *>(vt_bf16);
+    if (dim == 128) v_prep_kernel<128><<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(vp, len, lpad, s_b, s_h, s_l, vtp);
+    else v_prep_kernel<64><<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(vp, len, lpad, s_b, s_h, s_l, vtp);
     return check_launch("tu_sage_v_prep");
 }
 
@@ -558,7 +624,8 @@ extern "C" int32_t tu_sage_attn_fwd(const int8_t *q8, const float *q_scale, int6
                                     int64_t k_sh, int64_t k_sl, int64_t o_sb, int64_t o_sh, int64_t o_sl,
                                     float sm_scale, int32_t causal, void *stream) {
     using namespace tu;
-    TU_REQUIRE(dim == kD, "Sage attention kernel requires head_dim 128, got %lld", static_cast<long long>(dim));
+    TU_REQUIRE(dim == 64 || dim == 128, "Sage attention kernel requires head_dim 64 or 128, got %lld",
+               static_cast<long long>(dim));
     TU_REQUIRE(batch > 0 && hq > 0 && hkv > 0 && hq % hkv == 0, "Sage attention: hq must be a positive multiple of hkv");
     TU_REQUIRE(lq > 0 && lk > 0, "Sage attention requires non-empty sequences");
     TU_REQUIRE(lpad >= lk && lpad % kBKey == 0, "Sage attention: V^T padded length must cover lk, multiple of 64");
@@ -566,7 +633,7 @@ extern "C" int32_t tu_sage_attn_fwd(const int8_t *q8, const float *q_scale, int6
                "Sage attention needs blkq > 0 and blkk = 64 * 2^n");
     TU_REQUIRE(blkq <= 0x7fffffff && blkk <= 0x7fffffff, "Sage attention block sizes out of range");
     TU_REQUIRE((lq + kBQ - 1) / kBQ <= 0x7fffffff && batch * hq <= 65535, "Sage attention grid too large");
-    TU_REQUIRE(lk * k_sl < (int64_t{1} << 32) && kD * lpad * 2 < (int64_t{1} << 32),
+    TU_REQUIRE(lk * k_sl < (int64_t{1} << 32) && dim * lpad * 2 < (int64_t{1} << 32),
                "Sage attention: one head's K or V^T exceeds 4 GiB of addressable bytes");
     TU_REQUIRE(q8 && q_scale && k8 && k_scale && vt_bf16 && o_bf16, "Sage attention pointers must be non-null");
     TU_REQUIRE(sm_scale > 0.0f, "Sage attention sm_scale must be positive");
@@ -587,8 +654,13 @@ extern "C" int32_t tu_sage_attn_fwd(const int8_t *q8, const float *q_scale, int6
     q8, q_scale, static_cast<int>(blkq), k8, k_scale, kscale_shift, static_cast<const uint16_t *>(vt_bf16),      \
         static_cast<uint16_t *>(o_bf16), static_cast<int>(hq), groups, lq, lk, lpad, q_sb, q_sh, q_sl, k_sb, k_sh,  \
         k_sl, o_sb, o_sh, o_sl, sm_log2
-    if (causal) sage_attn_kernel<true><<<grid, kThreads, 0, s>>>(TU_ATTN_ARGS);
-    else sage_attn_kernel<false><<<grid, kThreads, 0, s>>>(TU_ATTN_ARGS);
+    if (dim == 128) {
+        if (causal) sage_attn_kernel<128, true><<<grid, kThreads, 0, s>>>(TU_ATTN_ARGS);
+        else sage_attn_kernel<128, false><<<grid, kThreads, 0, s>>>(TU_ATTN_ARGS);
+    } else {
+        if (causal) sage_attn_kernel<64, true><<<grid, kThreads, 0, s>>>(TU_ATTN_ARGS);
+        else sage_attn_kernel<64, false><<<grid, kThreads, 0, s>>>(TU_ATTN_ARGS);
+    }
 #undef TU_ATTN_ARGS
     return check_launch("tu_sage_attn_fwd");
 }

@@ -169,7 +169,7 @@ int32_t tu_sage_quant(const void *x_bf16, const void *mean_bf16, int64_t batch, 
 
 /* Writes V^T: vt[b][h][d][lpad] = v[b][h][key][d] for key < len and 0 for
  * len <= key < lpad (lpad % 64 == 0, lpad >= len).  v: bf16 with element
- * strides (s_b, s_h, s_l), channels contiguous; dim == 128.  This is the PV
+ * strides (s_b, s_h, s_l), channels contiguous; dim 64 or 128.  This is the PV
  * operand layout of tu_sage_attn_fwd (keys contiguous per channel).  It plays
  * the role of the reference's V staging in shared memory
  * (kernel/csrc/turing/sage/attn_utils.cuh:125-136, load_v_global_to_share). */
@@ -186,7 +186,9 @@ int32_t tu_sage_v_prep(const void *v_bf16, int64_t batch, int64_t heads, int64_t
  * k8: int8 likewise with hkv heads (hq % hkv == 0, GQA); vt: bf16
  * [batch, hkv, dim, lpad] from tu_sage_v_prep; o: bf16 by strides.
  * q_scale: fp32 [batch, hq, ceil(lq/blkq)]; k_scale: fp32 [batch, hkv, ceil(lk/blkk)].
- * dim == 128; blkq >= 1; blkk % 64 == 0.  causal: top-left aligned.
+ * dim 64 or 128 (the reference's two kernel widths, turing_sage/core.py
+ * :436-448; narrower heads are zero-padded by the caller); blkq >= 1;
+ * blkk % 64 == 0.  causal: top-left aligned.
  * Replaces qk_int8_sv_f16_accum_f32_attn
  * (kernel/csrc/turing/sage/qk_int_sv_f16_cuda_sm75.cu:984-1123), the kernel
  * behind turing_utils::sage_attention (turing_sage/custom_ops.py:137-168). */

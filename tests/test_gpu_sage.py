@@ -149,3 +149,47 @@ def test_smoothing_invariance(gpu_device):
     eb = attention_error_metrics(b.float().cpu(), ref)
     print(f"  smoothed cos={ea.cosine:.6f} raw cos={eb.cosine:.6f}", flush=True)
     assert ea.cosine >= 0.999 and ea.cosine >= eb.cosine - 1e-4
+
+
+@pytest.mark.parametrize("b,h,hkv,lq,lk,d,causal,layout", [
+    (1, 4, 4, 300, 333, 64, False, "HND"),
+    (2, 4, 2, 257, 129, 64, True, "HND"),
+    (1, 3, 3, 200, 700, 48, False, "NHD"),
+    (1, 24, 24, 8190, 8190, 64, False, "HND"),
+])
+def test_head_dim_64_kernel(gpu_device, b, h, hkv, lq, lk, d, causal, layout):
+    """head_dim <= 64 runs the 64-wide kernel (V^T of 64 channels, as the
+    reference pads to 64, turing_sage/core.py:436-448) and meets the gate
+    against the oracle's quantized math."""
+    print(f"[attn d64] b={b} h={h} hkv={hkv} lq={lq} lk={lk} d={d} causal={causal} {layout}", flush=True)
+    q, _, _ = inputs.attention(b, h, lq, d, 300 + lq)
+    _, k, v = inputs.attention(b, hkv, lk, d, 400 + lk)
+    to = (lambda t: t.transpose(1, 2).contiguous()) if layout == "NHD" else (lambda t: t)
+    state = core.prequantize_sageattn(to(q).to(gpu_device), to(k).to(gpu_device), to(v).to(gpu_device),
+                                      tensor_layout=layout, is_causal=causal)
+    assert state.value_t.shape[2] == 64 and state.query_int8.shape[-1] == 64
+    out = core.sageattn_from_prequantized(state)
+    torch.cuda.synchronize(gpu_device)
+    out = out.transpose(1, 2) if layout == "NHD" else out
+    assert out.shape == q.shape
+    rows = _sample_rows(b, h, lq, 128, lq + lk + d)
+    ref = _oracle_rows(q, k, v, rows, 128, 128, causal, d ** -0.5)
+    got = out.float().cpu()[rows[:, 0], rows[:, 1], rows[:, 2]]
+    res = attention_error_metrics(got, torch.from_numpy(ref), candidate_name="hip", reference_name="oracle")
+    print(f"  cos={res.cosine:.6f} max_abs={res.max_abs:.3e}", flush=True)
+    require_attention_correctness(res, **GATE)
+
+
+def test_head_dim_64_matches_the_128_wide_kernel(gpu_device):
+    """Zero channels change neither the codes nor the result: the 64-wide
+    kernel equals the 128-wide kernel on the same inputs padded to 128, to
+    the last rounding of the PV sums."""
+    q, k, v = inputs.attention(1, 4, 513, 64, 77)
+    dev = gpu_device
+    o64 = core.sageattn(q.to(dev), k.to(dev), v.to(dev))
+    pad = lambda t: torch.nn.functional.pad(t, (0, 64)).to(dev)  # noqa: E731
+    o128 = core.sageattn(pad(q), pad(k), pad(v), sm_scale=64 ** -0.5)[..., :64]
+    torch.cuda.synchronize(dev)
+    assert o64.shape == o128.shape
+    diff = (o64.float() - o128.float()).abs().max().item()
+    assert diff <= 2 ** -7 * o128.float().abs().max().item(), diff

@@ -37,10 +37,12 @@
 // registers as packed bf16 while the row absmax is reduced (cross-lane max,
 // one workgroup barrier); each lane then quantizes its own values and a
 // second, byte-sized wave-local transpose puts the codes back in column order
-// for 16-byte stores.  The division by bf16(scale) is a reciprocal multiply
-// plus one FMA correction (Markstein), which the CPU tests prove yields the
-// same INT8 code as IEEE division for every (value, scale) pair the quantizer
-// can produce.
+// for 16-byte stores.  The division by bf16(scale) is one multiply by its
+// correctly rounded reciprocal: its fp32 result can differ from the IEEE
+// quotient in the last place, but value and scale both carry 8 significant
+// bits, so the quotient is never that close to a bf16 rounding midpoint, and
+// the CPU tests check, over every (value, scale) pair the quantizer can
+// produce, that the INT8 code is the IEEE division's.
 #include <type_traits>
 
 #include "tu_common.h"
@@ -78,15 +80,6 @@ __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
     return v;
-}
-
-// Correctly rounded quotient a / b for the quantizer's domain, given
-// y = RN(1 / b): q0 = RN(a y), r = a - b q0 (exact by FMA), RN(q0 + r y).
-__device__ __forceinline__ float div_markstein(float a, float b, float y) {
-    const float q0 = a * y;
-    const float r = __builtin_fmaf(-q0, b, a);
-    const float q = __builtin_fmaf(r, y, q0);
-    return __builtin_isinf(a) ? a : q;
 }
 
 // Input activations, operation for operation the fixed fp32 sequences of the
@@ -194,8 +187,8 @@ __device__ __forceinline__ uint32_t elem_bits(float v) {
     else return hw_bf16_bits(v);
 }
 
-__device__ __forceinline__ int32_t quant_code(float v, float rs, float ry) {
-    const float divided = hw_bf16_round(div_markstein(v, rs, ry));
+__device__ __forceinline__ int32_t quant_code(float v, float ry) {
+    const float divided = hw_bf16_round(v * ry);
     float qf = __builtin_rintf(divided);
     qf = fminf(127.0f, fmaxf(-128.0f, qf));
     return static_cast<int32_t>(qf);
@@ -220,6 +213,40 @@ __device__ __forceinline__ float activate(float v, float up, std::integral_const
 }
 template <bool kF16>
 __device__ __forceinline__ float activate(float v, float up, std::integral_constant<int, 2>) { return swiglu(v, up); }
+
+// bf16 tanh-GELU by table.  The output is a function of the input's 16 bits:
+//   |x| in [2^-12, 8): a table of the 2 x 15 x 128 bf16 values there, built
+//     in LDS by each workgroup with activate<false> itself, so equal to it
+//     by construction;
+//   |x| < 2^-12: |inner| < 2^-12, so tanh_det returns inner unchanged and
+//     gelu = bf16((0.5 x) (1 + inner)) = bf16(0.5 x): 0.5 x is exact, and
+//     either 1 + inner rounds to 1 (|x| < 2^-24) or 0.5 x is a normal bf16
+//     value that a relative change below 2^-12 cannot round away from;
+//   8 <= |x| < inf: inner > 9, tanh_det returns +-1, gelu = x (x > 0) or -0;
+//   inf / NaN: activate<false> itself (rare branch).
+constexpr uint32_t kGeluLutLo = 115u << 7;  // magnitude bits of 2^-12
+constexpr int kGeluLutHalf = 15 * 128;      // exponents 2^-12 .. 2^2, 128 mantissas each
+constexpr int kGeluLut = 2 * kGeluLutHalf;  // both signs
+
+__device__ __forceinline__ uint32_t gelu_lut_entry(int idx) {
+    const uint32_t bits = (static_cast<uint32_t>(idx / kGeluLutHalf) << 15) |
+                          (kGeluLutLo + static_cast<uint32_t>(idx % kGeluLutHalf));
+    const float g = activate<false>(bf16_bits_to_f32(bits), 0.0f, std::integral_constant<int, 1>{});
+    return __float_as_uint(g) >> 16;  // exact: g is a bf16 value (or the canonical NaN)
+}
+
+__device__ __forceinline__ float gelu_by_table(uint32_t bits, const uint16_t *lut) {
+    const uint32_t mag = bits & 0x7fffu;
+    const float x = bf16_bits_to_f32(bits);
+    const uint32_t rel = mag - kGeluLutLo;
+    const uint32_t idx = min(rel, static_cast<uint32_t>(kGeluLutHalf - 1)) + (bits >> 15) * kGeluLutHalf;
+    const float from_table = bf16_bits_to_f32(lut[idx]);
+    const float tiny = bf16_round(0.5f * x);
+    const float big = x > 0.0f ? x : -0.0f;
+    float g = rel < static_cast<uint32_t>(kGeluLutHalf) ? from_table : (mag < kGeluLutLo ? tiny : big);
+    if (__builtin_expect(mag >= 0x7f80u, 0)) g = activate<false>(x, 0.0f, std::integral_constant<int, 1>{});
+    return g;
+}
 
 // Raw bf16 input of one lane for one pass: 16 columns (and 16 "up" columns
 // for SwiGLU).
@@ -255,11 +282,16 @@ __device__ __forceinline__ void load_lane(LaneInput<kAct> &in, const uint16_t *x
 // element index 16 L + p with L = l % (G/16), p = d0 + 4 d1.  After the
 // transpose a lane holds, for G = 256, p = L and t = d2 + 4 d3 = 0..15; for
 // G = 128, p = 2L and 2L + 1 (z[t] and z[8 + t]) with t = d2 + 4 d3 = 0..7.
+// rows_per_block: rows per workgroup, in order (> 1 only for the bf16 GELU,
+// whose table build is then shared by that many rows).
 template <int G, int kAct, int kPasses, bool kF16>
 __global__ __launch_bounds__(1024) void convrot_quant_i8_kernel(
-    const uint16_t *__restrict__ x, int8_t *__restrict__ q, float *__restrict__ scales, int k, int staged_scale) {
+    const uint16_t *__restrict__ x, int8_t *__restrict__ q, float *__restrict__ scales, int k, int staged_scale,
+    int64_t rows, int rows_per_block) {
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ float wave_amax[kMaxWaves];
+    constexpr bool kGeluTable = kAct == 1 && !kF16;
+    __shared__ uint16_t gelu_lut[kGeluTable ? kGeluLut : 1];
     constexpr int kLanesPerGroup = G / 16;
     // Transpose scratch: group gi starts at dword gi * kGroupDwords (padded so
     // the groups of a wave fall on different banks); element p of source lane
@@ -280,132 +312,147 @@ __global__ __launch_bounds__(1024) void convrot_quant_i8_kernel(
     const int nchunks = (k + kChunk - 1) / kChunk;
     const int64_t in_stride = kAct == 2 ? 2 * static_cast<int64_t>(k) : k;
 
-    const int64_t row = blockIdx.x;
-    const uint16_t *xrow = x + row * in_stride;
-    LaneInput<kAct> in[kPasses];
+    if constexpr (kGeluTable) {
+        for (int i = tid; i < kGeluLut; i += blockDim.x) gelu_lut[i] = static_cast<uint16_t>(gelu_lut_entry(i));
+        __syncthreads();
+    }
+    // one row per workgroup unless the GELU table is shared by several
+    const int64_t row0 = kGeluTable ? static_cast<int64_t>(blockIdx.x) * rows_per_block : blockIdx.x;
+    const int64_t row_end = kGeluTable ? min(rows, row0 + rows_per_block) : row0 + 1;
+    for (int64_t row = row0; row < row_end; ++row) {
+        const uint16_t *xrow = x + row * in_stride;
+        LaneInput<kAct> in[kPasses];
 #pragma unroll
-    for (int pass = 0; pass < kPasses; ++pass)
-        if (wave + pass * waves < nchunks) load_lane<kAct>(in[pass], xrow, k, (wave + pass * waves) * kChunk + 16 * lane);
-    float absmax = 0.0f;
-    uint32_t packed[kPasses][8];
+        for (int pass = 0; pass < kPasses; ++pass)
+            if (wave + pass * waves < nchunks) load_lane<kAct>(in[pass], xrow, k, (wave + pass * waves) * kChunk + 16 * lane);
+        float absmax = 0.0f;
+        uint32_t packed[kPasses][8];
 #pragma unroll
-    for (int pass = 0; pass < kPasses; ++pass) {
-        const int chunk = wave + pass * waves;
-        if (chunk >= nchunks) break;  // uniform across the wave
-        const bool active = chunk * kChunk + 16 * lane < k;  // whole groups are in or out (k % G == 0)
-        float v[16];
+        for (int pass = 0; pass < kPasses; ++pass) {
+            const int chunk = wave + pass * waves;
+            if (chunk >= nchunks) break;  // uniform across the wave
+            const bool active = chunk * kChunk + 16 * lane < k;  // whole groups are in or out (k % G == 0)
+            float v[16];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const uint32_t w = in[pass].x[j / 4][j % 4];
-            const uint32_t u = kAct == 2 ? in[pass].up[(j / 4) % (kAct == 2 ? 2 : 1)][j % 4] : 0u;
-            v[2 * j] = activate<kF16>(elem_to_f32<kF16>(w), elem_to_f32<kF16>(u),
-                                      std::integral_constant<int, kAct>{});
-            v[2 * j + 1] = activate<kF16>(elem_to_f32<kF16>(w >> 16), elem_to_f32<kF16>(u >> 16),
-                                          std::integral_constant<int, kAct>{});
-        }
-        // Digits d0 (stride 1) and d1 (stride 4) in registers (convrot_quant.cu:384-391).
-#pragma unroll
-        for (int d1 = 0; d1 < 4; ++d1) r4(v[4 * d1], v[4 * d1 + 1], v[4 * d1 + 2], v[4 * d1 + 3]);
-#pragma unroll
-        for (int d0 = 0; d0 < 4; ++d0) r4(v[d0], v[d0 + 4], v[d0 + 8], v[d0 + 12]);
-
-        // Wave-local transpose through LDS.
-        lds_wave_sync();  // earlier reads of the scratch are done
-#pragma unroll
-        for (int c = 0; c < 4; ++c)
-            *reinterpret_cast<f32x4 *>(grp + 16 * L + 4 * ((c + (L >> 2)) & 3)) =
-                f32x4{v[4 * c], v[4 * c + 1], v[4 * c + 2], v[4 * c + 3]};
-        lds_wave_sync();
-        float z[16];
-        if constexpr (G == 256) {
-#pragma unroll
-            for (int t = 0; t < 16; ++t) z[t] = grp[16 * t + 4 * (((L >> 2) + (t >> 2)) & 3) + (L & 3)];
-        } else {
-#pragma unroll
-            for (int t = 0; t < 8; ++t) {
-                const f32x2 pair = *reinterpret_cast<const f32x2 *>(
-                    grp + 16 * t + 4 * (((L >> 1) + (t >> 2)) & 3) + ((2 * L) & 3));
-                z[t] = pair.x;
-                z[8 + t] = pair.y;
-            }
-        }
-
-        // Digits d2 (stride 16) and d3 (stride 64) in registers (convrot_quant.cu:311-330).
-        if constexpr (G == 256) {
-#pragma unroll
-            for (int d3 = 0; d3 < 4; ++d3) r4(z[4 * d3], z[4 * d3 + 1], z[4 * d3 + 2], z[4 * d3 + 3]);
-#pragma unroll
-            for (int d2 = 0; d2 < 4; ++d2) r4(z[d2], z[d2 + 4], z[d2 + 8], z[d2 + 12]);
-        } else {
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-#pragma unroll
-                for (int d3 = 0; d3 < 2; ++d3)
-                    r4(z[8 * h + 4 * d3], z[8 * h + 4 * d3 + 1], z[8 * h + 4 * d3 + 2], z[8 * h + 4 * d3 + 3]);
-                // Radix-2 digit on stride 64: (1/sqrt2) [[1, 1], [1, -1]].
-#pragma unroll
-                for (int d2 = 0; d2 < 4; ++d2) {
-                    const float a0 = z[8 * h + d2], a1 = z[8 * h + d2 + 4];
-                    z[8 * h + d2] = kInvSqrt2 * (a0 + a1);
-                    z[8 * h + d2 + 4] = kInvSqrt2 * (a0 - a1);
+            for (int j = 0; j < 8; ++j) {
+                const uint32_t w = in[pass].x[j / 4][j % 4];
+                const uint32_t u = kAct == 2 ? in[pass].up[(j / 4) % (kAct == 2 ? 2 : 1)][j % 4] : 0u;
+                if constexpr (kGeluTable) {
+                    v[2 * j] = gelu_by_table(w & 0xffffu, gelu_lut);
+                    v[2 * j + 1] = gelu_by_table(w >> 16, gelu_lut);
+                } else {
+                    v[2 * j] = activate<kF16>(elem_to_f32<kF16>(w), elem_to_f32<kF16>(u),
+                                              std::integral_constant<int, kAct>{});
+                    v[2 * j + 1] = activate<kF16>(elem_to_f32<kF16>(w >> 16), elem_to_f32<kF16>(u >> 16),
+                                                  std::integral_constant<int, kAct>{});
                 }
             }
-        }
-        if (active) {
+            // Digits d0 (stride 1) and d1 (stride 4) in registers (convrot_quant.cu:384-391).
 #pragma unroll
-            for (int t = 0; t < 16; ++t) absmax = fmaxf(absmax, fabsf(z[t]));
-        }
+            for (int d1 = 0; d1 < 4; ++d1) r4(v[4 * d1], v[4 * d1 + 1], v[4 * d1 + 2], v[4 * d1 + 3]);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            // G = 256: t = 2j, 2j + 1 of p = L.  G = 128: p = 2L (low), 2L + 1 (high) of t = j.
-            const float lo = G == 256 ? z[2 * j] : z[j];
-            const float hi = G == 256 ? z[2 * j + 1] : z[8 + j];
-            packed[pass][j] = elem_bits<kF16>(lo) | (elem_bits<kF16>(hi) << 16);
-        }
-    }
+            for (int d0 = 0; d0 < 4; ++d0) r4(v[d0], v[d0 + 4], v[d0 + 8], v[d0 + 12]);
 
-    absmax = wave_max(absmax);
-    if (lane == 0) wave_amax[wave] = absmax;
-    __syncthreads();
-    float amax = wave_amax[0];
-    for (int w = 1; w < waves; ++w) amax = fmaxf(amax, wave_amax[w]);
-    const float clipped = fminf(amax, kF16 ? 65504.0f : 3.38953139e38f);
-    const float scale = fmaxf(staged_scale ? clipped * (1.0f / 127.0f) : clipped / 127.0f, 1.0e-30f);
-    if (tid == 0) scales[row] = scale;
-    const float rs = kF16 ? hw_f16_round(scale) : bf16_round(scale);
-    const float ry = 1.0f / rs;
-
-    int8_t *qrow = q + row * static_cast<int64_t>(k);
+            // Wave-local transpose through LDS.
+            lds_wave_sync();  // earlier reads of the scratch are done
 #pragma unroll
-    for (int pass = 0; pass < kPasses; ++pass) {
-        const int chunk = wave + pass * waves;
-        if (chunk >= nchunks) break;
-        const int col = chunk * kChunk + 16 * lane;
-        // Codes back to column order: element 16 t + p of group gi is byte
-        // gi * kCodeGroupBytes + 16 t + p of the wave's scratch.
-        lds_wave_sync();  // the scratch is free (transposed reads consumed)
-        unsigned char *gb = scr8 + gi * kCodeGroupBytes;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const uint32_t w = packed[pass][j];
-            uint32_t c0, c1;
-            if constexpr (kF16) {
-                c0 = static_cast<uint32_t>(quant_code_f16(f16_bits_to_f32(w & 0xffffu), rs)) & 0xffu;
-                c1 = static_cast<uint32_t>(quant_code_f16(f16_bits_to_f32(w >> 16), rs)) & 0xffu;
-            } else {
-                c0 = static_cast<uint32_t>(quant_code(bf16_bits_to_f32(w & 0xffffu), rs, ry)) & 0xffu;
-                c1 = static_cast<uint32_t>(quant_code(bf16_bits_to_f32(w >> 16), rs, ry)) & 0xffu;
-            }
+            for (int c = 0; c < 4; ++c)
+                *reinterpret_cast<f32x4 *>(grp + 16 * L + 4 * ((c + (L >> 2)) & 3)) =
+                    f32x4{v[4 * c], v[4 * c + 1], v[4 * c + 2], v[4 * c + 3]};
+            lds_wave_sync();
+            float z[16];
             if constexpr (G == 256) {
-                gb[32 * j + L] = static_cast<unsigned char>(c0);
-                gb[32 * j + 16 + L] = static_cast<unsigned char>(c1);
+#pragma unroll
+                for (int t = 0; t < 16; ++t) z[t] = grp[16 * t + 4 * (((L >> 2) + (t >> 2)) & 3) + (L & 3)];
             } else {
-                *reinterpret_cast<uint16_t *>(gb + 16 * j + 2 * L) = static_cast<uint16_t>(c0 | (c1 << 8));
+#pragma unroll
+                for (int t = 0; t < 8; ++t) {
+                    const f32x2 pair = *reinterpret_cast<const f32x2 *>(
+                        grp + 16 * t + 4 * (((L >> 1) + (t >> 2)) & 3) + ((2 * L) & 3));
+                    z[t] = pair.x;
+                    z[8 + t] = pair.y;
+                }
+            }
+
+            // Digits d2 (stride 16) and d3 (stride 64) in registers (convrot_quant.cu:311-330).
+            if constexpr (G == 256) {
+#pragma unroll
+                for (int d3 = 0; d3 < 4; ++d3) r4(z[4 * d3], z[4 * d3 + 1], z[4 * d3 + 2], z[4 * d3 + 3]);
+#pragma unroll
+                for (int d2 = 0; d2 < 4; ++d2) r4(z[d2], z[d2 + 4], z[d2 + 8], z[d2 + 12]);
+            } else {
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+#pragma unroll
+                    for (int d3 = 0; d3 < 2; ++d3)
+                        r4(z[8 * h + 4 * d3], z[8 * h + 4 * d3 + 1], z[8 * h + 4 * d3 + 2], z[8 * h + 4 * d3 + 3]);
+                    // Radix-2 digit on stride 64: (1/sqrt2) [[1, 1], [1, -1]].
+#pragma unroll
+                    for (int d2 = 0; d2 < 4; ++d2) {
+                        const float a0 = z[8 * h + d2], a1 = z[8 * h + d2 + 4];
+                        z[8 * h + d2] = kInvSqrt2 * (a0 + a1);
+                        z[8 * h + d2 + 4] = kInvSqrt2 * (a0 - a1);
+                    }
+                }
+            }
+            if (active) {
+#pragma unroll
+                for (int t = 0; t < 16; ++t) absmax = fmaxf(absmax, fabsf(z[t]));
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                // G = 256: t = 2j, 2j + 1 of p = L.  G = 128: p = 2L (low), 2L + 1 (high) of t = j.
+                const float lo = G == 256 ? z[2 * j] : z[j];
+                const float hi = G == 256 ? z[2 * j + 1] : z[8 + j];
+                packed[pass][j] = elem_bits<kF16>(lo) | (elem_bits<kF16>(hi) << 16);
             }
         }
-        lds_wave_sync();
-        const u32x4 codes = *reinterpret_cast<const u32x4 *>(gb + 16 * L);
-        if (col < k) *reinterpret_cast<u32x4 *>(qrow + col) = codes;
+
+        absmax = wave_max(absmax);
+        if (lane == 0) wave_amax[wave] = absmax;
+        __syncthreads();
+        float amax = wave_amax[0];
+        for (int w = 1; w < waves; ++w) amax = fmaxf(amax, wave_amax[w]);
+        const float clipped = fminf(amax, kF16 ? 65504.0f : 3.38953139e38f);
+        const float scale = fmaxf(staged_scale ? clipped * (1.0f / 127.0f) : clipped / 127.0f, 1.0e-30f);
+        if (tid == 0) scales[row] = scale;
+        const float rs = kF16 ? hw_f16_round(scale) : bf16_round(scale);
+        const float ry = 1.0f / rs;
+
+        int8_t *qrow = q + row * static_cast<int64_t>(k);
+#pragma unroll
+        for (int pass = 0; pass < kPasses; ++pass) {
+            const int chunk = wave + pass * waves;
+            if (chunk >= nchunks) break;
+            const int col = chunk * kChunk + 16 * lane;
+            // Codes back to column order: element 16 t + p of group gi is byte
+            // gi * kCodeGroupBytes + 16 t + p of the wave's scratch.
+            lds_wave_sync();  // the scratch is free (transposed reads consumed)
+            unsigned char *gb = scr8 + gi * kCodeGroupBytes;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const uint32_t w = packed[pass][j];
+                uint32_t c0, c1;
+                if constexpr (kF16) {
+                    c0 = static_cast<uint32_t>(quant_code_f16(f16_bits_to_f32(w & 0xffffu), rs)) & 0xffu;
+                    c1 = static_cast<uint32_t>(quant_code_f16(f16_bits_to_f32(w >> 16), rs)) & 0xffu;
+                } else {
+                    c0 = static_cast<uint32_t>(quant_code(bf16_bits_to_f32(w & 0xffffu), ry)) & 0xffu;
+                    c1 = static_cast<uint32_t>(quant_code(bf16_bits_to_f32(w >> 16), ry)) & 0xffu;
+                }
+                if constexpr (G == 256) {
+                    gb[32 * j + L] = static_cast<unsigned char>(c0);
+                    gb[32 * j + 16 + L] = static_cast<unsigned char>(c1);
+                } else {
+                    *reinterpret_cast<uint16_t *>(gb + 16 * j + 2 * L) = static_cast<uint16_t>(c0 | (c1 << 8));
+                }
+            }
+            lds_wave_sync();
+            const u32x4 codes = *reinterpret_cast<const u32x4 *>(gb + 16 * L);
+            if (col < k) *reinterpret_cast<u32x4 *>(qrow + col) = codes;
+        }
+        // the next row rewrites wave_amax: every wave has read this row's first
+        if (row + 1 < row_end) __syncthreads();
     }
 }
 
@@ -440,14 +487,16 @@ extern "C" int32_t tu_convrot_quant_i8(const void *x_bf16, int8_t *q, float *sca
     const size_t lds = static_cast<size_t>(waves) * kScratchBytes;
     hipStream_t s = static_cast<hipStream_t>(stream);
     const auto *xp = static_cast<const uint16_t *>(x_bf16);
-    const dim3 grid(static_cast<unsigned>(rows));
+    // The bf16 GELU builds a 7.5 KiB table per workgroup: 8 rows share it.
+    const int rpb = (act == TU_ACT_GELU_TANH && !f16) ? 8 : 1;
+    const dim3 grid(static_cast<unsigned>((rows + rpb - 1) / rpb));
 #define TU_CONVROT_LAUNCH_T(G, A, F)                                                                          \
     do {                                                                                                      \
         switch (passes) {                                                                                     \
-            case 1: convrot_quant_i8_kernel<G, A, 1, F><<<grid, waves * 64, lds, s>>>(xp, q, scale, k, staged_scale); break; \
-            case 2: convrot_quant_i8_kernel<G, A, 2, F><<<grid, waves * 64, lds, s>>>(xp, q, scale, k, staged_scale); break; \
-            case 3: convrot_quant_i8_kernel<G, A, 3, F><<<grid, waves * 64, lds, s>>>(xp, q, scale, k, staged_scale); break; \
-            default: convrot_quant_i8_kernel<G, A, 4, F><<<grid, waves * 64, lds, s>>>(xp, q, scale, k, staged_scale); break; \
+            case 1: convrot_quant_i8_kernel<G, A, 1, F><<<grid, waves * 64, lds, s>>>(xp, q, scale, k, staged_scale, rows, rpb); break; \
+            case 2: convrot_quant_i8_kernel<G, A, 2, F><<<grid, waves * 64, lds, s>>>(xp, q, scale, k, staged_scale, rows, rpb); break; \
+            case 3: convrot_quant_i8_kernel<G, A, 3, F><<<grid, waves * 64, lds, s>>>(xp, q, scale, k, staged_scale, rows, rpb); break; \
+            default: convrot_quant_i8_kernel<G, A, 4, F><<<grid, waves * 64, lds, s>>>(xp, q, scale, k, staged_scale, rows, rpb); break; \
         }                                                                                                     \
     } while (0)
 #define TU_CONVROT_LAUNCH(G, A)                   \

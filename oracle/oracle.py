@@ -61,10 +61,8 @@ def lib():
             L.or_convrot_quant_i8.argtypes = [_p, _i64, _i64, _i32, _i32, _i32, _p, _p]
             L.or_convrot_quant_i8_t.restype = _i32
             L.or_convrot_quant_i8_t.argtypes = [_p, _i64, _i64, _i32, _i32, _i32, _i32, _p, _p]
-            L.or_div_markstein_f32.restype = ctypes.c_float
-            L.or_div_markstein_f32.argtypes = [ctypes.c_float, ctypes.c_float]
-            L.or_check_markstein_quant.restype = _i64
-            L.or_check_markstein_quant.argtypes = [_p, _p]
+            L.or_check_recip_quant.restype = _i64
+            L.or_check_recip_quant.argtypes = [_p, _p]
             L.or_int8_gemm_i32.restype = _i32
             L.or_int8_gemm_i32.argtypes = [_p, _p, _i64, _i64, _i64, _p]
             L.or_int8_epilogue_bf16.restype = _i32
@@ -196,15 +194,11 @@ def swiglu(gate: float, up: float) -> float:
     return float(lib().or_swiglu(gate, up))
 
 
-def div_markstein(a: float, b: float) -> float:
-    return lib().or_div_markstein_f32(a, b)
-
-
-def check_markstein_quant() -> tuple[int, int, int]:
+def check_recip_quant() -> tuple[int, int, int]:
     """(code mismatches, pairs checked, fp32 quotient mismatches)."""
     pairs = ctypes.c_int64(0)
     fp32 = ctypes.c_int64(0)
-    bad = lib().or_check_markstein_quant(ctypes.byref(pairs), ctypes.byref(fp32))
+    bad = lib().or_check_recip_quant(ctypes.byref(pairs), ctypes.byref(fp32))
     return int(bad), int(pairs.value), int(fp32.value)
 
 

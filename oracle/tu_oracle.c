@@ -23,8 +23,9 @@
  *                             the rotation output, scale and quotient; zero /
  *                             tiny rows (division by fp16(scale) = 0); GELU
  *                             fp16 output vs torch float16 gelu(tanh)
- *   or_div_markstein_f32      pinned: exhaustive over the quantizer's bf16 domain
- *                             vs IEEE division (or_check_markstein_quant)
+ *   or_check_recip_quant      the GPU's reciprocal-multiply quotient gives the
+ *                             IEEE-division code on every pair of the
+ *                             quantizer's bf16 domain (exhaustive)
  *   or_int8_gemm_i32          pinned: numpy int64 matmul (brute force)
  *   or_int8_epilogue_bf16     pinned: fp64 closed form within bf16 rounding
  *   or_residual_gate_bf16     pinned: numpy fp64 product-plus-sum rounded once
@@ -261,52 +262,50 @@ OR_API int or_convrot_quant_i8(const uint16_t *x, int64_t rows, int64_t k, int g
     return or_convrot_quant_i8_t(x, rows, k, group, act, staged, 0, q, scales);
 }
 
-/* Division by reciprocal plus one FMA correction (Markstein): the GPU
- * quantizer uses this in place of an IEEE divide.  Exposed so the CPU tests
- * can compare it with IEEE division over every bf16 x bf16 pair.  The
- * reciprocal is the correctly rounded 1/b. */
-OR_API float or_div_markstein_f32(float a, float b) {
-    const float y = 1.0f / b;
-    const float q0 = a * y;
-    const float r = fmaf(-q0, b, a);
-    return fmaf(r, y, q0);
-}
-
-/* Exhaustive check of the Markstein quotient on the quantizer's domain:
- * every divisor b that bf16(scale) can take (positive normal bf16, 1e-30 <=
- * b <= 2^128/127) and every finite bf16 dividend a with |a| <= 130 b (the
- * row-buffer invariant |bf16(y)| <= bf16(absmax) <= 128.5 bf16(scale)).
- * Returns the number of pairs whose INT8 code
- * clamp(nearbyint(bf16(a / b))) differs between IEEE division and
- * or_div_markstein_f32; *pairs receives the number of pairs checked and
- * *fp32_mismatch the number of differing fp32 quotients. */
+/* The GPU quantizer forms the quotient bf16(y) / bf16(scale) as one multiply
+ * by the correctly rounded reciprocal of the (per-row) bf16 scale.
+ * or_check_recip_quant below proves, over every pair the quantizer can
+ * produce -- every divisor b that bf16(scale) can take (positive normal bf16,
+ * 1e-30 <= b <= 2^128/127) and every finite bf16 dividend a with |a| <= 130 b
+ * (the row-buffer invariant |bf16(y)| <= bf16(absmax) <= 128.5 bf16(scale))
+ * -- that the INT8 code clamp(nearbyint(bf16(q))) is the same as with IEEE
+ * division. */
 static inline int quant_code(float d) {
     float qf = nearbyintf(bf16_round_f32(d));
     qf = fminf(127.0f, fmaxf(-128.0f, qf));
     return (int)qf;
 }
 
-OR_API int64_t or_check_markstein_quant(int64_t *pairs, int64_t *fp32_mismatch) {
+/* The same domain with the quotient formed as a * RN(1 / b): one multiply
+ * by the correctly rounded reciprocal (what the GPU quantizer uses).  Its
+ * fp32 result can differ from a / b in the last place, but a and b both
+ * carry 8 significant bits, so a / b is never within 2^-17 (relative) of a
+ * bf16 rounding midpoint unless it is bf16-exact, and the two roundings of
+ * the reciprocal product stay within 2^-23: the bf16 quotient, and hence the
+ * code, is the same.  Returns the number of differing codes. */
+OR_API int64_t or_check_recip_quant(int64_t *pairs, int64_t *fp32_mismatch) {
     int64_t bad_code = 0, bad_fp32 = 0, n = 0;
 #pragma omp parallel for schedule(dynamic, 64) reduction(+ : bad_code, bad_fp32, n)
     for (uint32_t bb = 0x0080; bb < 0x7f80; ++bb) {
         const float b = u2f(bb << 16);
         if (b < 1.0e-30f || b > 3.38953139e38f / 127.0f * 1.01f) continue;
+        const float r = 1.0f / b;
         for (uint32_t ab = 0; ab < 0x10000; ++ab) {
             if ((ab & 0x7f80) == 0x7f80) continue; /* inf / nan */
             const float a = u2f(ab << 16);
             if (fabsf(a) > 130.0f * b) continue;
             ++n;
             const float ieee = a / b;
-            const float mk = or_div_markstein_f32(a, b);
-            if (f2u(ieee) != f2u(mk)) ++bad_fp32;
-            if (quant_code(ieee) != quant_code(mk)) ++bad_code;
+            const float rq = a * r;
+            if (f2u(ieee) != f2u(rq)) ++bad_fp32;
+            if (quant_code(ieee) != quant_code(rq)) ++bad_code;
         }
     }
     if (pairs) *pairs = n;
     if (fp32_mismatch) *fp32_mismatch = bad_fp32;
     return bad_code;
 }
+
 
 /* ------------------------------------------------------------------------ */
 /* INT8 x INT8 -> INT32: acc[m][n] = sum_k A[m][k] * W[n][k].                */

@@ -236,3 +236,24 @@ def test_row_buffer_ops_refuse_fp16(gpu_device):
         torch.ops.turing_utils.bf16_int8_convrot_quantize(x, 256)
     with pytest.raises(TypeError):
         torch.ops.turing_utils.bf16_gelu_int8_convrot_quantize(x, 256)
+
+
+@pytest.mark.parametrize("group", [128, 256])
+def test_gelu_quant_inf_nan_rows(gpu_device, group):
+    """+-inf and NaN inputs take the GELU's direct path (the table covers
+    finite inputs): codes and scales still equal the oracle's, with rows of
+    8 sharing one workgroup."""
+    print(f"[convrot gelu] inf / NaN rows group={group}", flush=True)
+    g = torch.Generator().manual_seed(group)
+    x = torch.randn(21, 512, generator=g)
+    x[3, 17] = float("inf")
+    x[5, 0] = float("-inf")
+    x[9, 300] = float("nan")
+    x[12, :] = float("-inf")
+    x[20, 5] = float("inf")
+    x[20, 6] = -9.5
+    xb = x.to(torch.bfloat16)
+    q, s = torch.ops.turing_utils.bf16_gelu_int8_convrot_quantize(xb.to(gpu_device), group)
+    q_ref, s_ref = oracle.convrot_quant(inputs.bits(xb), group, act=oracle.ACT_GELU_TANH)
+    np.testing.assert_array_equal(s.cpu().numpy().reshape(-1).view(np.uint32), s_ref.view(np.uint32))
+    np.testing.assert_array_equal(q.cpu().numpy(), q_ref)

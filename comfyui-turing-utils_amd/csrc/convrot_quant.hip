@@ -57,6 +57,13 @@ constexpr int kMaxCols = kChunk * kMaxWaves * kMaxPasses;
 constexpr int kScratchBytes = 8 * 144 * 4;  // per wave: the larger of the two padded layouts
 constexpr float kInvSqrt2 = 0.70710678118654752440f;
 typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// Two floats to two bf16 (low = a) by one v_cvt_pk_bf16_f32 (RNE; NaN
+// payloads unspecified, which the uses below tolerate).
+__device__ __forceinline__ uint32_t hw_bf16x2_bits(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{a, b}), bf16x2_t));
+}
 
 __device__ __forceinline__ void lds_wave_sync() {
     // LDS operations of one wave complete in order; this stops the compiler
@@ -159,9 +166,6 @@ __device__ __forceinline__ float swiglu(float gate, float up) { return (gate / (
 __device__ __forceinline__ uint16_t hw_bf16_bits(float v) {
     return __builtin_bit_cast(uint16_t, static_cast<__bf16>(v));
 }
-// Through the bit pattern, so the compiler does not re-round a later rint in
-// bf16 arithmetic.
-__device__ __forceinline__ float hw_bf16_round(float v) { return bf16_bits_to_f32(hw_bf16_bits(v)); }
 
 // fp16 (RNE by the hardware conversion) and back.  The empty asm pins the
 // fp32 value first, so the compiler cannot fold "fp32 multiply, then round to
@@ -187,11 +191,17 @@ __device__ __forceinline__ uint32_t elem_bits(float v) {
     else return hw_bf16_bits(v);
 }
 
-__device__ __forceinline__ int32_t quant_code(float v, float ry) {
-    const float divided = hw_bf16_round(v * ry);
+__device__ __forceinline__ int32_t code_of(float divided) {
     float qf = __builtin_rintf(divided);
     qf = fminf(127.0f, fmaxf(-128.0f, qf));
     return static_cast<int32_t>(qf);
+}
+
+// Codes of two values: both quotients rounded to bf16 by one conversion.
+__device__ __forceinline__ void quant_code2(float v0, float v1, float ry, int32_t &c0, int32_t &c1) {
+    const uint32_t d = hw_bf16x2_bits(v0 * ry, v1 * ry);
+    c0 = code_of(__uint_as_float(d << 16));
+    c1 = code_of(__uint_as_float(d & 0xffff0000u));
 }
 
 // fp16 elements: fp16(v / rs) with IEEE division (rs may be 0, see the top).
@@ -404,7 +414,8 @@ __global__ __launch_bounds__(1024) void convrot_quant_i8_kernel(
                 // G = 256: t = 2j, 2j + 1 of p = L.  G = 128: p = 2L (low), 2L + 1 (high) of t = j.
                 const float lo = G == 256 ? z[2 * j] : z[j];
                 const float hi = G == 256 ? z[2 * j + 1] : z[8 + j];
-                packed[pass][j] = elem_bits<kF16>(lo) | (elem_bits<kF16>(hi) << 16);
+                if constexpr (kF16) packed[pass][j] = elem_bits<kF16>(lo) | (elem_bits<kF16>(hi) << 16);
+                else packed[pass][j] = hw_bf16x2_bits(lo, hi);
             }
         }
 
@@ -437,8 +448,10 @@ __global__ __launch_bounds__(1024) void convrot_quant_i8_kernel(
                     c0 = static_cast<uint32_t>(quant_code_f16(f16_bits_to_f32(w & 0xffffu), rs)) & 0xffu;
                     c1 = static_cast<uint32_t>(quant_code_f16(f16_bits_to_f32(w >> 16), rs)) & 0xffu;
                 } else {
-                    c0 = static_cast<uint32_t>(quant_code(bf16_bits_to_f32(w & 0xffffu), ry)) & 0xffu;
-                    c1 = static_cast<uint32_t>(quant_code(bf16_bits_to_f32(w >> 16), ry)) & 0xffu;
+                    int32_t i0, i1;
+                    quant_code2(bf16_bits_to_f32(w & 0xffffu), __uint_as_float(w & 0xffff0000u), ry, i0, i1);
+                    c0 = static_cast<uint32_t>(i0) & 0xffu;
+                    c1 = static_cast<uint32_t>(i1) & 0xffu;
                 }
                 if constexpr (G == 256) {
                     gb[32 * j + L] = static_cast<unsigned char>(c0);

@@ -56,14 +56,6 @@ constexpr int kMaxPasses = 4;     // so a row holds at most 65536 columns
 constexpr int kMaxCols = kChunk * kMaxWaves * kMaxPasses;
 constexpr int kScratchBytes = 8 * 144 * 4;  // per wave: the larger of the two padded layouts
 constexpr float kInvSqrt2 = 0.70710678118654752440f;
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-
-// Two floats to two bf16 (low = a) by one v_cvt_pk_bf16_f32 (RNE; NaN
-// payloads unspecified, which the uses below tolerate).
-__device__ __forceinline__ uint32_t hw_bf16x2_bits(float a, float b) {
-    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{a, b}), bf16x2_t));
-}
 
 __device__ __forceinline__ void lds_wave_sync() {
     // LDS operations of one wave complete in order; this stops the compiler

@@ -310,29 +310,59 @@ __global__ __launch_bounds__(kThreads, kWaves / 4) void int8_gemm_kernel(
             wsv[i] = *reinterpret_cast<const f32x4 *>(ws + col);
             bv[i] = *reinterpret_cast<const f32x4 *>(bp + col);
         }
+        // With finite row scales and bias and finite nonzero column scales no
+        // value of the wave's tile can be NaN: float(acc) is finite, a product
+        // or sum of finite values overflows at most to +-inf, and +-inf times
+        // a nonzero scale plus a finite bias stays +-inf.  The hardware RNE
+        // conversion then equals bf16_rne_bits bit for bit, at one
+        // instruction per pair instead of about five per value; any other
+        // wave takes the software rounding (canonical 0x7fff NaN), and so does
+        // the residual variant, which has no registers to spare for both.
+        uint32_t finite_max = 0, ws_max = 0;
+#pragma unroll
+        for (int j = 0; j < kFragsM; ++j) finite_max = max(finite_max, __float_as_uint(arow[j]) & 0x7fffffffu);
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                finite_max = max(finite_max, __float_as_uint(bv[i][r]) & 0x7fffffffu);
+                // |ws| bits - 1 (unsigned): 0 wraps to 0xffffffff
+                ws_max = max(ws_max, (__float_as_uint(wsv[i][r]) & 0x7fffffffu) - 1u);
+            }
+        const bool hw_round = !kResidual &&
+            __builtin_amdgcn_ballot_w64(finite_max >= 0x7f800000u || ws_max >= 0x7f7fffffu) == 0;
         __syncthreads();
         int8_t *tile = &lds[0][0] + wave * kRows * 256;
+        auto stage_tile = [&](auto hw) {
 #pragma unroll
-        for (int j = 0; j < kFragsM; ++j) {
-            const int lrow = j * 16 + frow;
+            for (int j = 0; j < kFragsM; ++j) {
+                const int lrow = j * 16 + frow;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                float v[4];
+                for (int i = 0; i < 8; ++i) {
+                    float v[4];
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    float x = static_cast<float>(acc[i][j][r]);
-                    x = x * arow[j];
-                    x = x * wsv[i][r];
-                    if (bias) x = x + bv[i][r];
-                    v[r] = x;
+                    for (int r = 0; r < 4; ++r) {
+                        float x = static_cast<float>(acc[i][j][r]);
+                        x = x * arow[j];
+                        x = x * wsv[i][r];
+                        if (bias) x = x + bv[i][r];
+                        v[r] = x;
+                    }
+                    u32x2 packed;
+                    if constexpr (decltype(hw)::value) {
+                        packed.x = hw_bf16x2_bits(v[0], v[1]);
+                        packed.y = hw_bf16x2_bits(v[2], v[3]);
+                    } else {
+                        packed.x = pack_bf16x2(v[0], v[1]);
+                        packed.y = pack_bf16x2(v[2], v[3]);
+                    }
+                    const int chunk = (2 * i + (g >> 1)) ^ (lrow & 15);
+                    *reinterpret_cast<u32x2 *>(tile + lrow * 256 + chunk * 16 + (g & 1) * 8) = packed;
                 }
-                u32x2 packed;
-                packed.x = pack_bf16x2(v[0], v[1]);
-                packed.y = pack_bf16x2(v[2], v[3]);
-                const int chunk = (2 * i + (g >> 1)) ^ (lrow & 15);
-                *reinterpret_cast<u32x2 *>(tile + lrow * 256 + chunk * 16 + (g & 1) * 8) = packed;
             }
-        }
+        };
+        if (hw_round) stage_tile(std::true_type{});
+        else stage_tile(std::false_type{});
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");

@@ -36,6 +36,8 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
 // ---------------------------------------------------------------------------
 // bf16 <-> fp32.  Round-to-nearest-even with a canonical NaN (0x7fff), the
@@ -57,6 +59,13 @@ __device__ __forceinline__ float bf16_round(float v) { return bf16_bits_to_f32(b
 // Packs two floats to two bf16 (low = a) with the same rounding.
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
     return bf16_rne_bits(a) | (bf16_rne_bits(b) << 16);
+}
+
+// Two floats to two bf16 (low = a) by one v_cvt_pk_bf16_f32: RNE, equal to
+// pack_bf16x2 for every non-NaN input; a NaN keeps an unspecified NaN
+// payload instead of 0x7fff.
+__device__ __forceinline__ uint32_t hw_bf16x2_bits(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{a, b}), bf16x2_t));
 }
 
 }  // namespace tu

@@ -66,6 +66,43 @@ def test_int8_linear_epilogue_exact(gpu_device, m, n, k, with_bias):
     assert bad.size == 0, f"{len(bad)} outputs differ, first {bad[:5].tolist()}"
 
 
+def test_int8_linear_epilogue_nonfinite_scales(gpu_device):
+    """Waves whose scales and bias are finite (with nonzero column scales)
+    round on the hardware conversion, the others in software; both must give
+    the oracle's bits, canonical 0x7fff NaN included.  Row 70's scale
+    overflows the product to +-inf (a finite-scale wave: inf stays inf); row
+    200's meets a zero and a -0 column scale (inf * 0 = NaN); NaN and inf
+    sit in a row scale, a column scale and the bias."""
+    m, n, k = 300, 520, 192
+    print(f"[int8_linear nonfinite] m={m} n={n} k={k}", flush=True)
+    a = _rand_i8((m, k), 41)
+    w, ws, bias = inputs.weights(n, k, 43, True)
+    g = torch.Generator().manual_seed(5)
+    as_ = torch.empty(m).uniform_(1e-3, 1e-1, generator=g)
+    as_[5] = float("nan")
+    as_[70] = 3.0e38
+    as_[200] = 1.0e37
+    as_[260] = float("-inf")
+    ws[300] = 0.0
+    ws[301] = -0.0
+    ws[400] = float("inf")
+    ws[513] = float("nan")
+    bias = bias.clone()
+    bias[450] = float("nan")
+    bias[460] = float("-inf")
+    for b in (bias, None):
+        out = torch.ops.turing_utils.int8_linear(
+            a.to(gpu_device), w.to(gpu_device), as_.to(gpu_device), ws.to(gpu_device),
+            None if b is None else b.to(gpu_device))
+        torch.cuda.synchronize(gpu_device)
+        acc = oracle.int8_gemm_i32(a.numpy(), w.numpy())
+        ref = oracle.epilogue_bf16(acc, as_.numpy(), ws.numpy(), None if b is None else b.numpy())
+        got = inputs.bits(out)
+        assert (ref == 0x7FFF).any() and ((ref & 0x7FFF) == 0x7F80).any()
+        bad = np.argwhere(got != ref)
+        assert bad.size == 0, f"bias={b is not None}: {len(bad)} outputs differ, first {bad[:5].tolist()}"
+
+
 @pytest.mark.parametrize("gate_rows", [None, 1, 37])
 @pytest.mark.parametrize("m,n,k,with_bias", [(300, 264, 192, True), (257, 520, 1040, False), (96, 5120, 1536, True)])
 def test_int8_linear_residual_exact(gpu_device, m, n, k, with_bias, gate_rows):

@@ -15,9 +15,12 @@ value = (sum of 2MNK over the linears + 4 B H L^2 D) / step time, in TOPS.
 Per-kernel average durations come from HIP events recorded on torch's current
 stream, which is the stream every op of this package launches on, inside the
 timed region.  The roofline entry is for the kernel with the largest total
-time; its ``traffic`` (HBM bytes per launch) is read from profiles/traffic.json,
-written from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes of this script
-(``--copy-calibration`` adds the 1 GiB reference copy those passes scale by).
+time; its ``traffic`` is read from profiles/traffic.json: the bytes per launch
+the L2 requested from the fabric (rocprofv3 --pmc passes of this script over
+TCC_EA0_RDREQ_{32B,64B,128B} / TCC_EA0_WRREQ{,_64B}, request counts times their
+sizes; FETCH_SIZE / WRITE_SIZE scaled by ``--copy-calibration``'s 1 GiB copy
+agree within 1.3 %), an upper bound on HBM bytes since the Infinity Cache may
+serve part of them.
 cpu_baseline times the reference's CPU path -- its PyTorch fallback: bf16
 linear on the dequantized weight and bf16 scaled_dot_product_attention -- on a
 bounded sample of the same workload on this host's cores; the CPU oracle
@@ -154,7 +157,7 @@ def main():
     copy_gbs = copy_bandwidth(torch, dev)
     if args.copy_calibration:
         # one elementwise kernel that reads and writes exactly 1 GiB: the
-        # reference point for the FETCH_SIZE / WRITE_SIZE counters
+        # reference point for the byte counters
         src = torch.ones(1 << 28, dtype=torch.int32, device=dev)
         dst = torch.empty_like(src)
         torch.cuda.synchronize()
@@ -341,9 +344,9 @@ TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 
 
 def measured_traffic(kernel: str):
-    """HBM bytes per launch of ``kernel`` at this workload, from the committed
-    rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes (scaled by the same counters
-    on a 1 GiB copy), or None when no such measurement is committed."""
+    """Bytes per launch of ``kernel`` that its L2 requested from the fabric at
+    this workload (read + write requests times their sizes, from the committed
+    rocprofv3 --pmc passes), or None when no such measurement is committed."""
     try:
         with open(TRAFFIC_FILE) as f:
             entry = json.load(f).get(kernel)

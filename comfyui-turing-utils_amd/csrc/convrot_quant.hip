@@ -225,29 +225,64 @@ __device__ __forceinline__ float activate(float v, float up, std::integral_const
 //     either 1 + inner rounds to 1 (|x| < 2^-24) or 0.5 x is a normal bf16
 //     value that a relative change below 2^-12 cannot round away from;
 //   8 <= |x| < inf: inner > 9, tanh_det returns +-1, gelu = x (x > 0) or -0;
-//   inf / NaN: activate<false> itself (rare branch).
+//   inf / NaN: activate<false> itself (the caller's rare branch).
+// The table interleaves the signs: entry 2 (mag - kGeluLutLo) + sign.
 constexpr uint32_t kGeluLutLo = 115u << 7;  // magnitude bits of 2^-12
 constexpr int kGeluLutHalf = 15 * 128;      // exponents 2^-12 .. 2^2, 128 mantissas each
 constexpr int kGeluLut = 2 * kGeluLutHalf;  // both signs
 
 __device__ __forceinline__ uint32_t gelu_lut_entry(int idx) {
-    const uint32_t bits = (static_cast<uint32_t>(idx / kGeluLutHalf) << 15) |
-                          (kGeluLutLo + static_cast<uint32_t>(idx % kGeluLutHalf));
+    const uint32_t bits = (static_cast<uint32_t>(idx & 1) << 15) | (kGeluLutLo + static_cast<uint32_t>(idx >> 1));
     const float g = activate<false>(bf16_bits_to_f32(bits), 0.0f, std::integral_constant<int, 1>{});
     return __float_as_uint(g) >> 16;  // exact: g is a bf16 value (or the canonical NaN)
 }
 
-__device__ __forceinline__ float gelu_by_table(uint32_t bits, const uint16_t *lut) {
-    const uint32_t mag = bits & 0x7fffu;
-    const float x = bf16_bits_to_f32(bits);
-    const uint32_t rel = mag - kGeluLutLo;
-    const uint32_t idx = min(rel, static_cast<uint32_t>(kGeluLutHalf - 1)) + (bits >> 15) * kGeluLutHalf;
-    const float from_table = bf16_bits_to_f32(lut[idx]);
-    const float tiny = bf16_round(0.5f * x);
-    const float big = x > 0.0f ? x : -0.0f;
-    float g = rel < static_cast<uint32_t>(kGeluLutHalf) ? from_table : (mag < kGeluLutLo ? tiny : big);
-    if (__builtin_expect(mag >= 0x7f80u, 0)) g = activate<false>(x, 0.0f, std::integral_constant<int, 1>{});
-    return g;
+typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
+
+// 0xffff in each 16-bit half of x whose bit 15 is set, else 0 (one
+// v_pk_ashrrev_i16; written out because the compiler otherwise splits the
+// halves into compares and selects).  op_sel_hi:[0,1]: the high half also
+// takes its shift count from the low 16 bits of the constant 15.
+__device__ __forceinline__ uint32_t half_sign_masks(uint32_t x) {
+    uint32_t r;
+    asm("v_pk_ashrrev_i16 %0, 15, %1 op_sel_hi:[0,1]" : "=v"(r) : "v"(x));
+    return r;
+}
+
+// GELU of the two bf16 values packed in w (low half first) as two packed
+// bf16 results, on packed 16-bit integer arithmetic: per half,
+//   rel = mag - kGeluLutLo (wrapping: >= 0x8000 exactly for |x| < 2^-12,
+//         since mag - kGeluLutLo <= 0x7fff - kGeluLutLo < 0x8000 otherwise),
+//   rel < kGeluLutHalf: the table; rel >= 0x8000: bf16(0.5 x); else x or -0.
+// Split in two steps so that a lane's table reads can all be in flight
+// before the first is used: gelu_pair_table reads the two entries,
+// gelu_pair_select picks the results.
+__device__ __forceinline__ uint32_t gelu_pair_rel(uint32_t w) {
+    const u16x2 rel = __builtin_bit_cast(u16x2, w & 0x7fff7fffu) - static_cast<uint16_t>(kGeluLutLo);
+    return __builtin_bit_cast(uint32_t, rel);
+}
+
+__device__ __forceinline__ uint32_t gelu_pair_table(uint32_t w, uint32_t rel2, const uint16_t *lut) {
+    const u16x2 rel = __builtin_bit_cast(u16x2, rel2);
+    const u16x2 h = __builtin_bit_cast(u16x2, w);
+    const u16x2 limit = static_cast<uint16_t>(kGeluLutHalf - 1);
+    const u16x2 relc = rel < limit ? rel : limit;
+    // byte offsets of the entries: 4 relc + 2 sign (both < 2^13)
+    const uint32_t off = __builtin_bit_cast(uint32_t, static_cast<u16x2>((relc << 2) | ((h >> 14) & 2)));
+    const unsigned char *base = reinterpret_cast<const unsigned char *>(lut);
+    return static_cast<uint32_t>(*reinterpret_cast<const uint16_t *>(base + (off & 0xffffu))) |
+           (static_cast<uint32_t>(*reinterpret_cast<const uint16_t *>(base + (off >> 16))) << 16);
+}
+
+__device__ __forceinline__ uint32_t gelu_pair_select(uint32_t w, uint32_t rel2, uint32_t table) {
+    const uint32_t tiny = hw_bf16x2_bits(0.5f * __uint_as_float(w << 16), 0.5f * __uint_as_float(w & 0xffff0000u));
+    const uint32_t neg = half_sign_masks(w);
+    const uint32_t big = (w & ~neg) | (0x80008000u & neg);  // x, or -0 for negative x
+    const u16x2 past = __builtin_bit_cast(u16x2, rel2) - static_cast<uint16_t>(kGeluLutHalf);
+    const uint32_t table_or_tiny = half_sign_masks(__builtin_bit_cast(uint32_t, past));
+    const uint32_t is_tiny = half_sign_masks(rel2);
+    const uint32_t r = (table & table_or_tiny) | (big & ~table_or_tiny);
+    return (tiny & is_tiny) | (r & ~is_tiny);
 }
 
 // Raw bf16 input of one lane for one pass: 16 columns (and 16 "up" columns
@@ -335,14 +370,40 @@ __global__ __launch_bounds__(1024) void convrot_quant_i8_kernel(
             if (chunk >= nchunks) break;  // uniform across the wave
             const bool active = chunk * kChunk + 16 * lane < k;  // whole groups are in or out (k % G == 0)
             float v[16];
+            if constexpr (kGeluTable) {
+                // A half with bit 15 of (mag + 0x80) set is inf or NaN (no
+                // carry crosses halves); such lanes recompute with activate.
+                uint32_t nonfinite = 0, rel[8], table[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const uint32_t w = in[pass].x[j / 4][j % 4];
-                const uint32_t u = kAct == 2 ? in[pass].up[(j / 4) % (kAct == 2 ? 2 : 1)][j % 4] : 0u;
-                if constexpr (kGeluTable) {
-                    v[2 * j] = gelu_by_table(w & 0xffffu, gelu_lut);
-                    v[2 * j + 1] = gelu_by_table(w >> 16, gelu_lut);
-                } else {
+                for (int j = 0; j < 8; ++j) {
+                    const uint32_t w = in[pass].x[j / 4][j % 4];
+                    nonfinite |= (w & 0x7fff7fffu) + 0x00800080u;
+                    rel[j] = gelu_pair_rel(w);
+                    table[j] = gelu_pair_table(w, rel[j], gelu_lut);
+                }
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const uint32_t g = gelu_pair_select(in[pass].x[j / 4][j % 4], rel[j], table[j]);
+                    v[2 * j] = __uint_as_float(g << 16);
+                    v[2 * j + 1] = __uint_as_float(g & 0xffff0000u);
+                }
+                if (__builtin_expect(__builtin_amdgcn_ballot_w64((nonfinite & 0x80008000u) != 0) != 0, 0)) {
+                    if (nonfinite & 0x80008000u) {
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) {
+                            const uint32_t w = in[pass].x[j / 4][j % 4];
+                            v[2 * j] = activate<false>(bf16_bits_to_f32(w & 0xffffu), 0.0f,
+                                                       std::integral_constant<int, 1>{});
+                            v[2 * j + 1] = activate<false>(__uint_as_float(w & 0xffff0000u), 0.0f,
+                                                           std::integral_constant<int, 1>{});
+                        }
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const uint32_t w = in[pass].x[j / 4][j % 4];
+                    const uint32_t u = kAct == 2 ? in[pass].up[(j / 4) % (kAct == 2 ? 2 : 1)][j % 4] : 0u;
                     v[2 * j] = activate<kF16>(elem_to_f32<kF16>(w), elem_to_f32<kF16>(u),
                                               std::integral_constant<int, kAct>{});
                     v[2 * j + 1] = activate<kF16>(elem_to_f32<kF16>(w >> 16), elem_to_f32<kF16>(u >> 16),

@@ -111,14 +111,17 @@ def test_gelu_quant_exact(gpu_device, group, m, k, seed):
 
 
 def test_gelu_every_bf16_input(gpu_device):
-    """Every finite bf16 value x, one per row at column 0 of an otherwise zero
-    row: the row scale carries the bits of gelu(x), so the whole activation
-    domain is checked bit for bit against the oracle."""
+    """Every finite bf16 value x, one per row at columns 0 and 17 of an
+    otherwise zero row (the low half of one packed pair and the high half of
+    another): the row scale carries the bits of gelu(x), so the whole
+    activation domain is checked bit for bit against the oracle in both
+    halves."""
     print("[convrot gelu] every finite bf16 input", flush=True)
     bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
     bits = bits[(bits & 0x7F80) != 0x7F80]
     x = np.zeros((bits.size, 128), np.uint16)
     x[:, 0] = bits
+    x[:, 17] = bits
     xt = inputs.from_bits(x)
     q, s = torch.ops.turing_utils.bf16_gelu_int8_convrot_quantize(xt.to(gpu_device), 128)
     q_ref, s_ref = oracle.convrot_quant(x, 128, act=oracle.ACT_GELU_TANH)

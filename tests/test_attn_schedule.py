@@ -2,7 +2,9 @@
 
 ``sage_attn_kernel`` (csrc/sage_attn.hip) and ``w8a8_attn_kernel``
 (csrc/w8a8_attn.hip, 4 loads per tile instead of 6) run 8 waves in two groups that
-share one workgroup barrier per key tile.  Every wave executes, per tile t,
+share one workgroup barrier per key tile.  Group 0 issues a tile's loads
+between its MFMA and softmax clusters in the Sage kernel, and after the
+softmax in the W8A8 kernel (whose flushes wait on loads of their own).  Every wave executes, per tile t,
 an MFMA cluster M_t = {QK(t + 1), PV(t)} and a softmax cluster V_t; group 0
 orders an interval as [M_t, V_{t+1}], group 1 as [V_t, M_t], so the two
 groups' MFMA clusters overlap on each SIMD.  Group 0 alone streams the K and
@@ -29,7 +31,9 @@ import pytest
 
 K_STAGES = 5
 K_AHEAD = K_STAGES - 1
-LOADS_PER_TILE = 6  # per group-0 wave: 2 K + 4 V^T 1 KiB blocks
+# per kernel: 1 KiB blocks a group-0 wave loads per tile (Sage 2 K + 4 V^T,
+# W8A8 2 K + 2 V^T), and whether it issues them after the softmax
+KERNELS = {"sage": (6, False), "w8a8": (4, True)}
 KBKEY = 64
 KBQ = 256
 KWAVEQ = 32
@@ -62,8 +66,9 @@ class Wave:
         self.events.append(("softmax", (tile, masked)))
 
 
-def kernel_program(wave: int, lq: int, lk: int, causal: bool, qblock: int) -> Wave:
+def kernel_program(wave: int, lq: int, lk: int, causal: bool, qblock: int, kernel: str = "sage") -> Wave:
     """The kernel's control flow for one wave, statement for statement."""
+    LOADS_PER_TILE, issue_late = KERNELS[kernel]
     w = Wave(wave)
     grp, w4 = wave >> 2, wave & 3
     qblock0 = qblock * KBQ
@@ -104,18 +109,20 @@ def kernel_program(wave: int, lq: int, lk: int, causal: bool, qblock: int) -> Wa
     for it in range(main_steps):
         w.qk((it + 1) % K_STAGES, it + 1)
         w.pv(it % K_STAGES, it)
-        if grp == 0:
+        if grp == 0 and not issue_late:
             w.issue((it + K_AHEAD) % K_STAGES, tile_key0(it + K_AHEAD))
-        else:
+        if grp == 1:
             w.barrier()
         softmax(it + 1, False)
         if grp == 0:
+            if issue_late:
+                w.issue((it + K_AHEAD) % K_STAGES, tile_key0(it + K_AHEAD))
             w.wait((K_AHEAD - 2) * LOADS_PER_TILE)
             w.barrier()
     # remaining intervals: masked tiles, the last tile, causal tiles past the
     # wave's diagonal (barriers only)
     for it in range(main_steps, tiles):
-        if grp == 0:
+        if grp == 0 and not issue_late:
             w.issue((it + K_AHEAD) % K_STAGES, tile_key0(it + K_AHEAD))
         if it + 1 < my_tiles:
             w.qk((it + 1) % K_STAGES, it + 1)
@@ -126,13 +133,16 @@ def kernel_program(wave: int, lq: int, lk: int, causal: bool, qblock: int) -> Wa
         if it + 1 < my_tiles:
             softmax(it + 1, True)
         if grp == 0:
+            if issue_late:
+                w.issue((it + K_AHEAD) % K_STAGES, tile_key0(it + K_AHEAD))
             w.wait((K_AHEAD - 2) * LOADS_PER_TILE)
             w.barrier()
     return w, dict(tiles=tiles, my_tiles=my_tiles)
 
 
-def check_schedule(lq: int, lk: int, causal: bool, qblock: int):
-    waves = [kernel_program(i, lq, lk, causal, qblock) for i in range(8)]
+def check_schedule(lq: int, lk: int, causal: bool, qblock: int, kernel: str = "sage"):
+    LOADS_PER_TILE = KERNELS[kernel][0]
+    waves = [kernel_program(i, lq, lk, causal, qblock, kernel) for i in range(8)]
     progs = [w for w, _ in waves]
     # 1. equal barrier counts
     counts = [sum(1 for k, _ in p.events if k == "barrier") for p in progs]
@@ -214,29 +224,32 @@ def check_schedule(lq: int, lk: int, causal: bool, qblock: int):
         assert last_pv == info["my_tiles"] - 1 and last_sm == info["my_tiles"] - 1, (wi, info, last_pv)
 
 
+@pytest.mark.parametrize("kernel", sorted(KERNELS))
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("lk", [1, 2, 63, 64, 65, 127, 128, 129, 191, 256, 257, 300, 333, 511, 700, 1000, 32760])
-def test_schedule_every_block(causal, lk):
+def test_schedule_every_block(causal, lk, kernel):
     lq = lk if causal else max(lk, 300)
     for qblock in range((lq + KBQ - 1) // KBQ):
-        check_schedule(lq, lk, causal, qblock)
+        check_schedule(lq, lk, causal, qblock, kernel)
 
 
+@pytest.mark.parametrize("kernel", sorted(KERNELS))
 @pytest.mark.parametrize("lq,lk", list(itertools.product([1, 40, 129, 256, 257, 700], [1, 2, 64, 65, 151, 333])))
-def test_schedule_ragged_pairs(lq, lk):
+def test_schedule_ragged_pairs(lq, lk, kernel):
     for causal in (False, True):
         for qblock in range((lq + KBQ - 1) // KBQ):
-            check_schedule(lq, lk, causal, qblock)
+            check_schedule(lq, lk, causal, qblock, kernel)
 
 
-def test_model_catches_a_missing_wait():
-    """Planted mistake: without the loader's wait in the steady state, a
-    read finds its tile not yet resident."""
+@pytest.mark.parametrize("kernel", sorted(KERNELS))
+def test_model_catches_a_missing_wait(kernel):
+    """Planted mistake: loading one stage further ahead than the ring holds
+    overwrites a stage that is still to be read."""
     global K_AHEAD
     saved = K_AHEAD
     try:
-        K_AHEAD = 5  # loads one stage further ahead than the ring holds
+        K_AHEAD = 5
         with pytest.raises(AssertionError):
-            check_schedule(1000, 1000, False, 0)
+            check_schedule(1000, 1000, False, 0, kernel)
     finally:
         K_AHEAD = saved

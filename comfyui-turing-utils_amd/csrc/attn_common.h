@@ -1,6 +1,7 @@
 // Device helpers shared by the two gfx950 attention kernels (Sage bf16-PV
 // and dense W8A8): wait-count immediates, cross-lane row reductions, buffer
-// resources, the ping-pong barrier and the biased-accumulator constants.
+// resources, the workgroup barrier of the two-group schedule and the
+// biased-accumulator constants.
 #pragma once
 
 #include "tu_common.h"
@@ -58,8 +59,8 @@ constexpr float kBiasF = 12582912.0f;
 
 // Workgroup barrier that does not wait for memory (the LDS ring hand-off is
 // ordered by an explicit s_waitcnt vmcnt before it) and that no instruction
-// is scheduled across: the ping-pong phases must not leak MFMAs into the
-// other group's VALU phase.
+// is scheduled across: the two groups' MFMA and softmax clusters must keep
+// their places relative to the barrier.
 __device__ __forceinline__ void wg_barrier() {
     __builtin_amdgcn_sched_barrier(0);
     asm volatile("" ::: "memory");

@@ -305,9 +305,9 @@ __device__ __forceinline__ void mfma_cluster(const int8_t *kst, const int8_t *vs
                                              const i32x4 (&qf)[kQT][Geo<D>::kKSlices], i32x4 (&s)[4][kQT],
                                              const bf16x8 (&p)[2][kQT], SoftmaxState<D> &st, const bf16x8 &ones) {
     constexpr int kDS = Geo<D>::kDS, kSl = Geo<D>::kKSlices;
-    // This wave's MFMA cluster is the critical phase of the ping-pong: raise its
+    // This wave's MFMA cluster is the critical path of its interval: raise its
     // issue priority over the other group's softmax VALU on the same SIMD
-    // (measured about 1 % faster; raising the softmax phase instead was slower).
+    // (measured about 1 % faster; raising the softmax instead was slower).
     __builtin_amdgcn_s_setprio(3);
     i32x4 kf[4][kSl];
     bf16x8 va[kDS], vb[kDS];

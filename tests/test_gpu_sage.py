@@ -104,6 +104,29 @@ def test_attention_vs_oracle(gpu_device, b, h, hkv, lq, lk, d, causal, blkq, blk
     require_attention_correctness(res, **GATE)
 
 
+@pytest.mark.parametrize("b,h,hkv,l,causal,blkq,blkk", [
+    (1, 12, 12, 8190, True, 128, 128),   # config 2's shape, causal
+    (2, 8, 2, 2049, False, 16, 64),      # batch 2, GQA 4:1, the reference's production blocks
+    (2, 8, 2, 2049, True, 16, 64),
+])
+def test_attention_long_causal_and_gqa(gpu_device, b, h, hkv, l, causal, blkq, blkk):
+    """Long sequences with the causal diagonal crossing many key tiles, and
+    batch-2 GQA: sampled rows (first and last row included) against the
+    oracle within the gate."""
+    print(f"[attn long] b={b} h={h} hkv={hkv} l={l} causal={causal} blk=({blkq},{blkk})", flush=True)
+    q, _, _ = inputs.attention(b, h, l, 128, 300 + h)
+    _, k, v = inputs.attention(b, hkv, l, 128, 400 + h)
+    out = core.sageattn(q.to(gpu_device), k.to(gpu_device), v.to(gpu_device), tensor_layout="HND",
+                        is_causal=causal, BLKQ=blkq, BLKK=blkk)
+    torch.cuda.synchronize(gpu_device)
+    rows = _sample_rows(b, h, l, 128, l + h)
+    ref = _oracle_rows(q, k, v, rows, blkq, blkk, causal, 128 ** -0.5)
+    got = out.float().cpu()[rows[:, 0], rows[:, 1], rows[:, 2]]
+    res = attention_error_metrics(got, torch.from_numpy(ref), candidate_name="hip", reference_name="oracle")
+    print(f"  cos={res.cosine:.6f} max_abs={res.max_abs:.3e}", flush=True)
+    require_attention_correctness(res, **GATE)
+
+
 def test_attention_config2_rows(gpu_device):
     """BASELINE config 2 (B1 H12 L8190 D128, seed 1), 256 sampled rows vs the oracle."""
     q, k, v = inputs.attention(1, 12, 8190, 128, 1)

@@ -52,6 +52,7 @@ namespace {
 
 constexpr int kChunk = 1024;      // columns per wave pass: 64 lanes x 16
 constexpr int kMaxWaves = 16;
+constexpr int kTableThreads = 512;  // waves of a GELU-by-table workgroup, at most 8
 constexpr int kMaxPasses = 4;     // so a row holds at most 65536 columns
 constexpr int kMaxCols = kChunk * kMaxWaves * kMaxPasses;
 constexpr int kScratchBytes = 8 * 144 * 4;  // per wave: the larger of the two padded layouts
@@ -319,15 +320,18 @@ __device__ __forceinline__ void load_lane(LaneInput<kAct> &in, const uint16_t *x
 // element index 16 L + p with L = l % (G/16), p = d0 + 4 d1.  After the
 // transpose a lane holds, for G = 256, p = L and t = d2 + 4 d3 = 0..15; for
 // G = 128, p = 2L and 2L + 1 (z[t] and z[8 + t]) with t = d2 + 4 d3 = 0..7.
-// rows_per_block: rows per workgroup, in order (> 1 only for the bf16 GELU,
-// whose table build is then shared by that many rows).
-template <int G, int kAct, int kPasses, bool kF16>
-__global__ __launch_bounds__(1024) void convrot_quant_i8_kernel(
+// rows_per_block: rows per workgroup, in order (> 1 only for the bf16 GELU
+// by table, whose table build is then shared by that many rows).
+// kGeluTable: bf16 GELU by the LDS table, for rows of up to
+// kTableThreads / 64 waves; its launch bound leaves the kernel twice the
+// registers (the 1024-thread bound capped it at 128 VGPRs, and it spilled).
+template <int G, int kAct, int kPasses, bool kF16, bool kGeluTable = false>
+__global__ __launch_bounds__(kGeluTable ? kTableThreads : 1024) void convrot_quant_i8_kernel(
     const uint16_t *__restrict__ x, int8_t *__restrict__ q, float *__restrict__ scales, int k, int staged_scale,
     int64_t rows, int rows_per_block) {
+    static_assert(!kGeluTable || (kAct == 1 && !kF16), "the GELU table is for bf16 GELU input");
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ float wave_amax[kMaxWaves];
-    constexpr bool kGeluTable = kAct == 1 && !kF16;
     __shared__ uint16_t gelu_lut[kGeluTable ? kGeluLut : 1];
     constexpr int kLanesPerGroup = G / 16;
     // Transpose scratch: group gi starts at dword gi * kGroupDwords (padded so
@@ -553,22 +557,25 @@ extern "C" int32_t tu_convrot_quant_i8(const void *x_bf16, int8_t *q, float *sca
     const size_t lds = static_cast<size_t>(waves) * kScratchBytes;
     hipStream_t s = static_cast<hipStream_t>(stream);
     const auto *xp = static_cast<const uint16_t *>(x_bf16);
-    // The bf16 GELU builds a 7.5 KiB table per workgroup: 8 rows share it.
-    const int rpb = (act == TU_ACT_GELU_TANH && !f16) ? 8 : 1;
+    // The bf16 GELU of rows up to 8 waves builds a 7.5 KiB table per
+    // workgroup, which 8 rows share; wider rows compute every GELU.
+    const bool table = act == TU_ACT_GELU_TANH && !f16 && waves * 64 <= kTableThreads;
+    const int rpb = table ? 8 : 1;
     const dim3 grid(static_cast<unsigned>((rows + rpb - 1) / rpb));
-#define TU_CONVROT_LAUNCH_T(G, A, F)                                                                          \
-    do {                                                                                                      \
-        switch (passes) {                                                                                     \
-            case 1: convrot_quant_i8_kernel<G, A, 1, F><<<grid, waves * 64, lds, s>>>(xp, q, scale, k, staged_scale, rows, rpb); break; \
-            case 2: convrot_quant_i8_kernel<G, A, 2, F><<<grid, waves * 64, lds, s>>>(xp, q, scale, k, staged_scale, rows, rpb); break; \
-            case 3: convrot_quant_i8_kernel<G, A, 3, F><<<grid, waves * 64, lds, s>>>(xp, q, scale, k, staged_scale, rows, rpb); break; \
-            default: convrot_quant_i8_kernel<G, A, 4, F><<<grid, waves * 64, lds, s>>>(xp, q, scale, k, staged_scale, rows, rpb); break; \
-        }                                                                                                     \
+#define TU_CONVROT_LAUNCH_T(G, A, F, T)                                                                          \
+    do {                                                                                                         \
+        switch (passes) {                                                                                        \
+            case 1: convrot_quant_i8_kernel<G, A, 1, F, T><<<grid, waves * 64, lds, s>>>(xp, q, scale, k, staged_scale, rows, rpb); break; \
+            case 2: convrot_quant_i8_kernel<G, A, 2, F, T><<<grid, waves * 64, lds, s>>>(xp, q, scale, k, staged_scale, rows, rpb); break; \
+            case 3: convrot_quant_i8_kernel<G, A, 3, F, T><<<grid, waves * 64, lds, s>>>(xp, q, scale, k, staged_scale, rows, rpb); break; \
+            default: convrot_quant_i8_kernel<G, A, 4, F, T><<<grid, waves * 64, lds, s>>>(xp, q, scale, k, staged_scale, rows, rpb); break; \
+        }                                                                                                        \
     } while (0)
-#define TU_CONVROT_LAUNCH(G, A)                   \
-    do {                                          \
-        if (f16) TU_CONVROT_LAUNCH_T(G, A, true); \
-        else TU_CONVROT_LAUNCH_T(G, A, false);    \
+#define TU_CONVROT_LAUNCH(G, A)                                         \
+    do {                                                                \
+        if (f16) TU_CONVROT_LAUNCH_T(G, A, true, false);                \
+        else if (table) TU_CONVROT_LAUNCH_T(G, A, false, (A == 1));     \
+        else TU_CONVROT_LAUNCH_T(G, A, false, false);                   \
     } while (0)
     if (group == 256) {
         if (act == 0) TU_CONVROT_LAUNCH(256, 0);

@@ -15,7 +15,9 @@ value = (sum of 2MNK over the linears + 4 B H L^2 D) / step time, in TOPS.
 Per-kernel average durations come from HIP events recorded on torch's current
 stream, which is the stream every op of this package launches on, inside the
 timed region.  The roofline entry is for the kernel with the largest total
-time; its ``traffic`` is read from profiles/traffic.json: the bytes per launch
+time; its ``mfma_busy`` and ``clock_ghz`` come from profiles/mfma_counters.json
+(rocprofv3 --pmc passes of this script) and its ``traffic`` from
+profiles/traffic.json: the bytes per launch
 the L2 requested from the fabric (rocprofv3 --pmc passes of this script over
 TCC_EA0_RDREQ_{32B,64B,128B} / TCC_EA0_WRREQ{,_64B}, request counts times their
 sizes; FETCH_SIZE / WRITE_SIZE scaled by ``--copy-calibration``'s 1 GiB copy
@@ -212,6 +214,11 @@ def main():
         "frac": achieved / peak,
         "traffic": measured_traffic(dominant),
     }
+    counters = measured_mfma(dominant)
+    if bound == "mfma" and counters is not None:
+        # the committed rocprofv3 counters of the same kernel and workload
+        roofline["mfma_busy"] = counters["mfma_busy"]
+        roofline["clock_ghz"] = counters["clock_ghz"]
 
     extras = None if args.no_extras else extra_kernels(torch, dev, ops, lin, q, k_, v, copy_gbs)
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds)
@@ -341,6 +348,18 @@ def copy_bandwidth(torch, dev) -> float:
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
+MFMA_FILE = os.path.join(ROOT, "profiles", "mfma_counters.json")
+
+
+def measured_mfma(kernel: str):
+    """MFMA busy fraction and clock of ``kernel`` at this workload, from the
+    committed rocprofv3 --pmc passes (SQ_VALU_MFMA_BUSY_CYCLES over the SIMD
+    cycles; GRBM_GUI_ACTIVE over the kernel time), or None when not committed."""
+    try:
+        with open(MFMA_FILE) as f:
+            return json.load(f).get(kernel)
+    except (OSError, ValueError):
+        return None
 
 
 def measured_traffic(kernel: str):

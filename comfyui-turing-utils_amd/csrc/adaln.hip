@@ -72,11 +72,15 @@ __device__ __forceinline__ typename Elem<kT>::type from_f32(float v) {
 // passes; exact power-of-two scaling carries that to |a| in [2^-96, 2^100]
 // (no subnormal step), and anything else -- zero, tiny, huge, inf, NaN --
 // takes the IEEE division.
+// The range test is one wave-wide vote, so the common case costs no
+// exec-mask juggling; lanes out of range then take the division.
 __device__ __forceinline__ float div_rn(float a, float b, float y) {
     const uint32_t e = (__float_as_uint(a) >> 23) & 0xffu;
-    if (__builtin_expect(e - 31u >= 197u, 0)) return a / b;
+    const bool out = e - 31u >= 197u;
     const float q = a * y;
-    return __builtin_fmaf(__builtin_fmaf(-q, b, a), y, q);
+    float r = __builtin_fmaf(__builtin_fmaf(-q, b, a), y, q);
+    if (__builtin_expect(__builtin_amdgcn_ballot_w64(out) != 0, 0)) r = out ? a / b : r;
+    return r;
 }
 
 struct Welford {
@@ -115,8 +119,9 @@ struct Recips {
 
 // One workgroup per token row.  kPer > 0: the thread's columns t + 256 i
 // (i < kPer) and their modulation values stay in registers; kUniform: every
-// thread holds exactly hidden / 256 of them and all counts are known.
-template <int kT, int kPer, bool kUniform, bool kAffine>
+// thread holds exactly hidden / 256 of them and all counts are known (and
+// kExact: that number is kPer itself, so no column needs a bounds test).
+template <int kT, int kPer, bool kUniform, bool kAffine, bool kExact = false>
 __global__ __launch_bounds__(kThreads) void layer_norm_adaln_kernel(const typename Elem<kT>::type *__restrict__ x,
                                                                    const typename Elem<kT>::type *__restrict__ scale,
                                                                    const typename Elem<kT>::type *__restrict__ shift,
@@ -125,6 +130,7 @@ __global__ __launch_bounds__(kThreads) void layer_norm_adaln_kernel(const typena
                                                                    Recips rc) {
     typedef typename Elem<kT>::type E;
     __shared__ Welford trees[kThreads / 32];
+    __shared__ float row_stats[2];
     const int tid = threadIdx.x;
     const int64_t row = blockIdx.x;
     const int64_t b = row / len, t = row - b * len;
@@ -138,7 +144,7 @@ __global__ __launch_bounds__(kThreads) void layer_norm_adaln_kernel(const typena
     const E *sc = scale + (b * steps + mt) * hidden;
     const E *sh = shift + (b * steps + mt) * hidden;
     E *orow = out + row * hidden;
-    const int per = hidden / kThreads;  // kUniform: values per thread
+    const int per = kExact ? kPer : hidden / kThreads;  // kUniform: values per thread
 
     constexpr int kKeep = kPer > 0 ? kPer : 1;
     float v[kKeep], mod[kKeep], add[kKeep];
@@ -190,12 +196,23 @@ __global__ __launch_bounds__(kThreads) void layer_norm_adaln_kernel(const typena
         }
         if ((tid & 31) == 0) trees[tid >> 5] = w;
         __syncthreads();
-        mean = trees[0].mean;
-        float m2 = trees[0].m2;
+        // the in-order combine of the eight tree results, by the first wave
+        // only; the others take mean and variance from LDS
+        if (tid < 64) {
+            mean = trees[0].mean;
+            float m2 = trees[0].m2;
 #pragma unroll
-        for (int i = 1; i < kThreads / 32; ++i)
-            combine_known(mean, m2, trees[i].mean, trees[i].m2, static_cast<float>(i) * cnt, cnt, rc.total[i]);
-        var = div_rn(m2, static_cast<float>(hidden), rc.total[kThreads / 32 - 1]);
+            for (int i = 1; i < kThreads / 32; ++i)
+                combine_known(mean, m2, trees[i].mean, trees[i].m2, static_cast<float>(i) * cnt, cnt, rc.total[i]);
+            var = div_rn(m2, static_cast<float>(hidden), rc.total[kThreads / 32 - 1]);
+            if (tid == 0) {
+                row_stats[0] = mean;
+                row_stats[1] = var;
+            }
+        }
+        __syncthreads();
+        mean = row_stats[0];
+        var = row_stats[1];
     } else {
 #pragma unroll
         for (int off = 16; off > 0; off >>= 1) {
@@ -247,17 +264,19 @@ void launch(const void *xv, const void *scv, const void *shv, void *outv, int64_
         for (int lvl = 0; lvl < 5; ++lvl) rc.level[lvl] = 1.0f / static_cast<float>(per << (lvl + 1));
         for (int i = 1; i < kThreads / 32; ++i) rc.total[i] = 1.0f / static_cast<float>((i + 1) * 32 * per);
     }
-#define TU_LN(P, U) \
-    layer_norm_adaln_kernel<kT, P, U, kAffine><<<grid, kThreads, 0, s>>>(x, sc, sh, out, len, hidden, steps, eps, rc)
-#define TU_LN2(P) \
-    if (uniform) TU_LN(P, true); \
-    else TU_LN(P, false)
+#define TU_LN(P, U, X)                                                                       \
+    layer_norm_adaln_kernel<kT, P, U, kAffine, X><<<grid, kThreads, 0, s>>>(x, sc, sh, out, len, hidden, \
+                                                                            steps, eps, rc)
+#define TU_LN2(P)                                  \
+    if (uniform && per == P) TU_LN(P, true, true); \
+    else if (uniform) TU_LN(P, true, false);       \
+    else TU_LN(P, false, false)
     if (per <= 4) { TU_LN2(4); }
     else if (per <= 8) { TU_LN2(8); }
     else if (per <= 16) { TU_LN2(16); }
     else if (per <= 20) { TU_LN2(20); }
     else if (per <= kMaxPerThread) { TU_LN2(32); }
-    else TU_LN(0, false);
+    else TU_LN(0, false, false);
 #undef TU_LN2
 #undef TU_LN
 }

@@ -71,6 +71,35 @@ def test_offsets_bit_exact(gpu_device, offset):
         np.testing.assert_array_equal(_bits_of(out), _oracle(x, scale, shift, 1e-5))
 
 
+def test_division_edge_rows_bit_exact(gpu_device):
+    """Rows whose Welford and combine quotients leave the range where the
+    kernel's reciprocal-multiply division is exact, so the wave takes the
+    IEEE division for those lanes: all-zero rows, constant rows (every later
+    delta is 0), rows with exact zeros between normal values, tiny (1e-30)
+    and huge (1e30) values, and a row mixing all of them; widths 5120
+    (every count known) and 700 (ragged), bf16 and fp32."""
+    from comfyui_turing_utils_kernel import turing_layer_norm_adaln
+
+    for dtype in (torch.bfloat16, torch.float32):
+        for h in (5120, 700):
+            g = torch.Generator().manual_seed(h)
+            rows = [torch.zeros(h), torch.full((h,), 2.5), torch.randn(h, generator=g),
+                    torch.randn(h, generator=g) * 1e-30, torch.randn(h, generator=g) * 1e30,
+                    torch.randn(h, generator=g)]
+            rows[2][::3] = 0.0
+            mixed = rows[5]
+            mixed[::5] = 0.0
+            mixed[1::7] *= 1e-30
+            mixed[2::11] *= 1e25
+            x = torch.stack(rows).unsqueeze(0).to(dtype)
+            scale = (torch.randn(1, 1, h, generator=g) * 0.2).to(dtype)
+            shift = (torch.randn(1, 1, h, generator=g) * 0.2).to(dtype)
+            print(f"layer_norm_adaln edge rows {dtype} h={h}", flush=True)
+            out = turing_layer_norm_adaln(x.to(gpu_device), scale.to(gpu_device), shift.to(gpu_device), 1e-6)
+            torch.cuda.synchronize(gpu_device)
+            np.testing.assert_array_equal(_bits_of(out), _oracle(x, scale, shift, 1e-6))
+
+
 @pytest.mark.parametrize("case", ["x", "x/8", "x+100", "x+1000"])
 def test_reference_gate(gpu_device, case):
     """validate_wan_fusions.py:80-119: rtol 0.006 / atol 0.002 against torch

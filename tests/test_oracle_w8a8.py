@@ -1,7 +1,9 @@
 """Pins the W8A8 attention part of the CPU oracle without the GPU.
 
   * Hadamard: equals (1/sqrt D) H_D diag(s) with H_D the Sylvester matrix of
-    scipy.linalg.hadamard (fp64), preserves norms and Q.K dot products;
+    scipy.linalg.hadamard (fp64), preserves norms and Q.K dot products, and is
+    undone channel by channel by the inverse in the reference's validation
+    script, whose sign table is a second statement of s;
   * K anchor: the decision of an fp64 numpy restatement of the detector on
     inputs with a clear margin, the sampled-row formula, and the two regimes
     (a common channel offset is removed, centred keys keep -1);
@@ -50,6 +52,41 @@ def test_hadamard_is_signed_sylvester_matrix(d):
         e = np.zeros(d, np.float32)
         e[c] = 1.0
         np.testing.assert_allclose(oracle.w8a8_hadamard(e), r[:, c], atol=1e-7)
+
+
+def _inverse_rotation_of_validation_script(y: np.ndarray) -> np.ndarray:
+    """The reference validation script's inverse of the kernel rotation
+    (kernel/scripts/validate_compatible.py:613-629): in-place Sylvester
+    butterflies over spans 1, 2, 4, ..., then 1/sqrt(D), then the channel
+    signs of the script's own table (bit c of word c >> 5 clear -> -1).
+    That table is a second statement of the rotation's signs, independent of
+    the kernel source the oracle's table was taken from."""
+    words = (0x1035997B, 0x8087F5EE, 0xEE2E4E1A, 0x71132418)
+    d = y.shape[-1]
+    r = y.astype(np.float64)
+    span = 1
+    while span < d:
+        pairs = r.reshape(-1, 2, span)
+        r = np.concatenate((pairs[:, 0] + pairs[:, 1], pairs[:, 0] - pairs[:, 1]), axis=-1).reshape(d)
+        span *= 2
+    signs = np.array([1.0 if (words[c >> 5] >> (c & 31)) & 1 else -1.0 for c in range(d)])
+    return r / np.sqrt(d) * signs
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_hadamard_inverts_with_the_validation_scripts_sign_table(d):
+    # every basis vector comes back exactly where it started: a single sign
+    # bit that differs between the two tables, a flipped bit-to-sign mapping
+    # or the signs applied after the butterflies instead of before would send
+    # some e_c to -e_c or smear it over other channels
+    for c in range(d):
+        e = np.zeros(d, np.float32)
+        e[c] = 1.0
+        back = _inverse_rotation_of_validation_script(oracle.w8a8_hadamard(e))
+        np.testing.assert_allclose(back, e, atol=1e-6, err_msg=f"channel {c}")
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal(d).astype(np.float32)
+    np.testing.assert_allclose(_inverse_rotation_of_validation_script(oracle.w8a8_hadamard(x)), x, atol=1e-5)
 
 
 @pytest.mark.parametrize("d", [64, 128])

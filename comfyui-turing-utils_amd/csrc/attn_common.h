@@ -1,7 +1,6 @@
 // Device helpers shared by the two gfx950 attention kernels (Sage bf16-PV
-// and dense W8A8): wait-count immediates, cross-lane row reductions, buffer
-// resources, the workgroup barrier of the two-group schedule and the
-// biased-accumulator constants.
+// and dense W8A8): cross-lane row reductions, the workgroup barrier
+// of the two-group schedule and the biased-accumulator constants.
 #pragma once
 
 #include "tu_common.h"
@@ -11,13 +10,6 @@ namespace tu {
 typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr float kLog2e = 1.4426950408889634f;
-
-// s_waitcnt immediate that waits until at most n vector-memory operations are
-// outstanding and leaves the other counters alone (gfx9 encoding: vmcnt in
-// bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
-constexpr int vmcnt_imm(int n) { return (n & 0xf) | (0x7 << 4) | (0xf << 8) | ((n >> 4) << 14); }
-// s_waitcnt immediate: at most n LDS/scalar-memory operations outstanding.
-constexpr int lgkmcnt_imm(int n) { return 0xf | (0x7 << 4) | ((n & 0xf) << 8) | (0x3 << 14); }
 
 // Row maxima / sums across the 4 lane groups (xor 16, xor 32) with the
 // gfx950 permlane swaps: VALU only, no LDS traffic.
@@ -41,13 +33,6 @@ __device__ __forceinline__ float xsum_f32(float v) {
 }
 
 __device__ __forceinline__ int imax3(int a, int b, int c) { return max(max(a, b), c); }
-
-// Buffer resource over [base, base + bytes): raw (stride 0) dword access;
-// reads at or past `bytes` return zeros.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), static_cast<short>(0), static_cast<int>(bytes),
-                                             0x00020000);
-}
 
 // The QK^T accumulators start at kBias, the bit pattern of 1.5 * 2^23, so
 // each int32 result is the float 1.5 * 2^23 + dot exactly (|dot| <= 2^21 for

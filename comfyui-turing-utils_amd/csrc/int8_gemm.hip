@@ -23,8 +23,8 @@
 //     evict the activation and weight panels that neighbouring tiles re-read
 //     from L2 (measured: 15 % at qkv and ffn-up).
 //   * K steps of 128 bytes through a 2-stage LDS ring (2 x 64 KiB) filled by
-//     global_load_lds_dwordx4 (direct to LDS, no staging registers) one step
-//     ahead of the MFMAs.  Within a step the two 64-deep fragment sets are
+//     buffer_load_dwordx4 ... lds (direct to LDS, no staging registers) one
+//     step ahead of the MFMAs.  Within a step the two 64-deep fragment sets are
 //     double-buffered in registers: slice 1 is read from LDS while slice 0 is
 //     on the MFMAs, and slice 0 of the next step while slice 1 is.  Rows are 128 B; the 16-byte chunk index is
 //     XOR-swizzled with row bits 1..3 (applied through each lane's source
@@ -34,6 +34,8 @@
 //     range, walked in groups of 4 m-tiles for L2 reuse of the A and W panels
 //     (measured best among 2, 4, 6, 8, 16 and 32 once the output no longer
 //     pollutes L2).
+#include <type_traits>
+
 #include "tu_common.h"
 
 namespace tu {
@@ -52,6 +54,12 @@ constexpr int kWaves = 2 * kWavesM;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kFragsM = kBM / kWavesM / 16;  // 16-row activation fragments per wave
 constexpr int kGroupM = 4;
+// MFMAs of slice 0 issued before the step's barrier, covering the latency of
+// slice 1's LDS reads.
+#ifndef TU_GEMM_PRE
+#define TU_GEMM_PRE 16
+#endif
+constexpr int kPre = TU_GEMM_PRE;
 
 // LDS panel layout: 128-byte rows, the 16-byte chunk index XOR-swizzled with
 // row bits 1..3 (measured bank-conflict free for 16 lanes reading one chunk
@@ -124,9 +132,6 @@ constexpr int kStages = 2;
 constexpr int kStageBytes = 2 * kBM * kBK;  // activation panel + weight panel
 typedef __attribute__((address_space(3))) void lds_void;
 
-// s_waitcnt immediate: at most n vector-memory operations outstanding (gfx9
-// encoding: vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
-constexpr int vmcnt_imm(int n) { return (n & 0xf) | (0x7 << 4) | (0xf << 8) | ((n >> 4) << 14); }
 
 // Per-lane source offsets of the direct-to-LDS loads.  Wave w fills the 1 KiB
 // blocks w * kBlocksPerWave .. of each panel; in block b, lane l writes LDS row
@@ -154,16 +159,18 @@ __device__ __forceinline__ LoadGeom load_geom(int64_t m0, int64_t n0, int64_t m,
     return gm;
 }
 
-// Direct-to-LDS loads of one full K step (k0 + 128 <= K) into a ring stage.
-__device__ __forceinline__ void issue_step(int8_t *stage, const int8_t *a_panel, const int8_t *w_panel,
-                                           const LoadGeom &gm, int64_t k0, int wave) {
-    const int8_t *ab = a_panel + k0;
-    const int8_t *wb = w_panel + k0;
+// Direct-to-LDS loads of one full K step into a ring stage: buffer loads with
+// the lane's 32-bit offset within the panel and the panel start plus the
+// step's K offset (a_k0 / w_k0) as the scalar offset, so no 64-bit address is
+// formed per load.
+__device__ __forceinline__ void issue_step(int8_t *stage, __amdgpu_buffer_rsrc_t ars, __amdgpu_buffer_rsrc_t wrs,
+                                           const LoadGeom &gm, uint32_t a_k0, uint32_t w_k0, int wave) {
 #pragma unroll
     for (int i = 0; i < kBlocksPerWave; ++i) {
         const int block = kBlocksPerWave * wave + i;
-        __builtin_amdgcn_global_load_lds(ab + gm.a_off[i], (lds_void *)(stage + block * 1024), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds(wb + gm.w_off[i], (lds_void *)(stage + kBM * kBK + block * 1024), 16, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(ars, (lds_void *)(stage + block * 1024), 16, gm.a_off[i], a_k0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(wrs, (lds_void *)(stage + kBM * kBK + block * 1024), 16, gm.w_off[i],
+                                                 w_k0, 0, 0);
     }
 }
 
@@ -197,11 +204,18 @@ __global__ __launch_bounds__(kThreads, kWaves / 4) void int8_gemm_kernel(
 
     int tm, tn;
     tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+    // Uniform by construction; said explicitly so the panel buffer resources
+    // are formed in scalar registers.
+    tm = __builtin_amdgcn_readfirstlane(tm);
+    tn = __builtin_amdgcn_readfirstlane(tn);
     const int64_t m0 = static_cast<int64_t>(tm) * kBM;
     const int64_t n0 = static_cast<int64_t>(tn) * kBN;
-    const int8_t *a_panel = a + m0 * k;
-    const int8_t *w_panel = w + n0 * k;
     const LoadGeom gm = load_geom(m0, n0, m, n, k, wave, lane);
+    // Buffer resources over the whole operands (the host keeps m K and n K
+    // below 2^31); a panel's start goes into the scalar offset.
+    const __amdgpu_buffer_rsrc_t ars = make_rsrc(a, static_cast<uint32_t>(m * k));
+    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(w, static_cast<uint32_t>(n * k));
+    const uint32_t a_base = static_cast<uint32_t>(m0 * k), w_base = static_cast<uint32_t>(n0 * k);
 
     i32x4 acc[8][kFragsM];
 #pragma unroll
@@ -230,29 +244,67 @@ __global__ __launch_bounds__(kThreads, kWaves / 4) void int8_gemm_kernel(
             for (int j = 0; j < kFragsM; ++j)
                 acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(f.a[i], f.b[j], acc[i][j], 0, 0, 0);
     };
+    // MFMAs [b, e) of a slice in the same (i, j) order; b and e are constants
+    // at every call, so the loop unrolls to fixed accumulator registers.
+    auto mma_part = [&](const Frags &f, int b, int e) {
+#pragma unroll
+        for (int x = b; x < e; ++x)
+            acc[x / kFragsM][x % kFragsM] =
+                __builtin_amdgcn_mfma_i32_16x16x64_i8(f.a[x / kFragsM], f.b[x % kFragsM], acc[x / kFragsM][x % kFragsM], 0, 0, 0);
+    };
 
     const int full = static_cast<int>(k / kBK);
     if (full > 0) {
-        issue_step(lds[0], a_panel, w_panel, gm, 0, wave);
-        if (full > 1) issue_step(lds[1], a_panel, w_panel, gm, kBK, wave);
+        issue_step(lds[0], ars, wrs, gm, a_base, w_base, wave);
+        if (full > 1) issue_step(lds[1], ars, wrs, gm, a_base + kBK, w_base + kBK, wave);
         if (full > 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * kBlocksPerWave));
         else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
         __syncthreads();
         Frags f0, f1;
         load_frags(f0, lds[0], 0);
+        __builtin_amdgcn_s_waitcnt(lgkmcnt_imm(0));
+        // One K step:
+        //   slice 1 reads, with the first kPre MFMAs of slice 0 covering them
+        //   barrier: step s + 1 resident, every wave done reading stage s
+        //   rest of slice 0, interleaved with the loads of step s + 2
+        //   slice 1, interleaved with the reads of slice 0 of step s + 1
+        // so the MFMA pipe has work on both sides of the barrier.  Slice 0's
+        // fragments are in registers when a step starts (their reads retire
+        // at the end of the previous step), so only 12 LDS reads are ever in
+        // flight and no MFMA waits on one (with more than 15 in flight the
+        // compiler can only wait for all of them).  The loop body has no
+        // branches, which the register allocation needs: the last two steps
+        // load step full - 1 again into stages nobody reads any more, and
+        // those loads are retired after the loop, before the ring is reused.
+        constexpr int kMma = 8 * kFragsM;
 #pragma clang loop unroll(disable)
         for (int s = 0; s < full; ++s) {
-            // Slice 0 of step s on the MFMAs while slice 1 is read from LDS.
+            const uint32_t k2 = static_cast<uint32_t>(min(s + 2, full - 1) * kBK);
             load_frags(f1, lds[s & 1], 1);
-            mma(f0);
-            // Step s + 1 resident and every wave done reading stage s.
+            mma_part(f0, 0, kPre);
+            __builtin_amdgcn_sched_barrier(0);
             __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
             __syncthreads();
-            if (s + 2 < full) issue_step(lds[s & 1], a_panel, w_panel, gm, static_cast<int64_t>(s + 2) * kBK, wave);
-            // Slice 1 of step s on the MFMAs while slice 0 of step s + 1 is read.
-            if (s + 1 < full) load_frags(f0, lds[(s + 1) & 1], 0);
+            issue_step(lds[s & 1], ars, wrs, gm, a_base + k2, w_base + k2, wave);
+            mma_part(f0, kPre, kMma);
+#pragma unroll
+            for (int i = 0; i < 2 * kBlocksPerWave; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            load_frags(f0, lds[(s + 1) & 1], 0);
             mma(f1);
+#pragma unroll
+            for (int i = 0; i < 8 + kFragsM; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_waitcnt(lgkmcnt_imm(0));
+            __builtin_amdgcn_sched_barrier(0);
         }
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
     }
     if (full * kBK < k) {
         // Partial last step: register loads with zero fill past K.
@@ -441,6 +493,9 @@ int32_t check_gemm_args(const int8_t *a, const int8_t *w, const void *out, int64
                static_cast<long long>(k), static_cast<long long>(n));
     TU_REQUIRE(k < 131072, "INT8 GEMM K=%lld would overflow the int32 accumulator", static_cast<long long>(k));
     TU_REQUIRE((m + kBM - 1) / kBM * ((n + kBN - 1) / kBN) < 0x7fffffff, "INT8 GEMM grid too large");
+    TU_REQUIRE(m * k < (int64_t{1} << 31) && n * k < (int64_t{1} << 31),
+               "INT8 GEMM operands must hold fewer than 2^31 bytes (m*k=%lld n*k=%lld)",
+               static_cast<long long>(m * k), static_cast<long long>(n * k));
     TU_REQUIRE(a && w && out, "INT8 GEMM pointers must be non-null");
     TU_REQUIRE((reinterpret_cast<uintptr_t>(a) & 15) == 0 && (reinterpret_cast<uintptr_t>(w) & 15) == 0,
                "INT8 GEMM operands must be 16-byte aligned");

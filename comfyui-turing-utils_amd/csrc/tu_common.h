@@ -68,4 +68,18 @@ __device__ __forceinline__ uint32_t hw_bf16x2_bits(float a, float b) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{a, b}), bf16x2_t));
 }
 
+// s_waitcnt immediate that waits until at most n vector-memory operations are
+// outstanding and leaves the other counters alone (gfx9 encoding: vmcnt in
+// bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
+constexpr int vmcnt_imm(int n) { return (n & 0xf) | (0x7 << 4) | (0xf << 8) | ((n >> 4) << 14); }
+// s_waitcnt immediate: at most n LDS/scalar-memory operations outstanding.
+constexpr int lgkmcnt_imm(int n) { return 0xf | (0x7 << 4) | ((n & 0xf) << 8) | (0x3 << 14); }
+
+// Buffer resource over [base, base + bytes): raw (stride 0) dword access;
+// reads at or past `bytes` return zeros.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), static_cast<short>(0), static_cast<int>(bytes),
+                                             0x00020000);
+}
+
 }  // namespace tu

@@ -24,8 +24,9 @@ def _rand_i8(shape, seed):
 @pytest.mark.parametrize(
     "m,n,k",
     [(1, 8, 16), (7, 24, 48), (256, 256, 64), (300, 264, 192), (513, 520, 1040), (64, 8960, 1536), (40, 512, 13824),
-     # 1..5 and 7 K steps of 64 bytes through the four-stage ring, ragged M and N tiles
-     (257, 264, 128), (129, 8, 256), (520, 272, 320), (33, 1024, 448), (600, 512, 5120)],
+     # 1, 2 and 3 full 128-byte K steps with and without a partial last step (the
+     # main loop's last two steps reload the final step), ragged M and N tiles
+     (257, 264, 128), (129, 8, 256), (520, 272, 320), (65, 264, 384), (33, 1024, 448), (600, 512, 5120)],
 )
 def test_gemm_i32_exact(gpu_device, m, n, k):
     print(f"[gemm-i32] m={m} n={n} k={k}", flush=True)

@@ -159,18 +159,26 @@ __device__ __forceinline__ LoadGeom load_geom(int64_t m0, int64_t n0, int64_t m,
     return gm;
 }
 
+// A pointer that is the same in every lane, rebuilt from readfirstlane of
+// its two halves.
+__device__ __forceinline__ const int8_t *uniform_ptr(const int8_t *p) {
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
+    return reinterpret_cast<const int8_t *>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
 // Direct-to-LDS loads of one full K step into a ring stage: buffer loads with
-// the lane's 32-bit offset within the panel and the panel start plus the
-// step's K offset (a_k0 / w_k0) as the scalar offset, so no 64-bit address is
-// formed per load.
+// the lane's 32-bit offset within the panel and the step's K offset k0 as
+// the scalar offset, so no 64-bit address is formed per load.
 __device__ __forceinline__ void issue_step(int8_t *stage, __amdgpu_buffer_rsrc_t ars, __amdgpu_buffer_rsrc_t wrs,
-                                           const LoadGeom &gm, uint32_t a_k0, uint32_t w_k0, int wave) {
+                                           const LoadGeom &gm, uint32_t k0, int wave) {
 #pragma unroll
     for (int i = 0; i < kBlocksPerWave; ++i) {
         const int block = kBlocksPerWave * wave + i;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(ars, (lds_void *)(stage + block * 1024), 16, gm.a_off[i], a_k0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(ars, (lds_void *)(stage + block * 1024), 16, gm.a_off[i], k0, 0, 0);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(wrs, (lds_void *)(stage + kBM * kBK + block * 1024), 16, gm.w_off[i],
-                                                 w_k0, 0, 0);
+                                                 k0, 0, 0);
     }
 }
 
@@ -211,11 +219,12 @@ __global__ __launch_bounds__(kThreads, kWaves / 4) void int8_gemm_kernel(
     const int64_t m0 = static_cast<int64_t>(tm) * kBM;
     const int64_t n0 = static_cast<int64_t>(tn) * kBN;
     const LoadGeom gm = load_geom(m0, n0, m, n, k, wave, lane);
-    // Buffer resources over the whole operands (the host keeps m K and n K
-    // below 2^31); a panel's start goes into the scalar offset.
-    const __amdgpu_buffer_rsrc_t ars = make_rsrc(a, static_cast<uint32_t>(m * k));
-    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(w, static_cast<uint32_t>(n * k));
-    const uint32_t a_base = static_cast<uint32_t>(m0 * k), w_base = static_cast<uint32_t>(n0 * k);
+    // Buffer resources over the tile's two panels (256 rows of K bytes each,
+    // K < 2^17, so every offset fits in 32 bits).  The panel addresses are
+    // uniform; passing them through readfirstlane keeps the resources in
+    // scalar registers.
+    const __amdgpu_buffer_rsrc_t ars = make_rsrc(uniform_ptr(a + m0 * k), static_cast<uint32_t>(kBM * k));
+    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(uniform_ptr(w + n0 * k), static_cast<uint32_t>(kBN * k));
 
     i32x4 acc[8][kFragsM];
 #pragma unroll
@@ -255,8 +264,8 @@ __global__ __launch_bounds__(kThreads, kWaves / 4) void int8_gemm_kernel(
 
     const int full = static_cast<int>(k / kBK);
     if (full > 0) {
-        issue_step(lds[0], ars, wrs, gm, a_base, w_base, wave);
-        if (full > 1) issue_step(lds[1], ars, wrs, gm, a_base + kBK, w_base + kBK, wave);
+        issue_step(lds[0], ars, wrs, gm, 0, wave);
+        if (full > 1) issue_step(lds[1], ars, wrs, gm, kBK, wave);
         if (full > 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * kBlocksPerWave));
         else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
         __syncthreads();
@@ -285,7 +294,7 @@ __global__ __launch_bounds__(kThreads, kWaves / 4) void int8_gemm_kernel(
             __builtin_amdgcn_sched_barrier(0);
             __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
             __syncthreads();
-            issue_step(lds[s & 1], ars, wrs, gm, a_base + k2, w_base + k2, wave);
+            issue_step(lds[s & 1], ars, wrs, gm, k2, wave);
             mma_part(f0, kPre, kMma);
 #pragma unroll
             for (int i = 0; i < 2 * kBlocksPerWave; ++i) {
@@ -493,9 +502,6 @@ int32_t check_gemm_args(const int8_t *a, const int8_t *w, const void *out, int64
                static_cast<long long>(k), static_cast<long long>(n));
     TU_REQUIRE(k < 131072, "INT8 GEMM K=%lld would overflow the int32 accumulator", static_cast<long long>(k));
     TU_REQUIRE((m + kBM - 1) / kBM * ((n + kBN - 1) / kBN) < 0x7fffffff, "INT8 GEMM grid too large");
-    TU_REQUIRE(m * k < (int64_t{1} << 31) && n * k < (int64_t{1} << 31),
-               "INT8 GEMM operands must hold fewer than 2^31 bytes (m*k=%lld n*k=%lld)",
-               static_cast<long long>(m * k), static_cast<long long>(n * k));
     TU_REQUIRE(a && w && out, "INT8 GEMM pointers must be non-null");
     TU_REQUIRE((reinterpret_cast<uintptr_t>(a) & 15) == 0 && (reinterpret_cast<uintptr_t>(w) & 15) == 0,
                "INT8 GEMM operands must be 16-byte aligned");

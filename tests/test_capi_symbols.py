@@ -72,18 +72,6 @@ def test_argument_errors_are_reported_without_launching(lib):
     assert b"group" in lib.tu_last_error().lower()
 
 
-def test_gemm_operand_size_limit_is_refused_on_the_host(lib):
-    """The GEMM addresses its operands through 32-bit buffer offsets, so the
-    host refuses an activation or weight matrix of 2^31 bytes or more (here
-    2^20 x 4096) before any HIP call."""
-    rc = lib.tu_int8_gemm_i32(None, None, None, 1 << 20, 256, 4096, None)
-    assert rc != 0
-    assert b"2^31" in lib.tu_last_error()
-    rc = lib.tu_int8_gemm_i32(None, None, None, 256, 1 << 20, 4096, None)
-    assert rc != 0
-    assert b"2^31" in lib.tu_last_error()
-
-
 def test_package_import_fails_loudly_without_library(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "LIB_PATH", str(tmp_path / "missing.so"))
     monkeypatch.setattr(_lib, "_lib", None)

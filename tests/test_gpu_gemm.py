@@ -47,6 +47,26 @@ def test_gemm_i32_extremes(gpu_device):
     assert int(acc.min()) == int(acc.max()) == 16384 * k
 
 
+def test_gemm_i32_activation_past_2gib(gpu_device):
+    """An activation of more than 2^31 bytes (160000 x 13824, about 2.2 GB):
+    every operand offset the kernel forms is relative to a 256-row panel, so
+    nothing overflows 32 bits.  Rows across the whole range (first, last,
+    panel edges) are checked bit-exact against the oracle."""
+    m, n, k = 160000, 264, 13824
+    assert m * k > 2**31
+    print(f"[gemm-i32 >2GiB] m={m} n={n} k={k}", flush=True)
+    g = torch.Generator(device=gpu_device).manual_seed(11)
+    a = torch.randint(-128, 128, (m, k), generator=g, dtype=torch.int8, device=gpu_device)
+    w = _rand_i8((n, k), 12)
+    acc = torch.ops.turing_utils.int8_gemm_i32(a, w.to(gpu_device))
+    rows = torch.tensor([0, 1, 255, 256, 77777, 155391, 155392, m - 257, m - 2, m - 1])
+    a_rows = a[rows.to(gpu_device)].cpu()
+    got = acc[rows.to(gpu_device)].cpu().numpy()
+    del a, acc
+    torch.cuda.synchronize(gpu_device)
+    np.testing.assert_array_equal(got, oracle.int8_gemm_i32(a_rows.numpy(), w.numpy()))
+
+
 @pytest.mark.parametrize("with_bias", [True, False])
 @pytest.mark.parametrize("m,n,k", [(300, 264, 192), (96, 8960, 1536)])
 def test_int8_linear_epilogue_exact(gpu_device, m, n, k, with_bias):

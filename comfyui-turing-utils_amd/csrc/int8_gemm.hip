@@ -24,12 +24,12 @@
 //     from L2 (measured: 15 % at qkv and ffn-up).
 //   * K steps of 128 bytes through a 2-stage LDS ring (2 x 64 KiB) filled by
 //     buffer_load_dwordx4 ... lds (direct to LDS, no staging registers) one
-//     step ahead of the MFMAs.  Within a step the two 64-deep fragment sets are
-//     double-buffered in registers: slice 1 is read from LDS while slice 0 is
-//     on the MFMAs, and slice 0 of the next step while slice 1 is.  Rows are 128 B; the 16-byte chunk index is
-//     XOR-swizzled with row bits 1..3 (applied through each lane's source
-//     address).  A partial last K step (K % 128 != 0) is staged through
-//     registers with zero fill.
+//     step ahead of the MFMAs.  Within a step the two 64-deep fragment sets
+//     are double-buffered in registers: slice 1 is read from LDS while slice
+//     0 is on the MFMAs, and slice 0 of the next step while slice 1 is.  Rows
+//     are 128 B; the 16-byte chunk index is XOR-swizzled with row bits 1..3
+//     (applied through each lane's source address).  A partial last K step
+//     (K % 128 != 0) is staged through registers with zero fill.
 //   * Tiles are renumbered so each XCD (workgroup id mod 8) owns a contiguous
 //     range, walked in groups of 4 m-tiles for L2 reuse of the A and W panels
 //     (measured best among 2, 4, 6, 8, 16 and 32 once the output no longer
@@ -131,7 +131,6 @@ __device__ __forceinline__ void tile_coords(int bid, int tiles_m, int tiles_n, i
 constexpr int kStages = 2;
 constexpr int kStageBytes = 2 * kBM * kBK;  // activation panel + weight panel
 typedef __attribute__((address_space(3))) void lds_void;
-
 
 // Per-lane source offsets of the direct-to-LDS loads.  Wave w fills the 1 KiB
 // blocks w * kBlocksPerWave .. of each panel; in block b, lane l writes LDS row

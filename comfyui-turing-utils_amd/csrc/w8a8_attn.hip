@@ -15,7 +15,7 @@
 //
 // MI355X mapping (shared with the Sage kernel: 8 wave64, two groups of 4
 // whose MFMA and softmax clusters interleave, 32 query rows a wave, a
-// 5-stage LDS ring filled by buffer_load ... lds from group 0):
+// 4-stage LDS ring filled by buffer_load ... lds from group 0):
 //   * S^T = K Q^T on v_mfma_i32_16x16x64_i8 as in the Sage kernel, with the
 //     K rows permuted so that lane group g holds the 16 consecutive keys
 //     16 g .. 16 g + 15 of each query: exactly one 16-byte B operand of the
@@ -48,7 +48,7 @@ constexpr int kBKey = 64;
 constexpr int kKTileBytes = kBKey * kD;   // int8 K tile, 8 KiB
 constexpr int kVTileBytes = kD * kBKey;   // int8 V^T tile, 8 KiB
 constexpr int kStageBytes = kKTileBytes + kVTileBytes;
-constexpr int kStages = 5;
+constexpr int kStages = 4;
 constexpr int kAhead = kStages - 1;
 constexpr int kLoadsPerTile = 4;          // per group-0 wave: 2 K + 2 V^T 1 KiB blocks
 constexpr float kU8Offset = 7.9943534f;   // log2(255): the largest p is 255

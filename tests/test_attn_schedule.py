@@ -29,7 +29,7 @@ import itertools
 
 import pytest
 
-K_STAGES = 5
+K_STAGES = 4
 K_AHEAD = K_STAGES - 1
 # per kernel: 1 KiB blocks a group-0 wave loads per tile (Sage 2 K + 4 V^T,
 # W8A8 2 K + 2 V^T), and whether it issues them after the softmax

@@ -23,8 +23,9 @@
 //   * O^T = V^T P on v_mfma_i32_16x16x64_i8 (one MFMA covers the whole
 //     64-key tile).  CDNA4 multiplies signed x signed only, so P goes in as
 //     P - 128 and the 128 * sum_k v8 it drops is added back from per-tile
-//     prefix sums of the V codes.  p + (1.5 * 2^23 - 128) rounds p to an
-//     integer half-to-even and leaves P - 128 in the low byte.
+//     prefix sums of the V codes.  v_cvt_pk_u8_f32 rounds p to an integer
+//     half-to-even into its byte of the packed operand, and an XOR with
+//     0x80 per byte turns P into P - 128.
 //   * The PV products stay in int32 accumulators across tiles and are
 //     converted to fp32 only when the row maximum moves (the reference
 //     rescales O every tile; a rescale by 2^0 is exact) or every 512 tiles
@@ -52,7 +53,6 @@ constexpr int kStages = 4;
 constexpr int kAhead = kStages - 1;
 constexpr int kLoadsPerTile = 4;          // per group-0 wave: 2 K + 2 V^T 1 KiB blocks
 constexpr float kU8Offset = 7.9943534f;   // log2(255): the largest p is 255
-constexpr float kP8Magic = 12582784.0f;   // 1.5 * 2^23 - 128
 constexpr int kFlushTiles = 512;          // int32 headroom of the PV accumulators
 // Biased bit pattern of the masked raw score -5e6: the float kBiasF - 5e6.
 constexpr float kMaskedF = kBiasF - 5000000.0f;
@@ -219,7 +219,7 @@ __device__ __forceinline__ void softmax_tile8(const i32x4 (&s)[4][kQT], const fl
             float lsum = 0.0f;
 #pragma unroll
             for (int kt = 0; kt < 4; ++kt) {
-                uint32_t u[4];
+                uint32_t packed = 0;
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const float v = __int_as_float(s[kt][qt][r]);
@@ -227,11 +227,13 @@ __device__ __forceinline__ void softmax_tile8(const i32x4 (&s)[4][kQT], const fl
                                                                : __builtin_fmaf(v, f[qt], c[qt]);
                     const float p = __builtin_amdgcn_exp2f(x);
                     lsum += p;
-                    u[r] = __float_as_uint(p + kP8Magic);
+                    // byte r = rint(p): v_cvt_pk_u8_f32 rounds half to even
+                    // (checked against rint on every float in [0, 256]); p
+                    // <= 255 since the base sits log2(255) above the maximum
+                    packed = __builtin_amdgcn_cvt_pk_u8_f32(p, r, packed);
                 }
-                const uint32_t lo = __builtin_amdgcn_perm(u[1], u[0], 0x0c0c0400u);
-                const uint32_t hi = __builtin_amdgcn_perm(u[3], u[2], 0x0c0c0400u);
-                p8[qt][kt] = static_cast<int32_t>(__builtin_amdgcn_perm(hi, lo, 0x05040100u));
+                // P - 128 as signed bytes for the signed-only MFMA
+                p8[qt][kt] = static_cast<int32_t>(packed ^ 0x80808080u);
             }
             st.l[qt] += lsum;
         }

@@ -70,6 +70,14 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
          _f32, _i32, _c_void_p],
     ),
+    "tu_sage_attn_fwd_split": (
+        _i32,
+        [_c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p, _i64, _c_void_p, _i64, _c_void_p,
+         _i64, _i64, _i64, _i64, _i64, _i64,
+         _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+         _f32, _i32, _c_void_p, _i64, _c_void_p],
+    ),
+    "tu_sage_attn_kv_splits": (_i32, [_i64, _i64, _i64, _i64, _i32, _i32]),
     "tu_qk_rms_rope_int8": (
         _i32,
         [_c_void_p, _c_void_p, _i32, _i64, _i64, _i64, _i64, _i64, _i64,
@@ -110,7 +118,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
 }
 
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

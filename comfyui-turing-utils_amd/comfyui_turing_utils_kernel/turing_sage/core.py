@@ -201,8 +201,14 @@ def attention_from_vt(
     blkq: int = 128,
     blkk: int = 128,
     output: Optional[torch.Tensor] = None,
+    kv_splits: Optional[int] = None,
 ) -> torch.Tensor:
-    """Attention kernel only: quantized Q/K and V^T from ``value_transpose``."""
+    """Attention kernel only: quantized Q/K and V^T from ``value_transpose``.
+
+    ``kv_splits`` (this package only): key ranges computed by separate
+    workgroups and merged, for grids that fill the GPU badly; None lets
+    ``tu_sage_attn_kv_splits`` choose from the device's compute units, 1
+    never splits.  Non-causal only."""
     batch, hq, hkv, lq, lk = _check_qk(q_int8, q_scale, k_int8, k_scale, tensor_layout, blkq, blkk)
     width = q_int8.size(-1)
     lpad = (lk + 63) // 64 * 64
@@ -221,15 +227,48 @@ def attention_from_vt(
     _, _, osb, osh, osl = _layout_dims(output, tensor_layout)
     q_scale = q_scale.contiguous()
     k_scale = k_scale.contiguous()
+    if kv_splits is None:
+        splits = int(_lib.load().tu_sage_attn_kv_splits(batch, hq, lq, lk, int(bool(is_causal)),
+                                                        _compute_units(q_int8.device)))
+    else:
+        splits = int(kv_splits)
+        if splits < 1 or (is_causal and splits > 1):
+            raise ValueError("kv_splits must be >= 1, and 1 for causal attention")
     with torch.cuda.device(q_int8.device):
-        _lib.call(
-            "tu_sage_attn_fwd",
-            q_int8.data_ptr(), q_scale.data_ptr(), blkq, k_int8.data_ptr(), k_scale.data_ptr(), blkk,
-            value_t.data_ptr(), lpad, output.data_ptr(), batch, hq, hkv, lq, lk, width,
-            qsb, qsh, qsl, ksb, ksh, ksl, osb, osh, osl,
-            scale, int(bool(is_causal)), _lib.stream_of(q_int8.device),
-        )
+        if splits > 1:
+            # key ranges merged by a second kernel: fp32 partial O plus
+            # (exponent base, row sum) per row and range
+            tiles = (lk + 63) // 64
+            per = (tiles + splits - 1) // splits
+            used = (tiles + per - 1) // per
+            partial = torch.empty(used * batch * hq * lq * (width + 2), dtype=torch.float32, device=q_int8.device)
+            _lib.call(
+                "tu_sage_attn_fwd_split",
+                q_int8.data_ptr(), q_scale.data_ptr(), blkq, k_int8.data_ptr(), k_scale.data_ptr(), blkk,
+                value_t.data_ptr(), lpad, output.data_ptr(), batch, hq, hkv, lq, lk, width,
+                qsb, qsh, qsl, ksb, ksh, ksl, osb, osh, osl,
+                scale, splits, partial.data_ptr(), partial.numel() * 4, _lib.stream_of(q_int8.device),
+            )
+        else:
+            _lib.call(
+                "tu_sage_attn_fwd",
+                q_int8.data_ptr(), q_scale.data_ptr(), blkq, k_int8.data_ptr(), k_scale.data_ptr(), blkk,
+                value_t.data_ptr(), lpad, output.data_ptr(), batch, hq, hkv, lq, lk, width,
+                qsb, qsh, qsl, ksb, ksh, ksl, osb, osh, osl,
+                scale, int(bool(is_causal)), _lib.stream_of(q_int8.device),
+            )
     return output
+
+
+_CU_COUNT: dict = {}
+
+
+def _compute_units(device: torch.device) -> int:
+    """Compute units of ``device`` (cached): the round size of the attention grid."""
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    if index not in _CU_COUNT:
+        _CU_COUNT[index] = int(torch.cuda.get_device_properties(index).multi_processor_count)
+    return _CU_COUNT[index]
 
 
 def sageattn_prequantized(

@@ -392,12 +392,17 @@ __device__ __forceinline__ void mfma_cluster(const int8_t *kst, const int8_t *vs
 constexpr int kStages = 4;
 constexpr int kAhead = kStages - 1;
 
-template <int D, bool kCausal>
+// kSplit: the workgroup covers key tiles [blockIdx.z * split_tiles, + split_tiles)
+// of a non-causal attention and writes its unnormalized O with the row's
+// exponent base and row sum to `part` for sage_combine_kernel.
+template <int D, bool kCausal, bool kSplit = false>
 __global__ __launch_bounds__(kThreads, 1) void sage_attn_kernel(
     const int8_t *__restrict__ q8, const float *__restrict__ q_scale, int blkq, const int8_t *__restrict__ k8,
     const float *__restrict__ k_scale, int kscale_shift, const uint16_t *__restrict__ vt, uint16_t *__restrict__ o,
     int hq, int groups, int64_t lq, int64_t lk, int64_t lpad, int64_t q_sb, int64_t q_sh, int64_t q_sl,
-    int64_t k_sb, int64_t k_sh, int64_t k_sl, int64_t o_sb, int64_t o_sh, int64_t o_sl, float sm_log2) {
+    int64_t k_sb, int64_t k_sh, int64_t k_sl, int64_t o_sb, int64_t o_sh, int64_t o_sl, float sm_log2,
+    int split_tiles, float *__restrict__ part) {
+    static_assert(!(kSplit && kCausal), "key splits are for non-causal attention");
     constexpr int kSl = Geo<D>::kKSlices;
     constexpr int kLoadsPerTile = Geo<D>::kLoadsPerTile;
     __shared__ __align__(1024) int8_t lds[kStages][Geo<D>::kStageBytes];
@@ -425,14 +430,17 @@ __global__ __launch_bounds__(kThreads, 1) void sage_attn_kernel(
 
     int64_t key_end = lk;
     if constexpr (kCausal) key_end = min(lk, qblock0 + kBQ);
-    const int tiles = static_cast<int>((key_end + kBKey - 1) / kBKey);
+    // first key tile of this workgroup's key range (0 unless split)
+    const int tile_base = kSplit ? static_cast<int>(blockIdx.z) * split_tiles : 0;
+    int tiles = static_cast<int>((key_end + kBKey - 1) / kBKey);
+    if constexpr (kSplit) tiles = min(split_tiles, tiles - tile_base);
     // Tiles this wave computes: all of them, or up to its last query's
     // diagonal when causal.  Later tiles only keep the barrier count.
     int my_tiles = tiles;
     if constexpr (kCausal)
         my_tiles = static_cast<int>(min<int64_t>(tiles, max<int64_t>(1, (min(q0 + kWaveQ, lq) + kBKey - 1) / kBKey)));
     // Tiles at or past this one need the Lk-tail or causal mask.
-    int64_t mask_from = lk / kBKey;
+    int64_t mask_from = lk / kBKey - tile_base;
     if constexpr (kCausal) mask_from = min(mask_from, q0 / kBKey);
     const int first_masked = static_cast<int>(min<int64_t>(tiles, mask_from));
 
@@ -440,7 +448,7 @@ __global__ __launch_bounds__(kThreads, 1) void sage_attn_kernel(
     const __amdgpu_buffer_rsrc_t krs = make_rsrc(kp, static_cast<uint32_t>(lk * k_sl));
     const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vtp, static_cast<uint32_t>(D * lpad * 2));
     const uint32_t k_sl32 = static_cast<uint32_t>(k_sl);
-    auto tile_key0 = [&](int it) { return static_cast<uint32_t>(min(it, tiles - 1) * kBKey); };
+    auto tile_key0 = [&](int it) { return static_cast<uint32_t>((tile_base + min(it, tiles - 1)) * kBKey); };
 
     i32x4 qf[kQT][kSl];
     float qsc[kQT];
@@ -474,12 +482,12 @@ __global__ __launch_bounds__(kThreads, 1) void sage_attn_kernel(
     // softmax of tile it (it < my_tiles) into pb; mask_tag false promises
     // it < first_masked.
     auto softmax = [&](int it, auto mask_tag) {
-        const float kscale = ks_row[it >> kscale_shift];
+        const float kscale = ks_row[(tile_base + it) >> kscale_shift];
         float f[kQT];
 #pragma unroll
         for (int qt = 0; qt < kQT; ++qt) f[qt] = qsc[qt] * kscale;
         if (decltype(mask_tag)::value && it >= first_masked) {
-            const int64_t key0 = static_cast<int64_t>(it) * kBKey;
+            const int64_t key0 = static_cast<int64_t>(tile_base + it) * kBKey;
             const int key_lim = static_cast<int>(min(lk - key0, static_cast<int64_t>(kBKey)));
             const int q_rel =
                 static_cast<int>(max(min(q0 - key0, static_cast<int64_t>(kBKey)), static_cast<int64_t>(-kBQ)));
@@ -540,6 +548,24 @@ __global__ __launch_bounds__(kThreads, 1) void sage_attn_kernel(
     __builtin_amdgcn_s_waitcnt(0);
 
     // acc_o[ds][qt][r] = O[q0 + 16 qt + lc][16 ds + 4 g + r]; acc_l[qt][*] = l.
+    if constexpr (kSplit) {
+        // unnormalized O of this key range, then (m_used, l) per row:
+        // part = [splits][B * H][lq][D] fp32, followed by [splits][B * H][lq][2]
+        const int64_t rows = static_cast<int64_t>(gridDim.y) * lq;
+        const int64_t row0 = (static_cast<int64_t>(blockIdx.z) * gridDim.y + bh) * lq;
+        float *po = part + row0 * D;
+        float *pml = part + static_cast<int64_t>(gridDim.z) * rows * D + row0 * 2;
+#pragma unroll
+        for (int qt = 0; qt < kQT; ++qt) {
+            const int64_t qi = q0 + 16 * qt + lc;
+            if (qi >= lq) continue;
+#pragma unroll
+            for (int ds = 0; ds < Geo<D>::kDS; ++ds)
+                *reinterpret_cast<f32x4 *>(po + qi * D + 16 * ds + 4 * g) = st.acc_o[ds][qt];
+            if (g == 0) *reinterpret_cast<f32x2 *>(pml + qi * 2) = f32x2{st.m_used[qt], st.acc_l[qt][0]};
+        }
+        return;
+    }
     uint16_t *op = o + b * o_sb + h * o_sh;
 #pragma unroll
     for (int qt = 0; qt < kQT; ++qt) {
@@ -596,6 +622,46 @@ __global__ __launch_bounds__(256) void v_prep_kernel(const uint16_t *__restrict_
     }
 }
 
+// Merges the key-range partials of sage_attn_kernel<D, false, true>: per
+// row, M = max_s m_s, w_s = 2^(m_s - M), out = sum_s w_s O_s / sum_s w_s l_s
+// rounded to bf16.  D / 8 threads per row, 8 channels each.
+template <int D>
+__global__ __launch_bounds__(256) void sage_combine_kernel(const float *__restrict__ part, int splits, int hq,
+                                                           int64_t bh_rows, int64_t lq, uint16_t *__restrict__ o,
+                                                           int64_t o_sb, int64_t o_sh, int64_t o_sl) {
+    constexpr int kTpr = D / 8;  // threads per row
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * (256 / kTpr) + threadIdx.x / kTpr;
+    const int d0 = (threadIdx.x % kTpr) * 8;
+    const int64_t rows = bh_rows * lq;
+    if (row >= rows) return;
+    const float *ml = part + static_cast<int64_t>(splits) * rows * D;
+    float m = -INFINITY;
+    for (int sp = 0; sp < splits; ++sp) m = fmaxf(m, ml[(sp * rows + row) * 2]);
+    float l = 0.0f, acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    for (int sp = 0; sp < splits; ++sp) {
+        const float ms = ml[(sp * rows + row) * 2];
+        const float w = ms == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ms - m);
+        l = __builtin_fmaf(w, ml[(sp * rows + row) * 2 + 1], l);
+        const f32x4 *src = reinterpret_cast<const f32x4 *>(part + (sp * rows + row) * D + d0);
+        const f32x4 a = src[0], c = src[1];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            acc[e] = __builtin_fmaf(w, a[e], acc[e]);
+            acc[4 + e] = __builtin_fmaf(w, c[e], acc[4 + e]);
+        }
+    }
+    const float inv = 1.0f / l;
+    const int64_t bh = row / lq, q = row - bh * lq;
+    uint16_t *dst = o + (bh / hq) * o_sb + (bh % hq) * o_sh + q * o_sl + d0;
+    u32x2 lo, hi;
+    lo.x = pack_bf16x2(acc[0] * inv, acc[1] * inv);
+    lo.y = pack_bf16x2(acc[2] * inv, acc[3] * inv);
+    hi.x = pack_bf16x2(acc[4] * inv, acc[5] * inv);
+    hi.y = pack_bf16x2(acc[6] * inv, acc[7] * inv);
+    reinterpret_cast<u32x2 *>(dst)[0] = lo;
+    reinterpret_cast<u32x2 *>(dst)[1] = hi;
+}
+
 }  // namespace
 }  // namespace tu
 
@@ -618,13 +684,16 @@ extern "C" int32_t tu_sage_v_prep(const void *v_bf16, int64_t batch, int64_t hea
     return check_launch("tu_sage_v_prep");
 }
 
-extern "C" int32_t tu_sage_attn_fwd(const int8_t *q8, const float *q_scale, int64_t blkq, const int8_t *k8,
-                                    const float *k_scale, int64_t blkk, const void *vt_bf16, int64_t lpad,
-                                    void *o_bf16, int64_t batch, int64_t hq, int64_t hkv, int64_t lq, int64_t lk,
-                                    int64_t dim, int64_t q_sb, int64_t q_sh, int64_t q_sl, int64_t k_sb,
-                                    int64_t k_sh, int64_t k_sl, int64_t o_sb, int64_t o_sh, int64_t o_sl,
-                                    float sm_scale, int32_t causal, void *stream) {
-    using namespace tu;
+namespace tu {
+namespace {
+
+// Argument checks shared by the attention entry points (all on the host,
+// before any HIP call).
+int32_t check_attn_args(const int8_t *q8, const float *q_scale, int64_t blkq, const int8_t *k8, const float *k_scale,
+                        int64_t blkk, const void *vt_bf16, int64_t lpad, void *o_bf16, int64_t batch, int64_t hq,
+                        int64_t hkv, int64_t lq, int64_t lk, int64_t dim, int64_t q_sb, int64_t q_sh, int64_t q_sl,
+                        int64_t k_sb, int64_t k_sh, int64_t k_sl, int64_t o_sb, int64_t o_sh, int64_t o_sl,
+                        float sm_scale) {
     TU_REQUIRE(dim == 64 || dim == 128, "Sage attention kernel requires head_dim 64 or 128, got %lld",
                static_cast<long long>(dim));
     TU_REQUIRE(batch > 0 && hq > 0 && hkv > 0 && hq % hkv == 0, "Sage attention: hq must be a positive multiple of hkv");
@@ -644,7 +713,22 @@ extern "C" int32_t tu_sage_attn_fwd(const int8_t *q8, const float *q_scale, int6
     TU_REQUIRE((reinterpret_cast<uintptr_t>(vt_bf16) & 15) == 0 && o_sl % 4 == 0 && o_sh % 4 == 0 && o_sb % 4 == 0 &&
                    (reinterpret_cast<uintptr_t>(o_bf16) & 7) == 0,
                "Sage attention V^T/O must be aligned");
-    if (require_gfx950()) return -1;
+    return require_gfx950();
+}
+
+}  // namespace
+}  // namespace tu
+
+extern "C" int32_t tu_sage_attn_fwd(const int8_t *q8, const float *q_scale, int64_t blkq, const int8_t *k8,
+                                    const float *k_scale, int64_t blkk, const void *vt_bf16, int64_t lpad,
+                                    void *o_bf16, int64_t batch, int64_t hq, int64_t hkv, int64_t lq, int64_t lk,
+                                    int64_t dim, int64_t q_sb, int64_t q_sh, int64_t q_sl, int64_t k_sb,
+                                    int64_t k_sh, int64_t k_sl, int64_t o_sb, int64_t o_sh, int64_t o_sl,
+                                    float sm_scale, int32_t causal, void *stream) {
+    using namespace tu;
+    if (check_attn_args(q8, q_scale, blkq, k8, k_scale, blkk, vt_bf16, lpad, o_bf16, batch, hq, hkv, lq, lk, dim, q_sb,
+                        q_sh, q_sl, k_sb, k_sh, k_sl, o_sb, o_sh, o_sl, sm_scale))
+        return -1;
     const dim3 grid(static_cast<unsigned>((lq + kBQ - 1) / kBQ), static_cast<unsigned>(batch * hq));
     const float sm_log2 = sm_scale * kLog2e;
     hipStream_t s = static_cast<hipStream_t>(stream);
@@ -654,7 +738,7 @@ extern "C" int32_t tu_sage_attn_fwd(const int8_t *q8, const float *q_scale, int6
 #define TU_ATTN_ARGS                                                                                             \
     q8, q_scale, static_cast<int>(blkq), k8, k_scale, kscale_shift, static_cast<const uint16_t *>(vt_bf16),      \
         static_cast<uint16_t *>(o_bf16), static_cast<int>(hq), groups, lq, lk, lpad, q_sb, q_sh, q_sl, k_sb, k_sh,  \
-        k_sl, o_sb, o_sh, o_sl, sm_log2
+        k_sl, o_sb, o_sh, o_sl, sm_log2, 0, nullptr
     if (dim == 128) {
         if (causal) sage_attn_kernel<128, true><<<grid, kThreads, 0, s>>>(TU_ATTN_ARGS);
         else sage_attn_kernel<128, false><<<grid, kThreads, 0, s>>>(TU_ATTN_ARGS);
@@ -664,4 +748,79 @@ extern "C" int32_t tu_sage_attn_fwd(const int8_t *q8, const float *q_scale, int6
     }
 #undef TU_ATTN_ARGS
     return check_launch("tu_sage_attn_fwd");
+}
+
+// Key splits for a grid that fills the GPU badly: a workgroup's time is about
+// its key tiles plus a fixed ~4 tiles of prologue and epilogue, and the
+// workgroups run in rounds of `cus`; a split also pays ~2 tiles for the
+// partial write and the combine.  Splits keep at least 16 key tiles each.
+extern "C" int32_t tu_sage_attn_kv_splits(int64_t batch, int64_t hq, int64_t lq, int64_t lk, int32_t causal,
+                                          int32_t cus) {
+    using namespace tu;
+    if (causal || batch <= 0 || hq <= 0 || lq <= 0 || lk <= 0 || cus <= 0) return 1;
+    const int64_t wgs = (lq + kBQ - 1) / kBQ * batch * hq;
+    const int64_t tiles = (lk + kBKey - 1) / kBKey;
+    int32_t best = 1;
+    double best_cost = 0.0;
+    for (int32_t sp = 1; sp <= 8; ++sp) {
+        const int64_t per = (tiles + sp - 1) / sp;
+        if (sp > 1 && (per < 16 || (tiles + per - 1) / per != sp)) continue;
+        const double cost = static_cast<double>((sp * wgs + cus - 1) / cus) * (per + 4 + (sp > 1 ? 2 : 0));
+        if (sp == 1 || cost < best_cost) {
+            best = sp;
+            best_cost = cost;
+        }
+    }
+    return best;
+}
+
+extern "C" int32_t tu_sage_attn_fwd_split(const int8_t *q8, const float *q_scale, int64_t blkq, const int8_t *k8,
+                                          const float *k_scale, int64_t blkk, const void *vt_bf16, int64_t lpad,
+                                          void *o_bf16, int64_t batch, int64_t hq, int64_t hkv, int64_t lq,
+                                          int64_t lk, int64_t dim, int64_t q_sb, int64_t q_sh, int64_t q_sl,
+                                          int64_t k_sb, int64_t k_sh, int64_t k_sl, int64_t o_sb, int64_t o_sh,
+                                          int64_t o_sl, float sm_scale, int32_t kv_splits, void *partial,
+                                          int64_t partial_bytes, void *stream) {
+    using namespace tu;
+    const int64_t tiles = (lk + kBKey - 1) / kBKey;
+    TU_REQUIRE(kv_splits >= 1 && kv_splits <= tiles, "Sage attention: kv_splits must be in [1, key tiles], got %d",
+               kv_splits);
+    if (kv_splits == 1)
+        return tu_sage_attn_fwd(q8, q_scale, blkq, k8, k_scale, blkk, vt_bf16, lpad, o_bf16, batch, hq, hkv, lq, lk,
+                                dim, q_sb, q_sh, q_sl, k_sb, k_sh, k_sl, o_sb, o_sh, o_sl, sm_scale, 0, stream);
+    // every split non-empty: split_tiles = ceil(tiles / kv_splits), and the
+    // number of splits that covers
+    const int64_t split_tiles = (tiles + kv_splits - 1) / kv_splits;
+    const int64_t splits = (tiles + split_tiles - 1) / split_tiles;
+    const int64_t need = splits * batch * hq * lq * (dim + 2) * static_cast<int64_t>(sizeof(float));
+    TU_REQUIRE(partial && (reinterpret_cast<uintptr_t>(partial) & 15) == 0 && partial_bytes >= need,
+               "Sage attention split workspace must be 16-byte aligned and hold %lld bytes",
+               static_cast<long long>(need));
+    if (check_attn_args(q8, q_scale, blkq, k8, k_scale, blkk, vt_bf16, lpad, o_bf16, batch, hq, hkv, lq, lk, dim, q_sb,
+                        q_sh, q_sl, k_sb, k_sh, k_sl, o_sb, o_sh, o_sl, sm_scale))
+        return -1;
+    const dim3 grid(static_cast<unsigned>((lq + kBQ - 1) / kBQ), static_cast<unsigned>(batch * hq),
+                    static_cast<unsigned>(splits));
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    int kscale_shift = 0;
+    while ((kBKey << kscale_shift) < blkk) ++kscale_shift;
+    float *part = static_cast<float *>(partial);
+#define TU_SPLIT_ARGS                                                                                            \
+    q8, q_scale, static_cast<int>(blkq), k8, k_scale, kscale_shift, static_cast<const uint16_t *>(vt_bf16),      \
+        static_cast<uint16_t *>(o_bf16), static_cast<int>(hq), static_cast<int>(hq / hkv), lq, lk, lpad, q_sb,    \
+        q_sh, q_sl, k_sb, k_sh, k_sl, o_sb, o_sh, o_sl, sm_scale * kLog2e, static_cast<int>(split_tiles), part
+    const int64_t rows = batch * hq * lq;
+    if (dim == 128) {
+        sage_attn_kernel<128, false, true><<<grid, kThreads, 0, s>>>(TU_SPLIT_ARGS);
+        sage_combine_kernel<128><<<static_cast<unsigned>((rows + 15) / 16), 256, 0, s>>>(
+            part, static_cast<int>(splits), static_cast<int>(hq), batch * hq, lq, static_cast<uint16_t *>(o_bf16),
+            o_sb, o_sh, o_sl);
+    } else {
+        sage_attn_kernel<64, false, true><<<grid, kThreads, 0, s>>>(TU_SPLIT_ARGS);
+        sage_combine_kernel<64><<<static_cast<unsigned>((rows + 31) / 32), 256, 0, s>>>(
+            part, static_cast<int>(splits), static_cast<int>(hq), batch * hq, lq, static_cast<uint16_t *>(o_bf16),
+            o_sb, o_sh, o_sl);
+    }
+#undef TU_SPLIT_ARGS
+    return check_launch("tu_sage_attn_fwd_split");
 }

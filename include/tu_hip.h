@@ -199,6 +199,32 @@ int32_t tu_sage_attn_fwd(const int8_t *q8, const float *q_scale, int64_t blkq, c
                          int64_t k_sh, int64_t k_sl, int64_t o_sb, int64_t o_sh, int64_t o_sl,
                          float sm_scale, int32_t causal, void *stream);
 
+/* The same attention with the keys split into kv_splits ranges, for grids
+ * that fill the GPU badly (few heads x query blocks): each workgroup covers
+ * one query block and one key range and writes its unnormalized O, exponent
+ * base and row sum to `partial`; a second kernel merges the ranges,
+ * O = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s, and stores bf16.
+ * Non-causal only; 1 <= kv_splits <= ceil(lk / 64) (kv_splits = 1 is
+ * tu_sage_attn_fwd).  partial: fp32 workspace of at least
+ * splits * batch * hq * lq * (dim + 2) * 4 bytes, 16-byte aligned, where
+ * splits = ceil(T / ceil(T / kv_splits)) for T = ceil(lk / 64).  Results
+ * agree with tu_sage_attn_fwd to fp32 rounding of the merge and to the bf16
+ * rounding of P against each range's own exponent base.  The reference has
+ * no split form; its single kernel is qk_int_sv_f16_cuda_sm75.cu:984-1123. */
+int32_t tu_sage_attn_fwd_split(const int8_t *q8, const float *q_scale, int64_t blkq, const int8_t *k8,
+                               const float *k_scale, int64_t blkk, const void *vt_bf16, int64_t lpad,
+                               void *o_bf16, int64_t batch, int64_t hq, int64_t hkv, int64_t lq, int64_t lk,
+                               int64_t dim, int64_t q_sb, int64_t q_sh, int64_t q_sl, int64_t k_sb,
+                               int64_t k_sh, int64_t k_sl, int64_t o_sb, int64_t o_sh, int64_t o_sl,
+                               float sm_scale, int32_t kv_splits, void *partial, int64_t partial_bytes,
+                               void *stream);
+
+/* Number of key ranges tu_sage_attn_fwd_split should use on a GPU with `cus`
+ * compute units (1: do not split): workgroups run in rounds of `cus`, and
+ * each costs its key tiles plus a fixed part.  Host-only arithmetic, no HIP
+ * call; no counterpart in the reference. */
+int32_t tu_sage_attn_kv_splits(int64_t batch, int64_t hq, int64_t lq, int64_t lk, int32_t causal, int32_t cus);
+
 /* Sage attention: fused Q/K preprocessing -------------------------------- */
 
 /* RMSNorm + RoPE + per-tile INT8 of Q and K in one pass, the producer of the

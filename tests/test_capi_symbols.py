@@ -72,6 +72,26 @@ def test_argument_errors_are_reported_without_launching(lib):
     assert b"group" in lib.tu_last_error().lower()
 
 
+def test_attention_key_split_plan(lib):
+    """The split planner is host arithmetic: 256 workgroups a round, each
+    costing its key tiles plus a fixed part.  Config 2 (1.5 rounds) splits in
+    two, the bench shape (20 full rounds) and full grids do not, a grid of
+    half a round splits, causal never does, and every range keeps >= 16 key
+    tiles."""
+    plan = lambda b, h, lq, lk, causal=0, cus=256: lib.tu_sage_attn_kv_splits(b, h, lq, lk, causal, cus)  # noqa: E731
+    assert plan(1, 12, 8190, 8190) == 2
+    assert plan(1, 40, 32760, 32760) == 1
+    assert plan(1, 40, 8190, 8190) == 1
+    assert plan(2, 12, 8190, 8190) == 1
+    assert plan(1, 8, 4096, 4096) == 2
+    assert plan(1, 12, 8190, 8190, causal=1) == 1
+    assert plan(1, 1, 256, 64 * 20) == 1  # two ranges would hold 10 tiles each
+    for b, h, lq, lk in [(1, 2, 100000, 100000), (1, 3, 300, 50000), (1, 1, 256, 64 * 32)]:
+        n = plan(b, h, lq, lk)
+        tiles = (lk + 63) // 64
+        assert 1 <= n <= 8 and (n == 1 or (tiles + n - 1) // n >= 16)
+
+
 def test_package_import_fails_loudly_without_library(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "LIB_PATH", str(tmp_path / "missing.so"))
     monkeypatch.setattr(_lib, "_lib", None)

@@ -140,6 +140,43 @@ def test_attention_config2_rows(gpu_device):
     require_attention_correctness(res, **GATE)
 
 
+@pytest.mark.parametrize("b,h,hkv,lq,lk,d,blkq,blkk,splits", [
+    (1, 12, 12, 8190, 8190, 128, 128, 128, 2),   # config 2: the split the planner picks
+    (1, 4, 4, 700, 1000, 128, 128, 128, 3),      # ragged key tail in the last range
+    (2, 8, 2, 300, 2049, 128, 16, 64, 5),        # GQA, blkk 64, 33 tiles in ranges of 7: a 1-key last tile
+    (1, 4, 4, 513, 1600, 128, 128, 128, 5),      # 25 tiles over 5 ranges of 5: each starts mid K-scale block
+    (1, 6, 3, 257, 777, 64, 32, 64, 4),          # head_dim 64
+    (1, 2, 2, 1, 64, 128, 128, 128, 1),          # one tile: no split
+])
+def test_attention_key_splits(gpu_device, b, h, hkv, lq, lk, d, blkq, blkk, splits):
+    """Key-split attention (tu_sage_attn_fwd_split: key ranges merged by a
+    second kernel) against the oracle within the gate, and against the
+    unsplit kernel on the same quantized inputs (the two differ only by the
+    fp32 merge and by P's bf16 rounding against each range's own base)."""
+    print(f"[attn split] b={b} h={h} hkv={hkv} lq={lq} lk={lk} d={d} blk=({blkq},{blkk}) splits={splits}", flush=True)
+    q, _, _ = inputs.attention(b, h, lq, d, 500 + lq)
+    _, k, v = inputs.attention(b, hkv, lk, d, 600 + lk)
+    state = core.prequantize_sageattn(q.to(gpu_device), k.to(gpu_device), v.to(gpu_device), "HND",
+                                      BLKQ=blkq, BLKK=blkk)
+    args = (state.query_int8, state.query_scale, state.key_int8, state.key_scale, state.value_t)
+    kw = dict(tensor_layout="HND", sm_scale=d ** -0.5, blkq=blkq, blkk=blkk)
+    split = core.attention_from_vt(*args, **kw, kv_splits=splits)
+    whole = core.attention_from_vt(*args, **kw, kv_splits=1)
+    torch.cuda.synchronize(gpu_device)
+    rows = _sample_rows(b, h, lq, 96, lq + lk + splits)
+    ref = _oracle_rows(q, k, v, rows, blkq, blkk, False, d ** -0.5)
+    got = split.float().cpu()[rows[:, 0], rows[:, 1], rows[:, 2]]
+    res = attention_error_metrics(got, torch.from_numpy(ref), candidate_name="split", reference_name="oracle")
+    print(f"  vs oracle cos={res.cosine:.6f} max_abs={res.max_abs:.3e}", flush=True)
+    require_attention_correctness(res, **GATE)
+    both = attention_error_metrics(split.float().cpu().flatten(1), whole.float().cpu().flatten(1),
+                                   candidate_name="split", reference_name="whole")
+    print(f"  vs unsplit cos={both.cosine:.7f} max_abs={both.max_abs:.3e}", flush=True)
+    assert both.cosine >= 0.99999 and both.max_abs <= 1e-2
+    if splits == 1:
+        assert torch.equal(split, whole)
+
+
 def test_attention_nhd_and_op(gpu_device):
     """NHD layout through torch.ops.turing_utils.sage_attention equals the HND facade."""
     q, k, v = inputs.attention(2, 4, 200, 128, 5)

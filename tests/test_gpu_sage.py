@@ -177,6 +177,18 @@ def test_attention_key_splits(gpu_device, b, h, hkv, lq, lk, d, blkq, blkk, spli
         assert torch.equal(split, whole)
 
 
+def test_attention_key_splits_nhd_layout(gpu_device):
+    """The merge kernel writes through the output strides: a split NHD call
+    (the planner splits B1 H8 L4096 in two) equals the HND call bit for bit."""
+    q, k, v = inputs.attention(1, 8, 4096, 128, 21)
+    qd, kd, vd = q.to(gpu_device), k.to(gpu_device), v.to(gpu_device)
+    hnd = core.sageattn(qd, kd, vd, tensor_layout="HND")
+    nhd = core.sageattn(qd.transpose(1, 2).contiguous(), kd.transpose(1, 2).contiguous(),
+                        vd.transpose(1, 2).contiguous(), tensor_layout="NHD")
+    torch.cuda.synchronize(gpu_device)
+    assert torch.equal(nhd.transpose(1, 2), hnd)
+
+
 def test_attention_nhd_and_op(gpu_device):
     """NHD layout through torch.ops.turing_utils.sage_attention equals the HND facade."""
     q, k, v = inputs.attention(2, 4, 200, 128, 5)

@@ -783,8 +783,8 @@ extern "C" int32_t tu_sage_attn_fwd_split(const int8_t *q8, const float *q_scale
                                           int64_t partial_bytes, void *stream) {
     using namespace tu;
     const int64_t tiles = (lk + kBKey - 1) / kBKey;
-    TU_REQUIRE(kv_splits >= 1 && kv_splits <= tiles, "Sage attention: kv_splits must be in [1, key tiles], got %d",
-               kv_splits);
+    TU_REQUIRE(kv_splits >= 1 && kv_splits <= tiles && kv_splits <= 256,
+               "Sage attention: kv_splits must be in [1, min(key tiles, 256)], got %d", kv_splits);
     if (kv_splits == 1)
         return tu_sage_attn_fwd(q8, q_scale, blkq, k8, k_scale, blkk, vt_bf16, lpad, o_bf16, batch, hq, hkv, lq, lk,
                                 dim, q_sb, q_sh, q_sl, k_sb, k_sh, k_sl, o_sb, o_sh, o_sl, sm_scale, 0, stream);

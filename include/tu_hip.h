@@ -204,8 +204,8 @@ int32_t tu_sage_attn_fwd(const int8_t *q8, const float *q_scale, int64_t blkq, c
  * one query block and one key range and writes its unnormalized O, exponent
  * base and row sum to `partial`; a second kernel merges the ranges,
  * O = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s, and stores bf16.
- * Non-causal only; 1 <= kv_splits <= ceil(lk / 64) (kv_splits = 1 is
- * tu_sage_attn_fwd).  partial: fp32 workspace of at least
+ * Non-causal only; 1 <= kv_splits <= min(ceil(lk / 64), 256) (kv_splits = 1
+ * is tu_sage_attn_fwd).  partial: fp32 workspace of at least
  * splits * batch * hq * lq * (dim + 2) * 4 bytes, 16-byte aligned, where
  * splits = ceil(T / ceil(T / kv_splits)) for T = ceil(lk / 64).  Results
  * agree with tu_sage_attn_fwd to fp32 rounding of the merge and to the bf16

@@ -92,6 +92,22 @@ def test_attention_key_split_plan(lib):
         assert 1 <= n <= 8 and (n == 1 or (tiles + n - 1) // n >= 16)
 
 
+def test_attention_split_arguments_are_refused_on_the_host(lib):
+    """tu_sage_attn_fwd_split checks its split count and workspace before any
+    HIP call: more ranges than key tiles, more than 256, or a missing or
+    short workspace are errors with a message."""
+    def call(kv_splits, partial, nbytes, lk=4096):
+        return lib.tu_sage_attn_fwd_split(
+            None, None, 128, None, None, 128, None, 4096, None, 1, 8, 8, 4096, lk, 128,
+            0, 0, 0, 0, 0, 0, 0, 0, 0, 0.088, kv_splits, partial, nbytes, None)
+    assert call(65, 16, 1 << 30) != 0 and b"kv_splits" in lib.tu_last_error()     # 64 key tiles
+    assert call(300, 16, 1 << 30, lk=1 << 20) != 0 and b"256" in lib.tu_last_error()
+    assert call(0, 16, 1 << 30) != 0 and b"kv_splits" in lib.tu_last_error()
+    assert call(2, None, 1 << 30) != 0 and b"workspace" in lib.tu_last_error()
+    need = 2 * 1 * 8 * 4096 * (128 + 2) * 4
+    assert call(2, 16, need - 4) != 0 and str(need).encode() in lib.tu_last_error()
+
+
 def test_package_import_fails_loudly_without_library(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "LIB_PATH", str(tmp_path / "missing.so"))
     monkeypatch.setattr(_lib, "_lib", None)

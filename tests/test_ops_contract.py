@@ -150,6 +150,20 @@ def test_w8a8_refusals():
         quant.per_warp_int8_hadamard(q, q, BLKQ=128)
 
 
+def test_key_splits_refused_for_causal_attention():
+    """attention_from_vt checks an explicit kv_splits before any kernel call:
+    it must be >= 1, and 1 for causal attention (the split kernel is
+    non-causal)."""
+    q8 = torch.zeros(1, 2, 300, 128, dtype=torch.int8)
+    k8 = torch.zeros(1, 2, 2000, 128, dtype=torch.int8)
+    qs = torch.ones(1, 2, 3)
+    ks = torch.ones(1, 2, 16)
+    vt = torch.zeros(1, 2, 128, 2048, dtype=torch.bfloat16)
+    for splits, causal in ((2, True), (0, False)):
+        with pytest.raises(ValueError, match="kv_splits"):
+            core.attention_from_vt(q8, qs, k8, ks, vt, is_causal=causal, kv_splits=splits)
+
+
 def test_preflight_refuses_cpu():
     with pytest.raises(RuntimeError, match="GPU"):
         turing_sage.preflight(torch.device("cpu"))

@@ -230,9 +230,12 @@ __device__ __forceinline__ float activate(float v, float up, std::integral_const
 // The table interleaves the signs: entry 2 (mag - kGeluLutLo) + sign.
 constexpr uint32_t kGeluLutLo = 115u << 7;  // magnitude bits of 2^-12
 constexpr int kGeluLutHalf = 15 * 128;      // exponents 2^-12 .. 2^2, 128 mantissas each
-constexpr int kGeluLut = 2 * kGeluLutHalf;  // both signs
+// Both signs, each padded to 2048 entries so that any 11-bit rel indexes
+// inside the table (the padding is never selected).
+constexpr int kGeluLut = 2 * 2048;
 
 __device__ __forceinline__ uint32_t gelu_lut_entry(int idx) {
+    if ((idx >> 1) >= kGeluLutHalf) return 0u;  // padding
     const uint32_t bits = (static_cast<uint32_t>(idx & 1) << 15) | (kGeluLutLo + static_cast<uint32_t>(idx >> 1));
     const float g = activate<false>(bf16_bits_to_f32(bits), 0.0f, std::integral_constant<int, 1>{});
     return __float_as_uint(g) >> 16;  // exact: g is a bf16 value (or the canonical NaN)
@@ -255,24 +258,52 @@ __device__ __forceinline__ uint32_t half_sign_masks(uint32_t x) {
 //   rel = mag - kGeluLutLo (wrapping: >= 0x8000 exactly for |x| < 2^-12,
 //         since mag - kGeluLutLo <= 0x7fff - kGeluLutLo < 0x8000 otherwise),
 //   rel < kGeluLutHalf: the table; rel >= 0x8000: bf16(0.5 x); else x or -0.
-// Split in two steps so that a lane's table reads can all be in flight
-// before the first is used: gelu_pair_table reads the two entries,
-// gelu_pair_select picks the results.
+// Split in steps so that a lane's table reads can all be in flight before
+// the first is used: gelu_pair_lookup reads the two entries, then
+// gelu_pair_fast (a wave whose pass has no unusual input) or
+// gelu_pair_select (any input) picks the results.
 __device__ __forceinline__ uint32_t gelu_pair_rel(uint32_t w) {
     const u16x2 rel = __builtin_bit_cast(u16x2, w & 0x7fff7fffu) - static_cast<uint16_t>(kGeluLutLo);
     return __builtin_bit_cast(uint32_t, rel);
 }
 
-__device__ __forceinline__ uint32_t gelu_pair_table(uint32_t w, uint32_t rel2, const uint16_t *lut) {
-    const u16x2 rel = __builtin_bit_cast(u16x2, rel2);
-    const u16x2 h = __builtin_bit_cast(u16x2, w);
-    const u16x2 limit = static_cast<uint16_t>(kGeluLutHalf - 1);
-    const u16x2 relc = rel < limit ? rel : limit;
-    // byte offsets of the entries: 4 relc + 2 sign (both < 2^13)
-    const uint32_t off = __builtin_bit_cast(uint32_t, static_cast<u16x2>((relc << 2) | ((h >> 14) & 2)));
+// The table entries of both halves of w, at byte offset 4 (rel mod 2048) +
+// 2 sign: one packed shift of rel, one of w and one bit-select make both
+// offsets (entries of halves outside the table range are read, in bounds,
+// and never selected).
+__device__ __forceinline__ uint32_t gelu_pair_lookup(uint32_t w, uint32_t rel2, const uint16_t *lut) {
+    const uint32_t t = __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, rel2) << static_cast<uint16_t>(2));
+    const uint32_t sg = __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, w) >> static_cast<uint16_t>(14));
+    const uint32_t off = (t & 0x1ffd1ffdu) | (sg & 0xe002e002u);
     const unsigned char *base = reinterpret_cast<const unsigned char *>(lut);
     return static_cast<uint32_t>(*reinterpret_cast<const uint16_t *>(base + (off & 0xffffu))) |
            (static_cast<uint32_t>(*reinterpret_cast<const uint16_t *>(base + (off >> 16))) << 16);
+}
+
+// GELU of a pair whose halves all have exponent fields in [2, 254] (no zero,
+// subnormal, smallest-binade, inf or NaN input; gelu_pair_unusual flags the
+// others): rel < kGeluLutHalf the table; |x| < 2^-12 (rel >= 0x8000)
+// bf16(0.5 x), which for these exponent fields is x with its exponent field
+// lowered by one, exactly; otherwise |x| >= 8, x or -0.
+__device__ __forceinline__ uint32_t gelu_pair_fast(uint32_t w, uint32_t rel2, uint32_t table) {
+    const uint32_t tiny = __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, w) - static_cast<uint16_t>(0x80));
+    const uint32_t neg = half_sign_masks(w);
+    const uint32_t big = (w & ~neg) | (0x80008000u & neg);
+    // rel + (0x8000 - kGeluLutHalf), saturating: bit 15 set iff rel >= kGeluLutHalf
+    const u16x2 past = __builtin_elementwise_add_sat(__builtin_bit_cast(u16x2, rel2),
+                                                     static_cast<u16x2>(static_cast<uint16_t>(0x8000 - kGeluLutHalf)));
+    const uint32_t outside = half_sign_masks(__builtin_bit_cast(uint32_t, past));
+    const uint32_t is_tiny = half_sign_masks(rel2);
+    const uint32_t r = (big & outside) | (table & ~outside);
+    return (tiny & is_tiny) | (r & ~is_tiny);
+}
+
+// Bit 15 of a half set iff its exponent field is 0, 1 or 255: magnitude
+// bits - 0x100 (wrapping) + 0x180, saturating.
+__device__ __forceinline__ uint32_t gelu_pair_unusual(uint32_t w) {
+    const u16x2 mag = __builtin_bit_cast(u16x2, w & 0x7fff7fffu);
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_add_sat(mag - static_cast<uint16_t>(0x100),
+                                                                      static_cast<u16x2>(static_cast<uint16_t>(0x180))));
 }
 
 __device__ __forceinline__ uint32_t gelu_pair_select(uint32_t w, uint32_t rel2, uint32_t table) {
@@ -375,21 +406,37 @@ __global__ __launch_bounds__(kGeluTable ? kTableThreads : 1024) void convrot_qua
             const bool active = chunk * kChunk + 16 * lane < k;  // whole groups are in or out (k % G == 0)
             float v[16];
             if constexpr (kGeluTable) {
-                // A half with bit 15 of (mag + 0x80) set is inf or NaN (no
-                // carry crosses halves); such lanes recompute with activate.
-                uint32_t nonfinite = 0, rel[8], table[8];
+                uint32_t unusual = 0, rel[8], table[8];
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
                     const uint32_t w = in[pass].x[j / 4][j % 4];
-                    nonfinite |= (w & 0x7fff7fffu) + 0x00800080u;
+                    unusual |= gelu_pair_unusual(w);
                     rel[j] = gelu_pair_rel(w);
-                    table[j] = gelu_pair_table(w, rel[j], gelu_lut);
+                    table[j] = gelu_pair_lookup(w, rel[j], gelu_lut);
                 }
+                // The short select unless some active lane of the wave holds a
+                // zero, subnormal, smallest-binade, inf or NaN input in this
+                // pass (lanes past the row end hold zeros, never used).
+                const bool usual = __builtin_amdgcn_ballot_w64(active && (unusual & 0x80008000u) != 0) == 0;
+                uint32_t nonfinite = 0;
+                if (__builtin_expect(usual, 1)) {
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const uint32_t g = gelu_pair_select(in[pass].x[j / 4][j % 4], rel[j], table[j]);
-                    v[2 * j] = __uint_as_float(g << 16);
-                    v[2 * j + 1] = __uint_as_float(g & 0xffff0000u);
+                    for (int j = 0; j < 8; ++j) {
+                        const uint32_t g = gelu_pair_fast(in[pass].x[j / 4][j % 4], rel[j], table[j]);
+                        v[2 * j] = __uint_as_float(g << 16);
+                        v[2 * j + 1] = __uint_as_float(g & 0xffff0000u);
+                    }
+                } else {
+                    // A half with bit 15 of (mag + 0x80) set is inf or NaN (no
+                    // carry crosses halves); such lanes recompute with activate.
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const uint32_t w = in[pass].x[j / 4][j % 4];
+                        nonfinite |= (w & 0x7fff7fffu) + 0x00800080u;
+                        const uint32_t g = gelu_pair_select(w, rel[j], table[j]);
+                        v[2 * j] = __uint_as_float(g << 16);
+                        v[2 * j + 1] = __uint_as_float(g & 0xffff0000u);
+                    }
                 }
                 if (__builtin_expect(__builtin_amdgcn_ballot_w64((nonfinite & 0x80008000u) != 0) != 0, 0)) {
                     if (nonfinite & 0x80008000u) {

@@ -132,6 +132,28 @@ def test_gelu_every_bf16_input(gpu_device):
     np.testing.assert_array_equal(q.cpu().numpy(), q_ref)
 
 
+def test_gelu_every_bf16_input_beside_large_negatives(gpu_device):
+    """The same sweep with the rest of each row at -8.0 instead of 0:
+    gelu(-8) is -0, so the row scale still carries the bits of gelu(x), and a
+    wave's pass now holds no zero unless x is one. That sends every x with an
+    exponent field in [2, 254] through the short select (table, |x| >= 8, and
+    the exponent-lowering bf16(0.5 x) for |x| < 2^-12), which the zero rows
+    above never reach."""
+    print("[convrot gelu] every finite bf16 input beside -8.0", flush=True)
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    bits = bits[(bits & 0x7F80) != 0x7F80]
+    x = np.full((bits.size, 128), 0xC100, np.uint16)  # -8.0
+    x[:, 0] = bits
+    x[:, 17] = bits
+    xt = inputs.from_bits(x)
+    q, s = torch.ops.turing_utils.bf16_gelu_int8_convrot_quantize(xt.to(gpu_device), 128)
+    q_ref, s_ref = oracle.convrot_quant(x, 128, act=oracle.ACT_GELU_TANH)
+    got = s.cpu().numpy().reshape(-1).view(np.uint32)
+    bad = np.flatnonzero(got != s_ref.view(np.uint32))
+    assert bad.size == 0, f"{bad.size} scales differ, first inputs {[hex(int(v)) for v in bits[bad[:5]]]}"
+    np.testing.assert_array_equal(q.cpu().numpy(), q_ref)
+
+
 def test_swiglu_every_bf16_gate(gpu_device):
     """Every finite bf16 gate g with up = 1, one per row at column 0 of
     [gate | up] rows that are otherwise zero: the row scale carries the bits of

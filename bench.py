@@ -212,13 +212,18 @@ def main():
         "peak": peak,
         "unit": "TFLOP/s" if bound == "mfma" else "GB/s",
         "frac": achieved / peak,
-        "traffic": measured_traffic(dominant),
+        "traffic": None,
     }
-    counters = measured_mfma(dominant)
+    # committed rocprofv3 figures of the same kernel and workload, used only
+    # when they were captured from the kernel sources in this tree
+    traffic_src, mfma_src = counters_source(TRAFFIC_FILE), counters_source(MFMA_FILE)
+    if traffic_src["current"]:
+        roofline["traffic"] = measured_traffic(dominant)
+    counters = measured_mfma(dominant) if mfma_src["current"] else None
     if bound == "mfma" and counters is not None:
-        # the committed rocprofv3 counters of the same kernel and workload
         roofline["mfma_busy"] = counters["mfma_busy"]
         roofline["clock_ghz"] = counters["clock_ghz"]
+    roofline["counters_source"] = {"traffic": traffic_src, "mfma": mfma_src}
 
     extras = None if args.no_extras else extra_kernels(torch, dev, ops, lin, q, k_, v, copy_gbs)
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds)
@@ -256,13 +261,15 @@ def main():
 
 def extra_kernels(torch, dev, ops, lin, q, k, v, copy_gbs) -> dict:
     """Kernels of the path's next rows, timed outside the headline step (the
-    metric's workload is the four linears and the attention): the GELU-fused
+    metric's workload is the four linears and the attention): configs 1 and 2
+    (the Wan-1.3B linear and attention shapes), the GELU-fused
     ConvRot quantizer at FFN-down (K13824), the fused Q/K RMSNorm + RoPE +
     INT8 producer at the attention shape (row-scope RMSNorm, interleaved
     full-width RoPE, as in a Wan block), and the dense W8A8 attention variant
     (INT8 PV) with its rotated Q/K and channel-wise V quantizers."""
     from comfyui_turing_utils_kernel.turing_sage import core as sage_core, quant as sage_quant
     from comfyui_turing_utils_kernel.turing_sage.custom_ops import qk_rms_rope_int8
+    from tests import inputs
 
     def timed(fn, reps=10):
         fn()
@@ -276,6 +283,35 @@ def extra_kernels(torch, dev, ops, lin, q, k, v, copy_gbs) -> dict:
         return e0.elapsed_time(e1) / reps
 
     out = {}
+    # config 1: the Wan-1.3B FFN-up linear, 4096 x 1536 -> 8960 with bias
+    # (seed 0), its quantizer and GEMM timed separately
+    xc = inputs.activation(4096, 1536, 0).to(dev)
+    wc, wsc, bc = (t.to(dev) for t in inputs.weights(8960, 1536, 0))
+    qc, sc = ops.bf16_int8_convrot_quantize(xc, GROUP)
+    ms_q = timed(lambda: ops.bf16_int8_convrot_quantize(xc, GROUP), reps=50)
+    ms_g = timed(lambda: ops.int8_linear(qc, wc, sc, wsc, bc), reps=50)
+    flops = 2.0 * 4096 * 8960 * 1536
+    nbytes = 3.0 * xc.numel() + 4.0 * xc.shape[0]
+    out["c1_int8_gemm"] = {"ms_avg": ms_g, "tops": flops / ms_g / 1e9,
+                           "frac_int8_peak": flops / ms_g / 1e9 / PEAK_INT8_TOPS, "shape": [4096, 1536, 8960],
+                           "bias": True}
+    out["c1_convrot_quant"] = {"ms_avg": ms_q, "gbs": nbytes / ms_q / 1e6, "frac_copy": nbytes / ms_q / 1e6 / copy_gbs}
+    del xc, wc, wsc, bc, qc, sc
+    # config 2: Sage attention at B1 H12 L8190 D128 (seed 1), the kernel alone
+    # on prequantized Q/K and V^T; the planner's key split (kv_splits=None)
+    # and the unsplit kernel
+    from comfyui_turing_utils_kernel.turing_sage.core import attention_from_vt
+
+    q2, k2, v2 = (t.to(dev) for t in inputs.attention(1, 12, 8190, 128, 1))
+    st2 = sage_core.prequantize_sageattn(q2, k2, v2, "HND", BLKQ=BLK, BLKK=BLK)
+    a2 = (st2.query_int8, st2.query_scale, st2.key_int8, st2.key_scale, st2.value_t)
+    kw2 = dict(tensor_layout="HND", sm_scale=128 ** -0.5, blkq=BLK, blkk=BLK)
+    flops = 4.0 * 12 * 8190 * 8190 * 128
+    for tag, splits in (("c2_sage_attn", None), ("c2_sage_attn_unsplit", 1)):
+        ms = timed(lambda: attention_from_vt(*a2, **kw2, kv_splits=splits), reps=50)
+        out[tag] = {"ms_avg": ms, "tops": flops / ms / 1e9, "frac_int8_peak": flops / ms / 1e9 / PEAK_INT8_TOPS,
+                    "shape": [1, 12, 8190, 128]}
+    del q2, k2, v2, st2, a2
     x = next(t[3] for t in lin if t[1] == 13824)
     ms = timed(lambda: ops.bf16_gelu_int8_convrot_quantize(x, GROUP))
     nbytes = 3.0 * x.numel() + 4.0 * x.shape[0]
@@ -349,6 +385,33 @@ def copy_bandwidth(torch, dev) -> float:
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 MFMA_FILE = os.path.join(ROOT, "profiles", "mfma_counters.json")
+CSRC_DIR = os.path.join(ROOT, "comfyui-turing-utils_amd", "csrc")
+
+
+def kernel_sources_digest() -> str:
+    """sha256 (first 16 hex digits) over the HIP sources and headers the
+    kernels are built from, in name order: the version stamp of the
+    committed counter files, which carry the digest they were captured at."""
+    import hashlib
+
+    h = hashlib.sha256()
+    names = sorted(n for n in os.listdir(CSRC_DIR) if n.endswith((".hip", ".h")))
+    for name in names + ["../../include/tu_hip.h"]:
+        with open(os.path.join(CSRC_DIR, name), "rb") as f:
+            h.update(os.path.basename(name).encode() + b"\0" + f.read())
+    return h.hexdigest()[:16]
+
+
+def counters_source(path: str) -> dict:
+    """Where the roofline's committed counter figures come from, and whether
+    they were captured from the kernel sources in this tree."""
+    try:
+        with open(path) as f:
+            stamp = json.load(f).get("_kernel_sources")
+    except (OSError, ValueError):
+        stamp = None
+    return {"file": os.path.relpath(path, ROOT), "kernel_sources": stamp,
+            "current": stamp is not None and stamp == kernel_sources_digest()}
 
 
 def measured_mfma(kernel: str):

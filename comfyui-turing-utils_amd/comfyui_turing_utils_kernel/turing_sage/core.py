@@ -202,13 +202,21 @@ def attention_from_vt(
     blkk: int = 128,
     output: Optional[torch.Tensor] = None,
     kv_splits: Optional[int] = None,
+    workspace: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """Attention kernel only: quantized Q/K and V^T from ``value_transpose``.
 
     ``kv_splits`` (this package only): key ranges computed by separate
     workgroups and merged, for grids that fill the GPU badly; None lets
     ``tu_sage_attn_kv_splits`` choose from the device's compute units, 1
-    never splits.  Non-causal only."""
+    never splits.  Non-causal only.  A split call needs an fp32 workspace of
+    ``split_workspace_bytes(...)`` bytes (ranges x B x H x Lq x (D + 2) x 4:
+    about 100 MB at B1 H12 L8190 D128 with two ranges); it comes from
+    ``workspace`` (a contiguous float32 tensor on the Q/K device, at least
+    that large, reusable across calls on one stream) or else from torch's
+    caching allocator.  How many ranges None picks depends on the device's
+    compute-unit count, so results are bit-identical across devices only
+    with an explicit ``kv_splits``."""
     batch, hq, hkv, lq, lk = _check_qk(q_int8, q_scale, k_int8, k_scale, tensor_layout, blkq, blkk)
     width = q_int8.size(-1)
     lpad = (lk + 63) // 64 * 64
@@ -234,14 +242,18 @@ def attention_from_vt(
         splits = int(kv_splits)
         if splits < 1 or (is_causal and splits > 1):
             raise ValueError("kv_splits must be >= 1, and 1 for causal attention")
+    if splits > 1:
+        # key ranges merged by a second kernel: fp32 partial O plus
+        # (exponent base, row sum) per row and range
+        need = split_workspace_bytes(batch, hq, lq, lk, width, splits) // 4
+        if workspace is not None and (workspace.dtype != torch.float32 or workspace.device != q_int8.device
+                                      or not workspace.is_contiguous() or workspace.numel() < need):
+            raise ValueError(f"Sage split workspace must be a contiguous float32 tensor on the Q/K device "
+                             f"with at least {need} elements")
     with torch.cuda.device(q_int8.device):
         if splits > 1:
-            # key ranges merged by a second kernel: fp32 partial O plus
-            # (exponent base, row sum) per row and range
-            tiles = (lk + 63) // 64
-            per = (tiles + splits - 1) // splits
-            used = (tiles + per - 1) // per
-            partial = torch.empty(used * batch * hq * lq * (width + 2), dtype=torch.float32, device=q_int8.device)
+            partial = workspace if workspace is not None else torch.empty(need, dtype=torch.float32,
+                                                                          device=q_int8.device)
             _lib.call(
                 "tu_sage_attn_fwd_split",
                 q_int8.data_ptr(), q_scale.data_ptr(), blkq, k_int8.data_ptr(), k_scale.data_ptr(), blkk,
@@ -258,6 +270,15 @@ def attention_from_vt(
                 scale, int(bool(is_causal)), _lib.stream_of(q_int8.device),
             )
     return output
+
+
+def split_workspace_bytes(batch: int, hq: int, lq: int, lk: int, head_dim: int, kv_splits: int) -> int:
+    """Bytes of fp32 workspace a key-split call needs: per range and query
+    row, the unnormalized O (head_dim floats) plus exponent base and row sum."""
+    tiles = (lk + 63) // 64
+    per = (tiles + kv_splits - 1) // kv_splits
+    used = (tiles + per - 1) // per
+    return used * batch * hq * lq * (head_dim + 2) * 4
 
 
 _CU_COUNT: dict = {}

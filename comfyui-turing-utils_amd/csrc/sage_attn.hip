@@ -119,8 +119,12 @@ __device__ __forceinline__ LaneGeom<D> lane_geom(int wave, int lane, int64_t k_s
 // Direct-to-LDS buffer loads of the K and V^T tiles at key0 into one ring
 // stage.  Each buffer_load_dwordx4 ... lds moves 64 lanes x 16 B into 1 KiB of
 // contiguous LDS; the K row permutation and the chunk swizzle come from the
-// per-lane source offsets.  K rows at or past lk read as zeros (the buffer
-// range ends there); those keys are masked by the softmax.
+// per-lane source offsets.  The tile's key offset goes into the per-lane
+// offset, not the scalar one: the buffer range check covers only the
+// per-lane offset, so K rows at or past lk (the range ends at lk rows) read
+// as zeros instead of the bytes past the head's rows; those keys are masked
+// by the softmax.  V^T is padded to whole tiles, so its key offset can stay
+// scalar.
 // One overload per head dim: the host compilation pass rejects a template of
 // this function (the buffer builtins only exist for the device target), a
 // plain device function it accepts.
@@ -128,7 +132,7 @@ __device__ __forceinline__ LaneGeom<D> lane_geom(int wave, int lane, int64_t k_s
     constexpr int kK = Geo<D>::kKLoads, kV = Geo<D>::kVLoads;                                                      \
     _Pragma("unroll") for (int i = 0; i < kK; ++i)                                                                 \
         __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_void *)(stage + (kK * wave + i) * 1024), 16,            \
-                                                 gm.k_src[i], key0 * k_sl, 0, 0);                                  \
+                                                 gm.k_src[i] + key0 * k_sl, 0, 0, 0);                              \
     _Pragma("unroll") for (int i = 0; i < kV; ++i)                                                                 \
         __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_void *)(stage + Geo<D>::kKTileBytes + (kV * wave + i) * 1024), \
                                                  16, gm.v_src[i], key0 * 2, 0, 0);

@@ -90,12 +90,15 @@ __device__ __forceinline__ LaneGeom8 lane_geom8(int wave, int lane, int64_t k_sl
     return gm;
 }
 
+// The K tile's key offset is part of the per-lane offset, which is what the
+// buffer range check covers: K rows at or past lk read as zeros (masked
+// keys).  V^T is padded to whole tiles, so its key offset stays scalar.
 __device__ __forceinline__ void issue_tile8(int8_t *stage, __amdgpu_buffer_rsrc_t krs, __amdgpu_buffer_rsrc_t vrs,
                                             const LaneGeom8 &gm, uint32_t k_sl, uint32_t key0, int wave) {
 #pragma unroll
     for (int i = 0; i < 2; ++i)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_void *)(stage + (2 * wave + i) * 1024), 16, gm.k_src[i],
-                                                 key0 * k_sl, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_void *)(stage + (2 * wave + i) * 1024), 16,
+                                                 gm.k_src[i] + key0 * k_sl, 0, 0, 0);
 #pragma unroll
     for (int i = 0; i < 2; ++i)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_void *)(stage + kKTileBytes + (2 * wave + i) * 1024), 16,

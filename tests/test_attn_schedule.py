@@ -31,9 +31,10 @@ import pytest
 
 K_STAGES = 4
 K_AHEAD = K_STAGES - 1
-# per kernel: 1 KiB blocks a group-0 wave loads per tile (Sage 2 K + 4 V^T,
-# W8A8 2 K + 2 V^T), and whether it issues them after the softmax
-KERNELS = {"sage": (6, False), "w8a8": (4, True)}
+# per kernel: 1 KiB blocks a group-0 wave loads per tile (Sage head_dim 128:
+# 2 K + 4 V^T, Sage head_dim 64: 1 K + 2 V^T, W8A8 2 K + 2 V^T), and whether
+# it issues them after the softmax
+KERNELS = {"sage": (6, False), "sage64": (3, False), "w8a8": (4, True)}
 KBKEY = 64
 KBQ = 256
 KWAVEQ = 32
@@ -44,6 +45,7 @@ class Wave:
         self.wave = wave
         self.grp = wave >> 2
         self.events = []  # (kind, payload) in program order
+        self.tile_base = 0  # global index of local tile 0 (key splits)
 
     def barrier(self):
         self.events.append(("barrier", None))
@@ -66,29 +68,46 @@ class Wave:
         self.events.append(("softmax", (tile, masked)))
 
 
-def kernel_program(wave: int, lq: int, lk: int, causal: bool, qblock: int, kernel: str = "sage") -> Wave:
-    """The kernel's control flow for one wave, statement for statement."""
+def split_plan(lk: int, kv_splits: int):
+    """tu_sage_attn_fwd_split's ranges: split_tiles = ceil(tiles / kv_splits)
+    and the number of ranges that covers the key tiles."""
+    tiles = (lk + KBKEY - 1) // KBKEY
+    split_tiles = (tiles + kv_splits - 1) // kv_splits
+    return split_tiles, (tiles + split_tiles - 1) // split_tiles
+
+
+def kernel_program(wave: int, lq: int, lk: int, causal: bool, qblock: int, kernel: str = "sage",
+                   split_z: int | None = None, split_tiles: int = 0) -> Wave:
+    """The kernel's control flow for one wave, statement for statement.
+    split_z / split_tiles model the kSplit instantiation (blockIdx.z and its
+    key range); tiles are then numbered from the range's first tile, and the
+    loads carry global tile indices."""
     LOADS_PER_TILE, issue_late = KERNELS[kernel]
     w = Wave(wave)
     grp, w4 = wave >> 2, wave & 3
     qblock0 = qblock * KBQ
     q0 = qblock0 + grp * (KBQ // 2) + w4 * KWAVEQ
     key_end = min(lk, qblock0 + KBQ) if causal else lk
+    tile_base = split_z * split_tiles if split_z is not None else 0
     tiles = (key_end + KBKEY - 1) // KBKEY
+    if split_z is not None:
+        assert not causal
+        tiles = min(split_tiles, tiles - tile_base)
     my_tiles = tiles
     if causal:
         my_tiles = min(tiles, max(1, (min(q0 + KWAVEQ, lq) + KBKEY - 1) // KBKEY))
-    mask_from = lk // KBKEY
+    mask_from = lk // KBKEY - tile_base
     if causal:
         mask_from = min(mask_from, q0 // KBKEY)
     first_masked = min(tiles, mask_from)
-    tile_key0 = lambda it: min(it, tiles - 1)  # noqa: E731  (tile index the load reads)
+    tile_key0 = lambda it: tile_base + min(it, tiles - 1)  # noqa: E731  (global tile index the load reads)
 
     def softmax(it, mask_tag):
         if not mask_tag:
             assert it < first_masked, "unmasked softmax on a tile that needs a mask"
         w.softmax(it, mask_tag and it >= first_masked)
 
+    w.tile_base = tile_base
     if grp == 0:
         for j in range(K_AHEAD):
             w.issue(j, tile_key0(j))
@@ -140,9 +159,10 @@ def kernel_program(wave: int, lq: int, lk: int, causal: bool, qblock: int, kerne
     return w, dict(tiles=tiles, my_tiles=my_tiles)
 
 
-def check_schedule(lq: int, lk: int, causal: bool, qblock: int, kernel: str = "sage"):
+def check_schedule(lq: int, lk: int, causal: bool, qblock: int, kernel: str = "sage",
+                   split_z: int | None = None, split_tiles: int = 0):
     LOADS_PER_TILE = KERNELS[kernel][0]
-    waves = [kernel_program(i, lq, lk, causal, qblock, kernel) for i in range(8)]
+    waves = [kernel_program(i, lq, lk, causal, qblock, kernel, split_z, split_tiles) for i in range(8)]
     progs = [w for w, _ in waves]
     # 1. equal barrier counts
     counts = [sum(1 for k, _ in p.events if k == "barrier") for p in progs]
@@ -192,7 +212,7 @@ def check_schedule(lq: int, lk: int, causal: bool, qblock: int, kernel: str = "s
             for kind, pay in intervals[wi][k]:
                 if kind == "read":
                     stage, tile, _ = pay
-                    reads.append((k, wi, stage, tile))
+                    reads.append((k, wi, stage, progs[wi].tile_base + tile))
     # 3. every read finds its tile resident and not overwritten
     for k, wi, stage, tile in reads:
         hist = stage_content.get(stage, [])
@@ -229,7 +249,10 @@ def check_schedule(lq: int, lk: int, causal: bool, qblock: int, kernel: str = "s
 @pytest.mark.parametrize("lk", [1, 2, 63, 64, 65, 127, 128, 129, 191, 256, 257, 300, 333, 511, 700, 1000, 32760])
 def test_schedule_every_block(causal, lk, kernel):
     lq = lk if causal else max(lk, 300)
-    for qblock in range((lq + KBQ - 1) // KBQ):
+    nblk = (lq + KBQ - 1) // KBQ
+    # non-causal: the schedule does not depend on the query block
+    blocks = range(nblk) if causal else sorted({0, nblk - 1})
+    for qblock in blocks:
         check_schedule(lq, lk, causal, qblock, kernel)
 
 
@@ -239,6 +262,110 @@ def test_schedule_ragged_pairs(lq, lk, kernel):
     for causal in (False, True):
         for qblock in range((lq + KBQ - 1) // KBQ):
             check_schedule(lq, lk, causal, qblock, kernel)
+
+
+@pytest.mark.parametrize("kernel", ["sage", "sage64"])
+@pytest.mark.parametrize("lk", [1024, 1025, 1087, 1100, 2048, 4095, 8190, 32760])
+@pytest.mark.parametrize("kv_splits", [2, 3, 4, 5, 8])
+def test_schedule_key_splits(lk, kv_splits, kernel):
+    """The kSplit instantiation: every key range tu_sage_attn_fwd_split forms
+    (tile offsets, a truncated last range, mask_from shifted by the range's
+    first tile) keeps equal barrier counts and ring residency."""
+    tiles = (lk + KBKEY - 1) // KBKEY
+    if kv_splits > tiles:
+        pytest.skip("more ranges than key tiles")
+    split_tiles, splits = split_plan(lk, kv_splits)
+    covered = []
+    for z in range(splits):
+        lq = 300
+        for qblock in range((lq + KBQ - 1) // KBQ):
+            check_schedule(lq, lk, False, qblock, kernel, z, split_tiles)
+        w, info = kernel_program(0, 300, lk, False, 0, kernel, z, split_tiles)
+        covered += [z * split_tiles + t for t in range(info["my_tiles"])]
+    assert covered == list(range(tiles)), "key ranges must cover every tile exactly once"
+
+
+# --- K tile loads: the byte range each lane's buffer load touches ----------
+# The loads are raw buffer loads over [kp, kp + lk * k_sl) with the tile's key
+# offset in the per-lane offset (the part the range check covers) and a zero
+# scalar offset; a lane whose offset is at or past the range end reads zeros.
+
+
+def kperm_sage(p: int) -> int:
+    i, kt = p & 15, (p >> 4) & 1
+    return (p & ~31) + 8 * (i >> 2) + 4 * kt + (i & 3)
+
+
+def kperm_w8a8(p: int) -> int:
+    i, kt = p & 15, p >> 4
+    return 16 * (i >> 2) + 4 * kt + (i & 3)
+
+
+def k_load_offsets(kernel: str, k_sl: int):
+    """(row, per-lane offset relative to key0's row) of every group-0 lane's K
+    loads: lane_geom / lane_geom8's k_src."""
+    out = []
+    for w4 in range(4):
+        for lane in range(64):
+            if kernel == "sage64":
+                row = w4 * 16 + (lane >> 2)
+                out.append((kperm_sage(row), kperm_sage(row) * k_sl + ((lane & 3) ^ ((row >> 2) & 3)) * 16))
+                continue
+            for i in range(2):
+                row = (2 * w4 + i) * 8 + (lane >> 3)
+                perm = kperm_sage(row) if kernel == "sage" else kperm_w8a8(row)
+                out.append((perm, perm * k_sl + ((lane & 7) ^ ((row >> 1) & 7)) * 16))
+    return out
+
+
+@pytest.mark.parametrize("kernel", sorted(KERNELS))
+@pytest.mark.parametrize("lk", [1, 2, 63, 64, 65, 100, 127, 129, 333, 1000, 8190])
+@pytest.mark.parametrize("layout", ["HND", "NHD3"])
+@pytest.mark.parametrize("kv_splits", [1, 3])
+def test_k_loads_stay_in_bounds(kernel, lk, layout, kv_splits):
+    """Every K byte a lane reads lies in a visible key row of its own head
+    (row < lk, bytes within head_dim), or the lane's offset is at or past the
+    buffer range end, so it reads zeros.  NHD3: three kv heads interleaved, the
+    last head's rows end at the allocation's end."""
+    d = 64 if kernel == "sage64" else 128
+    nh = 3 if layout == "NHD3" else 1
+    k_sl = nh * d
+    head_off = (nh - 1) * d  # the last head: its rows end at the allocation end
+    alloc_end = lk * k_sl  # bytes of the K tensor
+    rng = lk * k_sl  # buffer range from the head's base
+    splits = [(None, 0)]
+    if kv_splits > 1 and kernel != "w8a8" and (lk + KBKEY - 1) // KBKEY >= kv_splits:
+        st, n = split_plan(lk, kv_splits)
+        splits = [(z, st) for z in range(n)]
+    offs = k_load_offsets(kernel, k_sl)
+    for z, st in splits:
+        prog, info = kernel_program(0, 300, lk, False, 0, kernel, z, st)
+        for kind, pay in prog.events:
+            if kind != "issue":
+                continue
+            key0 = pay[1] * KBKEY
+            for perm, off in offs:
+                voff = off + key0 * k_sl
+                assert voff < 2 ** 32
+                if voff >= rng:
+                    continue  # out of range: zero-filled
+                key = key0 + perm
+                assert key < lk, f"key {key} past lk {lk} read from memory"
+                chunk = voff - key * k_sl
+                assert 0 <= chunk and chunk + 16 <= d
+                assert head_off + voff + 16 <= alloc_end
+
+
+def test_k_bound_model_catches_a_scalar_offset():
+    """Planted mistake: with the key offset in the scalar offset (not range
+    checked) a ragged last tile reads rows past lk."""
+    lk, k_sl = 100, 128
+    bad = False
+    for perm, off in k_load_offsets("sage", k_sl):
+        key0 = 64
+        if off < lk * k_sl and key0 + perm >= lk:  # the check sees only `off`
+            bad = True
+    assert bad
 
 
 @pytest.mark.parametrize("kernel", sorted(KERNELS))

@@ -175,6 +175,13 @@ def test_attention_key_splits(gpu_device, b, h, hkv, lq, lk, d, blkq, blkk, spli
     assert both.cosine >= 0.99999 and both.max_abs <= 1e-2
     if splits == 1:
         assert torch.equal(split, whole)
+    else:
+        # a caller workspace (stale NaN contents) gives the same bits
+        need = core.split_workspace_bytes(b, h, lq, lk, d, splits) // 4
+        ws = torch.full((need + 5,), float("nan"), dtype=torch.float32, device=gpu_device)
+        again = core.attention_from_vt(*args, **kw, kv_splits=splits, workspace=ws)
+        torch.cuda.synchronize(gpu_device)
+        assert torch.equal(again, split)
 
 
 def test_attention_key_splits_nhd_layout(gpu_device):

@@ -164,6 +164,26 @@ def test_key_splits_refused_for_causal_attention():
             core.attention_from_vt(q8, qs, k8, ks, vt, is_causal=causal, kv_splits=splits)
 
 
+def test_key_split_workspace_checked_and_sized():
+    """A caller workspace for a split call is checked before any kernel call,
+    and split_workspace_bytes matches what tu_sage_attn_fwd_split requires:
+    ranges x B x H x Lq x (D + 2) fp32 values, ranges = ceil(tiles / per)."""
+    q8 = torch.zeros(1, 2, 300, 128, dtype=torch.int8)
+    k8 = torch.zeros(1, 2, 2000, 128, dtype=torch.int8)
+    qs = torch.ones(1, 2, 3)
+    ks = torch.ones(1, 2, 16)
+    vt = torch.zeros(1, 2, 128, 2048, dtype=torch.bfloat16)
+    need = core.split_workspace_bytes(1, 2, 300, 2000, 128, 2) // 4
+    assert need == 2 * 1 * 2 * 300 * 130
+    # 32 tiles over 5 ranges: 7 per range covers them in 5 ranges
+    assert core.split_workspace_bytes(1, 1, 1, 2048, 64, 5) == 5 * 66 * 4
+    # 33 tiles over 8 ranges: 5 per range covers them in 7 ranges
+    assert core.split_workspace_bytes(2, 3, 10, 2049, 128, 8) == 7 * 2 * 3 * 10 * 130 * 4
+    for bad in (torch.zeros(need - 1), torch.zeros(need, dtype=torch.float64), torch.zeros(2 * need)[::2]):
+        with pytest.raises(ValueError, match="workspace"):
+            core.attention_from_vt(q8, qs, k8, ks, vt, kv_splits=2, workspace=bad)
+
+
 def test_preflight_refuses_cpu():
     with pytest.raises(RuntimeError, match="GPU"):
         turing_sage.preflight(torch.device("cpu"))

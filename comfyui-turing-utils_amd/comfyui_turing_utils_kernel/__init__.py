@@ -17,6 +17,7 @@ from .ops import (
     turing_gelu_int8_convrot_quantize,
     turing_int8_gemm_i32,
     turing_int8_linear,
+    turing_int8_linear_out,
     turing_layer_norm_adaln,
     turing_swiglu_int8_convrot_quantize,
 )
@@ -34,6 +35,7 @@ __all__ = [
     "turing_gelu_int8_convrot_quantize",
     "turing_int8_gemm_i32",
     "turing_int8_linear",
+    "turing_int8_linear_out",
     "turing_layer_norm_adaln",
     "turing_sage",
     "turing_swiglu_int8_convrot_quantize",

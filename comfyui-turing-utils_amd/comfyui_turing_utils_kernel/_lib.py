@@ -36,6 +36,14 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _i32,
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _c_void_p],
     ),
+    "tu_int8_gemm_f16": (
+        _i32,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _c_void_p],
+    ),
+    "tu_int8_gemm_f32": (
+        _i32,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _c_void_p],
+    ),
     "tu_int8_gemm_bf16_residual": (
         _i32,
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p, _i64, _i64,
@@ -106,7 +114,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          _c_void_p, _i64, _c_void_p, _i32,
          _i64, _i64, _i64, _i64, _i64, _i64,
          _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
-         _f32, _i32, _f32, _c_void_p],
+         _f32, _i32, _c_void_p],
     ),
     "tu_layer_norm_adaln": (
         _i32,
@@ -118,7 +126,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
 }
 
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

@@ -84,10 +84,13 @@ def int8_linear(
         w_scale = w_scale.expand(n)
     if w_scale.numel() != n:
         raise ValueError(f"W8A8 weight scale must be scalar or have {n} values, got {w_scale.numel()}")
-    out = torch.ops.turing_utils.int8_linear(q, weight.contiguous(), s_x.reshape(-1), w_scale.contiguous(), bias)
     out_dtype = out_dtype or x.dtype
-    if out.dtype != out_dtype:
-        out = out.to(out_dtype)
+    if out_dtype == torch.bfloat16:
+        out = torch.ops.turing_utils.int8_linear(q, weight.contiguous(), s_x.reshape(-1), w_scale.contiguous(), bias)
+    else:
+        # fp16 / fp32: the epilogue rounds its fp32 value once, to out_dtype
+        out = torch.ops.turing_utils.int8_linear_out(q, weight.contiguous(), s_x.reshape(-1), w_scale.contiguous(),
+                                                     bias, out_dtype)
     return out.reshape(*original_shape[:-1], n)
 
 

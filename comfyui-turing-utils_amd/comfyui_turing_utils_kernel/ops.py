@@ -13,7 +13,9 @@ Differences from the reference, by design of this MI355X build:
     build's fixed fp32 sequences (bit-identical to the CPU oracle), not
     CUDA's tanhf / expf;
   * ``int8_gemm_i32`` is an extra op exposing the raw INT32 accumulator of
-    the same GEMM kernel, used for bit-exact parity checks.
+    the same GEMM kernel, used for bit-exact parity checks;
+  * ``int8_linear_out`` is an extra op writing the same epilogue in fp16 or
+    fp32 (the output_dtype the plugin hands comfy-kitchen's fused linear).
 """
 from __future__ import annotations
 
@@ -91,6 +93,48 @@ def turing_int8_linear(
 @turing_int8_linear.register_fake
 def _turing_int8_linear_fake(activation, weight, activation_scale, weight_scale, bias=None):
     return torch.empty((activation.size(0), weight.size(0)), dtype=torch.bfloat16, device=activation.device)
+
+
+_OUT_ENTRY = {torch.bfloat16: "tu_int8_gemm_bf16", torch.float16: "tu_int8_gemm_f16",
+              torch.float32: "tu_int8_gemm_f32"}
+
+
+@torch.library.custom_op("turing_utils::int8_linear_out", mutates_args=())
+def turing_int8_linear_out(
+    activation: torch.Tensor,
+    weight: torch.Tensor,
+    activation_scale: torch.Tensor,
+    weight_scale: torch.Tensor,
+    bias: torch.Tensor | None,
+    out_dtype: torch.dtype,
+) -> torch.Tensor:
+    """int8_linear with the epilogue value ((acc * as) * ws) + bias written in
+    ``out_dtype``: bf16 (int8_linear itself), fp16 rounded once from fp32
+    (NaN as 0x7e00), or fp32 unrounded.  The output_dtype of the plugin's
+    GEMM call (comfyui_turing_utils/quantization/dispatch.py:538-615), which
+    the reference serves through comfy-kitchen; no counterpart among the
+    reference package's ops."""
+    if out_dtype not in _OUT_ENTRY:
+        raise TypeError(f"INT8 linear out_dtype must be bfloat16, float16 or float32, got {out_dtype}")
+    activation, weight, activation_scale, weight_scale, bias, m, n, k = _linear_args(
+        activation, weight, activation_scale, weight_scale, bias)
+    out = torch.empty((m, n), dtype=out_dtype, device=activation.device)
+    if m == 0:
+        return out
+    with torch.cuda.device(activation.device):
+        _lib.call(
+            _OUT_ENTRY[out_dtype],
+            activation.data_ptr(), weight.data_ptr(), activation_scale.data_ptr(), weight_scale.data_ptr(),
+            _lib.ptr(bias), out.data_ptr(), m, n, k, _lib.stream_of(activation.device),
+        )
+    return out
+
+
+@turing_int8_linear_out.register_fake
+def _turing_int8_linear_out_fake(activation, weight, activation_scale, weight_scale, bias, out_dtype):
+    if out_dtype not in _OUT_ENTRY:
+        raise TypeError(f"INT8 linear out_dtype must be bfloat16, float16 or float32, got {out_dtype}")
+    return torch.empty((activation.size(0), weight.size(0)), dtype=out_dtype, device=activation.device)
 
 
 def _check_residual(residual, gate, gate_rows, m, n) -> None:

@@ -599,20 +599,10 @@ def prequantize_w8a8attn(
                                         is_causal=is_causal)
 
 
-W8A8_EXP_HEADROOM = 0.0  # exponent headroom of the W8A8 kernel's running maximum (0: exact)
-
-
-def w8a8attn_from_prequantized(quantized: PrequantizedW8A8Attention, *,
-                               exp_headroom: Optional[float] = None) -> torch.Tensor:
+def w8a8attn_from_prequantized(quantized: PrequantizedW8A8Attention) -> torch.Tensor:
     """Runs the dense W8A8 kernel (reference sol_sparse_sageattn_from_prequantized,
-    core.py:916-982, W8A8 force-dense branch).  Output [B, Hq, Lq, head_dim]
-    in the input dtype.  ``exp_headroom`` (default ``W8A8_EXP_HEADROOM``): 0
-    keeps the reference's exact running row maximum; h > 0 lets a row's
-    exponent base move only when its maximum passes it, and then to that
-    maximum + h."""
-    headroom = W8A8_EXP_HEADROOM if exp_headroom is None else float(exp_headroom)
-    if not 0.0 <= headroom <= 4.0:
-        raise ValueError("exp_headroom must be in [0, 4]")
+    core.py:916-982, W8A8 force-dense branch) with the reference's exact
+    running row maximum.  Output [B, Hq, Lq, head_dim] in the input dtype."""
     q8, k8 = quantized.query_int8, quantized.key_int8
     batch, hq, lq, dim = q8.shape
     hkv, lk = k8.size(1), k8.size(2)
@@ -628,7 +618,7 @@ def w8a8attn_from_prequantized(quantized: PrequantizedW8A8Attention, *,
             quantized.value_int8.size(-1), out.data_ptr(), int(quantized.output_dtype == torch.float16),
             batch, hq, hkv, lq, lk, dim, q8.stride(0), q8.stride(1), q8.stride(2),
             k8.stride(0), k8.stride(1), k8.stride(2), out.stride(0), out.stride(1), out.stride(2),
-            float(quantized.sm_scale), int(quantized.is_causal), headroom, _lib.stream_of(device),
+            float(quantized.sm_scale), int(quantized.is_causal), _lib.stream_of(device),
         )
     return out[..., : quantized.original_head_dim]
 
@@ -644,13 +634,11 @@ def w8a8attn(
     key_tile_tokens: int = 0,
     rotate_qk: bool = True,
     stabilize_k: bool = True,
-    exp_headroom: Optional[float] = None,
 ) -> torch.Tensor:
     """Dense INT8 QK / INT8 PV attention, the reference's ``w8a8attn``
     (core.py:657-708): NHD inputs are made HND-contiguous, Q/K rotated by
     the shared Hadamard transform (K centred on its anchor), V quantized per
-    channel, P packed to unsigned 8 bits with the exp2 offset log2(255).
-    ``exp_headroom``: see ``w8a8attn_from_prequantized``."""
+    channel, P packed to unsigned 8 bits with the exp2 offset log2(255)."""
     if tensor_layout not in {"HND", "NHD"}:
         raise ValueError(f"Unsupported tensor_layout: {tensor_layout}")
     if tensor_layout == "NHD":
@@ -668,7 +656,7 @@ def w8a8attn(
         q_hnd, k_hnd, v_hnd, tensor_layout="HND", sm_scale=sm_scale, key_tile_tokens=key_tile_tokens,
         rotate_qk=rotate_qk, stabilize_k=stabilize_k, is_causal=bool(is_causal),
     )
-    output = w8a8attn_from_prequantized(quantized, exp_headroom=exp_headroom)
+    output = w8a8attn_from_prequantized(quantized)
     return output.transpose(1, 2) if tensor_layout == "NHD" else output
 
 

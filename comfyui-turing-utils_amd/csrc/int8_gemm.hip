@@ -4,6 +4,9 @@
 // :1185-1219 with the CUTLASS EVT epilogue of :480-525):
 //   acc[m][n] = sum_k a[m][k] * w[n][k]            (exact int32)
 //   out[m][n] = bf16_rn(((float(acc) * as[m]) * ws[n]) + bias[n])
+// The same fp32 value is also written rounded once to fp16 (RNE, NaN as
+// 0x7e00) or unrounded as fp32: the output_dtype of the plugin's GEMM call
+// (comfyui_turing_utils/quantization/dispatch.py:538-615).
 // a and w are both K-contiguous ("TN"), so every MFMA operand is a 16-byte
 // contiguous load along K.
 //
@@ -189,13 +192,19 @@ struct Frags {
 // (1, 1) in bf16: the gate of a residual add without one.
 constexpr uint32_t kBf16OnePair = 0x3f803f80u;
 
+// Output kinds of the kernel's epilogue.
+constexpr int kOutBf16 = 0;  // bf16_rn of the fp32 epilogue value (LDS-staged row stores)
+constexpr int kOutF16 = 1;   // fp16_rn of the same value (LDS-staged row stores)
+constexpr int kOutF32 = 2;   // the fp32 value itself (direct 16-byte stores)
+constexpr int kOutI32 = 3;   // the int32 accumulator (direct 16-byte stores)
+
 // kResidual: out = bf16_rn(fma(y, gate[row / gate_rows][col], residual[row][col]))
 // with y the bf16 epilogue value (gate 1 when absent).  residual may be out
 // (in place), so neither carries __restrict__: each output chunk is read as
 // residual and then written by the same lane, and no lane stores a chunk
 // that another lane reads (clamped reads past the last row feed only rows
 // that are never stored).
-template <bool kI32Out, bool kResidual>
+template <int kOut, bool kResidual>
 __global__ __launch_bounds__(kThreads, kWaves / 4) void int8_gemm_kernel(
     const int8_t *__restrict__ a, const int8_t *__restrict__ w, const float *__restrict__ as,
     const float *__restrict__ ws, const float *__restrict__ bias, void *out,
@@ -331,7 +340,7 @@ __global__ __launch_bounds__(kThreads, kWaves / 4) void int8_gemm_kernel(
     // acc[i][j][r] = C[m = m0 + wm*16*kFragsM + 16j + (lane & 15)]
     //                  [n = n0 + wn*128 + 16i + 4*(lane >> 4) + r]
     const int g = lane >> 4;
-    if constexpr (kI32Out) {
+    if constexpr (kOut == kOutI32) {
 #pragma unroll
         for (int j = 0; j < kFragsM; ++j) {
             const int64_t row = m0 + wm * 16 * kFragsM + j * 16 + (lane & 15);
@@ -343,12 +352,41 @@ __global__ __launch_bounds__(kThreads, kWaves / 4) void int8_gemm_kernel(
                 __builtin_nontemporal_store(acc[i][j], reinterpret_cast<i32x4 *>(static_cast<int32_t *>(out) + row * n + col));
             }
         }
+    } else if constexpr (kOut == kOutF32) {
+        // fp32 values straight from the accumulators: each lane holds 4
+        // consecutive columns of one row, one 16-byte store per 16 x 16 block
+        // (no rounding, so no staging for row-wide stores either).
+        const float *bp = bias ? bias : ws;
+#pragma unroll
+        for (int j = 0; j < kFragsM; ++j) {
+            const int64_t row = m0 + wm * 16 * kFragsM + j * 16 + (lane & 15);
+            const float xs = as[min(row, m - 1)];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int64_t col = n0 + wn * 128 + i * 16 + 4 * g;
+                const int64_t cc = min(col, n - 4);
+                const f32x4 wsv = *reinterpret_cast<const f32x4 *>(ws + cc);
+                const f32x4 bv = *reinterpret_cast<const f32x4 *>(bp + cc);
+                f32x4 v;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    float x = static_cast<float>(acc[i][j][r]);
+                    x = x * xs;
+                    x = x * wsv[r];
+                    if (bias) x = x + bv[r];
+                    v[r] = x;
+                }
+                if (row < m && col < n)  // n % 8 == 0: a group of 4 is all in or all out
+                    __builtin_nontemporal_store(v, reinterpret_cast<f32x4 *>(static_cast<float *>(out) + row * n + col));
+            }
+        }
     } else {
-        // bf16 tile of this wave (16 kFragsM rows x 128 columns) staged through
-        // LDS, so that global stores write whole rows: the ring is free once
-        // every wave is past its last fragment read.  Rows of 256 B; the
-        // 16-byte chunk index is XORed with the row's low 4 bits (both the
+        // 16-bit tile of this wave (16 kFragsM rows x 128 columns) staged
+        // through LDS, so that global stores write whole rows: the ring is
+        // free once every wave is past its last fragment read.  Rows of 256 B;
+        // the 16-byte chunk index is XORed with the row's low 4 bits (both the
         // 8-byte writes below and the 16-byte row reads are conflict free).
+        static_assert(kOut == kOutBf16 || !kResidual, "the residual epilogue writes bf16");
         constexpr int kRows = 16 * kFragsM;
         static_assert(kWaves * kRows * 256 <= kStages * kStageBytes, "epilogue tile exceeds the LDS ring");
         const int frow = lane & 15;
@@ -409,7 +447,17 @@ __global__ __launch_bounds__(kThreads, kWaves / 4) void int8_gemm_kernel(
                         v[r] = x;
                     }
                     u32x2 packed;
-                    if constexpr (decltype(hw)::value) {
+                    if constexpr (kOut == kOutF16) {
+                        // RNE by the hardware conversion; only the slow path
+                        // can meet a NaN, which it writes as 0x7e00
+                        if constexpr (decltype(hw)::value) {
+                            packed.x = hw_f16x2_bits(v[0], v[1]);
+                            packed.y = hw_f16x2_bits(v[2], v[3]);
+                        } else {
+                            packed.x = pack_f16x2(v[0], v[1]);
+                            packed.y = pack_f16x2(v[2], v[3]);
+                        }
+                    } else if constexpr (decltype(hw)::value) {
                         packed.x = hw_bf16x2_bits(v[0], v[1]);
                         packed.y = hw_bf16x2_bits(v[2], v[3]);
                     } else {
@@ -508,16 +556,27 @@ int32_t check_gemm_args(const int8_t *a, const int8_t *w, const void *out, int64
     return require_gfx950();
 }
 
-template <bool kI32Out, bool kResidual = false>
+template <int kOut, bool kResidual = false>
 int32_t launch_gemm(const int8_t *a, const int8_t *w, const float *as, const float *ws, const float *bias,
                     void *out, int64_t m, int64_t n, int64_t k, void *stream, const uint16_t *residual = nullptr,
                     const uint16_t *gate = nullptr, int64_t gate_rows = 1) {
     if (m == 0) return 0;
     const int tiles_m = static_cast<int>((m + kBM - 1) / kBM);
     const int tiles_n = static_cast<int>((n + kBN - 1) / kBN);
-    int8_gemm_kernel<kI32Out, kResidual><<<dim3(tiles_m * tiles_n), kThreads, 0, static_cast<hipStream_t>(stream)>>>(
+    int8_gemm_kernel<kOut, kResidual><<<dim3(tiles_m * tiles_n), kThreads, 0, static_cast<hipStream_t>(stream)>>>(
         a, w, as, ws, bias, out, m, n, k, tiles_m, tiles_n, residual, gate, gate_rows);
-    return check_launch(kI32Out ? "tu_int8_gemm_i32" : kResidual ? "tu_int8_gemm_bf16_residual" : "tu_int8_gemm_bf16");
+    return check_launch(kOut == kOutI32   ? "tu_int8_gemm_i32"
+                        : kResidual       ? "tu_int8_gemm_bf16_residual"
+                        : kOut == kOutF16 ? "tu_int8_gemm_f16"
+                        : kOut == kOutF32 ? "tu_int8_gemm_f32"
+                                          : "tu_int8_gemm_bf16");
+}
+
+int32_t check_epilogue_args(const float *a_scale, const float *w_scale, const float *bias) {
+    TU_REQUIRE(a_scale && w_scale, "INT8 GEMM scales must be non-null");
+    TU_REQUIRE((reinterpret_cast<uintptr_t>(w_scale) & 15) == 0 && (reinterpret_cast<uintptr_t>(bias) & 15) == 0,
+               "INT8 GEMM weight scale and bias must be 16-byte aligned");
+    return 0;
 }
 
 }  // namespace
@@ -527,11 +586,23 @@ extern "C" int32_t tu_int8_gemm_bf16(const int8_t *a, const int8_t *w, const flo
                                      const float *w_scale, const float *bias, void *out_bf16, int64_t m,
                                      int64_t n, int64_t k, void *stream) {
     using namespace tu;
-    if (check_gemm_args(a, w, out_bf16, m, n, k)) return -1;
-    TU_REQUIRE(a_scale && w_scale, "INT8 GEMM scales must be non-null");
-    TU_REQUIRE((reinterpret_cast<uintptr_t>(w_scale) & 15) == 0 && (reinterpret_cast<uintptr_t>(bias) & 15) == 0,
-               "INT8 GEMM weight scale and bias must be 16-byte aligned");
-    return launch_gemm<false>(a, w, a_scale, w_scale, bias, out_bf16, m, n, k, stream);
+    if (check_gemm_args(a, w, out_bf16, m, n, k) || check_epilogue_args(a_scale, w_scale, bias)) return -1;
+    return launch_gemm<kOutBf16>(a, w, a_scale, w_scale, bias, out_bf16, m, n, k, stream);
+}
+
+extern "C" int32_t tu_int8_gemm_f16(const int8_t *a, const int8_t *w, const float *a_scale, const float *w_scale,
+                                    const float *bias, void *out_f16, int64_t m, int64_t n, int64_t k,
+                                    void *stream) {
+    using namespace tu;
+    if (check_gemm_args(a, w, out_f16, m, n, k) || check_epilogue_args(a_scale, w_scale, bias)) return -1;
+    return launch_gemm<kOutF16>(a, w, a_scale, w_scale, bias, out_f16, m, n, k, stream);
+}
+
+extern "C" int32_t tu_int8_gemm_f32(const int8_t *a, const int8_t *w, const float *a_scale, const float *w_scale,
+                                    const float *bias, float *out, int64_t m, int64_t n, int64_t k, void *stream) {
+    using namespace tu;
+    if (check_gemm_args(a, w, out, m, n, k) || check_epilogue_args(a_scale, w_scale, bias)) return -1;
+    return launch_gemm<kOutF32>(a, w, a_scale, w_scale, bias, out, m, n, k, stream);
 }
 
 extern "C" int32_t tu_int8_gemm_bf16_residual(const int8_t *a, const int8_t *w, const float *a_scale,
@@ -547,7 +618,7 @@ extern "C" int32_t tu_int8_gemm_bf16_residual(const int8_t *a, const int8_t *w, 
                "INT8 GEMM weight scale, bias, residual and gate must be 16-byte aligned");
     TU_REQUIRE(!gate_bf16 || gate_rows > 0, "INT8 GEMM gate_rows must be positive with a gate (got %lld)",
                static_cast<long long>(gate_rows));
-    return launch_gemm<false, true>(a, w, a_scale, w_scale, bias, out_bf16, m, n, k, stream,
+    return launch_gemm<kOutBf16, true>(a, w, a_scale, w_scale, bias, out_bf16, m, n, k, stream,
                                     static_cast<const uint16_t *>(residual_bf16),
                                     static_cast<const uint16_t *>(gate_bf16), gate_bf16 ? gate_rows : 1);
 }
@@ -556,7 +627,7 @@ extern "C" int32_t tu_int8_gemm_i32(const int8_t *a, const int8_t *w, int32_t *a
                                     int64_t k, void *stream) {
     using namespace tu;
     if (check_gemm_args(a, w, acc, m, n, k)) return -1;
-    return launch_gemm<true>(a, w, nullptr, nullptr, nullptr, acc, m, n, k, stream);
+    return launch_gemm<kOutI32>(a, w, nullptr, nullptr, nullptr, acc, m, n, k, stream);
 }
 
 extern "C" int32_t tu_dequant_i32_bf16(const int32_t *acc, int64_t acc_ld, const float *a_scale,

@@ -68,6 +68,21 @@ __device__ __forceinline__ uint32_t hw_bf16x2_bits(float a, float b) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{a, b}), bf16x2_t));
 }
 
+// fp16 <-> fp32.  Two floats to two fp16 (low = a) by the hardware
+// conversion: round-to-nearest-even, overflow to +-inf, fp16 subnormals kept;
+// a NaN keeps an unspecified NaN payload.
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t hw_f16x2_bits(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{a, b}), f16x2_t));
+}
+// The same with every NaN written as 0x7e00 (quiet, positive).
+__device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
+    uint32_t r = hw_f16x2_bits(a, b);
+    if (a != a) r = (r & 0xffff0000u) | 0x7e00u;
+    if (b != b) r = (r & 0x0000ffffu) | 0x7e000000u;
+    return r;
+}
+
 // s_waitcnt immediate that waits until at most n vector-memory operations are
 // outstanding and leaves the other counters alone (gfx9 encoding: vmcnt in
 // bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).

@@ -176,8 +176,7 @@ __device__ __forceinline__ void flush_segment(W8State &st, int tile, const int32
 // rescale when one moved, then P - 128 packed as the PV B operands p8[qt]
 // (dword kt = keys 16 g + 4 kt .. + 3 of query 16 qt + lc) and l += p.
 __device__ __forceinline__ void softmax_tile8(const i32x4 (&s)[4][kQT], const float (&f)[kQT], W8State &st,
-                                              i32x4 (&p8)[kQT], int tile, const int32_t *__restrict__ vpre, int g,
-                                              float headroom) {
+                                              i32x4 (&p8)[kQT], int tile, const int32_t *__restrict__ vpre, int g) {
     float mlane[kQT];
     bool need = false;
 #pragma unroll
@@ -197,10 +196,9 @@ __device__ __forceinline__ void softmax_tile8(const i32x4 (&s)[4][kQT], const fl
         flush_segment(st, tile, vpre, g);
 #pragma unroll
         for (int qt = 0; qt < kQT; ++qt) {
-            // a row whose maximum passed the base moves it to that maximum
-            // plus the headroom (0: the reference's exact running maximum)
+            // the reference's exact running maximum
             const float mx = xmax_f32(mlane[qt]);
-            const float m_new = mx > st.m_used[qt] ? mx + headroom : st.m_used[qt];
+            const float m_new = mx > st.m_used[qt] ? mx : st.m_used[qt];
             const float alpha = __builtin_amdgcn_exp2f(st.m_used[qt] - m_new);  // 2^-inf = 0 on the first tile
             st.m_used[qt] = m_new;
             st.l[qt] *= alpha;
@@ -308,7 +306,7 @@ __global__ __launch_bounds__(kThreads, 1) void w8a8_attn_kernel(
     const float *__restrict__ k_scale, const int8_t *__restrict__ vt, const float *__restrict__ v_scale,
     const int32_t *__restrict__ v_prefix, uint16_t *__restrict__ o, int hq, int groups, int64_t lq, int64_t lk,
     int64_t lpad, int64_t nqs, int64_t nks, int64_t q_sb, int64_t q_sh, int64_t q_sl, int64_t k_sb, int64_t k_sh,
-    int64_t k_sl, int64_t o_sb, int64_t o_sh, int64_t o_sl, float sm_log2, float headroom) {
+    int64_t k_sl, int64_t o_sb, int64_t o_sh, int64_t o_sl, float sm_log2) {
     __shared__ __align__(1024) int8_t lds[kStages][kStageBytes];
 
     const int tid = threadIdx.x;
@@ -389,7 +387,7 @@ __global__ __launch_bounds__(kThreads, 1) void w8a8_attn_kernel(
                 static_cast<int>(max(min(q0 - key0, static_cast<int64_t>(kBKey)), static_cast<int64_t>(-kBQ)));
             mask_tile8<kCausal>(s, key_lim, q_rel, g, lc);
         }
-        softmax_tile8(s, f, st, p8, it, vpre, g, headroom);
+        softmax_tile8(s, f, st, p8, it, vpre, g);
     };
 
     // The schedule of the Sage kernel (sage_attn.hip): one barrier per key
@@ -474,10 +472,9 @@ extern "C" int32_t tu_w8a8_attn_fwd(const int8_t *q8, const float *q_scale, int6
                                     int64_t batch, int64_t hq, int64_t hkv, int64_t lq, int64_t lk, int64_t dim,
                                     int64_t q_sb, int64_t q_sh, int64_t q_sl, int64_t k_sb, int64_t k_sh,
                                     int64_t k_sl, int64_t o_sb, int64_t o_sh, int64_t o_sl, float sm_scale,
-                                    int32_t causal, float exp_headroom, void *stream) {
+                                    int32_t causal, void *stream) {
     using namespace tu;
     TU_REQUIRE(dim == kD, "W8A8 attention kernel requires head_dim 128, got %lld", static_cast<long long>(dim));
-    TU_REQUIRE(exp_headroom >= 0.0f && exp_headroom <= 4.0f, "W8A8 attention exp_headroom must be in [0, 4]");
     TU_REQUIRE(batch > 0 && hq > 0 && hkv > 0 && hq % hkv == 0, "W8A8 attention: hq must be a positive multiple of hkv");
     TU_REQUIRE(lq > 0 && lk > 0, "W8A8 attention requires non-empty sequences");
     TU_REQUIRE(lpad == (lk + kBKey - 1) / kBKey * kBKey, "W8A8 attention: V^T padded length must be ceil(lk/64)*64");
@@ -503,7 +500,7 @@ extern "C" int32_t tu_w8a8_attn_fwd(const int8_t *q8, const float *q_scale, int6
     const int groups = static_cast<int>(hq / hkv);
 #define TU_W8_ARGS                                                                                            \
     q8, q_scale, k8, k_scale, vt, v_scale, v_prefix, static_cast<uint16_t *>(out), static_cast<int>(hq), groups, \
-        lq, lk, lpad, nqs, nks, q_sb, q_sh, q_sl, k_sb, k_sh, k_sl, o_sb, o_sh, o_sl, sm_log2, exp_headroom
+        lq, lk, lpad, nqs, nks, q_sb, q_sh, q_sl, k_sb, k_sh, k_sl, o_sb, o_sh, o_sl, sm_log2
     if (causal) {
         if (out_fp16) w8a8_attn_kernel<true, true><<<grid, kThreads, 0, s>>>(TU_W8_ARGS);
         else w8a8_attn_kernel<true, false><<<grid, kThreads, 0, s>>>(TU_W8_ARGS);

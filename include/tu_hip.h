@@ -94,6 +94,22 @@ int32_t tu_int8_gemm_bf16(const int8_t *a, const int8_t *w, const float *a_scale
                           const float *w_scale, const float *bias, void *out_bf16, int64_t m,
                           int64_t n, int64_t k, void *stream);
 
+/* The same GEMM and epilogue value, written as fp16 rounded once from fp32
+ * (round-to-nearest-even, overflow to +-inf, fp16 subnormals kept, every NaN
+ * as 0x7e00): out: fp16 [m, n] row-major.  Replaces the fp16 output_dtype of
+ * the plugin's W8A8 GEMM call (comfyui_turing_utils/quantization/
+ * dispatch.py:538-615, output_dtype = out_dtype or x.dtype at :660-668),
+ * which the reference serves through comfy-kitchen's fused INT8 linear. */
+int32_t tu_int8_gemm_f16(const int8_t *a, const int8_t *w, const float *a_scale,
+                         const float *w_scale, const float *bias, void *out_f16, int64_t m,
+                         int64_t n, int64_t k, void *stream);
+
+/* The same epilogue value unrounded: out: fp32 [m, n] row-major, the fp32
+ * output_dtype of the same call (dispatch.py:538-615, :660-668). */
+int32_t tu_int8_gemm_f32(const int8_t *a, const int8_t *w, const float *a_scale,
+                         const float *w_scale, const float *bias, float *out, int64_t m,
+                         int64_t n, int64_t k, void *stream);
+
 /* The same GEMM with a gated residual add fused into the epilogue, for a DiT
  * block's x + y * gate: out[m][n] = bf16_rn(fma(y, g, residual[m][n])) with
  * y the tu_int8_gemm_bf16 value above, g = gate[m / gate_rows][n] (bf16 [G, n],
@@ -316,10 +332,6 @@ int32_t tu_w8a8_quant_v(const void *v, int32_t dtype, int64_t batch, int64_t hea
  *       p = 2^(fma(s, f, -m)), P = cvt.rni.sat.u8(p), l += p,
  *       O += P . vq (exact), O and l rescaled by 2^(m_old - m)
  *   out = O / l * v_scale[channel], bf16 (out_fp16 0) or fp16 (1)
- * exp_headroom in [0, 4]: 0 keeps the reference's exact running maximum m;
- * h > 0 moves a row's base only when its maximum passes the base, and then
- * to that maximum + h (so P <= 255 * 2^-h right after a move, and fewer
- * tiles move it).
  * q8, k8: int8 by element strides (16-byte aligned rows), dim == 128, GQA
  * hq % hkv == 0; q_scale: fp32 [batch, hq, nqs >= ceil(lq/16)]; k_scale:
  * fp32 [batch, hkv, nks >= ceil(lk/64)]; vq, v_scale, prefix from
@@ -335,7 +347,7 @@ int32_t tu_w8a8_attn_fwd(const int8_t *q8, const float *q_scale, int64_t nqs, co
                          int64_t batch, int64_t hq, int64_t hkv, int64_t lq, int64_t lk, int64_t dim,
                          int64_t q_sb, int64_t q_sh, int64_t q_sl, int64_t k_sb, int64_t k_sh,
                          int64_t k_sl, int64_t o_sb, int64_t o_sh, int64_t o_sl, float sm_scale,
-                         int32_t causal, float exp_headroom, void *stream);
+                         int32_t causal, void *stream);
 
 /* Wan block: LayerNorm + AdaLN --------------------------------------------- */
 

@@ -67,6 +67,10 @@ def lib():
             L.or_int8_gemm_i32.argtypes = [_p, _p, _i64, _i64, _i64, _p]
             L.or_int8_epilogue_bf16.restype = _i32
             L.or_int8_epilogue_bf16.argtypes = [_p, _i64, _p, _p, _i32, _p, _i64, _i64, _p]
+            L.or_int8_epilogue_f32.restype = _i32
+            L.or_int8_epilogue_f32.argtypes = [_p, _i64, _p, _p, _i32, _p, _i64, _i64, _p]
+            L.or_int8_epilogue_f16.restype = _i32
+            L.or_int8_epilogue_f16.argtypes = [_p, _i64, _p, _p, _i32, _p, _i64, _i64, _p]
             L.or_residual_gate_bf16.restype = _i32
             L.or_residual_gate_bf16.argtypes = [_p, _p, _p, _i64, _i64, _i64, _p]
             L.or_sage_kmean.restype = _i32
@@ -229,6 +233,32 @@ def epilogue_bf16(acc: np.ndarray, a_scale: np.ndarray, w_scale: np.ndarray,
     _check(lib().or_int8_epilogue_bf16(_ptr(acc), ld, _ptr(a_scale), _ptr(w_scale), scalar,
                                        None if b is None else _ptr(b), m, cols, _ptr(out)), "epilogue")
     return out
+
+
+def _epilogue_out(fn: str, dtype, acc, a_scale, w_scale, bias, cols):
+    acc = np.ascontiguousarray(acc, dtype=np.int32)
+    m, ld = acc.shape
+    cols = ld if cols is None else cols
+    a_scale = np.ascontiguousarray(a_scale, dtype=np.float32).reshape(-1)
+    w_scale = np.ascontiguousarray(w_scale, dtype=np.float32).reshape(-1)
+    b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32).reshape(-1)
+    out = np.empty((m, cols), dtype=dtype)
+    _check(getattr(lib(), fn)(_ptr(acc), ld, _ptr(a_scale), _ptr(w_scale), int(w_scale.size == 1),
+                              None if b is None else _ptr(b), m, cols, _ptr(out)), "epilogue")
+    return out
+
+
+def epilogue_f32(acc: np.ndarray, a_scale: np.ndarray, w_scale: np.ndarray, bias: np.ndarray | None = None,
+                 cols: int | None = None) -> np.ndarray:
+    """fp32 [M, cols] of ((acc * as) * ws) + bias, step by step (the fp32
+    output_dtype of the W8A8 GEMM)."""
+    return _epilogue_out("or_int8_epilogue_f32", np.float32, acc, a_scale, w_scale, bias, cols)
+
+
+def epilogue_f16(acc: np.ndarray, a_scale: np.ndarray, w_scale: np.ndarray, bias: np.ndarray | None = None,
+                 cols: int | None = None) -> np.ndarray:
+    """fp16 bits [M, cols] of that value rounded once (RNE; NaN as 0x7e00)."""
+    return _epilogue_out("or_int8_epilogue_f16", np.uint16, acc, a_scale, w_scale, bias, cols)
 
 
 def residual_gate_bf16(y_bits: np.ndarray, residual_bits: np.ndarray, gate_bits: np.ndarray | None = None,

@@ -28,6 +28,8 @@
  *                             quantizer's bf16 domain (exhaustive)
  *   or_int8_gemm_i32          pinned: numpy int64 matmul (brute force)
  *   or_int8_epilogue_bf16     pinned: fp64 closed form within bf16 rounding
+ *   or_int8_epilogue_f32/_f16 pinned: numpy float32 step-by-step products and
+ *                             sum (bit-exact), numpy float16 cast of that value
  *   or_residual_gate_bf16     pinned: numpy fp64 product-plus-sum rounded once
  *   or_sage_kmean             pinned: fp64 mean within one bf16 ulp
  *   or_sage_quant             pinned: invariants (max|q|==127, dequant error)
@@ -348,6 +350,37 @@ OR_API int or_int8_epilogue_bf16(const int32_t *acc, int64_t acc_ld, const float
             out[i * n + j] = or_f32_to_bf16_rne(v);
         }
     }
+    return 0;
+}
+
+/* The same epilogue value unrounded (fp32 output_dtype) and rounded once to  */
+/* fp16 (fp16 output_dtype; dispatch.py:538-615, :660-668): RNE, overflow to  */
+/* +-inf, subnormals kept, every NaN written as 0x7e00.                      */
+static inline float epilogue_value(const int32_t *acc, int64_t acc_ld, const float *as, const float *ws,
+                                   int ws_scalar, const float *bias, int64_t i, int64_t j) {
+    float v = (float)acc[i * acc_ld + j];
+    v = v * as[i];
+    v = v * ws[ws_scalar ? 0 : j];
+    if (bias) v = v + bias[j];
+    return v;
+}
+
+OR_API int or_int8_epilogue_f32(const int32_t *acc, int64_t acc_ld, const float *as, const float *ws,
+                                int ws_scalar, const float *bias, int64_t m, int64_t n, float *out) {
+    for (int64_t i = 0; i < m; ++i)
+        for (int64_t j = 0; j < n; ++j) out[i * n + j] = epilogue_value(acc, acc_ld, as, ws, ws_scalar, bias, i, j);
+    return 0;
+}
+
+OR_API uint16_t or_f32_to_f16_rne(float value);
+
+OR_API int or_int8_epilogue_f16(const int32_t *acc, int64_t acc_ld, const float *as, const float *ws,
+                                int ws_scalar, const float *bias, int64_t m, int64_t n, uint16_t *out) {
+    for (int64_t i = 0; i < m; ++i)
+        for (int64_t j = 0; j < n; ++j) {
+            const float v = epilogue_value(acc, acc_ld, as, ws, ws_scalar, bias, i, j);
+            out[i * n + j] = v != v ? (uint16_t)0x7e00U : or_f32_to_f16_rne(v);
+        }
     return 0;
 }
 

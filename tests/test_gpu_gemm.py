@@ -214,3 +214,90 @@ def test_dequantize_exact(gpu_device, cols, scalar):
     out = torch.ops.turing_utils.dequantize_int8_bf16(acc.to(gpu_device), as_.to(gpu_device), ws.to(gpu_device), cols)
     ref = oracle.epilogue_bf16(acc.numpy(), as_.numpy(), ws.numpy(), None, cols=cols)
     np.testing.assert_array_equal(inputs.bits(out), ref)
+
+
+def _linear_out_check(got: torch.Tensor, acc, as_, ws, bias, out_dtype):
+    """Bit-exact comparison of int8_linear_out against the oracle's fp16 / fp32
+    epilogue (fp32: NaN positions, bits elsewhere)."""
+    b = None if bias is None else bias.numpy()
+    if out_dtype == torch.float16:
+        ref = oracle.epilogue_f16(acc, as_.numpy(), ws.numpy(), b)
+        g = got.cpu().view(torch.int16).numpy().view(np.uint16)
+        bad = np.argwhere(g != ref)
+    else:
+        ref = oracle.epilogue_f32(acc, as_.numpy(), ws.numpy(), b)
+        g = got.cpu().numpy()
+        nan = np.isnan(ref)
+        assert np.array_equal(np.isnan(g), nan)
+        bad = np.argwhere((g.view(np.uint32) != ref.view(np.uint32)) & ~nan)
+    assert bad.size == 0, f"{len(bad)} outputs differ, first {bad[:5].tolist()}"
+
+
+@pytest.mark.parametrize("out_dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("with_bias", [True, False])
+@pytest.mark.parametrize("m,n,k", [(300, 264, 192), (96, 8960, 1536), (513, 520, 1040)])
+def test_int8_linear_out_exact(gpu_device, m, n, k, with_bias, out_dtype):
+    """int8_linear_out: the epilogue value rounded once to fp16 (not through
+    bf16), or kept in fp32, bit-exact against the oracle on ragged tiles."""
+    print(f"[int8_linear_out] m={m} n={n} k={k} bias={with_bias} {out_dtype}", flush=True)
+    a = _rand_i8((m, k), 15 + m)
+    w, ws, bias = inputs.weights(n, k, 19, with_bias)
+    g = torch.Generator().manual_seed(13)
+    as_ = torch.empty(m).uniform_(1e-3, 1e-1, generator=g)
+    dev = gpu_device
+    out = torch.ops.turing_utils.int8_linear_out(a.to(dev), w.to(dev), as_.to(dev), ws.to(dev),
+                                                 None if bias is None else bias.to(dev), out_dtype)
+    torch.cuda.synchronize(dev)
+    assert out.dtype == out_dtype and out.shape == (m, n)
+    _linear_out_check(out, oracle.int8_gemm_i32(a.numpy(), w.numpy()), as_, ws, bias, out_dtype)
+
+
+@pytest.mark.parametrize("out_dtype", [torch.float16, torch.float32])
+def test_int8_linear_out_edges(gpu_device, out_dtype):
+    """fp16 overflow to +-inf, the 65504 rounding boundary, fp16 subnormals,
+    and non-finite scales and bias (NaN written as 0x7e00 in fp16), on both
+    the hardware-rounding waves and the guarded ones."""
+    m, n, k = 300, 520, 192
+    print(f"[int8_linear_out edges] {out_dtype}", flush=True)
+    a = _rand_i8((m, k), 47)
+    w, ws, bias = inputs.weights(n, k, 53, True)
+    g = torch.Generator().manual_seed(7)
+    as_ = torch.empty(m).uniform_(1e-3, 1e-1, generator=g)
+    as_[10] = 40.0        # |y| in the thousands to past 65520: fp16 +-inf
+    as_[11] = 1e-7        # fp16 subnormals and zeros
+    as_[12] = 4e-9
+    as_[100] = float("nan")
+    as_[200] = float("inf")
+    ws[30] = 0.0
+    ws[300] = float("-inf")
+    bias = bias.clone()
+    bias[40] = float("nan")
+    dev = gpu_device
+    acc = oracle.int8_gemm_i32(a.numpy(), w.numpy())
+    for b in (None, bias):
+        out = torch.ops.turing_utils.int8_linear_out(a.to(dev), w.to(dev), as_.to(dev), ws.to(dev),
+                                                     None if b is None else b.to(dev), out_dtype)
+        torch.cuda.synchronize(dev)
+        _linear_out_check(out, acc, as_, ws, b, out_dtype)
+    if out_dtype == torch.float16:
+        h = out.cpu().float()
+        assert torch.isinf(h).any() and (h[11].abs() < 6.1e-5).any() and torch.isnan(h).any()
+
+
+@pytest.mark.parametrize("out_dtype", [torch.float16, torch.float32])
+def test_int8_linear_out_config1_rows(gpu_device, out_dtype):
+    """Config 1 (4096 x 1536 -> 8960 with bias) in fp16 and fp32: 128 sampled
+    rows bit-exact; the bf16 op's output equals the fp32 output rounded to
+    bf16 everywhere."""
+    x = inputs.activation(4096, 1536, 0)
+    w, ws, bias = inputs.weights(8960, 1536, 0)
+    dev = gpu_device
+    q, s = torch.ops.turing_utils.bf16_int8_convrot_quantize(x.to(dev), 128)
+    out = torch.ops.turing_utils.int8_linear_out(q, w.to(dev), s, ws.to(dev), bias.to(dev), out_dtype)
+    bf = torch.ops.turing_utils.int8_linear(q, w.to(dev), s, ws.to(dev), bias.to(dev))
+    torch.cuda.synchronize(dev)
+    rows = np.sort(np.random.default_rng(1).choice(4096, 128, replace=False))
+    acc = oracle.int8_gemm_i32(q.cpu().numpy()[rows], w.numpy())
+    _linear_out_check(out[torch.from_numpy(rows).to(dev)], acc, s.cpu().reshape(-1)[rows], ws, bias, out_dtype)
+    if out_dtype == torch.float32:
+        assert torch.equal(out.to(torch.bfloat16), bf)

@@ -69,19 +69,30 @@ def test_int8_linear_config1_3d(gpu_device, ws_kind):
     assert bad.size == 0, f"{len(bad)} outputs differ, first {bad[:5].tolist()}"
 
 
-def test_int8_linear_out_dtype_fp16_and_group_256(gpu_device):
-    """out_dtype=float16: the bf16 epilogue output converted by torch; G=256 is
-    the reference's own group (its default)."""
-    print("[integration linear] out fp16, G=256", flush=True)
+@pytest.mark.parametrize("out_dtype", [torch.float16, torch.float32])
+def test_int8_linear_out_dtype_and_group_256(gpu_device, out_dtype):
+    """out_dtype=float16 / float32: the epilogue's fp32 value rounded once to
+    fp16 (no bf16 step), or kept in fp32; G=256 is the reference's own group
+    (its default)."""
+    print(f"[integration linear] out {out_dtype}, G=256", flush=True)
     x = inputs.activation(384, 1536, 5)
     w, ws, bias = inputs.weights(1024, 1536, 5)
     out = integration.int8_linear(x.view(3, 128, 1536).to(gpu_device), w.to(gpu_device), ws.to(gpu_device),
-                                  bias.to(gpu_device), out_dtype=torch.float16, convrot=True)
+                                  bias.to(gpu_device), out_dtype=out_dtype, convrot=True)
     torch.cuda.synchronize(gpu_device)
-    assert out.shape == (3, 128, 1024) and out.dtype == torch.float16
-    rows = np.arange(384, dtype=np.int64)
-    ref = inputs.from_bits(_oracle_linear(x, rows, w, ws, bias, 256, oracle.ACT_NONE)).to(torch.float16)
-    assert torch.equal(out.reshape(384, 1024).cpu(), ref)
+    assert out.shape == (3, 128, 1024) and out.dtype == out_dtype
+    q, s = oracle.convrot_quant(inputs.bits(x), 256)
+    acc = oracle.int8_gemm_i32(q, w.numpy())
+    got = out.reshape(384, 1024).cpu()
+    if out_dtype == torch.float16:
+        ref = oracle.epilogue_f16(acc, s, ws.numpy(), bias.numpy())
+        np.testing.assert_array_equal(got.view(torch.int16).numpy().view(np.uint16), ref)
+        # one rounding, not two: some values differ from the bf16 output cast to fp16
+        via_bf16 = inputs.from_bits(oracle.epilogue_bf16(acc, s, ws.numpy(), bias.numpy())).to(torch.float16)
+        assert not torch.equal(got, via_bf16)
+    else:
+        ref = oracle.epilogue_f32(acc, s, ws.numpy(), bias.numpy())
+        np.testing.assert_array_equal(got.numpy().view(np.uint32), ref.view(np.uint32))
 
 
 def test_int8_linear_ffn_down_gelu(gpu_device):

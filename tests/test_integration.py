@@ -134,6 +134,93 @@ def test_int8_linear_contract(monkeypatch):
     assert out.shape == (2, 5, 48)
 
 
+# The keyword set comfy-kitchen's registry validates and forwards to a
+# registered backend's int8_linear: the params of the plugin's "int8_linear"
+# FunctionConstraints (comfyui_turing_utils/quantization/dispatch.py:879-898),
+# which are the parameters of dispatch.int8_linear (dispatch.py:618-627).
+KITCHEN_INT8_LINEAR_PARAMS = ("x", "weight", "weight_scale", "bias", "out_dtype", "convrot", "convrot_groupsize",
+                              "input_act")
+
+
+def _record_linear_ops(monkeypatch):
+    """Wraps the quantizer and GEMM ops the linear path calls (their fake
+    implementations on meta tensors) and records what each received."""
+    import comfyui_turing_utils_kernel.integration as integ
+
+    calls = []
+    real = torch.ops.turing_utils
+
+    class Ops:
+        def __getattr__(self, name):
+            op = getattr(real, name)
+
+            def wrapped(*args, **kwargs):
+                calls.append((name, args, kwargs))
+                return op(*args, **kwargs)
+
+            return wrapped
+
+    class Torch:  # integration.torch with .ops.turing_utils recorded
+        def __getattr__(self, name):
+            return getattr(torch, name)
+
+    fake_torch = Torch()
+    fake_torch.ops = type("O", (), {"turing_utils": Ops()})()
+    monkeypatch.setattr(integ, "torch", fake_torch)
+    monkeypatch.setattr(integ, "is_supported_device", lambda device: True)
+    return calls
+
+
+def test_int8_linear_takes_the_plugin_call_forms(monkeypatch):
+    """Every argument set through which the plugin reaches int8_linear, as
+    literals, against integration.int8_linear (the function a gfx950 build
+    registers or calls in dispatch.int8_linear's place):
+      * Kitchen registry: all eight keywords (dispatch.py:879-898);
+      * the W8A8 preflight's Kitchen calls (dispatch.py:245-252, :256-264):
+        (x, weight, weight_scale) positional, then out_dtype, convrot,
+        convrot_groupsize and input_act by keyword;
+      * the fused-activation linear (fusions.py:80-89): (x, qdata, scale)
+        positional, bias, out_dtype=x.dtype, convrot=True, convrot_groupsize
+        and input_act by keyword.
+    Each must reach the quantizer with the caller's group and activation and
+    the GEMM op of the caller's out_dtype, without importing comfy_kitchen."""
+    import sys
+
+    assert tuple(inspect.signature(integration.int8_linear).parameters) == KITCHEN_INT8_LINEAR_PARAMS
+    calls = _record_linear_ops(monkeypatch)
+    x = torch.empty((2, 16, 256), dtype=torch.bfloat16, device="meta")
+    w = torch.empty((64, 256), dtype=torch.int8, device="meta")
+    ws = torch.empty((), dtype=torch.float32, device="meta")
+    bias = torch.empty((64,), dtype=torch.bfloat16, device="meta")
+
+    registry_kwargs = dict(x=x, weight=w, weight_scale=ws, bias=bias, out_dtype=torch.float16, convrot=True,
+                           convrot_groupsize=256, input_act=None)
+    assert tuple(registry_kwargs) == KITCHEN_INT8_LINEAR_PARAMS
+    out = integration.int8_linear(**registry_kwargs)
+    assert out.shape == (2, 16, 64) and out.dtype == torch.float16
+    assert [c[0] for c in calls] == ["bf16_int8_convrot_quantize", "int8_linear_out"]
+    assert calls[0][1][1] == 256 and calls[0][2] == {"swiglu": False}
+    assert calls[1][1][5] is torch.float16
+
+    calls.clear()  # preflight form, bf16 out
+    out = integration.int8_linear(x, w, ws, out_dtype=torch.bfloat16, convrot=True, convrot_groupsize=256)
+    assert out.dtype == torch.bfloat16 and [c[0] for c in calls] == ["bf16_int8_convrot_quantize", "int8_linear"]
+
+    calls.clear()  # preflight SwiGLU form
+    xs = torch.empty((2, 16, 512), dtype=torch.bfloat16, device="meta")
+    out = integration.int8_linear(xs, w, ws, out_dtype=torch.bfloat16, convrot=True, convrot_groupsize=256,
+                                  input_act="swiglu")
+    assert out.shape == (2, 16, 64) and calls[0][2] == {"swiglu": True}
+
+    calls.clear()  # fusions.py form, GELU folded, fp32 out
+    out = integration.int8_linear(x, w, ws, bias=bias, out_dtype=torch.float32, convrot=True,
+                                  convrot_groupsize=128, input_act="gelu_tanh")
+    assert out.dtype == torch.float32
+    assert [c[0] for c in calls] == ["bf16_gelu_int8_convrot_quantize", "int8_linear_out"]
+    assert calls[0][1][1] == 128 and calls[1][1][5] is torch.float32
+    assert "comfy_kitchen" not in sys.modules
+
+
 def test_int8_linear_declines_what_it_cannot_serve():
     x = torch.zeros((3, 256), dtype=torch.bfloat16)
     w = torch.zeros((16, 256), dtype=torch.int8)

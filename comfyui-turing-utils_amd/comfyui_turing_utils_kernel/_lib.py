@@ -44,6 +44,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _i32,
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _c_void_p],
     ),
+    "tu_int8_gemm_ex": (
+        _i32,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i32, _i64, _i64, _i64, _i32, _c_void_p],
+    ),
+    "tu_int8_gemm_tile_policy": (_i32, [_i64, _i64, _i32]),
     "tu_int8_gemm_bf16_residual": (
         _i32,
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p, _i64, _i64,

@@ -44,7 +44,9 @@
 namespace tu {
 namespace {
 
-constexpr int kBM = 256;  // activation rows per workgroup
+// Activation rows per workgroup: 256, or 128 for grids that 256-row tiles
+// would fill in few, partly empty rounds (the tile policy; the wave grid and
+// the weight tile stay the same).
 constexpr int kBN = 256;  // weight rows (output columns) per workgroup
 constexpr int kBK = 128;  // bytes of K per step (two 64-deep MFMA slices)
 // Waves per workgroup: 2 along the weight rows x kWavesM along the activation
@@ -55,57 +57,69 @@ constexpr int kBK = 128;  // bytes of K per step (two 64-deep MFMA slices)
 constexpr int kWavesM = TU_GEMM_WAVES_M;
 constexpr int kWaves = 2 * kWavesM;
 constexpr int kThreads = 64 * kWaves;
-constexpr int kFragsM = kBM / kWavesM / 16;  // 16-row activation fragments per wave
 constexpr int kGroupM = 4;
-// MFMAs of slice 0 issued before the step's barrier, covering the latency of
-// slice 1's LDS reads.
-#ifndef TU_GEMM_PRE
-#define TU_GEMM_PRE 16
+#ifndef TU_GEMM_HALF_TILE_COST
+#define TU_GEMM_HALF_TILE_COST 0.635
 #endif
-constexpr int kPre = TU_GEMM_PRE;
+
+// Geometry of a workgroup tile with BM activation rows.
+template <int BM>
+struct Tile {
+    static_assert(BM == 256 || BM == 128, "activation tile of 256 or 128 rows");
+    static constexpr int kFragsM = BM / kWavesM / 16;  // 16-row activation fragments per wave
+    static constexpr int kMma = 8 * kFragsM;           // MFMAs per 64-deep slice and wave
+    // MFMAs of slice 0 issued before the step's barrier, covering the latency
+    // of slice 1's LDS reads (the rest cover the next step's loads)
+    static constexpr int kPre = BM == 256 ? 16 : 8;
+    static constexpr int kABlocks = BM * 128 / 1024 / kWaves;   // 1 KiB activation blocks per wave and step
+    static constexpr int kWBlocks = kBN * 128 / 1024 / kWaves;  // 1 KiB weight blocks per wave and step
+    static constexpr int kLoads = kABlocks + kWBlocks;          // vector-memory loads per wave and step
+    static constexpr int kStageBytes = (BM + kBN) * 128;        // activation panel + weight panel
+    static constexpr int kChunksA = BM * 8 / kThreads;          // 16-byte chunks per thread, register path
+    static constexpr int kChunksW = kBN * 8 / kThreads;
+};
 
 // LDS panel layout: 128-byte rows, the 16-byte chunk index XOR-swizzled with
 // row bits 1..3 (measured bank-conflict free for 16 lanes reading one chunk
 // of 16 consecutive rows; 64-byte rows with a 2-bit swizzle were not).
 __device__ __forceinline__ int swz(int row, int chunk) { return row * kBK + ((chunk ^ ((row >> 1) & 7)) << 4); }
 
+template <int BM>
 struct TileLoad {
-    i32x4 a[2048 / kThreads];
-    i32x4 w[2048 / kThreads];
+    i32x4 a[Tile<BM>::kChunksA];
+    i32x4 w[Tile<BM>::kChunksW];
 };
 
-// Loads the 256 x 64 B activation and weight panels of step k0 into registers.
-// Rows past the end are clamped (their results are never stored); columns past
-// K are zero.
-__device__ __forceinline__ void load_tiles(TileLoad &t, const int8_t *__restrict__ a,
+// Loads the BM x 128 B activation and 256 x 128 B weight panels of step k0
+// into registers.  Rows past the end are clamped (their results are never
+// stored); columns past K are zero.
+template <int BM>
+__device__ __forceinline__ void load_tiles(TileLoad<BM> &t, const int8_t *__restrict__ a,
                                            const int8_t *__restrict__ w, int64_t m0, int64_t n0,
                                            int64_t m, int64_t n, int64_t k, int64_t k0, int tid) {
 #pragma unroll
-    for (int i = 0; i < 2048 / kThreads; ++i) {
+    for (int i = 0; i < Tile<BM>::kChunksW; ++i) {
         const int id = tid + kThreads * i;
         const int row = id >> 3;
-        const int chunk = id & 7;
-        const int64_t kk = k0 + chunk * 16;
-        const int64_t ra = min(m0 + row, m - 1);
+        const int64_t kk = k0 + (id & 7) * 16;
         const int64_t rw = min(n0 + row, n - 1);
-        if (kk < k) {
-            t.a[i] = *reinterpret_cast<const i32x4 *>(a + ra * k + kk);
-            t.w[i] = *reinterpret_cast<const i32x4 *>(w + rw * k + kk);
-        } else {
-            t.a[i] = i32x4{0, 0, 0, 0};
-            t.w[i] = i32x4{0, 0, 0, 0};
+        t.w[i] = kk < k ? *reinterpret_cast<const i32x4 *>(w + rw * k + kk) : i32x4{0, 0, 0, 0};
+        if (i < Tile<BM>::kChunksA) {
+            const int64_t ra = min(m0 + row, m - 1);
+            t.a[i] = kk < k ? *reinterpret_cast<const i32x4 *>(a + ra * k + kk) : i32x4{0, 0, 0, 0};
         }
     }
 }
 
-__device__ __forceinline__ void store_tiles(const TileLoad &t, int8_t *lds_a, int8_t *lds_w, int tid) {
+template <int BM>
+__device__ __forceinline__ void store_tiles(const TileLoad<BM> &t, int8_t *lds_a, int8_t *lds_w, int tid) {
 #pragma unroll
-    for (int i = 0; i < 2048 / kThreads; ++i) {
+    for (int i = 0; i < Tile<BM>::kChunksW; ++i) {
         const int id = tid + kThreads * i;
         const int row = id >> 3;
         const int chunk = id & 7;
-        *reinterpret_cast<i32x4 *>(lds_a + swz(row, chunk)) = t.a[i];
         *reinterpret_cast<i32x4 *>(lds_w + swz(row, chunk)) = t.w[i];
+        if (i < Tile<BM>::kChunksA) *reinterpret_cast<i32x4 *>(lds_a + swz(row, chunk)) = t.a[i];
     }
 }
 
@@ -132,30 +146,35 @@ __device__ __forceinline__ void tile_coords(int bid, int tiles_m, int tiles_n, i
 }
 
 constexpr int kStages = 2;
-constexpr int kStageBytes = 2 * kBM * kBK;  // activation panel + weight panel
 typedef __attribute__((address_space(3))) void lds_void;
 
 // Per-lane source offsets of the direct-to-LDS loads.  Wave w fills the 1 KiB
-// blocks w * kBlocksPerWave .. of each panel; in block b, lane l writes LDS row
-// 8 b + l / 8, physical chunk l % 8, which holds logical chunk
-// (l % 8) ^ ((row >> 1) & 7) of that row.  Offsets are relative to the
-// panel's first row at K offset 0 (32-bit: a panel row index times K plus a
-// chunk offset; rows past the end are clamped, their results never stored).
-constexpr int kBlocksPerWave = 32 / kWaves;  // 1 KiB blocks of each 32 KiB panel
-
+// blocks w * kABlocks .. of the activation panel and w * kWBlocks .. of the
+// weight panel; in block b, lane l writes LDS row 8 b + l / 8, physical chunk
+// l % 8, which holds logical chunk (l % 8) ^ ((row >> 1) & 7) of that row.
+// Offsets are relative to the panel's first row at K offset 0 (32-bit: a
+// panel row index times K plus a chunk offset; rows past the end are
+// clamped, their results never stored).
+template <int BM>
 struct LoadGeom {
-    uint32_t a_off[kBlocksPerWave];
-    uint32_t w_off[kBlocksPerWave];
+    uint32_t a_off[Tile<BM>::kABlocks];
+    uint32_t w_off[Tile<BM>::kWBlocks];
 };
 
-__device__ __forceinline__ LoadGeom load_geom(int64_t m0, int64_t n0, int64_t m, int64_t n, int64_t k, int wave,
-                                              int lane) {
-    LoadGeom gm;
+template <int BM>
+__device__ __forceinline__ LoadGeom<BM> load_geom(int64_t m0, int64_t n0, int64_t m, int64_t n, int64_t k, int wave,
+                                                  int lane) {
+    LoadGeom<BM> gm;
 #pragma unroll
-    for (int i = 0; i < kBlocksPerWave; ++i) {
-        const int row = 8 * (kBlocksPerWave * wave + i) + (lane >> 3);
+    for (int i = 0; i < Tile<BM>::kABlocks; ++i) {
+        const int row = 8 * (Tile<BM>::kABlocks * wave + i) + (lane >> 3);
         const int c = (lane & 7) ^ ((row >> 1) & 7);
         gm.a_off[i] = static_cast<uint32_t>((min(m0 + row, m - 1) - m0) * k + c * 16);
+    }
+#pragma unroll
+    for (int i = 0; i < Tile<BM>::kWBlocks; ++i) {
+        const int row = 8 * (Tile<BM>::kWBlocks * wave + i) + (lane >> 3);
+        const int c = (lane & 7) ^ ((row >> 1) & 7);
         gm.w_off[i] = static_cast<uint32_t>((min(n0 + row, n - 1) - n0) * k + c * 16);
     }
     return gm;
@@ -173,20 +192,30 @@ __device__ __forceinline__ const int8_t *uniform_ptr(const int8_t *p) {
 // Direct-to-LDS loads of one full K step into a ring stage: buffer loads with
 // the lane's 32-bit offset within the panel and the step's K offset k0 as
 // the scalar offset, so no 64-bit address is formed per load.
-__device__ __forceinline__ void issue_step(int8_t *stage, __amdgpu_buffer_rsrc_t ars, __amdgpu_buffer_rsrc_t wrs,
-                                           const LoadGeom &gm, uint32_t k0, int wave) {
-#pragma unroll
-    for (int i = 0; i < kBlocksPerWave; ++i) {
-        const int block = kBlocksPerWave * wave + i;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(ars, (lds_void *)(stage + block * 1024), 16, gm.a_off[i], k0, 0, 0);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(wrs, (lds_void *)(stage + kBM * kBK + block * 1024), 16, gm.w_off[i],
-                                                 k0, 0, 0);
+// One overload per tile height: the host compilation pass rejects a template
+// of this function (the buffer builtins exist only for the device target).
+#define TU_ISSUE_STEP_BODY(BM)                                                                                   \
+    _Pragma("unroll") for (int i = 0; i < Tile<BM>::kWBlocks; ++i) {                                            \
+        if (i < Tile<BM>::kABlocks)                                                                             \
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ars, (lds_void *)(stage + (Tile<BM>::kABlocks * wave + i) * 1024), \
+                                                     16, gm.a_off[i], k0, 0, 0);                                \
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(                                                               \
+            wrs, (lds_void *)(stage + BM * kBK + (Tile<BM>::kWBlocks * wave + i) * 1024), 16, gm.w_off[i], k0, 0, 0); \
     }
+__device__ __forceinline__ void issue_step(int8_t *stage, __amdgpu_buffer_rsrc_t ars, __amdgpu_buffer_rsrc_t wrs,
+                                           const LoadGeom<256> &gm, uint32_t k0, int wave) {
+    TU_ISSUE_STEP_BODY(256)
 }
+__device__ __forceinline__ void issue_step(int8_t *stage, __amdgpu_buffer_rsrc_t ars, __amdgpu_buffer_rsrc_t wrs,
+                                           const LoadGeom<128> &gm, uint32_t k0, int wave) {
+    TU_ISSUE_STEP_BODY(128)
+}
+#undef TU_ISSUE_STEP_BODY
 
+template <int BM>
 struct Frags {
-    i32x4 a[8];        // weight rows (MFMA A operand)
-    i32x4 b[kFragsM];  // activation rows (MFMA B operand)
+    i32x4 a[8];                     // weight rows (MFMA A operand)
+    i32x4 b[Tile<BM>::kFragsM];     // activation rows (MFMA B operand)
 };
 
 // (1, 1) in bf16: the gate of a residual add without one.
@@ -204,12 +233,15 @@ constexpr int kOutI32 = 3;   // the int32 accumulator (direct 16-byte stores)
 // residual and then written by the same lane, and no lane stores a chunk
 // that another lane reads (clamped reads past the last row feed only rows
 // that are never stored).
-template <int kOut, bool kResidual>
+template <int BM, int kOut, bool kResidual>
 __global__ __launch_bounds__(kThreads, kWaves / 4) void int8_gemm_kernel(
     const int8_t *__restrict__ a, const int8_t *__restrict__ w, const float *__restrict__ as,
     const float *__restrict__ ws, const float *__restrict__ bias, void *out,
     int64_t m, int64_t n, int64_t k, int tiles_m, int tiles_n, const uint16_t *residual, const uint16_t *gate,
     int64_t gate_rows) {
+    constexpr int kBM = BM;
+    constexpr int kFragsM = Tile<BM>::kFragsM;
+    constexpr int kStageBytes = Tile<BM>::kStageBytes;
     __shared__ __align__(1024) int8_t lds[kStages][kStageBytes];
 
     const int tid = threadIdx.x;
@@ -226,8 +258,8 @@ __global__ __launch_bounds__(kThreads, kWaves / 4) void int8_gemm_kernel(
     tn = __builtin_amdgcn_readfirstlane(tn);
     const int64_t m0 = static_cast<int64_t>(tm) * kBM;
     const int64_t n0 = static_cast<int64_t>(tn) * kBN;
-    const LoadGeom gm = load_geom(m0, n0, m, n, k, wave, lane);
-    // Buffer resources over the tile's two panels (256 rows of K bytes each,
+    const LoadGeom<BM> gm = load_geom<BM>(m0, n0, m, n, k, wave, lane);
+    // Buffer resources over the tile's two panels (BM and 256 rows of K bytes,
     // K < 2^17, so every offset fits in 32 bits).  The panel addresses are
     // uniform; passing them through readfirstlane keeps the resources in
     // scalar registers.
@@ -243,7 +275,7 @@ __global__ __launch_bounds__(kThreads, kWaves / 4) void int8_gemm_kernel(
     const int frag_row = lane & 15;
     const int frag_chunk = lane >> 4;
     // Fragments of 64-deep slice kk (0 or 1) of a stage.
-    auto load_frags = [&](Frags &f, const int8_t *stage, int kk) {
+    auto load_frags = [&](Frags<BM> &f, const int8_t *stage, int kk) {
         const int8_t *la = stage;
         const int8_t *lw = stage + kBM * kBK;
 #pragma unroll
@@ -254,7 +286,7 @@ __global__ __launch_bounds__(kThreads, kWaves / 4) void int8_gemm_kernel(
         for (int i = 0; i < 8; ++i)
             f.a[i] = *reinterpret_cast<const i32x4 *>(lw + swz(wn * 128 + i * 16 + frag_row, 4 * kk + frag_chunk));
     };
-    auto mma = [&](const Frags &f) {
+    auto mma = [&](const Frags<BM> &f) {
 #pragma unroll
         for (int i = 0; i < 8; ++i)
 #pragma unroll
@@ -263,7 +295,7 @@ __global__ __launch_bounds__(kThreads, kWaves / 4) void int8_gemm_kernel(
     };
     // MFMAs [b, e) of a slice in the same (i, j) order; b and e are constants
     // at every call, so the loop unrolls to fixed accumulator registers.
-    auto mma_part = [&](const Frags &f, int b, int e) {
+    auto mma_part = [&](const Frags<BM> &f, int b, int e) {
 #pragma unroll
         for (int x = b; x < e; ++x)
             acc[x / kFragsM][x % kFragsM] =
@@ -274,10 +306,10 @@ __global__ __launch_bounds__(kThreads, kWaves / 4) void int8_gemm_kernel(
     if (full > 0) {
         issue_step(lds[0], ars, wrs, gm, 0, wave);
         if (full > 1) issue_step(lds[1], ars, wrs, gm, kBK, wave);
-        if (full > 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * kBlocksPerWave));
+        if (full > 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(Tile<BM>::kLoads));
         else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
         __syncthreads();
-        Frags f0, f1;
+        Frags<BM> f0, f1;
         load_frags(f0, lds[0], 0);
         __builtin_amdgcn_s_waitcnt(lgkmcnt_imm(0));
         // One K step:
@@ -293,7 +325,7 @@ __global__ __launch_bounds__(kThreads, kWaves / 4) void int8_gemm_kernel(
         // branches, which the register allocation needs: the last two steps
         // load step full - 1 again into stages nobody reads any more, and
         // those loads are retired after the loop, before the ring is reused.
-        constexpr int kMma = 8 * kFragsM;
+        constexpr int kMma = Tile<BM>::kMma, kPre = Tile<BM>::kPre;
 #pragma clang loop unroll(disable)
         for (int s = 0; s < full; ++s) {
             const uint32_t k2 = static_cast<uint32_t>(min(s + 2, full - 1) * kBK);
@@ -305,7 +337,7 @@ __global__ __launch_bounds__(kThreads, kWaves / 4) void int8_gemm_kernel(
             issue_step(lds[s & 1], ars, wrs, gm, k2, wave);
             mma_part(f0, kPre, kMma);
 #pragma unroll
-            for (int i = 0; i < 2 * kBlocksPerWave; ++i) {
+            for (int i = 0; i < Tile<BM>::kLoads; ++i) {
                 __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             }
@@ -326,11 +358,11 @@ __global__ __launch_bounds__(kThreads, kWaves / 4) void int8_gemm_kernel(
     if (full * kBK < k) {
         // Partial last step: register loads with zero fill past K.
         __syncthreads();
-        TileLoad t;
-        load_tiles(t, a, w, m0, n0, m, n, k, static_cast<int64_t>(full) * kBK, tid);
-        store_tiles(t, lds[0], lds[0] + kBM * kBK, tid);
+        TileLoad<BM> t;
+        load_tiles<BM>(t, a, w, m0, n0, m, n, k, static_cast<int64_t>(full) * kBK, tid);
+        store_tiles<BM>(t, lds[0], lds[0] + kBM * kBK, tid);
         __syncthreads();
-        Frags f;
+        Frags<BM> f;
         load_frags(f, lds[0], 0);
         mma(f);
         load_frags(f, lds[0], 1);
@@ -548,7 +580,7 @@ int32_t check_gemm_args(const int8_t *a, const int8_t *w, const void *out, int64
     TU_REQUIRE(k % 16 == 0 && n % 8 == 0, "INT8 GEMM requires K%%16==0 and N%%8==0 (K=%lld N=%lld)",
                static_cast<long long>(k), static_cast<long long>(n));
     TU_REQUIRE(k < 131072, "INT8 GEMM K=%lld would overflow the int32 accumulator", static_cast<long long>(k));
-    TU_REQUIRE((m + kBM - 1) / kBM * ((n + kBN - 1) / kBN) < 0x7fffffff, "INT8 GEMM grid too large");
+    TU_REQUIRE((m + 127) / 128 * ((n + kBN - 1) / kBN) < 0x7fffffff, "INT8 GEMM grid too large");
     TU_REQUIRE(a && w && out, "INT8 GEMM pointers must be non-null");
     TU_REQUIRE((reinterpret_cast<uintptr_t>(a) & 15) == 0 && (reinterpret_cast<uintptr_t>(w) & 15) == 0,
                "INT8 GEMM operands must be 16-byte aligned");
@@ -556,15 +588,59 @@ int32_t check_gemm_args(const int8_t *a, const int8_t *w, const void *out, int64
     return require_gfx950();
 }
 
+// Compute units of the current device (cached per device id).
+int32_t device_cus(int &cus) {
+    static int cache[64];
+    int dev = 0;
+    hipError_t err = hipGetDevice(&dev);
+    if (err != hipSuccess) return fail("hipGetDevice failed: %s", hipGetErrorString(err));
+    if (dev >= 0 && dev < 64 && cache[dev] > 0) {
+        cus = cache[dev];
+        return 0;
+    }
+    err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (err != hipSuccess || cus <= 0) return fail("hipDeviceGetAttribute(CU count) failed: %s", hipGetErrorString(err));
+    if (dev >= 0 && dev < 64) cache[dev] = cus;
+    return 0;
+}
+
+// Time of a round of 128-row tiles relative to a round of 256-row tiles of the
+// same N and K, measured on MI355X: 0.635 at N 8960 / K 1536 and at N 5120 /
+// K 5120 (a tile's fixed part, the epilogue's stores and the first loads, does
+// not halve with its rows).
+constexpr double kHalfTileCost = TU_GEMM_HALF_TILE_COST;
+
+// Tile policy from the grid: one workgroup per CU, so tiles run in rounds of
+// `cus`; 128-row tiles are chosen when their rounds cost less than the
+// 256-row tiles' (a grid of a few, partly empty rounds).
+int pick_tile_policy(int64_t m, int64_t n, int cus) {
+    const int64_t tn = (n + kBN - 1) / kBN;
+    const int64_t r256 = ((m + 255) / 256 * tn + cus - 1) / cus;
+    const int64_t r128 = ((m + 127) / 128 * tn + cus - 1) / cus;
+    return static_cast<double>(r128) * kHalfTileCost < static_cast<double>(r256) ? TU_GEMM_TILE_128 : TU_GEMM_TILE_256;
+}
+
 template <int kOut, bool kResidual = false>
 int32_t launch_gemm(const int8_t *a, const int8_t *w, const float *as, const float *ws, const float *bias,
                     void *out, int64_t m, int64_t n, int64_t k, void *stream, const uint16_t *residual = nullptr,
-                    const uint16_t *gate = nullptr, int64_t gate_rows = 1) {
+                    const uint16_t *gate = nullptr, int64_t gate_rows = 1, int policy = TU_GEMM_TILE_AUTO) {
     if (m == 0) return 0;
-    const int tiles_m = static_cast<int>((m + kBM - 1) / kBM);
+    if (policy == TU_GEMM_TILE_AUTO) {
+        int cus = 0;
+        if (device_cus(cus)) return -1;
+        policy = pick_tile_policy(m, n, cus);
+    }
     const int tiles_n = static_cast<int>((n + kBN - 1) / kBN);
-    int8_gemm_kernel<kOut, kResidual><<<dim3(tiles_m * tiles_n), kThreads, 0, static_cast<hipStream_t>(stream)>>>(
-        a, w, as, ws, bias, out, m, n, k, tiles_m, tiles_n, residual, gate, gate_rows);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (policy == TU_GEMM_TILE_128) {
+        const int tiles_m = static_cast<int>((m + 127) / 128);
+        int8_gemm_kernel<128, kOut, kResidual><<<dim3(tiles_m * tiles_n), kThreads, 0, st>>>(
+            a, w, as, ws, bias, out, m, n, k, tiles_m, tiles_n, residual, gate, gate_rows);
+    } else {
+        const int tiles_m = static_cast<int>((m + 255) / 256);
+        int8_gemm_kernel<256, kOut, kResidual><<<dim3(tiles_m * tiles_n), kThreads, 0, st>>>(
+            a, w, as, ws, bias, out, m, n, k, tiles_m, tiles_n, residual, gate, gate_rows);
+    }
     return check_launch(kOut == kOutI32   ? "tu_int8_gemm_i32"
                         : kResidual       ? "tu_int8_gemm_bf16_residual"
                         : kOut == kOutF16 ? "tu_int8_gemm_f16"
@@ -653,4 +729,37 @@ extern "C" int32_t tu_dequant_i32_bf16(const int32_t *acc, int64_t acc_ld, const
         else dequant_kernel<false, false><<<grid, 256, 0, s>>>(acc, acc_ld, a_scale, w_scale, o, m, cols);
     }
     return check_launch("tu_dequant_i32_bf16");
+}
+
+extern "C" int32_t tu_int8_gemm_ex(const int8_t *a, const int8_t *w, const float *a_scale, const float *w_scale,
+                                   const float *bias, void *out, int32_t out_type, int64_t m, int64_t n, int64_t k,
+                                   int32_t tile_policy, void *stream) {
+    using namespace tu;
+    TU_REQUIRE(tile_policy == TU_GEMM_TILE_AUTO || tile_policy == TU_GEMM_TILE_256 || tile_policy == TU_GEMM_TILE_128,
+               "INT8 GEMM tile_policy must be 0 (auto), 1 (256 x 256) or 2 (128 x 256), got %d", tile_policy);
+    if (check_gemm_args(a, w, out, m, n, k)) return -1;
+    switch (out_type) {
+    case TU_OUT_I32:
+        return launch_gemm<kOutI32>(a, w, nullptr, nullptr, nullptr, out, m, n, k, stream, nullptr, nullptr, 1,
+                                    tile_policy);
+    case TU_OUT_BF16:
+        if (check_epilogue_args(a_scale, w_scale, bias)) return -1;
+        return launch_gemm<kOutBf16>(a, w, a_scale, w_scale, bias, out, m, n, k, stream, nullptr, nullptr, 1,
+                                     tile_policy);
+    case TU_OUT_F16:
+        if (check_epilogue_args(a_scale, w_scale, bias)) return -1;
+        return launch_gemm<kOutF16>(a, w, a_scale, w_scale, bias, out, m, n, k, stream, nullptr, nullptr, 1,
+                                    tile_policy);
+    case TU_OUT_F32:
+        if (check_epilogue_args(a_scale, w_scale, bias)) return -1;
+        return launch_gemm<kOutF32>(a, w, a_scale, w_scale, bias, out, m, n, k, stream, nullptr, nullptr, 1,
+                                    tile_policy);
+    default:
+        return fail("INT8 GEMM out_type must be 0 (bf16), 1 (fp16), 2 (fp32) or 3 (int32), got %d", out_type);
+    }
+}
+
+extern "C" int32_t tu_int8_gemm_tile_policy(int64_t m, int64_t n, int32_t cus) {
+    if (m <= 0 || n <= 0 || cus <= 0) return TU_GEMM_TILE_256;
+    return tu::pick_tile_policy(m, n, cus);
 }

@@ -110,6 +110,31 @@ int32_t tu_int8_gemm_f32(const int8_t *a, const int8_t *w, const float *a_scale,
                          const float *w_scale, const float *bias, float *out, int64_t m,
                          int64_t n, int64_t k, void *stream);
 
+/* Output types and tile policies of tu_int8_gemm_ex. */
+#define TU_OUT_BF16 0
+#define TU_OUT_F16 1
+#define TU_OUT_F32 2
+#define TU_OUT_I32 3
+#define TU_GEMM_TILE_AUTO 0 /* chosen from the grid: tu_int8_gemm_tile_policy */
+#define TU_GEMM_TILE_256 1  /* 256 x 256 output tiles */
+#define TU_GEMM_TILE_128 2  /* 128 (rows of a) x 256 output tiles */
+
+/* The GEMM above with its output type and tile policy as arguments: out_type
+ * TU_OUT_BF16 / _F16 / _F32 as tu_int8_gemm_bf16 / _f16 / _f32, TU_OUT_I32 as
+ * tu_int8_gemm_i32 (scales and bias ignored, may be NULL).  Every tile policy
+ * gives the same bits.  Replaces the low-level binding's tile_policy argument
+ * (kernel/csrc/bindings.cpp:872-879 -> kernel/csrc/turing/w4a8.cu:799-858,
+ * where policy 0 is the heuristic and 1-5 force a CUTLASS tile). */
+int32_t tu_int8_gemm_ex(const int8_t *a, const int8_t *w, const float *a_scale, const float *w_scale,
+                        const float *bias, void *out, int32_t out_type, int64_t m, int64_t n, int64_t k,
+                        int32_t tile_policy, void *stream);
+
+/* The tile policy TU_GEMM_TILE_AUTO picks for an m x n output on a device
+ * with `cus` compute units: TU_GEMM_TILE_128 when the 128-row tiles' rounds
+ * of `cus` workgroups cost less than the 256-row tiles' (host only, no HIP
+ * call).  Counterpart of the heuristic of w4a8.cu:837-851. */
+int32_t tu_int8_gemm_tile_policy(int64_t m, int64_t n, int32_t cus);
+
 /* The same GEMM with a gated residual add fused into the epilogue, for a DiT
  * block's x + y * gate: out[m][n] = bf16_rn(fma(y, g, residual[m][n])) with
  * y the tu_int8_gemm_bf16 value above, g = gate[m / gate_rows][n] (bf16 [G, n],

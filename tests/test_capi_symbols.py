@@ -92,6 +92,33 @@ def test_attention_key_split_plan(lib):
         assert 1 <= n <= 8 and (n == 1 or (tiles + n - 1) // n >= 16)
 
 
+def test_gemm_tile_policy_plan(lib):
+    """The GEMM's tile policy is host arithmetic over rounds of one workgroup
+    per CU: the four config-4 shapes (10-30 full rounds of 256-row tiles)
+    keep 256-row tiles; grids of a few partly empty rounds take 128-row tiles
+    when their rounds (each 0.635 of a 256-row round, measured) cost less,
+    which config 1 (3 rounds against 5) does not;
+    bad arguments fall back to 256-row tiles.  tu_int8_gemm_ex refuses an
+    unknown policy or output type before any HIP call."""
+    pol = lambda m, n, cus=256: lib.tu_int8_gemm_tile_policy(m, n, cus)  # noqa: E731
+    for n in (15360, 5120, 13824):
+        assert pol(32760, n) == 1
+    assert pol(4096, 8960) == 1                  # config 1: 3 rounds against 5 x 0.635
+    assert pol(2048, 8960) == 2                  # 2 rounds against 3 x 0.635
+    assert pol(256 * 16, 256 * 16) == 1          # exactly one full round
+    assert pol(300, 264) == 2                    # 4 tiles or 6 half tiles: one round either way
+    assert pol(0, 8960) == 1 and pol(4096, 8960, 0) == 1
+    for m, n in ((4096, 8960), (8192, 8960), (2048, 3072), (32760, 15360)):
+        # the rule: 128-row tiles when their rounds x the half-tile cost are fewer
+        t256 = -(-m // 256) * -(-n // 256)
+        t128 = -(-m // 128) * -(-n // 256)
+        r256, r128 = -(-t256 // 256), -(-t128 // 256)
+        assert pol(m, n) == (2 if r128 * 0.635 < r256 else 1)
+    assert lib.tu_int8_gemm_ex(None, None, None, None, None, None, 0, 16, 16, 16, 3, None) != 0
+    assert b"tile_policy" in lib.tu_last_error()
+    assert lib.tu_int8_gemm_ex(None, None, None, None, None, None, 7, 16, 16, 16, 0, None) != 0
+
+
 def test_attention_split_arguments_are_refused_on_the_host(lib):
     """tu_sage_attn_fwd_split checks its split count and workspace before any
     HIP call: more ranges than key tiles, more than 256, or a missing or

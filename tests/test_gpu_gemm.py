@@ -301,3 +301,62 @@ def test_int8_linear_out_config1_rows(gpu_device, out_dtype):
     _linear_out_check(out[torch.from_numpy(rows).to(dev)], acc, s.cpu().reshape(-1)[rows], ws, bias, out_dtype)
     if out_dtype == torch.float32:
         assert torch.equal(out.to(torch.bfloat16), bf)
+
+
+OUT_TYPES = {"bf16": (0, torch.bfloat16), "f16": (1, torch.float16), "f32": (2, torch.float32), "i32": (3, torch.int32)}
+
+
+@pytest.mark.parametrize("policy", [1, 2])
+@pytest.mark.parametrize("out", sorted(OUT_TYPES))
+@pytest.mark.parametrize("m,n,k", [(1, 8, 16), (129, 8, 256), (300, 264, 192), (513, 520, 1040), (257, 264, 384),
+                                   (200, 1024, 5120)])
+def test_gemm_tile_policies_exact(gpu_device, m, n, k, out, policy):
+    """tu_int8_gemm_ex with each tile policy forced (1: 256 x 256 tiles, 2:
+    128 x 256) and each output type: bit-exact against the oracle on ragged M
+    and N tiles, partial last K steps and one-tile grids."""
+    from comfyui_turing_utils_kernel import _lib
+
+    print(f"[gemm ex] m={m} n={n} k={k} out={out} policy={policy}", flush=True)
+    code, dtype = OUT_TYPES[out]
+    a = _rand_i8((m, k), 3 * m + k)
+    w, ws, bias = inputs.weights(n, k, 23, True)
+    g = torch.Generator().manual_seed(m)
+    as_ = torch.empty(m).uniform_(1e-3, 1e-1, generator=g)
+    dev = gpu_device
+    ad, wd, asd, wsd, bd = a.to(dev), w.to(dev), as_.to(dev), ws.to(dev), bias.to(dev)
+    res = torch.empty((m, n), dtype=dtype, device=dev)
+    with torch.cuda.device(dev):
+        _lib.call("tu_int8_gemm_ex", ad.data_ptr(), wd.data_ptr(), asd.data_ptr(), wsd.data_ptr(), bd.data_ptr(),
+                  res.data_ptr(), code, m, n, k, policy, _lib.stream_of(dev))
+    torch.cuda.synchronize(dev)
+    acc = oracle.int8_gemm_i32(a.numpy(), w.numpy())
+    if out == "i32":
+        np.testing.assert_array_equal(res.cpu().numpy(), acc)
+    elif out == "bf16":
+        np.testing.assert_array_equal(inputs.bits(res), oracle.epilogue_bf16(acc, as_.numpy(), ws.numpy(), bias.numpy()))
+    else:
+        _linear_out_check(res, acc, as_, ws, bias, dtype)
+
+
+@pytest.mark.parametrize("policy", [1, 2])
+def test_gemm_tile_policies_config1(gpu_device, policy):
+    """Config 1 (4096 x 1536 -> 8960, bias) with each tile policy: identical
+    bf16 output, 128 sampled rows bit-exact against the oracle."""
+    from comfyui_turing_utils_kernel import _lib
+
+    x = inputs.activation(4096, 1536, 0)
+    w, ws, bias = inputs.weights(8960, 1536, 0)
+    dev = gpu_device
+    q, s = torch.ops.turing_utils.bf16_int8_convrot_quantize(x.to(dev), 128)
+    wd, wsd, bd = w.to(dev), ws.to(dev), bias.to(dev)
+    out = torch.empty((4096, 8960), dtype=torch.bfloat16, device=dev)
+    with torch.cuda.device(dev):
+        _lib.call("tu_int8_gemm_ex", q.data_ptr(), wd.data_ptr(), s.data_ptr(), wsd.data_ptr(), bd.data_ptr(),
+                  out.data_ptr(), 0, 4096, 8960, 1536, policy, _lib.stream_of(dev))
+    ref_op = torch.ops.turing_utils.int8_linear(q, wd, s, wsd, bd)
+    torch.cuda.synchronize(dev)
+    assert torch.equal(out, ref_op)
+    rows = np.sort(np.random.default_rng(2).choice(4096, 128, replace=False))
+    acc = oracle.int8_gemm_i32(q.cpu().numpy()[rows], w.numpy())
+    ref = oracle.epilogue_bf16(acc, s.cpu().numpy().reshape(-1)[rows], ws.numpy(), bias.numpy())
+    np.testing.assert_array_equal(inputs.bits(out)[rows], ref)

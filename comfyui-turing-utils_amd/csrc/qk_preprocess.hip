@@ -25,7 +25,9 @@
 // consecutive lanes, so the head-scope sum is a lane butterfly.  The
 // normalized tile goes through LDS once so RoPE can take its pair partner
 // from any pack (split-half pairs and partial rot_dim included).  Row-scope
-// rrms comes from a one-wave-per-token pre-pass into caller scratch.
+// rrms comes from a pre-pass into caller scratch.  Interleaved RoPE over the
+// whole head (or none) takes a fast path that processes a group of heads per
+// workgroup (qk_rope_quant_heads_kernel).
 #include <type_traits>
 
 #include "w8a8_common.h"
@@ -295,45 +297,216 @@ __global__ __launch_bounds__(kQkThreads) void qk_rope_quant_kernel(QkArgs args) 
     }
 }
 
-// Row-scope rrms: one wave per (token, batch) of Q then K.  Each group of
-// D/8 lanes reduces one head's sum of squares (same order as the head
-// scope); the head sums are then added in head order.
-template <bool kFp16, int D>
-__global__ __launch_bounds__(64) void row_rrms_kernel(QkArgs args) {
+// Fast path for interleaved RoPE over the whole head (or no RoPE) with the
+// frequencies in their contiguous [.., pair, 2, 2] layout: one workgroup
+// (4 wave64) per 64-token chunk and group of kHeadGroup heads of Q or of K,
+// chunk-major.  Wave w owns tokens 16 w .. 16 w + 15 of the chunk (one Q
+// scale tile); lane l owns pack l % P of tokens 16 w + l / P + (64 / P) i,
+// i < kItems (P = D / 8 packs a token).  A lane's frequency words and
+// row-scope rrms do not depend on the head, so they are loaded once per chunk
+// and kept in registers for the group's heads (the general kernel reads the
+// frequency table again for every head).  The Q amax is a wave reduction;
+// K's 64-token amax adds one LDS exchange per head.  Per element the
+// arithmetic is the general kernel's, operation for operation.
+#ifndef TU_QK_HEAD_GROUP
+#define TU_QK_HEAD_GROUP 8
+#endif
+constexpr int kHeadGroup = TU_QK_HEAD_GROUP;
+
+template <bool kFp16, int D, bool kRow, bool kRope>
+__global__ __launch_bounds__(kQkThreads) void qk_rope_quant_heads_kernel(QkArgs args) {
     constexpr int kPacks = D / 8;
-    constexpr int kHeadsPerPass = 64 / kPacks;
-    const int lane = threadIdx.x;
+    constexpr int kTokStep = 64 / kPacks;   // tokens one lane row of a wave covers
+    constexpr int kItems = 16 / kTokStep;   // (token, pack) items per lane
+    __shared__ float kamax[2][kQkThreads / 64];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t b = blockIdx.y;
-    int64_t t = blockIdx.x;
-    const int which = t < args.len[0] ? 0 : 1;
-    if (which) t -= args.len[0];
+    const int64_t nch_q = (args.len[0] + kChunk - 1) / kChunk;
+    const int64_t grp_q = (args.heads[0] + kHeadGroup - 1) / kHeadGroup;
+    int64_t task = blockIdx.x;
+    const int which = task < grp_q * nch_q ? 0 : 1;
+    if (which) task -= grp_q * nch_q;
+    const int64_t len = args.len[which];
     const int64_t heads = args.heads[which];
-    const uint16_t *xrow = args.x[which] + b * args.x_sb[which] + t * args.x_sl[which];
-    const int grp = lane / kPacks, pack = lane % kPacks;
-    float total = 0.0f;
-    for (int64_t h0 = 0; h0 < heads; h0 += kHeadsPerPass) {
-        const int64_t h = h0 + grp;
-        u32x4 raw = u32x4{0u, 0u, 0u, 0u};
-        if (h < heads) raw = *reinterpret_cast<const u32x4 *>(xrow + h * args.x_sh[which] + pack * 8);
-        float s = 0.0f;
+    const int64_t groups = (heads + kHeadGroup - 1) / kHeadGroup;
+    const int64_t chunk = task / groups;
+    const int64_t h0 = (task - chunk * groups) * kHeadGroup;
+    const int hn = static_cast<int>(min<int64_t>(kHeadGroup, heads - h0));
+    const int pack = lane % kPacks;
+    const int64_t tok0 = chunk * kChunk + 16 * wave + lane / kPacks;
+
+    bool valid[kItems];
+    float rr[kItems];
+    u32x4 fa[kItems], fb[kItems];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const float lo = t_to_f32<kFp16>(raw[j] & 0xffffu), hi = t_to_f32<kFp16>(raw[j] >> 16);
-            s = __builtin_fmaf(lo, lo, s);
-            s = __builtin_fmaf(hi, hi, s);
-        }
-#pragma unroll
-        for (int off = kPacks / 2; off > 0; off >>= 1) s = s + __shfl_xor(s, off, kPacks);
-        // Heads of this pass in order (group leaders at lanes g * kPacks).
-#pragma unroll
-        for (int g = 0; g < kHeadsPerPass; ++g) {
-            const float hs = __shfl(s, g * kPacks, 64);
-            if (h0 + g < heads) total = total + hs;
+    for (int i = 0; i < kItems; ++i) {
+        const int64_t t = tok0 + kTokStep * i;
+        valid[i] = t < len;
+        rr[i] = 0.0f;
+        if constexpr (kRow) rr[i] = valid[i] ? args.rrms[which][b * len + t] : 0.0f;
+        fa[i] = fb[i] = u32x4{0u, 0u, 0u, 0u};
+        if constexpr (kRope) {
+            if (valid[i]) {
+                const uint16_t *frow = args.freqs + (args.f_batches == 1 ? 0 : b) * args.f_sb +
+                                       (args.f_len == 1 ? 0 : t) * args.f_sl + pack * 16;
+                fa[i] = *reinterpret_cast<const u32x4 *>(frow);
+                fb[i] = *reinterpret_cast<const u32x4 *>(frow + 8);
+            }
         }
     }
-    if (lane == 0) {
+    const int64_t nt = args.ntiles[which];
+    // the group's rows one head ahead: head hh + 1's loads are in flight
+    // while head hh is computed
+    const uint16_t *xtok = args.x[which] + b * args.x_sb[which] + pack * 8;
+    const int64_t x_sh = args.x_sh[which], x_sl = args.x_sl[which];
+    auto load_head = [&](int64_t h, u32x4 (&r)[kItems]) {
+#pragma unroll
+        for (int i = 0; i < kItems; ++i)
+            r[i] = valid[i] ? *reinterpret_cast<const u32x4 *>(xtok + h * x_sh + (tok0 + kTokStep * i) * x_sl)
+                            : u32x4{0u, 0u, 0u, 0u};
+    };
+    u32x4 next[kItems];
+    load_head(h0, next);
+    for (int hh = 0; hh < hn; ++hh) {
+        const int64_t h = h0 + hh;
+        const u32x4 wraw = *reinterpret_cast<const u32x4 *>(args.norm[which] + (kRow ? h * D : 0) + pack * 8);
+        u32x4 raw[kItems];
+#pragma unroll
+        for (int i = 0; i < kItems; ++i) raw[i] = next[i];
+        if (hh + 1 < hn) load_head(h + 1, next);
+        float y[kItems][8];
+        float amax = 0.0000001f;
+#pragma unroll
+        for (int i = 0; i < kItems; ++i) {
+            float v[8];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                v[2 * j] = t_to_f32<kFp16>(raw[i][j] & 0xffffu);
+                v[2 * j + 1] = t_to_f32<kFp16>(raw[i][j] >> 16);
+            }
+            float rrms;
+            if constexpr (kRow) {
+                rrms = rr[i];
+            } else {
+                // every lane of the token's pack group takes part, valid or not
+                float sq = 0.0f;
+#pragma unroll
+                for (int c = 0; c < 8; ++c) sq = __builtin_fmaf(v[c], v[c], sq);
+#pragma unroll
+                for (int off = kPacks / 2; off > 0; off >>= 1) sq = sq + __shfl_xor(sq, off, kPacks);
+                rrms = 1.0f / __builtin_sqrtf(sq / static_cast<float>(D) + args.eps);
+            }
+            float a[8];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                a[2 * j] = t_round<kFp16>((v[2 * j] * rrms) * t_to_f32<kFp16>(wraw[j] & 0xffffu));
+                a[2 * j + 1] = t_round<kFp16>((v[2 * j + 1] * rrms) * t_to_f32<kFp16>(wraw[j] >> 16));
+            }
+            float pmax = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                float val = a[j];
+                if constexpr (kRope) {
+                    // pair j >> 1 of the pack; its matrix row j & 1
+                    const int pi = j >> 1, comp = j & 1;
+                    const uint32_t word = (pi < 2 ? fa[i] : fb[i])[(pi & 1) * 2 + comp];
+                    const float f0 = t_to_f32<kFp16>(word & 0xffffu), f1 = t_to_f32<kFp16>(word >> 16);
+                    val = t_round<kFp16>(__builtin_fmaf(f1, a[2 * pi + 1], f0 * a[2 * pi]));
+                }
+                y[i][j] = val;
+                pmax = fmaxf(pmax, fabsf(val));
+            }
+            if (valid[i]) amax = fmaxf(amax, pmax);
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+        float inv;
+        if (which == 0) {
+            if (lane == 0) args.scale[0][(b * heads + h) * nt + chunk * 4 + wave] = amax / 127.0f;
+            inv = 127.0f / amax;
+        } else {
+            if (lane == 0) kamax[hh & 1][wave] = amax;
+            __syncthreads();
+            float kmax = 0.0000001f;
+#pragma unroll
+            for (int w = 0; w < kQkThreads / 64; ++w) kmax = fmaxf(kmax, kamax[hh & 1][w]);
+            if (tid == 0) args.scale[1][(b * heads + h) * nt + chunk] = kmax / 127.0f;
+            inv = 127.0f / kmax;
+        }
+        int8_t *obase = args.out[which] + b * args.o_sb[which] + h * args.o_sh[which];
+#pragma unroll
+        for (int i = 0; i < kItems; ++i) {
+            if (!valid[i]) continue;
+            uint32_t w2[2] = {0u, 0u};
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float r = fminf(127.0f, fmaxf(-127.0f, __builtin_rintf(y[i][j] * inv)));
+                w2[j >> 2] |= (static_cast<uint32_t>(static_cast<int32_t>(r)) & 0xffu) << (8 * (j & 3));
+            }
+            *reinterpret_cast<u32x2 *>(obase + (tok0 + kTokStep * i) * args.o_sl[which] + pack * 8) = u32x2{w2[0], w2[1]};
+        }
+    }
+}
+
+// Row-scope rrms, batched: one wave per 64 / P tokens (P = D / 8 packs a
+// token), four waves a workgroup, Q tokens then K tokens.  Each lane group of
+// P lanes owns a token; the heads' loads go out kRrmsBatch at a time, and the
+// per-head sums are the general pre-pass's (8-channel FMA chain, butterfly
+// across the packs), added to the token's total in head order.
+constexpr int kRrmsBatch = 8;
+
+template <bool kFp16, int D>
+__global__ __launch_bounds__(kQkThreads) void row_rrms_batched_kernel(QkArgs args) {
+    constexpr int kPacks = D / 8;
+    constexpr int kTokPerWave = 64 / kPacks;
+    constexpr int kTokPerBlock = kTokPerWave * kQkThreads / 64;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int64_t b = blockIdx.y;
+    const int64_t nblk_q = (args.len[0] + kTokPerBlock - 1) / kTokPerBlock;
+    int64_t blk = blockIdx.x;
+    const int which = blk < nblk_q ? 0 : 1;
+    if (which) blk -= nblk_q;
+    const int64_t len = args.len[which];
+    const int64_t t = blk * kTokPerBlock + (tid >> 6) * kTokPerWave + lane / kPacks;
+    const int pack = lane % kPacks;
+    const bool valid = t < len;
+    const int64_t heads = args.heads[which];
+    const uint16_t *xrow = args.x[which] + b * args.x_sb[which] + (valid ? t : 0) * args.x_sl[which] + pack * 8;
+    float total = 0.0f;
+    // one batch of heads ahead: batch n + 1's loads are in flight while
+    // batch n is summed
+    const int64_t x_sh = args.x_sh[which];
+    auto load_batch = [&](int64_t h0, u32x4 (&r)[kRrmsBatch]) {
+#pragma unroll
+        for (int g = 0; g < kRrmsBatch; ++g)
+            r[g] = valid && h0 + g < heads ? *reinterpret_cast<const u32x4 *>(xrow + (h0 + g) * x_sh)
+                                           : u32x4{0u, 0u, 0u, 0u};
+    };
+    u32x4 next[kRrmsBatch];
+    load_batch(0, next);
+    for (int64_t h0 = 0; h0 < heads; h0 += kRrmsBatch) {
+        u32x4 raw[kRrmsBatch];
+#pragma unroll
+        for (int g = 0; g < kRrmsBatch; ++g) raw[g] = next[g];
+        if (h0 + kRrmsBatch < heads) load_batch(h0 + kRrmsBatch, next);
+#pragma unroll
+        for (int g = 0; g < kRrmsBatch; ++g) {
+            float s = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float lo = t_to_f32<kFp16>(raw[g][j] & 0xffffu), hi = t_to_f32<kFp16>(raw[g][j] >> 16);
+                s = __builtin_fmaf(lo, lo, s);
+                s = __builtin_fmaf(hi, hi, s);
+            }
+#pragma unroll
+            for (int off = kPacks / 2; off > 0; off >>= 1) s = s + __shfl_xor(s, off, kPacks);
+            if (h0 + g < heads) total = total + s;
+        }
+    }
+    if (valid && pack == 0) {
         const float r = 1.0f / __builtin_sqrtf(total / static_cast<float>(heads * D) + args.eps);
-        args.rrms[which][b * args.len[which] + t] = r;
+        args.rrms[which][b * len + t] = r;
     }
 }
 
@@ -415,9 +588,30 @@ void launch_quant(const QkArgs &args, dim3 grid, bool split, bool row, hipStream
 
 template <bool kFp16, int D>
 int32_t launch_qk(const QkArgs &args, int64_t batch, bool split, bool row, bool rotate, hipStream_t s) {
+    // interleaved RoPE over the whole head (contiguous frequencies) or none,
+    // no rotation: the head-group fast path
+    const bool fast = !rotate && !split && (args.rot_dim == 0 || (args.rot_dim == D && args.f_contig));
     if (row) {
-        const dim3 g(static_cast<unsigned>(args.len[0] + args.len[1]), static_cast<unsigned>(batch));
-        row_rrms_kernel<kFp16, D><<<g, 64, 0, s>>>(args);
+        constexpr int kTokPerBlock = 64 / (D / 8) * kQkThreads / 64;
+        const dim3 g(static_cast<unsigned>((args.len[0] + kTokPerBlock - 1) / kTokPerBlock +
+                                           (args.len[1] + kTokPerBlock - 1) / kTokPerBlock),
+                     static_cast<unsigned>(batch));
+        row_rrms_batched_kernel<kFp16, D><<<g, kQkThreads, 0, s>>>(args);
+    }
+    if (fast) {
+        const int64_t gq = (args.heads[0] + kHeadGroup - 1) / kHeadGroup;
+        const int64_t gk = (args.heads[1] + kHeadGroup - 1) / kHeadGroup;
+        const dim3 grid(static_cast<unsigned>(gq * ((args.len[0] + kChunk - 1) / kChunk) +
+                                              gk * ((args.len[1] + kChunk - 1) / kChunk)),
+                        static_cast<unsigned>(batch));
+        if (args.rot_dim == 0) {
+            if (row) qk_rope_quant_heads_kernel<kFp16, D, true, false><<<grid, kQkThreads, 0, s>>>(args);
+            else qk_rope_quant_heads_kernel<kFp16, D, false, false><<<grid, kQkThreads, 0, s>>>(args);
+        } else {
+            if (row) qk_rope_quant_heads_kernel<kFp16, D, true, true><<<grid, kQkThreads, 0, s>>>(args);
+            else qk_rope_quant_heads_kernel<kFp16, D, false, true><<<grid, kQkThreads, 0, s>>>(args);
+        }
+        return check_launch("tu_qk_rms_rope_int8");
     }
     if (args.anchors != nullptr) {
         const dim3 ga(static_cast<unsigned>(args.heads[1]), static_cast<unsigned>(batch));

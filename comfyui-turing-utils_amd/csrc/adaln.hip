@@ -249,6 +249,167 @@ __global__ __launch_bounds__(kThreads) void layer_norm_adaln_kernel(const typena
     }
 }
 
+// ---------------------------------------------------------------------------
+// 16-bit rows with hidden = 256 per (per <= kPer): the same statistics in the
+// same order, computed by half-waves.  Virtual thread t of the reference's
+// 256 (columns t, t + 256, ...) is chain e = t & 7 of lane p = t >> 3 of a
+// 32-lane half-wave, so column block i of a lane's 8 chains is the 16
+// contiguous bytes at 256 i + 8 p: every load and store is 16 bytes wide.
+// The 32-thread tree levels of offset 16 and 8 are lane swaps (p ^ 2, p ^ 1,
+// DPP within a quad of lanes); offsets 4, 2, 1 combine chains of one lane.
+// One row per half-wave, eight rows per workgroup.
+// ---------------------------------------------------------------------------
+template <int kT>
+__device__ __forceinline__ float lo16(uint32_t w) {
+    if constexpr (kT == 1) return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w)));
+    else return __uint_as_float(w << 16);
+}
+template <int kT>
+__device__ __forceinline__ float hi16(uint32_t w) {
+    if constexpr (kT == 1) return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w >> 16)));
+    else return __uint_as_float(w & 0xffff0000u);
+}
+template <int kT>
+__device__ __forceinline__ float unpack16(const u32x4 &v, int e) {
+    return (e & 1) ? hi16<kT>(v[e >> 1]) : lo16<kT>(v[e >> 1]);
+}
+
+// Value from lane (lane & ~3) | (lane & 3 ^ kXor) of the same quad (DPP).
+template <int kXor>
+__device__ __forceinline__ float quad_xor(float v) {
+    constexpr int kSel = kXor == 2 ? 0x4e : 0xb1;  // quad_perm [2,3,0,1] / [1,0,3,2]
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), kSel, 0xf, 0xf, false));
+}
+
+template <int kT, int kPer, bool kAffine>
+__global__ __launch_bounds__(kThreads) void layer_norm_rows16_kernel(const uint16_t *__restrict__ x,
+                                                                    const uint16_t *__restrict__ scale,
+                                                                    const uint16_t *__restrict__ shift,
+                                                                    uint16_t *__restrict__ out, int64_t rows,
+                                                                    int64_t len, int hidden, int per, int64_t steps,
+                                                                    float eps, Recips rc) {
+    const int tid = threadIdx.x;
+    const int p = tid & 31;  // lane of the half-wave: virtual threads 8 p .. 8 p + 7
+    const int64_t row_raw = static_cast<int64_t>(blockIdx.x) * (kThreads / 32) + (tid >> 5);
+    // a half-wave past the last row computes the last row again and stores nothing
+    const int64_t row = min(row_raw, rows - 1);
+    const int64_t b = row / len, t = row - b * len;
+    int64_t mt = 0;
+    if (steps > 1) {
+        const int64_t repeats = len / steps;
+        const int64_t group = repeats * steps == len ? repeats : repeats + 1;
+        mt = min(t / max<int64_t>(group, 1), steps - 1);
+    }
+    const uint16_t *xr = x + row * hidden + 8 * p;
+    const uint16_t *sc = scale + (b * steps + mt) * hidden + 8 * p;
+    const uint16_t *sh = shift + (b * steps + mt) * hidden + 8 * p;
+
+    u32x4 xs[kPer];
+#pragma unroll
+    for (int i = 0; i < kPer; ++i)
+        if (i < per) xs[i] = *reinterpret_cast<const u32x4 *>(xr + 256 * i);
+
+    // Welford over each chain's columns in order; the count at step i is
+    // i + 1 for every chain.  One wave-wide vote per step for the 8 ranges.
+    float mean[8], m2[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) mean[e] = m2[e] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        if (i < per) {
+            const float n = static_cast<float>(i + 1), y = 1.0f / static_cast<float>(i + 1);
+            float v[8], delta[8], r[8];
+            bool out_any = false;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                v[e] = unpack16<kT>(xs[i], e);
+                delta[e] = v[e] - mean[e];
+                const uint32_t ex = (__float_as_uint(delta[e]) >> 23) & 0xffu;
+                out_any = out_any || ex - 31u >= 197u;
+                const float q = delta[e] * y;
+                r[e] = __builtin_fmaf(__builtin_fmaf(-q, n, delta[e]), y, q);
+            }
+            if (__builtin_expect(__builtin_amdgcn_ballot_w64(out_any) != 0, 0)) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const uint32_t ex = (__float_as_uint(delta[e]) >> 23) & 0xffu;
+                    if (ex - 31u >= 197u) r[e] = delta[e] / n;
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                mean[e] = mean[e] + r[e];
+                m2[e] = __builtin_fmaf(delta[e], v[e] - mean[e], m2[e]);
+            }
+        }
+    }
+
+    // 32-thread trees: offset 16 = lane p ^ 2, offset 8 = lane p ^ 1, then
+    // offsets 4, 2, 1 between the chains of lane p = 0 (mod 4).
+    float cnt = static_cast<float>(per);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const float r_mean = quad_xor<2>(mean[e]), r_m2 = quad_xor<2>(m2[e]);
+        combine_known(mean[e], m2[e], r_mean, r_m2, cnt, cnt, rc.level[0]);
+    }
+    cnt += cnt;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const float r_mean = quad_xor<1>(mean[e]), r_m2 = quad_xor<1>(m2[e]);
+        combine_known(mean[e], m2[e], r_mean, r_m2, cnt, cnt, rc.level[1]);
+    }
+    cnt += cnt;
+#pragma unroll
+    for (int lvl = 2, half = 4; lvl < 5; ++lvl, half >>= 1) {
+#pragma unroll
+        for (int e = 0; e < half; ++e) combine_known(mean[e], m2[e], mean[e + half], m2[e + half], cnt, cnt, rc.level[lvl]);
+        cnt += cnt;
+    }
+    // the eight tree results (lanes 0, 4, .., 28 of the half-wave, chain 0),
+    // combined in order by every lane
+    const int base = (tid & 32) << 2;  // byte address of lane 0 of this half
+    float tm = __int_as_float(__builtin_amdgcn_ds_bpermute(base, __float_as_int(mean[0])));
+    float tv = __int_as_float(__builtin_amdgcn_ds_bpermute(base, __float_as_int(m2[0])));
+#pragma unroll
+    for (int j = 1; j < kThreads / 32; ++j) {
+        const float om = __int_as_float(__builtin_amdgcn_ds_bpermute(base + 16 * j, __float_as_int(mean[0])));
+        const float ov = __int_as_float(__builtin_amdgcn_ds_bpermute(base + 16 * j, __float_as_int(m2[0])));
+        combine_known(tm, tv, om, ov, static_cast<float>(j) * cnt, cnt, rc.total[j]);
+    }
+    const float var = div_rn(tv, static_cast<float>(hidden), rc.total[kThreads / 32 - 1]);
+    const float mu = tm;
+    const float inv = 1.0f / __builtin_sqrtf(var + eps);
+    if (row_raw >= rows) return;
+
+    uint16_t *orow = out + row * hidden + 8 * p;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        if (i < per) {
+            const u32x4 sv = *reinterpret_cast<const u32x4 *>(sc + 256 * i);
+            const u32x4 hv = *reinterpret_cast<const u32x4 *>(sh + 256 * i);
+            u32x4 o;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                uint16_t half[2];
+#pragma unroll
+                for (int k = 0; k < 2; ++k) {
+                    const int e = 2 * j + k;
+                    const float value = unpack16<kT>(xs[i], e), s = unpack16<kT>(sv, e), h = unpack16<kT>(hv, e);
+                    if constexpr (kAffine) {
+                        half[k] = from_f32<kT>(__builtin_fmaf((value - mu) * inv, s, h));
+                    } else {
+                        const float nv = t_round<kT>((value - mu) * inv);
+                        const float m = t_round<kT>(1.0f + s);
+                        half[k] = from_f32<kT>(__builtin_fmaf(nv, m, h));
+                    }
+                }
+                o[j] = static_cast<uint32_t>(half[0]) | (static_cast<uint32_t>(half[1]) << 16);
+            }
+            *reinterpret_cast<u32x4 *>(orow + 256 * i) = o;
+        }
+    }
+}
+
 template <int kT, bool kAffine>
 void launch(const void *xv, const void *scv, const void *shv, void *outv, int64_t rows, int64_t len, int hidden,
             int64_t steps, float eps, hipStream_t s) {
@@ -263,6 +424,25 @@ void launch(const void *xv, const void *scv, const void *shv, void *outv, int64_
         // host IEEE division: RN(1 / n)
         for (int lvl = 0; lvl < 5; ++lvl) rc.level[lvl] = 1.0f / static_cast<float>(per << (lvl + 1));
         for (int i = 1; i < kThreads / 32; ++i) rc.total[i] = 1.0f / static_cast<float>((i + 1) * 32 * per);
+    }
+    if constexpr (kT != 2) {
+        const bool aligned = ((reinterpret_cast<uintptr_t>(xv) | reinterpret_cast<uintptr_t>(scv) |
+                               reinterpret_cast<uintptr_t>(shv) | reinterpret_cast<uintptr_t>(outv)) & 15) == 0;
+        if (uniform && aligned) {
+            const dim3 g16(static_cast<unsigned>((rows + kThreads / 32 - 1) / (kThreads / 32)));
+            const uint16_t *x16 = static_cast<const uint16_t *>(xv), *sc16 = static_cast<const uint16_t *>(scv),
+                           *sh16 = static_cast<const uint16_t *>(shv);
+            uint16_t *o16 = static_cast<uint16_t *>(outv);
+#define TU_LN16(P) \
+    layer_norm_rows16_kernel<kT, P, kAffine><<<g16, kThreads, 0, s>>>(x16, sc16, sh16, o16, rows, len, hidden, per, steps, eps, rc)
+            if (per <= 4) TU_LN16(4);
+            else if (per <= 8) TU_LN16(8);
+            else if (per <= 16) TU_LN16(16);
+            else if (per <= 20) TU_LN16(20);
+            else TU_LN16(32);
+#undef TU_LN16
+            return;
+        }
     }
 #define TU_LN(P, U, X)                                                                       \
     layer_norm_adaln_kernel<kT, P, U, kAffine, X><<<grid, kThreads, 0, s>>>(x, sc, sh, out, len, hidden, \

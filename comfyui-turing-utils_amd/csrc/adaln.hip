@@ -281,18 +281,8 @@ __device__ __forceinline__ float quad_xor(float v) {
     return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), kSel, 0xf, 0xf, false));
 }
 
-template <int kT, int kPer, bool kAffine>
-__global__ __launch_bounds__(kThreads) void layer_norm_rows16_kernel(const uint16_t *__restrict__ x,
-                                                                    const uint16_t *__restrict__ scale,
-                                                                    const uint16_t *__restrict__ shift,
-                                                                    uint16_t *__restrict__ out, int64_t rows,
-                                                                    int64_t len, int hidden, int per, int64_t steps,
-                                                                    float eps, Recips rc) {
-    const int tid = threadIdx.x;
-    const int p = tid & 31;  // lane of the half-wave: virtual threads 8 p .. 8 p + 7
-    const int64_t row_raw = static_cast<int64_t>(blockIdx.x) * (kThreads / 32) + (tid >> 5);
-    // a half-wave past the last row computes the last row again and stores nothing
-    const int64_t row = min(row_raw, rows - 1);
+// Modulation row of token row `row`: b * steps + mt.
+__device__ __forceinline__ int64_t modulation_row(int64_t row, int64_t len, int64_t steps) {
     const int64_t b = row / len, t = row - b * len;
     int64_t mt = 0;
     if (steps > 1) {
@@ -300,14 +290,71 @@ __global__ __launch_bounds__(kThreads) void layer_norm_rows16_kernel(const uint1
         const int64_t group = repeats * steps == len ? repeats : repeats + 1;
         mt = min(t / max<int64_t>(group, 1), steps - 1);
     }
+    return b * steps + mt;
+}
+
+// True when the Markstein quotient of div_rn does not cover a: the biased
+// exponent of a is outside [31, 227], i.e. |a| < 2^-96 (zero and subnormals
+// included), |a| >= 2^101, inf or NaN.
+__device__ __forceinline__ bool div_out(float a) {
+    const float m = fabsf(a);
+    return !(m >= 0x1p-96f) || !(m < 0x1p101f);
+}
+
+// The output's per-column factors, the same for every row of one modulation
+// row: m = T(1 + scale) (AdaLN) or weight (affine), and shift / bias, as fp32.
+// Staged in LDS once per workgroup: [0, hidden) m, [hidden, 2 hidden) shift.
+template <int kT, bool kAffine>
+__device__ __forceinline__ void stage_modulation(float *mod, const uint16_t *__restrict__ sc,
+                                                 const uint16_t *__restrict__ sh, int hidden) {
+    for (int c = 8 * static_cast<int>(threadIdx.x); c < hidden; c += 8 * kThreads) {
+        const u32x4 sv = *reinterpret_cast<const u32x4 *>(sc + c);
+        const u32x4 hv = *reinterpret_cast<const u32x4 *>(sh + c);
+        f32x4 m0, m1, h0, h1;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float s = unpack16<kT>(sv, e);
+            const float m = kAffine ? s : t_round<kT>(1.0f + s);
+            const float h = unpack16<kT>(hv, e);
+            if (e < 4) { m0[e] = m; h0[e] = h; } else { m1[e - 4] = m; h1[e - 4] = h; }
+        }
+        *reinterpret_cast<f32x4 *>(mod + c) = m0;
+        *reinterpret_cast<f32x4 *>(mod + c + 4) = m1;
+        *reinterpret_cast<f32x4 *>(mod + hidden + c) = h0;
+        *reinterpret_cast<f32x4 *>(mod + hidden + c + 4) = h1;
+    }
+}
+
+template <int kT, int kPer, bool kAffine>
+__global__ __launch_bounds__(kThreads) void layer_norm_rows16_kernel(const uint16_t *__restrict__ x,
+                                                                    const uint16_t *__restrict__ scale,
+                                                                    const uint16_t *__restrict__ shift,
+                                                                    uint16_t *__restrict__ out, int64_t rows,
+                                                                    int64_t len, int hidden, int per, int64_t steps,
+                                                                    float eps, Recips rc) {
+    extern __shared__ __align__(16) float mod[];
+    const int tid = threadIdx.x;
+    const int p = tid & 31;  // lane of the half-wave: virtual threads 8 p .. 8 p + 7
+    const int64_t row0 = static_cast<int64_t>(blockIdx.x) * (kThreads / 32);
+    const int64_t row_raw = row0 + (tid >> 5);
+    // a half-wave past the last row computes the last row again and stores nothing
+    const int64_t row = min(row_raw, rows - 1);
+    const int64_t mrow = modulation_row(row, len, steps);
+    // the workgroup's first row's modulation row goes to LDS; a half-wave
+    // whose row has another one (batch or step boundary) reads its own
+    const int64_t mrow0 = modulation_row(row0, len, steps);
+    const bool staged = mrow == mrow0;
     const uint16_t *xr = x + row * hidden + 8 * p;
-    const uint16_t *sc = scale + (b * steps + mt) * hidden + 8 * p;
-    const uint16_t *sh = shift + (b * steps + mt) * hidden + 8 * p;
+    const uint16_t *sc = scale + mrow * hidden + 8 * p;
+    const uint16_t *sh = shift + mrow * hidden + 8 * p;
 
     u32x4 xs[kPer];
 #pragma unroll
     for (int i = 0; i < kPer; ++i)
         if (i < per) xs[i] = *reinterpret_cast<const u32x4 *>(xr + 256 * i);
+
+    stage_modulation<kT, kAffine>(mod, scale + mrow0 * hidden, shift + mrow0 * hidden, hidden);
+    __syncthreads();
 
     // Welford over each chain's columns in order; the count at step i is
     // i + 1 for every chain.  One wave-wide vote per step for the 8 ranges.
@@ -324,17 +371,14 @@ __global__ __launch_bounds__(kThreads) void layer_norm_rows16_kernel(const uint1
             for (int e = 0; e < 8; ++e) {
                 v[e] = unpack16<kT>(xs[i], e);
                 delta[e] = v[e] - mean[e];
-                const uint32_t ex = (__float_as_uint(delta[e]) >> 23) & 0xffu;
-                out_any = out_any || ex - 31u >= 197u;
+                out_any = out_any || div_out(delta[e]);
                 const float q = delta[e] * y;
                 r[e] = __builtin_fmaf(__builtin_fmaf(-q, n, delta[e]), y, q);
             }
             if (__builtin_expect(__builtin_amdgcn_ballot_w64(out_any) != 0, 0)) {
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const uint32_t ex = (__float_as_uint(delta[e]) >> 23) & 0xffu;
-                    if (ex - 31u >= 197u) r[e] = delta[e] / n;
-                }
+                for (int e = 0; e < 8; ++e)
+                    if (div_out(delta[e])) r[e] = delta[e] / n;
             }
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
@@ -382,11 +426,31 @@ __global__ __launch_bounds__(kThreads) void layer_norm_rows16_kernel(const uint1
     if (row_raw >= rows) return;
 
     uint16_t *orow = out + row * hidden + 8 * p;
+    const float *mod_m = mod + 8 * p, *mod_h = mod + hidden + 8 * p;
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
         if (i < per) {
-            const u32x4 sv = *reinterpret_cast<const u32x4 *>(sc + 256 * i);
-            const u32x4 hv = *reinterpret_cast<const u32x4 *>(sh + 256 * i);
+            float mv[8], hv[8];
+            if (staged) {
+                const f32x4 m0 = *reinterpret_cast<const f32x4 *>(mod_m + 256 * i);
+                const f32x4 m1 = *reinterpret_cast<const f32x4 *>(mod_m + 256 * i + 4);
+                const f32x4 h0 = *reinterpret_cast<const f32x4 *>(mod_h + 256 * i);
+                const f32x4 h1 = *reinterpret_cast<const f32x4 *>(mod_h + 256 * i + 4);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    mv[e] = m0[e]; mv[e + 4] = m1[e];
+                    hv[e] = h0[e]; hv[e + 4] = h1[e];
+                }
+            } else {
+                const u32x4 sv = *reinterpret_cast<const u32x4 *>(sc + 256 * i);
+                const u32x4 shv = *reinterpret_cast<const u32x4 *>(sh + 256 * i);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float s = unpack16<kT>(sv, e);
+                    mv[e] = kAffine ? s : t_round<kT>(1.0f + s);
+                    hv[e] = unpack16<kT>(shv, e);
+                }
+            }
             u32x4 o;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -394,13 +458,12 @@ __global__ __launch_bounds__(kThreads) void layer_norm_rows16_kernel(const uint1
 #pragma unroll
                 for (int k = 0; k < 2; ++k) {
                     const int e = 2 * j + k;
-                    const float value = unpack16<kT>(xs[i], e), s = unpack16<kT>(sv, e), h = unpack16<kT>(hv, e);
+                    const float value = unpack16<kT>(xs[i], e);
                     if constexpr (kAffine) {
-                        half[k] = from_f32<kT>(__builtin_fmaf((value - mu) * inv, s, h));
+                        half[k] = from_f32<kT>(__builtin_fmaf((value - mu) * inv, mv[e], hv[e]));
                     } else {
                         const float nv = t_round<kT>((value - mu) * inv);
-                        const float m = t_round<kT>(1.0f + s);
-                        half[k] = from_f32<kT>(__builtin_fmaf(nv, m, h));
+                        half[k] = from_f32<kT>(__builtin_fmaf(nv, mv[e], hv[e]));
                     }
                 }
                 o[j] = static_cast<uint32_t>(half[0]) | (static_cast<uint32_t>(half[1]) << 16);
@@ -434,7 +497,8 @@ void launch(const void *xv, const void *scv, const void *shv, void *outv, int64_
                            *sh16 = static_cast<const uint16_t *>(shv);
             uint16_t *o16 = static_cast<uint16_t *>(outv);
 #define TU_LN16(P) \
-    layer_norm_rows16_kernel<kT, P, kAffine><<<g16, kThreads, 0, s>>>(x16, sc16, sh16, o16, rows, len, hidden, per, steps, eps, rc)
+    layer_norm_rows16_kernel<kT, P, kAffine><<<g16, kThreads, 2 * hidden * sizeof(float), s>>>(x16, sc16, sh16, o16, rows, len, \
+                                                                                           hidden, per, steps, eps, rc)
             if (per <= 4) TU_LN16(4);
             else if (per <= 8) TU_LN16(8);
             else if (per <= 16) TU_LN16(16);

@@ -58,6 +58,37 @@ __device__ __forceinline__ float t_round(float v) {
     else return __uint_as_float(static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(v))) << 16);
 }
 
+// t_round of a pair: bf16 rounds both with one v_cvt_pk_bf16_f32 (the
+// conversion t_round's cast compiles to), fp16 one value at a time.
+template <bool kFp16>
+__device__ __forceinline__ void t_round2(float &a, float &b) {
+    asm volatile("" : "+v"(a), "+v"(b));
+    if constexpr (kFp16) {
+        a = static_cast<float>(static_cast<_Float16>(a));
+        b = static_cast<float>(static_cast<_Float16>(b));
+    } else {
+        const uint32_t w = hw_bf16x2_bits(a, b);
+        a = __uint_as_float(w << 16);
+        b = __uint_as_float(w & 0xffff0000u);
+    }
+}
+
+// INT8 codes of four values, packed little-endian: clamp(rint(y * inv),
+// -127, 127).  The clamp comes first (the bounds are integers, so clamping
+// and rounding commute; a NaN product clamps to -127 as fminf(127,
+// fmaxf(-127, rint(NaN))) does), then adding 1.5 * 2^23 rounds half to even
+// to an integer whose two's complement sits in the low byte of the sum.
+__device__ __forceinline__ uint32_t quant_pack4(float y0, float y1, float y2, float y3, float inv) {
+    const float ys[4] = {y0, y1, y2, y3};
+    uint32_t w = 0u;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const float c = fminf(127.0f, fmaxf(-127.0f, ys[k] * inv));
+        w |= (__float_as_uint(c + 12582912.0f) & 0xffu) << (8 * k);
+    }
+    return w;
+}
+
 struct QkArgs {
     const uint16_t *x[2];        // Q, K
     const uint16_t *norm[2];
@@ -355,6 +386,20 @@ __global__ __launch_bounds__(kQkThreads) void qk_rope_quant_heads_kernel(QkArgs 
             }
         }
     }
+    // the frequency words as fp32, once for all of the group's heads:
+    // fr[i][2 j], fr[i][2 j + 1] = (f0, f1) of output channel j of the pack
+    float fr[kRope ? kItems : 1][16];
+    if constexpr (kRope) {
+#pragma unroll
+        for (int i = 0; i < kItems; ++i)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int pi = j >> 1, comp = j & 1;
+                const uint32_t word = (pi < 2 ? fa[i] : fb[i])[(pi & 1) * 2 + comp];
+                fr[i][2 * j] = t_to_f32<kFp16>(word & 0xffffu);
+                fr[i][2 * j + 1] = t_to_f32<kFp16>(word >> 16);
+            }
+    }
     const int64_t nt = args.ntiles[which];
     // the group's rows one head ahead: head hh + 1's loads are in flight
     // while head hh is computed
@@ -400,22 +445,24 @@ __global__ __launch_bounds__(kQkThreads) void qk_rope_quant_heads_kernel(QkArgs 
             float a[8];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                a[2 * j] = t_round<kFp16>((v[2 * j] * rrms) * t_to_f32<kFp16>(wraw[j] & 0xffffu));
-                a[2 * j + 1] = t_round<kFp16>((v[2 * j + 1] * rrms) * t_to_f32<kFp16>(wraw[j] >> 16));
+                a[2 * j] = (v[2 * j] * rrms) * t_to_f32<kFp16>(wraw[j] & 0xffffu);
+                a[2 * j + 1] = (v[2 * j + 1] * rrms) * t_to_f32<kFp16>(wraw[j] >> 16);
+                t_round2<kFp16>(a[2 * j], a[2 * j + 1]);
             }
             float pmax = 0.0f;
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                float val = a[j];
+            for (int pi = 0; pi < 4; ++pi) {
+                float v0 = a[2 * pi], v1 = a[2 * pi + 1];
                 if constexpr (kRope) {
-                    // pair j >> 1 of the pack; its matrix row j & 1
-                    const int pi = j >> 1, comp = j & 1;
-                    const uint32_t word = (pi < 2 ? fa[i] : fb[i])[(pi & 1) * 2 + comp];
-                    const float f0 = t_to_f32<kFp16>(word & 0xffffu), f1 = t_to_f32<kFp16>(word >> 16);
-                    val = t_round<kFp16>(__builtin_fmaf(f1, a[2 * pi + 1], f0 * a[2 * pi]));
+                    // pair pi of the pack: output channel 2 pi + comp takes
+                    // row comp of the pair's matrix
+                    v0 = __builtin_fmaf(fr[i][4 * pi + 1], a[2 * pi + 1], fr[i][4 * pi] * a[2 * pi]);
+                    v1 = __builtin_fmaf(fr[i][4 * pi + 3], a[2 * pi + 1], fr[i][4 * pi + 2] * a[2 * pi]);
+                    t_round2<kFp16>(v0, v1);
                 }
-                y[i][j] = val;
-                pmax = fmaxf(pmax, fabsf(val));
+                y[i][2 * pi] = v0;
+                y[i][2 * pi + 1] = v1;
+                pmax = fmaxf(pmax, fmaxf(fabsf(v0), fabsf(v1)));
             }
             if (valid[i]) amax = fmaxf(amax, pmax);
         }
@@ -438,13 +485,9 @@ __global__ __launch_bounds__(kQkThreads) void qk_rope_quant_heads_kernel(QkArgs 
 #pragma unroll
         for (int i = 0; i < kItems; ++i) {
             if (!valid[i]) continue;
-            uint32_t w2[2] = {0u, 0u};
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const float r = fminf(127.0f, fmaxf(-127.0f, __builtin_rintf(y[i][j] * inv)));
-                w2[j >> 2] |= (static_cast<uint32_t>(static_cast<int32_t>(r)) & 0xffu) << (8 * (j & 3));
-            }
-            *reinterpret_cast<u32x2 *>(obase + (tok0 + kTokStep * i) * args.o_sl[which] + pack * 8) = u32x2{w2[0], w2[1]};
+            const u32x2 w2{quant_pack4(y[i][0], y[i][1], y[i][2], y[i][3], inv),
+                           quant_pack4(y[i][4], y[i][5], y[i][6], y[i][7], inv)};
+            *reinterpret_cast<u32x2 *>(obase + (tok0 + kTokStep * i) * args.o_sl[which] + pack * 8) = w2;
         }
     }
 }

@@ -107,6 +107,7 @@ struct QkArgs {
     float eps;
     const int32_t *anchors;   // K stabilisation [B][Hk] (W8A8 variant) or null
     float *anchor_values;     // [B][Hk][D]: the anchor row's processed values
+    int k_only;               // row pre-pass / head-group kernel: K's tasks only
 };
 
 template <bool kFp16, int D, bool kSplit, bool kRow, bool kRotate>
@@ -355,7 +356,7 @@ __global__ __launch_bounds__(kQkThreads) void qk_rope_quant_heads_kernel(QkArgs 
     const int64_t b = blockIdx.y;
     const int64_t nch_q = (args.len[0] + kChunk - 1) / kChunk;
     const int64_t grp_q = (args.heads[0] + kHeadGroup - 1) / kHeadGroup;
-    int64_t task = blockIdx.x;
+    int64_t task = blockIdx.x + (args.k_only ? grp_q * nch_q : 0);
     const int which = task < grp_q * nch_q ? 0 : 1;
     if (which) task -= grp_q * nch_q;
     const int64_t len = args.len[which];
@@ -492,6 +493,151 @@ __global__ __launch_bounds__(kQkThreads) void qk_rope_quant_heads_kernel(QkArgs 
     }
 }
 
+// Row-scope Q in one pass over HBM.  A Q scale tile is 16 tokens of one
+// head, so one workgroup (4 wave64) takes a 16-token tile of every head:
+// wave w owns heads w, w + 4, .. (at most kHPW), each as kItems (token, pack)
+// items per lane laid out as in the head-group kernel.  First pass: each
+// head's sum of squares per token, computed as the row pre-pass computes it
+// (8-channel FMA chain, butterfly across the token's packs), into LDS; the
+// first 16 lanes add each token's heads in order and publish rrms.  Second
+// pass: every head is read again -- the workgroup's 160 KB (Wan: 40 heads)
+// was just read, so this comes from L2 or MALL, not HBM -- then normalized,
+// rotated and quantized with the head-group kernel's arithmetic.  Keeping the
+// rows in registers instead needs 253 VGPRs, one workgroup per CU, and ran
+// slower (0.369 against 0.342 ms for the two-pass path).  K keeps the
+// pre-pass: a K scale tile is 64 tokens, and 64 tokens of every head do not
+// stay in the caches between two passes.
+constexpr int kRowQThreads = 256;
+
+template <bool kFp16, int D, bool kRope, int kHPW>
+__global__ __launch_bounds__(kRowQThreads) __attribute__((amdgpu_waves_per_eu(3))) void qk_rowq_kernel(QkArgs args) {
+    constexpr int kPacks = D / 8;
+    constexpr int kTokStep = 64 / kPacks;   // tokens one lane row of a wave covers
+    constexpr int kItems = kQTile / kTokStep;
+    constexpr int kWaves = kRowQThreads / 64;
+    __shared__ float hsum[kQTile][kWaves * kHPW];
+    __shared__ float rr_s[kQTile];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int64_t b = blockIdx.y;
+    const int64_t tile = blockIdx.x;
+    const int64_t len = args.len[0], heads = args.heads[0];
+    const int pack = lane % kPacks, trow = lane / kPacks;
+    const int64_t tok0 = tile * kQTile + trow;
+    const int64_t x_sh = args.x_sh[0], x_sl = args.x_sl[0];
+    const uint16_t *xtok = args.x[0] + b * args.x_sb[0] + pack * 8;
+
+    bool valid[kItems];
+    u32x4 fa[kItems], fb[kItems];
+#pragma unroll
+    for (int i = 0; i < kItems; ++i) {
+        const int64_t t = tok0 + kTokStep * i;
+        valid[i] = t < len;
+        fa[i] = fb[i] = u32x4{0u, 0u, 0u, 0u};
+        if constexpr (kRope) {
+            if (valid[i]) {
+                const uint16_t *frow = args.freqs + (args.f_batches == 1 ? 0 : b) * args.f_sb +
+                                       (args.f_len == 1 ? 0 : t) * args.f_sl + pack * 16;
+                fa[i] = *reinterpret_cast<const u32x4 *>(frow);
+                fb[i] = *reinterpret_cast<const u32x4 *>(frow + 8);
+            }
+        }
+    }
+    auto load_head = [&](int64_t h, u32x4 (&r)[kItems]) {
+#pragma unroll
+        for (int i = 0; i < kItems; ++i)
+            r[i] = valid[i] && h < heads
+                       ? *reinterpret_cast<const u32x4 *>(xtok + h * x_sh + (tok0 + kTokStep * i) * x_sl)
+                       : u32x4{0u, 0u, 0u, 0u};
+    };
+    // two head buffers: head k + 1's loads are in flight while head k is used
+    u32x4 xr[2][kItems];
+    load_head(wave, xr[0]);
+#pragma unroll
+    for (int k = 0; k < kHPW; ++k) {
+        const int h = wave + kWaves * k;
+        if (k + 1 < kHPW) load_head(wave + kWaves * (k + 1), xr[(k + 1) & 1]);
+        const u32x4 (&xk)[kItems] = xr[k & 1];
+#pragma unroll
+        for (int i = 0; i < kItems; ++i) {
+            float sq = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float lo = t_to_f32<kFp16>(xk[i][j] & 0xffffu), hi = t_to_f32<kFp16>(xk[i][j] >> 16);
+                sq = __builtin_fmaf(lo, lo, sq);
+                sq = __builtin_fmaf(hi, hi, sq);
+            }
+#pragma unroll
+            for (int off = kPacks / 2; off > 0; off >>= 1) sq = sq + __shfl_xor(sq, off, kPacks);
+            if (pack == 0 && h < heads) hsum[kTokStep * i + trow][h] = sq;
+        }
+    }
+    __syncthreads();
+    if (tid < kQTile) {
+        float total = 0.0f;
+        for (int h = 0; h < heads; ++h) total = total + hsum[tid][h];
+        rr_s[tid] = 1.0f / __builtin_sqrtf(total / static_cast<float>(heads * D) + args.eps);
+    }
+    __syncthreads();
+    float rr[kItems];
+#pragma unroll
+    for (int i = 0; i < kItems; ++i) rr[i] = rr_s[kTokStep * i + trow];
+
+    const int64_t nt = args.ntiles[0];
+    load_head(wave, xr[0]);
+#pragma unroll
+    for (int k = 0; k < kHPW; ++k) {
+        const int64_t h = wave + kWaves * k;
+        if (h >= heads) break;
+        if (k + 1 < kHPW) load_head(wave + kWaves * (k + 1), xr[(k + 1) & 1]);
+        const u32x4 (&xk)[kItems] = xr[k & 1];
+        const u32x4 wraw = *reinterpret_cast<const u32x4 *>(args.norm[0] + h * D + pack * 8);
+        float y[kItems][8];
+        float amax = 0.0000001f;
+#pragma unroll
+        for (int i = 0; i < kItems; ++i) {
+            float a[8];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                a[2 * j] = (t_to_f32<kFp16>(xk[i][j] & 0xffffu) * rr[i]) * t_to_f32<kFp16>(wraw[j] & 0xffffu);
+                a[2 * j + 1] = (t_to_f32<kFp16>(xk[i][j] >> 16) * rr[i]) * t_to_f32<kFp16>(wraw[j] >> 16);
+                t_round2<kFp16>(a[2 * j], a[2 * j + 1]);
+            }
+            float pmax = 0.0f;
+#pragma unroll
+            for (int pi = 0; pi < 4; ++pi) {
+                float v0 = a[2 * pi], v1 = a[2 * pi + 1];
+                if constexpr (kRope) {
+                    // row comp of pair pi is word 2 (pi & 1) + comp of fa
+                    // (pi < 2) or fb, kept packed to save registers
+                    const uint32_t w0 = (pi < 2 ? fa[i] : fb[i])[(pi & 1) * 2];
+                    const uint32_t w1 = (pi < 2 ? fa[i] : fb[i])[(pi & 1) * 2 + 1];
+                    v0 = __builtin_fmaf(t_to_f32<kFp16>(w0 >> 16), a[2 * pi + 1], t_to_f32<kFp16>(w0 & 0xffffu) * a[2 * pi]);
+                    v1 = __builtin_fmaf(t_to_f32<kFp16>(w1 >> 16), a[2 * pi + 1], t_to_f32<kFp16>(w1 & 0xffffu) * a[2 * pi]);
+                    t_round2<kFp16>(v0, v1);
+                }
+                y[i][2 * pi] = v0;
+                y[i][2 * pi + 1] = v1;
+                pmax = fmaxf(pmax, fmaxf(fabsf(v0), fabsf(v1)));
+            }
+            if (valid[i]) amax = fmaxf(amax, pmax);
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+        if (lane == 0) args.scale[0][(b * heads + h) * nt + tile] = amax / 127.0f;
+        const float inv = 127.0f / amax;
+        int8_t *obase = args.out[0] + b * args.o_sb[0] + h * args.o_sh[0];
+#pragma unroll
+        for (int i = 0; i < kItems; ++i) {
+            if (!valid[i]) continue;
+            const u32x2 w2{quant_pack4(y[i][0], y[i][1], y[i][2], y[i][3], inv),
+                           quant_pack4(y[i][4], y[i][5], y[i][6], y[i][7], inv)};
+            *reinterpret_cast<u32x2 *>(obase + (tok0 + kTokStep * i) * args.o_sl[0] + pack * 8) = w2;
+        }
+    }
+}
+
 // Row-scope rrms, batched: one wave per 64 / P tokens (P = D / 8 packs a
 // token), four waves a workgroup, Q tokens then K tokens.  Each lane group of
 // P lanes owns a token; the heads' loads go out kRrmsBatch at a time, and the
@@ -507,7 +653,7 @@ __global__ __launch_bounds__(kQkThreads) void row_rrms_batched_kernel(QkArgs arg
     const int tid = threadIdx.x, lane = tid & 63;
     const int64_t b = blockIdx.y;
     const int64_t nblk_q = (args.len[0] + kTokPerBlock - 1) / kTokPerBlock;
-    int64_t blk = blockIdx.x;
+    int64_t blk = blockIdx.x + (args.k_only ? nblk_q : 0);
     const int which = blk < nblk_q ? 0 : 1;
     if (which) blk -= nblk_q;
     const int64_t len = args.len[which];
@@ -634,6 +780,29 @@ int32_t launch_qk(const QkArgs &args, int64_t batch, bool split, bool row, bool 
     // interleaved RoPE over the whole head (contiguous frequencies) or none,
     // no rotation: the head-group fast path
     const bool fast = !rotate && !split && (args.rot_dim == 0 || (args.rot_dim == D && args.f_contig));
+    if (fast && row && args.heads[0] <= 40) {
+        // Q in one pass; K: its row pre-pass, then the head-group kernel
+        QkArgs ka = args;
+        ka.k_only = 1;
+        constexpr int kTokPerBlock = 64 / (D / 8) * kQkThreads / 64;
+        const dim3 gr(static_cast<unsigned>((args.len[1] + kTokPerBlock - 1) / kTokPerBlock),
+                      static_cast<unsigned>(batch));
+        row_rrms_batched_kernel<kFp16, D><<<gr, kQkThreads, 0, s>>>(ka);
+        const dim3 gq(static_cast<unsigned>(args.ntiles[0]), static_cast<unsigned>(batch));
+        const bool small = args.heads[0] <= 16;
+        constexpr int kSmall = 16 / (kRowQThreads / 64), kLarge = 40 / (kRowQThreads / 64);
+#define TU_ROWQ(R) \
+    if (small) qk_rowq_kernel<kFp16, D, R, kSmall><<<gq, kRowQThreads, 0, s>>>(args); \
+    else qk_rowq_kernel<kFp16, D, R, kLarge><<<gq, kRowQThreads, 0, s>>>(args)
+        if (args.rot_dim == 0) { TU_ROWQ(false); }
+        else { TU_ROWQ(true); }
+#undef TU_ROWQ
+        const int64_t gk = (args.heads[1] + kHeadGroup - 1) / kHeadGroup;
+        const dim3 grid(static_cast<unsigned>(gk * ((args.len[1] + kChunk - 1) / kChunk)), static_cast<unsigned>(batch));
+        if (args.rot_dim == 0) qk_rope_quant_heads_kernel<kFp16, D, true, false><<<grid, kQkThreads, 0, s>>>(ka);
+        else qk_rope_quant_heads_kernel<kFp16, D, true, true><<<grid, kQkThreads, 0, s>>>(ka);
+        return check_launch("tu_qk_rms_rope_int8");
+    }
     if (row) {
         constexpr int kTokPerBlock = 64 / (D / 8) * kQkThreads / 64;
         const dim3 g(static_cast<unsigned>((args.len[0] + kTokPerBlock - 1) / kTokPerBlock +

@@ -271,8 +271,9 @@ int32_t tu_sage_attn_kv_splits(int64_t batch, int64_t hq, int64_t lq, int64_t lk
 /* RMSNorm + RoPE + per-tile INT8 of Q and K in one pass, the producer of the
  * attention's Q/K (Q per 16-token tile, K per 64-token tile):
  *   rrms  = 1 / sqrt(sumsq / n + eps)    norm_scope 0: the token's head row
- *           (n = dim); 1: all heads of the token (n = heads * dim), computed
- *           into q_rrms / k_rrms (fp32 [batch, len] scratch)
+ *           (n = dim); 1: all heads of the token (n = heads * dim); q_rrms /
+ *           k_rrms are fp32 [batch, len] scratch for it (their contents
+ *           afterwards are not part of the result)
  *   a_c   = T((x_c * rrms) * w_c)        T = bf16 (dtype 0) or fp16 (dtype 1);
  *           w = norm[c] (scope 0) or norm[head * dim + c] (scope 1)
  *   c < rot_dim: y_c = T(fma(f[pair][comp][1], a_second, f[pair][comp][0] * a_first))

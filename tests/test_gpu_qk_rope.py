@@ -67,6 +67,19 @@ def test_exact_vs_oracle(gpu_device, dtype, d, scope, split, rot):
     _check_exact(q, k, qw, kw, freqs, rot, scope, split, "HND", gpu_device)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("hq,hk,rot_full", [(24, 8, True), (17, 1, False), (40, 40, False), (3, 5, True)])
+def test_row_scope_head_counts(gpu_device, dtype, d, hq, hk, rot_full):
+    """Row-scope RMSNorm with interleaved full-width RoPE (or none): Q in one
+    pass over all heads of a 16-token tile (heads split unevenly over the
+    workgroup's waves), K through its pre-pass; ragged token count."""
+    rot = d if rot_full else 0
+    print(f"[qk-rope] row heads {dtype} d={d} hq={hq} hk={hk} rot={rot}", flush=True)
+    q, k, qw, kw, freqs = _case(1, hq, hk, 150, d, dtype, "row", rot, 1, 150, 300 + hq + d)
+    _check_exact(q, k, qw, kw, freqs, rot, "row", False, "HND", gpu_device)
+
+
 @pytest.mark.parametrize("scope", ["head", "row"])
 def test_nhd_strided_and_broadcast_freqs(gpu_device, scope):
     """Wan's call: HND views of an NHD projection ([B, L, H, D].transpose(1, 2)),

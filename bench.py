@@ -30,7 +30,7 @@ bounded sample of the same workload on this host's cores; the CPU oracle
 beside it on the same sample.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
-                       [--cpu-seconds S] [--copy-calibration] [--no-extras]
+                       [--cpu-seconds S] [--copy-calibration] [--no-extras] [--power-probe]
 """
 from __future__ import annotations
 
@@ -66,6 +66,9 @@ def parse_args():
                    help="after the timed steps, copy 1 GiB once (HBM-counter calibration for rocprofv3 --pmc)")
     p.add_argument("--no-extras", action="store_true",
                    help="skip the next-row kernels timed outside the step (short runs under rocprofv3 --pmc)")
+    p.add_argument("--power-probe", action="store_true",
+                   help="only time the qkv GEMM and the attention kernel on the bench inputs and on all-zero "
+                        "operands of the same shapes (three launches each), print one JSON line and exit")
     return p.parse_args()
 
 
@@ -133,6 +136,9 @@ def main():
     timer = KernelTimer(torch)
     ops = torch.ops.turing_utils
     sm_scale = ATTN["d"] ** -0.5
+    if args.power_probe:
+        print(json.dumps(power_probe(torch, ops, lin[0], q, k_, v)))
+        return 0
 
     def step():
         for name, _, _, x, w, ws in lin:
@@ -226,6 +232,8 @@ def main():
     roofline["counters_source"] = {"traffic": traffic_src, "mfma": mfma_src}
 
     extras = None if args.no_extras else extra_kernels(torch, dev, ops, lin, q, k_, v, copy_gbs)
+    if extras is not None:
+        extras["power_probe"] = power_probe(torch, ops, lin[0], q, k_, v)
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds)
 
     record = {
@@ -257,6 +265,49 @@ def main():
     }
     print(json.dumps(record))
     return 0
+
+
+def power_probe(torch, ops, qkv, q, k, v) -> dict:
+    """The qkv GEMM and the attention kernel, each launched three times on the
+    bench inputs and three times on all-zero operands of the same shapes (the
+    scales and the launch are unchanged).  The GEMM runs the same instruction
+    stream either way (its only data-dependent branch, the epilogue's
+    finiteness test, takes the same side); the attention's rescale test is
+    rarely taken on either.  So a shorter time on zeros is a higher clock:
+    multipliers and buses that do not toggle draw less power, and MI355X
+    holds these loops at its board power limit on the bench data."""
+    from comfyui_turing_utils_kernel.turing_sage import quant as sage_quant
+    from comfyui_turing_utils_kernel.turing_sage.core import attention_from_vt
+
+    def timed(fn, reps=3):
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    _, kk, n, x, w, ws = qkv
+    qa, sa = ops.bf16_int8_convrot_quantize(x, GROUP)
+    qz, wz = torch.zeros_like(qa), torch.zeros_like(w)
+    out = {}
+    ms_r = timed(lambda: ops.int8_linear(qa, w, sa, ws, None))
+    ms_z = timed(lambda: ops.int8_linear(qz, wz, sa, ws, None))
+    out["int8_gemm_qkv"] = {"ms_bench_data": ms_r, "ms_zero_operands": ms_z, "ratio": ms_r / ms_z}
+    del qa, qz, wz
+    mean = sage_quant.key_channel_mean(k, "HND")
+    q8, qs = sage_quant.quantize_per_block(q, BLK, "HND")
+    k8, ks = sage_quant.quantize_per_block(k, BLK, "HND", mean)
+    vt, _ = sage_quant.value_transpose(v, "HND")
+    kw = dict(tensor_layout="HND", sm_scale=ATTN["d"] ** -0.5, blkq=BLK, blkk=BLK)
+    ms_r = timed(lambda: attention_from_vt(q8, qs, k8, ks, vt, **kw))
+    q8z, k8z, vtz = torch.zeros_like(q8), torch.zeros_like(k8), torch.zeros_like(vt)
+    ms_z = timed(lambda: attention_from_vt(q8z, qs, k8z, ks, vtz, **kw))
+    out["sage_attn"] = {"ms_bench_data": ms_r, "ms_zero_operands": ms_z, "ratio": ms_r / ms_z}
+    return out
 
 
 def extra_kernels(torch, dev, ops, lin, q, k, v, copy_gbs) -> dict:

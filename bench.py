@@ -221,8 +221,8 @@ def main():
         "traffic": None,
     }
     # committed rocprofv3 figures of the same kernel and workload, used only
-    # when they were captured from the kernel sources in this tree
-    traffic_src, mfma_src = counters_source(TRAFFIC_FILE), counters_source(MFMA_FILE)
+    # when they were captured from that kernel's sources in this tree
+    traffic_src, mfma_src = counters_source(TRAFFIC_FILE, dominant), counters_source(MFMA_FILE, dominant)
     if traffic_src["current"]:
         roofline["traffic"] = measured_traffic(dominant)
     counters = measured_mfma(dominant) if mfma_src["current"] else None
@@ -439,30 +439,43 @@ MFMA_FILE = os.path.join(ROOT, "profiles", "mfma_counters.json")
 CSRC_DIR = os.path.join(ROOT, "comfyui-turing-utils_amd", "csrc")
 
 
-def kernel_sources_digest() -> str:
-    """sha256 (first 16 hex digits) over the HIP sources and headers the
-    kernels are built from, in name order: the version stamp of the
-    committed counter files, which carry the digest they were captured at."""
+# The sources each bench kernel is built from (the headers every kernel
+# includes are added by kernel_sources_digest).
+KERNEL_SOURCES = (
+    ("convrot_quant", ("convrot_quant.hip",)),
+    ("int8_gemm", ("int8_gemm.hip",)),
+    ("sage_kmean", ("sage_quant.hip",)),
+    ("sage_quant", ("sage_quant.hip",)),
+    ("sage_v_prep", ("sage_attn.hip", "attn_common.h")),
+    ("sage_attn", ("sage_attn.hip", "attn_common.h")),
+)
+
+
+def kernel_sources_digest(kernel: str) -> str:
+    """sha256 (first 16 hex digits) over the HIP sources and headers ``kernel``
+    (a bench kernel name) is built from, in name order: the version stamp
+    each entry of the committed counter files carries."""
     import hashlib
 
+    files = next(f for prefix, f in KERNEL_SOURCES if kernel.startswith(prefix))
     h = hashlib.sha256()
-    names = sorted(n for n in os.listdir(CSRC_DIR) if n.endswith((".hip", ".h")))
-    for name in names + ["../../include/tu_hip.h"]:
+    for name in sorted(files + ("tu_common.h",)) + ["../../include/tu_hip.h"]:
         with open(os.path.join(CSRC_DIR, name), "rb") as f:
             h.update(os.path.basename(name).encode() + b"\0" + f.read())
     return h.hexdigest()[:16]
 
 
-def counters_source(path: str) -> dict:
-    """Where the roofline's committed counter figures come from, and whether
-    they were captured from the kernel sources in this tree."""
+def counters_source(path: str, kernel: str) -> dict:
+    """Where the roofline's committed counter figures for ``kernel`` come
+    from, and whether they were captured from the kernel's sources in this
+    tree."""
     try:
         with open(path) as f:
-            stamp = json.load(f).get("_kernel_sources")
+            stamp = (json.load(f).get(kernel) or {}).get("_kernel_sources")
     except (OSError, ValueError):
         stamp = None
     return {"file": os.path.relpath(path, ROOT), "kernel_sources": stamp,
-            "current": stamp is not None and stamp == kernel_sources_digest()}
+            "current": stamp is not None and stamp == kernel_sources_digest(kernel)}
 
 
 def measured_mfma(kernel: str):

@@ -30,6 +30,7 @@
 // workgroup (qk_rope_quant_heads_kernel).
 #include <type_traits>
 
+#include "attn_common.h"
 #include "w8a8_common.h"
 
 namespace tu {
@@ -73,6 +74,20 @@ __device__ __forceinline__ void t_round2(float &a, float &b) {
     }
 }
 
+// t_round2 that also returns the rounded pair as packed T bits (low = a),
+// for kernels that keep rounded values packed.  The fp16 pair conversion is
+// the same round-to-nearest-even as the single-value cast.
+template <bool kFp16>
+__device__ __forceinline__ uint32_t t_round2w(float &a, float &b) {
+    asm volatile("" : "+v"(a), "+v"(b));
+    uint32_t w;
+    if constexpr (kFp16) w = hw_f16x2_bits(a, b);
+    else w = hw_bf16x2_bits(a, b);
+    a = t_to_f32<kFp16>(w & 0xffffu);
+    b = t_to_f32<kFp16>(w >> 16);
+    return w;
+}
+
 // INT8 codes of four values, packed little-endian: clamp(rint(y * inv),
 // -127, 127).  The clamp comes first (the bounds are integers, so clamping
 // and rounding commute; a NaN product clamps to -127 as fminf(127,
@@ -87,6 +102,49 @@ __device__ __forceinline__ uint32_t quant_pack4(float y0, float y1, float y2, fl
         w |= (__float_as_uint(c + 12582912.0f) & 0xffu) << (8 * k);
     }
     return w;
+}
+
+// v + (v of lane i ^ kOff), the step of a butterfly sum over the P lanes of a
+// token (P = 8 or 16 consecutive lanes, kOff < P), as __shfl_xor(v, kOff, P)
+// gives it but without index arithmetic: DPP quad permutations for 1 and 2,
+// row rotation by 8 (lane (i + 8) mod 16 is lane i ^ 8), and a bit-mode
+// ds_swizzle for 4.  Addition is commutative, so the sums are bit-identical.
+template <int kOff>
+__device__ __forceinline__ float butterfly_add(float v) {
+    int o;
+    if constexpr (kOff == 1) o = __builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xf, 0xf, false);
+    else if constexpr (kOff == 2) o = __builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xf, 0xf, false);
+    else if constexpr (kOff == 8) o = __builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xf, 0xf, false);
+    else o = __builtin_amdgcn_ds_swizzle(__float_as_int(v), (kOff << 10) | 0x1f);
+    return v + __int_as_float(o);
+}
+template <int kPacks>
+__device__ __forceinline__ float pack_sum(float v) {
+    if constexpr (kPacks == 16) v = butterfly_add<8>(v);
+    v = butterfly_add<4>(v);
+    v = butterfly_add<2>(v);
+    return butterfly_add<1>(v);
+}
+
+// Maximum over the wave of non-negative floats that are not NaN, compared as
+// integers (their bit patterns order as the values do): DPP within rows of
+// 16, then the permlane swaps across rows.
+__device__ __forceinline__ float wave_max_nonneg(float v) {
+    int b = __float_as_int(v);
+    b = max(b, __builtin_amdgcn_mov_dpp(b, 0x128, 0xf, 0xf, false));   // row_ror:8
+    b = max(b, __builtin_amdgcn_mov_dpp(b, 0x124, 0xf, 0xf, false));   // row_ror:4
+    b = max(b, __builtin_amdgcn_mov_dpp(b, 0x4E, 0xf, 0xf, false));
+    b = max(b, __builtin_amdgcn_mov_dpp(b, 0xB1, 0xf, 0xf, false));
+    return __int_as_float(xmax_i32(b));
+}
+
+// max(m, |a|, |b|) in one instruction.  A quiet NaN operand is passed over
+// (IEEE maxNum), as fmaxf passes it over; a and b are never signalling NaNs
+// here (they come out of hardware conversions).
+__device__ __forceinline__ float max3_abs(float m, float a, float b) {
+    float r;
+    asm("v_max3_f32 %0, %1, |%2|, |%3|" : "=v"(r) : "v"(m), "v"(a), "v"(b));
+    return r;
 }
 
 struct QkArgs {
@@ -439,8 +497,7 @@ __global__ __launch_bounds__(kQkThreads) void qk_rope_quant_heads_kernel(QkArgs 
                 float sq = 0.0f;
 #pragma unroll
                 for (int c = 0; c < 8; ++c) sq = __builtin_fmaf(v[c], v[c], sq);
-#pragma unroll
-                for (int off = kPacks / 2; off > 0; off >>= 1) sq = sq + __shfl_xor(sq, off, kPacks);
+                sq = pack_sum<kPacks>(sq);
                 rrms = 1.0f / __builtin_sqrtf(sq / static_cast<float>(D) + args.eps);
             }
             float a[8];
@@ -463,12 +520,11 @@ __global__ __launch_bounds__(kQkThreads) void qk_rope_quant_heads_kernel(QkArgs 
                 }
                 y[i][2 * pi] = v0;
                 y[i][2 * pi + 1] = v1;
-                pmax = fmaxf(pmax, fmaxf(fabsf(v0), fabsf(v1)));
+                pmax = max3_abs(pmax, v0, v1);
             }
-            if (valid[i]) amax = fmaxf(amax, pmax);
+            if (valid[i]) amax = __int_as_float(max(__float_as_int(amax), __float_as_int(pmax)));
         }
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+        amax = wave_max_nonneg(amax);
         float inv;
         if (which == 0) {
             if (lane == 0) args.scale[0][(b * heads + h) * nt + chunk * 4 + wave] = amax / 127.0f;
@@ -478,7 +534,8 @@ __global__ __launch_bounds__(kQkThreads) void qk_rope_quant_heads_kernel(QkArgs 
             __syncthreads();
             float kmax = 0.0000001f;
 #pragma unroll
-            for (int w = 0; w < kQkThreads / 64; ++w) kmax = fmaxf(kmax, kamax[hh & 1][w]);
+            for (int w = 0; w < kQkThreads / 64; ++w)
+                kmax = __int_as_float(max(__float_as_int(kmax), __float_as_int(kamax[hh & 1][w])));
             if (tid == 0) args.scale[1][(b * heads + h) * nt + chunk] = kmax / 127.0f;
             inv = 127.0f / kmax;
         }
@@ -568,8 +625,7 @@ __global__ __launch_bounds__(kRowQThreads) __attribute__((amdgpu_waves_per_eu(3)
                 sq = __builtin_fmaf(lo, lo, sq);
                 sq = __builtin_fmaf(hi, hi, sq);
             }
-#pragma unroll
-            for (int off = kPacks / 2; off > 0; off >>= 1) sq = sq + __shfl_xor(sq, off, kPacks);
+            sq = pack_sum<kPacks>(sq);
             if (pack == 0 && h < heads) hsum[kTokStep * i + trow][h] = sq;
         }
     }
@@ -619,12 +675,11 @@ __global__ __launch_bounds__(kRowQThreads) __attribute__((amdgpu_waves_per_eu(3)
                 }
                 y[i][2 * pi] = v0;
                 y[i][2 * pi + 1] = v1;
-                pmax = fmaxf(pmax, fmaxf(fabsf(v0), fabsf(v1)));
+                pmax = max3_abs(pmax, v0, v1);
             }
-            if (valid[i]) amax = fmaxf(amax, pmax);
+            if (valid[i]) amax = __int_as_float(max(__float_as_int(amax), __float_as_int(pmax)));
         }
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+        amax = wave_max_nonneg(amax);
         if (lane == 0) args.scale[0][(b * heads + h) * nt + tile] = amax / 127.0f;
         const float inv = 127.0f / amax;
         int8_t *obase = args.out[0] + b * args.o_sb[0] + h * args.o_sh[0];
@@ -635,6 +690,259 @@ __global__ __launch_bounds__(kRowQThreads) __attribute__((amdgpu_waves_per_eu(3)
                            quant_pack4(y[i][4], y[i][5], y[i][6], y[i][7], inv)};
             *reinterpret_cast<u32x2 *>(obase + (tok0 + kTokStep * i) * args.o_sl[0] + pack * 8) = w2;
         }
+    }
+}
+
+// Row-scope Q, streamed (17 to 48 heads): one workgroup of 16 wave64 per CU
+// walks 16-token Q tiles (task k, k + grid, .. over batch x tiles), every
+// head of a tile at once as in qk_rowq_kernel, but each row is read from HBM
+// once and the next tile's reads are in flight while the current tile is
+// normalized and quantized.  Wave w owns heads w, w + 16 and w + 32: head w
+// arrives in registers (two buffers, alternate tiles), the other two through
+// buffer_load ... lds into two LDS regions of the wave's own, each reloaded
+// with the next tile's rows as soon as the wave has read it.  Per tile:
+// (1) each head's per-token sum of squares, computed as the row pre-pass
+// computes it, into LDS; (2) wave t adds token t's heads in order and
+// publishes rrms; (3) every head is normalized, rotated and quantized with
+// the head-group kernel's arithmetic.  Two barriers a tile.  Buffer offsets
+// are 32-bit: the host requires a batch's rows to span less than 2 GiB, and
+// rows past the sequence read as zeros (their offsets are past the range).
+// Compute units of the current device (cached per device id): the streamed
+// kernel's grid.
+int32_t device_cus(int &cus) {
+    static int cache[64];
+    int dev = 0;
+    hipError_t err = hipGetDevice(&dev);
+    if (err != hipSuccess) return fail("hipGetDevice failed: %s", hipGetErrorString(err));
+    if (dev >= 0 && dev < 64 && cache[dev] > 0) {
+        cus = cache[dev];
+        return 0;
+    }
+    err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (err != hipSuccess || cus <= 0) return fail("hipDeviceGetAttribute(CU count) failed: %s", hipGetErrorString(err));
+    if (dev >= 0 && dev < 64) cache[dev] = cus;
+    return 0;
+}
+
+constexpr int kRowSWaves = 16;
+constexpr int kRowSThreads = kRowSWaves * 64;
+constexpr int kRowSMaxHeads = 3 * kRowSWaves;
+constexpr uint32_t kRowSPast = 0x80000000u;   // an offset past every range
+
+__device__ __forceinline__ u32x4 rows_load16(__amdgpu_buffer_rsrc_t rs, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
+}
+// 64 lanes x 16 B into 1 KiB of LDS at `dst` (wave-uniform), lane order.
+__device__ __forceinline__ void rows_load16_lds(__amdgpu_buffer_rsrc_t rs, int8_t *dst, uint32_t off) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void *)dst, 16, off, 0, 0, 0);
+}
+
+template <bool kFp16, int D, bool kRope>
+__global__ __launch_bounds__(kRowSThreads) void qk_rowq_stream_kernel(QkArgs args, uint32_t ntasks, uint32_t span,
+                                                                    uint32_t f_span) {
+    constexpr int kPacks = D / 8;
+    constexpr int kTokStep = 64 / kPacks;   // tokens one lane row of a wave covers
+    constexpr int kItems = kQTile / kTokStep;
+    constexpr int kHeadBytes = kItems * 1024;
+    __shared__ __align__(1024) int8_t ring[2 * kRowSWaves * kHeadBytes];
+    __shared__ __align__(16) float hsum[kQTile][kRowSMaxHeads];
+    __shared__ float rr_s[kQTile];
+    // The tile's frequency rows: fstage receives them as stored (chunk 2 i + c
+    // holds lane l's 16 bytes c of item i's row segment), fconv holds them
+    // as fp32, converted once per tile for all heads (chunk 4 i + p holds
+    // pair p's 2x2 row-major matrix of lane l's item i).
+    constexpr int kStageBytes = kRope ? 2 * kItems * 1024 : 16;
+    constexpr int kConvBytes = kRope ? 4 * kItems * 1024 : 16;
+    __shared__ __align__(1024) int8_t fstage[kStageBytes];
+    __shared__ __align__(1024) int8_t fconv[kConvBytes];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // 32-bit task arithmetic: batch x tiles < 2^31 (checked on the host)
+    const uint32_t len = static_cast<uint32_t>(args.len[0]), heads = static_cast<uint32_t>(args.heads[0]);
+    const uint32_t nt = static_cast<uint32_t>(args.ntiles[0]);
+    const int pack = lane % kPacks, trow = lane / kPacks;
+    const uint32_t x_sh2 = static_cast<uint32_t>(args.x_sh[0] * 2), x_sl2 = static_cast<uint32_t>(args.x_sl[0] * 2);
+    int8_t *const region[2] = {ring + wave * kHeadBytes, ring + (kRowSWaves + wave) * kHeadBytes};
+    const uint32_t nheads_w = (heads - wave + kRowSWaves - 1) / kRowSWaves;
+    const int nmine = static_cast<int>(nheads_w < 3u ? nheads_w : 3u);
+
+    // the task's rows: head `wave` into xa, the wave's other heads into its
+    // LDS regions; `from` selects which of those (0 registers, 1 + r region r)
+    auto issue_rows = [&](uint32_t task, int from, int upto, u32x4 (&xa)[kItems]) {
+        const uint32_t b = task / nt, tile = task - b * nt;
+        const __amdgpu_buffer_rsrc_t rs = make_rsrc(args.x[0] + b * args.x_sb[0], span);
+        uint32_t off[kItems];
+#pragma unroll
+        for (int i = 0; i < kItems; ++i) {
+            const uint32_t t = tile * kQTile + trow + kTokStep * i;
+            off[i] = t < len ? t * x_sl2 + pack * 16 : kRowSPast;
+        }
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+            if (k < from || k >= upto) continue;
+            const uint32_t hoff = static_cast<uint32_t>(wave + kRowSWaves * k) * x_sh2;
+            if (k == 0) {
+#pragma unroll
+                for (int i = 0; i < kItems; ++i) xa[i] = rows_load16(rs, off[i] + hoff);
+            } else {
+#pragma unroll
+                for (int i = 0; i < kItems; ++i) rows_load16_lds(rs, region[k - 1] + i * 1024, off[i] + hoff);
+            }
+        }
+    };
+    // wave n < 2 kItems loads chunk n of the task's frequency rows
+    auto issue_freqs = [&](uint32_t task) {
+        if constexpr (kRope) {
+            if (wave < 2 * kItems) {
+                const uint32_t b = task / nt, tile = task - b * nt;
+                const __amdgpu_buffer_rsrc_t rs =
+                    make_rsrc(args.freqs + (args.f_batches == 1 ? 0 : b) * args.f_sb, f_span);
+                const int i = wave >> 1;
+                const uint32_t t = tile * kQTile + trow + kTokStep * i;
+                const uint32_t off = t >= len ? kRowSPast
+                                              : (args.f_len == 1 ? 0u : t) * static_cast<uint32_t>(args.f_sl * 2) +
+                                                    pack * 32 + (wave & 1) * 16;
+                rows_load16_lds(rs, fstage + wave * 1024, off);
+            }
+        }
+    };
+    auto read_region = [&](int r, u32x4 (&xk)[kItems]) {
+#pragma unroll
+        for (int i = 0; i < kItems; ++i)
+            xk[i] = *reinterpret_cast<const u32x4 *>(region[r] + i * 1024 + lane * 16);
+    };
+
+    auto run = [&](uint32_t task, u32x4 (&xa)[kItems], u32x4 (&xa_next)[kItems]) {
+        const uint32_t b = task / nt, tile = task - b * nt;
+        const uint32_t next = task + gridDim.x;
+        const bool more = next < ntasks;
+        bool valid[kItems];
+#pragma unroll
+        for (int i = 0; i < kItems; ++i) valid[i] = tile * kQTile + trow + kTokStep * i < len;
+        // this task's rows (and frequencies) have arrived
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        // (1) per-head sums of squares
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+            if (k >= nmine) break;
+            const int h = wave + kRowSWaves * k;
+            u32x4 xk[kItems];
+            if (k == 0) {
+#pragma unroll
+                for (int i = 0; i < kItems; ++i) xk[i] = xa[i];
+            } else {
+                read_region(k - 1, xk);
+            }
+#pragma unroll
+            for (int i = 0; i < kItems; ++i) {
+                float sq = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float lo = t_to_f32<kFp16>(xk[i][j] & 0xffffu), hi = t_to_f32<kFp16>(xk[i][j] >> 16);
+                    sq = __builtin_fmaf(lo, lo, sq);
+                    sq = __builtin_fmaf(hi, hi, sq);
+                }
+                sq = pack_sum<kPacks>(sq);
+                if (pack == 0) hsum[kTokStep * i + trow][h] = sq;
+            }
+        }
+        __syncthreads();
+        if constexpr (kRope) {
+            // every wave is past the last tile's reads of fconv, and this
+            // tile's rows are in fstage
+            if (tid < 4 * kItems * 64) {
+                const int i = tid >> 8, p = (tid >> 6) & 3, l = tid & 63;
+                const u32x2 w = *reinterpret_cast<const u32x2 *>(fstage + (2 * i + (p >> 1)) * 1024 + l * 16 +
+                                                                 (p & 1) * 8);
+                *reinterpret_cast<f32x4 *>(fconv + (4 * i + p) * 1024 + l * 16) =
+                    f32x4{t_to_f32<kFp16>(w[0] & 0xffffu), t_to_f32<kFp16>(w[0] >> 16),
+                          t_to_f32<kFp16>(w[1] & 0xffffu), t_to_f32<kFp16>(w[1] >> 16)};
+            }
+        }
+        // (2) wave t: token t's heads in order
+        {
+            float total = 0.0f;
+            for (uint32_t h = 0; h < heads; ++h) total = total + hsum[wave][h];
+            if (lane == 0) rr_s[wave] = 1.0f / __builtin_sqrtf(total / static_cast<float>(heads * D) + args.eps);
+        }
+        __syncthreads();
+        float rr[kItems];
+#pragma unroll
+        for (int i = 0; i < kItems; ++i) rr[i] = rr_s[kTokStep * i + trow];
+
+        // (3) normalize, rotate, quantize; the next task's loads go out as
+        // each head's source is free.  The LDS heads go first, so their
+        // regions are refilled early; the register head (double-buffered)
+        // goes last.
+        // fstage was read before the barrier above
+        if (more) issue_freqs(next);
+#pragma unroll
+        for (int kk = 0; kk < 3; ++kk) {
+            const int k = (kk + 1) % 3;
+            if (k >= nmine) continue;
+            if (k == 0 && more) issue_rows(next, 0, 1, xa_next);
+            const uint32_t h = wave + kRowSWaves * k;
+            const u32x4 wraw = *reinterpret_cast<const u32x4 *>(args.norm[0] + h * D + pack * 8);
+            float y[kItems][8];
+            float amax = 0.0000001f;
+#pragma unroll
+            for (int i = 0; i < kItems; ++i) {
+                const u32x4 xi = k == 0 ? xa[i] : *reinterpret_cast<const u32x4 *>(region[k - 1] + i * 1024 + lane * 16);
+                float a[8];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    a[2 * j] = (t_to_f32<kFp16>(xi[j] & 0xffffu) * rr[i]) * t_to_f32<kFp16>(wraw[j] & 0xffffu);
+                    a[2 * j + 1] = (t_to_f32<kFp16>(xi[j] >> 16) * rr[i]) * t_to_f32<kFp16>(wraw[j] >> 16);
+                    t_round2<kFp16>(a[2 * j], a[2 * j + 1]);
+                }
+                float pmax = 0.0f;
+#pragma unroll
+                for (int pi = 0; pi < 4; ++pi) {
+                    float v0 = a[2 * pi], v1 = a[2 * pi + 1];
+                    if constexpr (kRope) {
+                        const f32x4 f = *reinterpret_cast<const f32x4 *>(fconv + (4 * i + pi) * 1024 + lane * 16);
+                        v0 = __builtin_fmaf(f[1], a[2 * pi + 1], f[0] * a[2 * pi]);
+                        v1 = __builtin_fmaf(f[3], a[2 * pi + 1], f[2] * a[2 * pi]);
+                        t_round2<kFp16>(v0, v1);
+                    }
+                    y[i][2 * pi] = v0;
+                    y[i][2 * pi + 1] = v1;
+                    pmax = max3_abs(pmax, v0, v1);
+                }
+                if (valid[i]) amax = __int_as_float(max(__float_as_int(amax), __float_as_int(pmax)));
+            }
+            amax = wave_max_nonneg(amax);
+            if (k > 0 && more) {
+                // the region's reads have returned before it is refilled
+                __builtin_amdgcn_s_waitcnt(lgkmcnt_imm(0));
+                issue_rows(next, k, k + 1, xa_next);
+            }
+            if (lane == 0) args.scale[0][(static_cast<int64_t>(b) * heads + h) * nt + tile] = amax / 127.0f;
+            const float inv = 127.0f / amax;
+            int8_t *obase = args.out[0] + b * args.o_sb[0] + h * args.o_sh[0];
+#pragma unroll
+            for (int i = 0; i < kItems; ++i) {
+                if (!valid[i]) continue;
+                const u32x2 w2{quant_pack4(y[i][0], y[i][1], y[i][2], y[i][3], inv),
+                               quant_pack4(y[i][4], y[i][5], y[i][6], y[i][7], inv)};
+                *reinterpret_cast<u32x2 *>(obase + (tile * kQTile + trow + kTokStep * i) * args.o_sl[0] + pack * 8) = w2;
+            }
+        }
+    };
+
+    uint32_t task = blockIdx.x;
+    if (task >= ntasks) return;
+    u32x4 xa0[kItems], xa1[kItems];
+    issue_rows(task, 0, nmine, xa0);
+    issue_freqs(task);
+    for (;;) {
+        run(task, xa0, xa1);
+        task += gridDim.x;
+        if (task >= ntasks) break;
+        run(task, xa1, xa0);
+        task += gridDim.x;
+        if (task >= ntasks) break;
     }
 }
 
@@ -688,8 +996,7 @@ __global__ __launch_bounds__(kQkThreads) void row_rrms_batched_kernel(QkArgs arg
                 s = __builtin_fmaf(lo, lo, s);
                 s = __builtin_fmaf(hi, hi, s);
             }
-#pragma unroll
-            for (int off = kPacks / 2; off > 0; off >>= 1) s = s + __shfl_xor(s, off, kPacks);
+            s = pack_sum<kPacks>(s);
             if (h0 + g < heads) total = total + s;
         }
     }
@@ -780,7 +1087,13 @@ int32_t launch_qk(const QkArgs &args, int64_t batch, bool split, bool row, bool 
     // interleaved RoPE over the whole head (contiguous frequencies) or none,
     // no rotation: the head-group fast path
     const bool fast = !rotate && !split && (args.rot_dim == 0 || (args.rot_dim == D && args.f_contig));
-    if (fast && row && args.heads[0] <= 40) {
+    // the streamed Q kernel: a batch's Q rows within 2 GiB of 32-bit offsets
+    const int64_t q_span = ((args.heads[0] - 1) * args.x_sh[0] + (args.len[0] - 1) * args.x_sl[0] + D) * 2;
+    // and its frequency rows (one batch of them) likewise
+    const int64_t f_span = args.rot_dim == 0 ? 0 : ((args.f_len - 1) * args.f_sl + 2 * D) * 2;
+    const bool stream = fast && row && args.heads[0] > 16 && args.heads[0] <= kRowSMaxHeads && q_span < (1ll << 31) &&
+                        f_span < (1ll << 31) && args.ntiles[0] * batch < (1ll << 31);
+    if (fast && row && (stream || args.heads[0] <= 40)) {
         // Q in one pass; K: its row pre-pass, then the head-group kernel
         QkArgs ka = args;
         ka.k_only = 1;
@@ -788,15 +1101,28 @@ int32_t launch_qk(const QkArgs &args, int64_t batch, bool split, bool row, bool 
         const dim3 gr(static_cast<unsigned>((args.len[1] + kTokPerBlock - 1) / kTokPerBlock),
                       static_cast<unsigned>(batch));
         row_rrms_batched_kernel<kFp16, D><<<gr, kQkThreads, 0, s>>>(ka);
-        const dim3 gq(static_cast<unsigned>(args.ntiles[0]), static_cast<unsigned>(batch));
-        const bool small = args.heads[0] <= 16;
-        constexpr int kSmall = 16 / (kRowQThreads / 64), kLarge = 40 / (kRowQThreads / 64);
+        if (stream) {
+            int cus = 0;
+            if (device_cus(cus)) return -1;
+            const uint32_t ntasks = static_cast<uint32_t>(args.ntiles[0] * batch);
+            const unsigned grid = ntasks < static_cast<uint32_t>(cus) ? ntasks : static_cast<unsigned>(cus);
+            const uint32_t span = static_cast<uint32_t>(q_span);
+            if (args.rot_dim == 0)
+                qk_rowq_stream_kernel<kFp16, D, false><<<grid, kRowSThreads, 0, s>>>(args, ntasks, span, 0u);
+            else
+                qk_rowq_stream_kernel<kFp16, D, true><<<grid, kRowSThreads, 0, s>>>(args, ntasks, span,
+                                                                                   static_cast<uint32_t>(f_span));
+        } else {
+            const dim3 gq(static_cast<unsigned>(args.ntiles[0]), static_cast<unsigned>(batch));
+            const bool small = args.heads[0] <= 16;
+            constexpr int kSmall = 16 / (kRowQThreads / 64), kLarge = 40 / (kRowQThreads / 64);
 #define TU_ROWQ(R) \
     if (small) qk_rowq_kernel<kFp16, D, R, kSmall><<<gq, kRowQThreads, 0, s>>>(args); \
     else qk_rowq_kernel<kFp16, D, R, kLarge><<<gq, kRowQThreads, 0, s>>>(args)
-        if (args.rot_dim == 0) { TU_ROWQ(false); }
-        else { TU_ROWQ(true); }
+            if (args.rot_dim == 0) { TU_ROWQ(false); }
+            else { TU_ROWQ(true); }
 #undef TU_ROWQ
+        }
         const int64_t gk = (args.heads[1] + kHeadGroup - 1) / kHeadGroup;
         const dim3 grid(static_cast<unsigned>(gk * ((args.len[1] + kChunk - 1) / kChunk)), static_cast<unsigned>(batch));
         if (args.rot_dim == 0) qk_rope_quant_heads_kernel<kFp16, D, true, false><<<grid, kQkThreads, 0, s>>>(ka);

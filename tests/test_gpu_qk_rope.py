@@ -80,6 +80,42 @@ def test_row_scope_head_counts(gpu_device, dtype, d, hq, hk, rot_full):
     _check_exact(q, k, qw, kw, freqs, rot, "row", False, "HND", gpu_device)
 
 
+@pytest.mark.parametrize("dtype,d,rot_full,layout", [(torch.bfloat16, 128, True, "HND"),
+                                                     (torch.float16, 128, False, "NHD"),
+                                                     (torch.bfloat16, 64, True, "NHD"),
+                                                     (torch.float16, 64, True, "HND")])
+def test_row_scope_streamed_tiles(gpu_device, dtype, d, rot_full, layout):
+    """Row-scope Q with 17-48 heads runs one workgroup per CU that walks
+    several 16-token tiles, loading the next tile while it quantizes the
+    current one.  Three batches of 7000 tokens give 1320 tiles: every
+    workgroup runs five or six of them (an uneven count), across batch
+    boundaries and into the ragged and padded tiles; all of it bit-exact."""
+    rot = d if rot_full else 0
+    print(f"[qk-rope] streamed row {dtype} d={d} rot={rot} {layout}", flush=True)
+    q, k, qw, kw, freqs = _case(3, 20, 4, 7000, d, dtype, "row", rot, 3, 7000, 500 + d + rot, layout=layout)
+    _check_exact(q, k, qw, kw, freqs, rot, "row", False, layout, gpu_device)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("scope,hq", [("row", 20), ("row", 4), ("head", 20)])
+def test_non_finite_inputs(gpu_device, dtype, scope, hq):
+    """NaN, +-inf and the type's largest values in Q and K: a NaN row
+    normalizes to NaN and quantizes to -127 while its tile's amax passes it
+    over, as fmaxf does; every path (streamed row-scope Q, the one-pass and
+    head-group kernels) bit-exact against the oracle."""
+    print(f"[qk-rope] non-finite {dtype} {scope} hq={hq}", flush=True)
+    q, k, qw, kw, freqs = _case(1, hq, 2, 300, 128, dtype, scope, 128, 1, 300, 77 + hq)
+    big = torch.finfo(dtype).max
+    for x in (q, k):
+        x[0, 0, 5, 3] = float("nan")
+        x[0, 1, 40, :] = float("nan")
+        x[0, 1, 70, 9] = float("inf")
+        x[0, 0, 130, 0] = -float("inf")
+        x[0, 1, 200, 17] = big
+        x[0, 0, 201, 18] = -big
+    _check_exact(q, k, qw, kw, freqs, 128, scope, False, "HND", gpu_device)
+
+
 @pytest.mark.parametrize("scope", ["head", "row"])
 def test_nhd_strided_and_broadcast_freqs(gpu_device, scope):
     """Wan's call: HND views of an NHD projection ([B, L, H, D].transpose(1, 2)),

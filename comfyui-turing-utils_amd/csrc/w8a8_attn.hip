@@ -121,15 +121,21 @@ __device__ __forceinline__ void qk_tile8(const int8_t *stage, const LaneGeom8 &g
 }
 
 // Wave softmax state.  acc_i holds the PV products of tiles [seg, current)
-// in int32 (with P - 128 operands), acc_o the fp32 sum of earlier segments
-// rescaled to m_used; l is this lane's part of the row sum of p.
+// in int32 (with P - 128 operands).  acc_o and l are kept at a fixed
+// exponent base per query, the first one: a segment computed at base m_used
+// enters them scaled by beta = 2^(m_used - that base), so a move of the
+// running maximum rescales nothing (O / l does not depend on the base).  The
+// fixed base moves up to m_used, with acc_o and l rescaled, only when beta
+// passes kRebase.
 struct W8State {
     float m_used[kQT];
+    float beta[kQT];
     float l[kQT];
     f32x4 acc_o[8][kQT];
     i32x4 acc_i[8][kQT];
     int seg;
 };
+constexpr float kRebase = 0x1p64f;
 
 template <bool kCausal>
 __device__ __forceinline__ void mask_tile8(i32x4 (&s)[4][kQT], int key_lim, int q_rel, int g, int lc) {
@@ -151,7 +157,7 @@ __device__ __forceinline__ void mask_tile8(i32x4 (&s)[4][kQT], int key_lim, int 
 }
 
 // Adds the int32 segment [st.seg, tile) to acc_o: acc_i + 128 * (sum of the
-// segment's V codes per channel), then clears acc_i.
+// segment's V codes per channel), scaled by beta, then clears acc_i.
 __device__ __forceinline__ void flush_segment(W8State &st, int tile, const int32_t *__restrict__ vpre, int g) {
     if (tile > st.seg) {
         const int32_t *hi = vpre + static_cast<int64_t>(tile) * kD + 4 * g;
@@ -164,7 +170,8 @@ __device__ __forceinline__ void flush_segment(W8State &st, int tile, const int32
             for (int qt = 0; qt < kQT; ++qt) {
                 const i32x4 tot = st.acc_i[ds][qt] + corr;
 #pragma unroll
-                for (int r = 0; r < 4; ++r) st.acc_o[ds][qt][r] += static_cast<float>(tot[r]);
+                for (int r = 0; r < 4; ++r)
+                    st.acc_o[ds][qt][r] = __builtin_fmaf(static_cast<float>(tot[r]), st.beta[qt], st.acc_o[ds][qt][r]);
                 st.acc_i[ds][qt] = i32x4{0, 0, 0, 0};
             }
         }
@@ -194,16 +201,27 @@ __device__ __forceinline__ void softmax_tile8(const i32x4 (&s)[4][kQT], const fl
     }
     if (__any(need) || tile - st.seg >= kFlushTiles) {
         flush_segment(st, tile, vpre, g);
+        bool rebase = false;
 #pragma unroll
         for (int qt = 0; qt < kQT; ++qt) {
             // the reference's exact running maximum
             const float mx = xmax_f32(mlane[qt]);
             const float m_new = mx > st.m_used[qt] ? mx : st.m_used[qt];
-            const float alpha = __builtin_amdgcn_exp2f(st.m_used[qt] - m_new);  // 2^-inf = 0 on the first tile
+            // the first tile fixes the base (acc_o and l are still 0)
+            st.beta[qt] = st.m_used[qt] == -INFINITY ? 1.0f
+                                                     : st.beta[qt] * __builtin_amdgcn_exp2f(m_new - st.m_used[qt]);
             st.m_used[qt] = m_new;
-            st.l[qt] *= alpha;
+            rebase = rebase || st.beta[qt] > kRebase;
+        }
+        if (__any(rebase)) {
 #pragma unroll
-            for (int ds = 0; ds < 8; ++ds) st.acc_o[ds][qt] *= alpha;
+            for (int qt = 0; qt < kQT; ++qt) {
+                const float alpha = 1.0f / st.beta[qt];
+                st.beta[qt] = 1.0f;
+                st.l[qt] *= alpha;
+#pragma unroll
+                for (int ds = 0; ds < 8; ++ds) st.acc_o[ds][qt] *= alpha;
+            }
         }
     }
     float c[kQT];
@@ -236,7 +254,7 @@ __device__ __forceinline__ void softmax_tile8(const i32x4 (&s)[4][kQT], const fl
                 // P - 128 as signed bytes for the signed-only MFMA
                 p8[qt][kt] = static_cast<int32_t>(packed ^ 0x80808080u);
             }
-            st.l[qt] += lsum;
+            st.l[qt] = __builtin_fmaf(lsum, st.beta[qt], st.l[qt]);
         }
     };
     if (__any(exact)) make_p(std::true_type{});
@@ -364,6 +382,7 @@ __global__ __launch_bounds__(kThreads, 1) void w8a8_attn_kernel(
 #pragma unroll
     for (int qt = 0; qt < kQT; ++qt) {
         st.m_used[qt] = -INFINITY;
+        st.beta[qt] = 1.0f;
         st.l[qt] = 0.0f;
 #pragma unroll
         for (int ds = 0; ds < 8; ++ds) {

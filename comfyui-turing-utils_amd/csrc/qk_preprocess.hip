@@ -1088,10 +1088,13 @@ int32_t launch_qk(const QkArgs &args, int64_t batch, bool split, bool row, bool 
     // no rotation: the head-group fast path
     const bool fast = !rotate && !split && (args.rot_dim == 0 || (args.rot_dim == D && args.f_contig));
     // the streamed Q kernel: a batch's Q rows within 2 GiB of 32-bit offsets
+    // (non-negative head, token and frequency strides)
+    const bool q_strides_ok = args.x_sh[0] >= 0 && args.x_sl[0] >= 0 && (args.rot_dim == 0 || args.f_sl >= 0);
     const int64_t q_span = ((args.heads[0] - 1) * args.x_sh[0] + (args.len[0] - 1) * args.x_sl[0] + D) * 2;
     // and its frequency rows (one batch of them) likewise
     const int64_t f_span = args.rot_dim == 0 ? 0 : ((args.f_len - 1) * args.f_sl + 2 * D) * 2;
-    const bool stream = fast && row && args.heads[0] > 16 && args.heads[0] <= kRowSMaxHeads && q_span < (1ll << 31) &&
+    const bool stream = fast && row && q_strides_ok && args.heads[0] > 16 && args.heads[0] <= kRowSMaxHeads &&
+                        q_span < (1ll << 31) &&
                         f_span < (1ll << 31) && args.ntiles[0] * batch < (1ll << 31);
     if (fast && row && (stream || args.heads[0] <= 40)) {
         // Q in one pass; K: its row pre-pass, then the head-group kernel

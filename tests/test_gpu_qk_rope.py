@@ -96,6 +96,15 @@ def test_row_scope_streamed_tiles(gpu_device, dtype, d, rot_full, layout):
     _check_exact(q, k, qw, kw, freqs, rot, "row", False, layout, gpu_device)
 
 
+@pytest.mark.parametrize("d", [64, 128])
+def test_row_scope_streamed_broadcast_freqs(gpu_device, d):
+    """The streamed row-scope Q kernel with one frequency row for every token
+    and batch (f_batches = f_len = 1), 33 heads."""
+    print(f"[qk-rope] streamed row broadcast freqs d={d}", flush=True)
+    q, k, qw, kw, freqs = _case(2, 33, 3, 301, d, torch.bfloat16, "row", d, 1, 1, 900 + d)
+    _check_exact(q, k, qw, kw, freqs, d, "row", False, "HND", gpu_device)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("scope,hq", [("row", 20), ("row", 4), ("head", 20)])
 def test_non_finite_inputs(gpu_device, dtype, scope, hq):

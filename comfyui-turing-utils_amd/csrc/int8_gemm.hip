@@ -44,10 +44,9 @@
 namespace tu {
 namespace {
 
-// Activation rows per workgroup: 256, or 128 for grids that 256-row tiles
-// would fill in few, partly empty rounds (the tile policy; the wave grid and
-// the weight tile stay the same).
-constexpr int kBN = 256;  // weight rows (output columns) per workgroup
+// Workgroup tile: BM activation rows x BN weight rows (output columns).
+// 256 x 256, or for grids that those would fill in few, partly empty rounds
+// (the tile policy) 128 x 256 or 256 x 192; the wave grid stays the same.
 constexpr int kBK = 128;  // bytes of K per step (two 64-deep MFMA slices)
 // Waves per workgroup: 2 along the weight rows x kWavesM along the activation
 // rows; each wave owns a 128 x (256 / kWavesM) output tile.
@@ -62,21 +61,28 @@ constexpr int kGroupM = 4;
 #define TU_GEMM_HALF_TILE_COST 0.635
 #endif
 
-// Geometry of a workgroup tile with BM activation rows.
-template <int BM>
+// Geometry of a workgroup tile with BM activation rows and BN weight rows.
+template <int BM, int BN>
 struct Tile {
-    static_assert(BM == 256 || BM == 128, "activation tile of 256 or 128 rows");
+    static_assert((BM == 256 && (BN == 256 || BN == 192)) || (BM == 128 && BN == 256), "tile of 256 x 256, 128 x 256 or 256 x 192");
     static constexpr int kFragsM = BM / kWavesM / 16;  // 16-row activation fragments per wave
-    static constexpr int kMma = 8 * kFragsM;           // MFMAs per 64-deep slice and wave
+    static constexpr int kFragsN = BN / 2 / 16;        // 16-row weight fragments per wave (its half of the tile)
+    static constexpr int kMma = kFragsN * kFragsM;     // MFMAs per 64-deep slice and wave
     // MFMAs of slice 0 issued before the step's barrier, covering the latency
     // of slice 1's LDS reads (the rest cover the next step's loads)
-    static constexpr int kPre = BM == 256 ? 16 : 8;
+    static constexpr int kPre = kMma / 2;
     static constexpr int kABlocks = BM * 128 / 1024 / kWaves;   // 1 KiB activation blocks per wave and step
-    static constexpr int kWBlocks = kBN * 128 / 1024 / kWaves;  // 1 KiB weight blocks per wave and step
+    static constexpr int kWBlocks = BN * 128 / 1024 / kWaves;   // 1 KiB weight blocks per wave and step
+    static constexpr int kBlocks = kABlocks > kWBlocks ? kABlocks : kWBlocks;
     static constexpr int kLoads = kABlocks + kWBlocks;          // vector-memory loads per wave and step
-    static constexpr int kStageBytes = (BM + kBN) * 128;        // activation panel + weight panel
+    static constexpr int kStageBytes = (BM + BN) * 128;         // activation panel + weight panel
     static constexpr int kChunksA = BM * 8 / kThreads;          // 16-byte chunks per thread, register path
-    static constexpr int kChunksW = kBN * 8 / kThreads;
+    static constexpr int kChunksW = BN * 8 / kThreads;
+    static constexpr int kChunks = kChunksA > kChunksW ? kChunksA : kChunksW;
+    static constexpr int kRows = 16 * kFragsM;                  // activation rows per wave
+    // LDS: the K-step ring, and after the main loop each wave's 16-bit output
+    // tile (kRows rows of 256 bytes) staged for row-wide stores
+    static constexpr int kLdsBytes = 2 * kStageBytes > kWaves * kRows * 256 ? 2 * kStageBytes : kWaves * kRows * 256;
 };
 
 // LDS panel layout: 128-byte rows, the 16-byte chunk index XOR-swizzled with
@@ -84,42 +90,44 @@ struct Tile {
 // of 16 consecutive rows; 64-byte rows with a 2-bit swizzle were not).
 __device__ __forceinline__ int swz(int row, int chunk) { return row * kBK + ((chunk ^ ((row >> 1) & 7)) << 4); }
 
-template <int BM>
+template <int BM, int BN>
 struct TileLoad {
-    i32x4 a[Tile<BM>::kChunksA];
-    i32x4 w[Tile<BM>::kChunksW];
+    i32x4 a[Tile<BM, BN>::kChunksA];
+    i32x4 w[Tile<BM, BN>::kChunksW];
 };
 
-// Loads the BM x 128 B activation and 256 x 128 B weight panels of step k0
+// Loads the BM x 128 B activation and BN x 128 B weight panels of step k0
 // into registers.  Rows past the end are clamped (their results are never
 // stored); columns past K are zero.
-template <int BM>
-__device__ __forceinline__ void load_tiles(TileLoad<BM> &t, const int8_t *__restrict__ a,
+template <int BM, int BN>
+__device__ __forceinline__ void load_tiles(TileLoad<BM, BN> &t, const int8_t *__restrict__ a,
                                            const int8_t *__restrict__ w, int64_t m0, int64_t n0,
                                            int64_t m, int64_t n, int64_t k, int64_t k0, int tid) {
 #pragma unroll
-    for (int i = 0; i < Tile<BM>::kChunksW; ++i) {
+    for (int i = 0; i < Tile<BM, BN>::kChunks; ++i) {
         const int id = tid + kThreads * i;
         const int row = id >> 3;
         const int64_t kk = k0 + (id & 7) * 16;
-        const int64_t rw = min(n0 + row, n - 1);
-        t.w[i] = kk < k ? *reinterpret_cast<const i32x4 *>(w + rw * k + kk) : i32x4{0, 0, 0, 0};
-        if (i < Tile<BM>::kChunksA) {
+        if (i < Tile<BM, BN>::kChunksW) {
+            const int64_t rw = min(n0 + row, n - 1);
+            t.w[i] = kk < k ? *reinterpret_cast<const i32x4 *>(w + rw * k + kk) : i32x4{0, 0, 0, 0};
+        }
+        if (i < Tile<BM, BN>::kChunksA) {
             const int64_t ra = min(m0 + row, m - 1);
             t.a[i] = kk < k ? *reinterpret_cast<const i32x4 *>(a + ra * k + kk) : i32x4{0, 0, 0, 0};
         }
     }
 }
 
-template <int BM>
-__device__ __forceinline__ void store_tiles(const TileLoad<BM> &t, int8_t *lds_a, int8_t *lds_w, int tid) {
+template <int BM, int BN>
+__device__ __forceinline__ void store_tiles(const TileLoad<BM, BN> &t, int8_t *lds_a, int8_t *lds_w, int tid) {
 #pragma unroll
-    for (int i = 0; i < Tile<BM>::kChunksW; ++i) {
+    for (int i = 0; i < Tile<BM, BN>::kChunks; ++i) {
         const int id = tid + kThreads * i;
         const int row = id >> 3;
         const int chunk = id & 7;
-        *reinterpret_cast<i32x4 *>(lds_w + swz(row, chunk)) = t.w[i];
-        if (i < Tile<BM>::kChunksA) *reinterpret_cast<i32x4 *>(lds_a + swz(row, chunk)) = t.a[i];
+        if (i < Tile<BM, BN>::kChunksW) *reinterpret_cast<i32x4 *>(lds_w + swz(row, chunk)) = t.w[i];
+        if (i < Tile<BM, BN>::kChunksA) *reinterpret_cast<i32x4 *>(lds_a + swz(row, chunk)) = t.a[i];
     }
 }
 
@@ -155,25 +163,25 @@ typedef __attribute__((address_space(3))) void lds_void;
 // Offsets are relative to the panel's first row at K offset 0 (32-bit: a
 // panel row index times K plus a chunk offset; rows past the end are
 // clamped, their results never stored).
-template <int BM>
+template <int BM, int BN>
 struct LoadGeom {
-    uint32_t a_off[Tile<BM>::kABlocks];
-    uint32_t w_off[Tile<BM>::kWBlocks];
+    uint32_t a_off[Tile<BM, BN>::kABlocks];
+    uint32_t w_off[Tile<BM, BN>::kWBlocks];
 };
 
-template <int BM>
-__device__ __forceinline__ LoadGeom<BM> load_geom(int64_t m0, int64_t n0, int64_t m, int64_t n, int64_t k, int wave,
-                                                  int lane) {
-    LoadGeom<BM> gm;
+template <int BM, int BN>
+__device__ __forceinline__ LoadGeom<BM, BN> load_geom(int64_t m0, int64_t n0, int64_t m, int64_t n, int64_t k,
+                                                      int wave, int lane) {
+    LoadGeom<BM, BN> gm;
 #pragma unroll
-    for (int i = 0; i < Tile<BM>::kABlocks; ++i) {
-        const int row = 8 * (Tile<BM>::kABlocks * wave + i) + (lane >> 3);
+    for (int i = 0; i < Tile<BM, BN>::kABlocks; ++i) {
+        const int row = 8 * (Tile<BM, BN>::kABlocks * wave + i) + (lane >> 3);
         const int c = (lane & 7) ^ ((row >> 1) & 7);
         gm.a_off[i] = static_cast<uint32_t>((min(m0 + row, m - 1) - m0) * k + c * 16);
     }
 #pragma unroll
-    for (int i = 0; i < Tile<BM>::kWBlocks; ++i) {
-        const int row = 8 * (Tile<BM>::kWBlocks * wave + i) + (lane >> 3);
+    for (int i = 0; i < Tile<BM, BN>::kWBlocks; ++i) {
+        const int row = 8 * (Tile<BM, BN>::kWBlocks * wave + i) + (lane >> 3);
         const int c = (lane & 7) ^ ((row >> 1) & 7);
         gm.w_off[i] = static_cast<uint32_t>((min(n0 + row, n - 1) - n0) * k + c * 16);
     }
@@ -194,28 +202,34 @@ __device__ __forceinline__ const int8_t *uniform_ptr(const int8_t *p) {
 // the scalar offset, so no 64-bit address is formed per load.
 // One overload per tile height: the host compilation pass rejects a template
 // of this function (the buffer builtins exist only for the device target).
-#define TU_ISSUE_STEP_BODY(BM)                                                                                   \
-    _Pragma("unroll") for (int i = 0; i < Tile<BM>::kWBlocks; ++i) {                                            \
-        if (i < Tile<BM>::kABlocks)                                                                             \
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(ars, (lds_void *)(stage + (Tile<BM>::kABlocks * wave + i) * 1024), \
-                                                     16, gm.a_off[i], k0, 0, 0);                                \
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(                                                               \
-            wrs, (lds_void *)(stage + BM * kBK + (Tile<BM>::kWBlocks * wave + i) * 1024), 16, gm.w_off[i], k0, 0, 0); \
+#define TU_ISSUE_STEP_BODY(BM, BN)                                                                               \
+    _Pragma("unroll") for (int i = 0; i < Tile<BM, BN>::kBlocks; ++i) {                                         \
+        if (i < Tile<BM, BN>::kABlocks)                                                                         \
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(                                                           \
+                ars, (lds_void *)(stage + (Tile<BM, BN>::kABlocks * wave + i) * 1024), 16, gm.a_off[i], k0, 0, 0); \
+        if (i < Tile<BM, BN>::kWBlocks)                                                                         \
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(                                                           \
+                wrs, (lds_void *)(stage + BM * kBK + (Tile<BM, BN>::kWBlocks * wave + i) * 1024), 16, gm.w_off[i], \
+                k0, 0, 0);                                                                                      \
     }
 __device__ __forceinline__ void issue_step(int8_t *stage, __amdgpu_buffer_rsrc_t ars, __amdgpu_buffer_rsrc_t wrs,
-                                           const LoadGeom<256> &gm, uint32_t k0, int wave) {
-    TU_ISSUE_STEP_BODY(256)
+                                           const LoadGeom<256, 256> &gm, uint32_t k0, int wave) {
+    TU_ISSUE_STEP_BODY(256, 256)
 }
 __device__ __forceinline__ void issue_step(int8_t *stage, __amdgpu_buffer_rsrc_t ars, __amdgpu_buffer_rsrc_t wrs,
-                                           const LoadGeom<128> &gm, uint32_t k0, int wave) {
-    TU_ISSUE_STEP_BODY(128)
+                                           const LoadGeom<128, 256> &gm, uint32_t k0, int wave) {
+    TU_ISSUE_STEP_BODY(128, 256)
+}
+__device__ __forceinline__ void issue_step(int8_t *stage, __amdgpu_buffer_rsrc_t ars, __amdgpu_buffer_rsrc_t wrs,
+                                           const LoadGeom<256, 192> &gm, uint32_t k0, int wave) {
+    TU_ISSUE_STEP_BODY(256, 192)
 }
 #undef TU_ISSUE_STEP_BODY
 
-template <int BM>
+template <int BM, int BN>
 struct Frags {
-    i32x4 a[8];                     // weight rows (MFMA A operand)
-    i32x4 b[Tile<BM>::kFragsM];     // activation rows (MFMA B operand)
+    i32x4 a[Tile<BM, BN>::kFragsN];  // weight rows (MFMA A operand)
+    i32x4 b[Tile<BM, BN>::kFragsM];  // activation rows (MFMA B operand)
 };
 
 // (1, 1) in bf16: the gate of a residual add without one.
@@ -233,21 +247,23 @@ constexpr int kOutI32 = 3;   // the int32 accumulator (direct 16-byte stores)
 // residual and then written by the same lane, and no lane stores a chunk
 // that another lane reads (clamped reads past the last row feed only rows
 // that are never stored).
-template <int BM, int kOut, bool kResidual>
+template <int BM, int BN, int kOut, bool kResidual>
 __global__ __launch_bounds__(kThreads, kWaves / 4) void int8_gemm_kernel(
     const int8_t *__restrict__ a, const int8_t *__restrict__ w, const float *__restrict__ as,
     const float *__restrict__ ws, const float *__restrict__ bias, void *out,
     int64_t m, int64_t n, int64_t k, int tiles_m, int tiles_n, const uint16_t *residual, const uint16_t *gate,
     int64_t gate_rows) {
     constexpr int kBM = BM;
-    constexpr int kFragsM = Tile<BM>::kFragsM;
-    constexpr int kStageBytes = Tile<BM>::kStageBytes;
-    __shared__ __align__(1024) int8_t lds[kStages][kStageBytes];
+    constexpr int kFragsM = Tile<BM, BN>::kFragsM;
+    constexpr int kFragsN = Tile<BM, BN>::kFragsN;
+    constexpr int kStageBytes = Tile<BM, BN>::kStageBytes;
+    __shared__ __align__(1024) int8_t lds_mem[Tile<BM, BN>::kLdsBytes];
+    auto lds = [&](int st) { return lds_mem + st * kStageBytes; };
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wn = wave / kWavesM;  // which 128-row half of the W tile
+    const int wn = wave / kWavesM;  // which half (BN / 2 rows) of the W tile
     const int wm = wave % kWavesM;  // which activation-row slice of the tile
 
     int tm, tn;
@@ -257,25 +273,25 @@ __global__ __launch_bounds__(kThreads, kWaves / 4) void int8_gemm_kernel(
     tm = __builtin_amdgcn_readfirstlane(tm);
     tn = __builtin_amdgcn_readfirstlane(tn);
     const int64_t m0 = static_cast<int64_t>(tm) * kBM;
-    const int64_t n0 = static_cast<int64_t>(tn) * kBN;
-    const LoadGeom<BM> gm = load_geom<BM>(m0, n0, m, n, k, wave, lane);
+    const int64_t n0 = static_cast<int64_t>(tn) * BN;
+    const LoadGeom<BM, BN> gm = load_geom<BM, BN>(m0, n0, m, n, k, wave, lane);
     // Buffer resources over the tile's two panels (BM and 256 rows of K bytes,
     // K < 2^17, so every offset fits in 32 bits).  The panel addresses are
     // uniform; passing them through readfirstlane keeps the resources in
     // scalar registers.
     const __amdgpu_buffer_rsrc_t ars = make_rsrc(uniform_ptr(a + m0 * k), static_cast<uint32_t>(kBM * k));
-    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(uniform_ptr(w + n0 * k), static_cast<uint32_t>(kBN * k));
+    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(uniform_ptr(w + n0 * k), static_cast<uint32_t>(BN * k));
 
-    i32x4 acc[8][kFragsM];
+    i32x4 acc[kFragsN][kFragsM];
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < kFragsN; ++i)
 #pragma unroll
         for (int j = 0; j < kFragsM; ++j) acc[i][j] = i32x4{0, 0, 0, 0};
 
     const int frag_row = lane & 15;
     const int frag_chunk = lane >> 4;
     // Fragments of 64-deep slice kk (0 or 1) of a stage.
-    auto load_frags = [&](Frags<BM> &f, const int8_t *stage, int kk) {
+    auto load_frags = [&](Frags<BM, BN> &f, const int8_t *stage, int kk) {
         const int8_t *la = stage;
         const int8_t *lw = stage + kBM * kBK;
 #pragma unroll
@@ -283,17 +299,17 @@ __global__ __launch_bounds__(kThreads, kWaves / 4) void int8_gemm_kernel(
             f.b[j] = *reinterpret_cast<const i32x4 *>(
                 la + swz(wm * 16 * kFragsM + j * 16 + frag_row, 4 * kk + frag_chunk));
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
-            f.a[i] = *reinterpret_cast<const i32x4 *>(lw + swz(wn * 128 + i * 16 + frag_row, 4 * kk + frag_chunk));
+        for (int i = 0; i < kFragsN; ++i)
+            f.a[i] = *reinterpret_cast<const i32x4 *>(lw + swz(wn * (BN / 2) + i * 16 + frag_row, 4 * kk + frag_chunk));
     };
     // A slice's MFMAs walk the (i, j) fragment grid as a snake: j runs up on
     // even i and down on odd i, so consecutive MFMAs always share one operand
     // (at a row change the activation fragment stays).  Under the board power
     // limit the fewer operand changes measured 0.5-1 % faster at the Wan
     // shapes; each accumulator's K order, and so every result, is unchanged.
-    auto mma = [&](const Frags<BM> &f) {
+    auto mma = [&](const Frags<BM, BN> &f) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
+        for (int i = 0; i < kFragsN; ++i)
 #pragma unroll
             for (int jj = 0; jj < kFragsM; ++jj) {
                 const int j = (i & 1) ? kFragsM - 1 - jj : jj;
@@ -302,7 +318,7 @@ __global__ __launch_bounds__(kThreads, kWaves / 4) void int8_gemm_kernel(
     };
     // MFMAs [b, e) of a slice in the same order; b and e are constants at
     // every call, so the loop unrolls to fixed accumulator registers.
-    auto mma_part = [&](const Frags<BM> &f, int b, int e) {
+    auto mma_part = [&](const Frags<BM, BN> &f, int b, int e) {
 #pragma unroll
         for (int x = b; x < e; ++x) {
             const int i = x / kFragsM;
@@ -313,13 +329,13 @@ __global__ __launch_bounds__(kThreads, kWaves / 4) void int8_gemm_kernel(
 
     const int full = static_cast<int>(k / kBK);
     if (full > 0) {
-        issue_step(lds[0], ars, wrs, gm, 0, wave);
-        if (full > 1) issue_step(lds[1], ars, wrs, gm, kBK, wave);
-        if (full > 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(Tile<BM>::kLoads));
+        issue_step(lds(0), ars, wrs, gm, 0, wave);
+        if (full > 1) issue_step(lds(1), ars, wrs, gm, kBK, wave);
+        if (full > 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(Tile<BM, BN>::kLoads));
         else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
         __syncthreads();
-        Frags<BM> f0, f1;
-        load_frags(f0, lds[0], 0);
+        Frags<BM, BN> f0, f1;
+        load_frags(f0, lds(0), 0);
         __builtin_amdgcn_s_waitcnt(lgkmcnt_imm(0));
         // One K step:
         //   slice 1 reads, with the first kPre MFMAs of slice 0 covering them
@@ -334,27 +350,27 @@ __global__ __launch_bounds__(kThreads, kWaves / 4) void int8_gemm_kernel(
         // branches, which the register allocation needs: the last two steps
         // load step full - 1 again into stages nobody reads any more, and
         // those loads are retired after the loop, before the ring is reused.
-        constexpr int kMma = Tile<BM>::kMma, kPre = Tile<BM>::kPre;
+        constexpr int kMma = Tile<BM, BN>::kMma, kPre = Tile<BM, BN>::kPre;
 #pragma clang loop unroll(disable)
         for (int s = 0; s < full; ++s) {
             const uint32_t k2 = static_cast<uint32_t>(min(s + 2, full - 1) * kBK);
-            load_frags(f1, lds[s & 1], 1);
+            load_frags(f1, lds(s & 1), 1);
             mma_part(f0, 0, kPre);
             __builtin_amdgcn_sched_barrier(0);
             __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
             __syncthreads();
-            issue_step(lds[s & 1], ars, wrs, gm, k2, wave);
+            issue_step(lds(s & 1), ars, wrs, gm, k2, wave);
             mma_part(f0, kPre, kMma);
 #pragma unroll
-            for (int i = 0; i < Tile<BM>::kLoads; ++i) {
+            for (int i = 0; i < Tile<BM, BN>::kLoads; ++i) {
                 __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             }
             __builtin_amdgcn_sched_barrier(0);
-            load_frags(f0, lds[(s + 1) & 1], 0);
+            load_frags(f0, lds((s + 1) & 1), 0);
             mma(f1);
 #pragma unroll
-            for (int i = 0; i < 8 + kFragsM; ++i) {
+            for (int i = 0; i < kFragsN + kFragsM; ++i) {
                 __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             }
@@ -367,19 +383,19 @@ __global__ __launch_bounds__(kThreads, kWaves / 4) void int8_gemm_kernel(
     if (full * kBK < k) {
         // Partial last step: register loads with zero fill past K.
         __syncthreads();
-        TileLoad<BM> t;
-        load_tiles<BM>(t, a, w, m0, n0, m, n, k, static_cast<int64_t>(full) * kBK, tid);
-        store_tiles<BM>(t, lds[0], lds[0] + kBM * kBK, tid);
+        TileLoad<BM, BN> t;
+        load_tiles<BM, BN>(t, a, w, m0, n0, m, n, k, static_cast<int64_t>(full) * kBK, tid);
+        store_tiles<BM, BN>(t, lds(0), lds(0) + kBM * kBK, tid);
         __syncthreads();
-        Frags<BM> f;
-        load_frags(f, lds[0], 0);
+        Frags<BM, BN> f;
+        load_frags(f, lds(0), 0);
         mma(f);
-        load_frags(f, lds[0], 1);
+        load_frags(f, lds(0), 1);
         mma(f);
     }
 
     // acc[i][j][r] = C[m = m0 + wm*16*kFragsM + 16j + (lane & 15)]
-    //                  [n = n0 + wn*128 + 16i + 4*(lane >> 4) + r]
+    //                  [n = n0 + wn*BN/2 + 16i + 4*(lane >> 4) + r]
     const int g = lane >> 4;
     if constexpr (kOut == kOutI32) {
 #pragma unroll
@@ -387,8 +403,8 @@ __global__ __launch_bounds__(kThreads, kWaves / 4) void int8_gemm_kernel(
             const int64_t row = m0 + wm * 16 * kFragsM + j * 16 + (lane & 15);
             if (row >= m) continue;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const int64_t col = n0 + wn * 128 + i * 16 + 4 * g;
+            for (int i = 0; i < kFragsN; ++i) {
+                const int64_t col = n0 + wn * (BN / 2) + i * 16 + 4 * g;
                 if (col >= n) continue;  // n % 8 == 0, so a group of 4 is all in or all out
                 __builtin_nontemporal_store(acc[i][j], reinterpret_cast<i32x4 *>(static_cast<int32_t *>(out) + row * n + col));
             }
@@ -403,8 +419,8 @@ __global__ __launch_bounds__(kThreads, kWaves / 4) void int8_gemm_kernel(
             const int64_t row = m0 + wm * 16 * kFragsM + j * 16 + (lane & 15);
             const float xs = as[min(row, m - 1)];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const int64_t col = n0 + wn * 128 + i * 16 + 4 * g;
+            for (int i = 0; i < kFragsN; ++i) {
+                const int64_t col = n0 + wn * (BN / 2) + i * 16 + 4 * g;
                 const int64_t cc = min(col, n - 4);
                 const f32x4 wsv = *reinterpret_cast<const f32x4 *>(ws + cc);
                 const f32x4 bv = *reinterpret_cast<const f32x4 *>(bp + cc);
@@ -429,10 +445,9 @@ __global__ __launch_bounds__(kThreads, kWaves / 4) void int8_gemm_kernel(
         // 8-byte writes below and the 16-byte row reads are conflict free).
         static_assert(kOut == kOutBf16 || !kResidual, "the residual epilogue writes bf16");
         constexpr int kRows = 16 * kFragsM;
-        static_assert(kWaves * kRows * 256 <= kStages * kStageBytes, "epilogue tile exceeds the LDS ring");
         const int frow = lane & 15;
         const int64_t row_base = m0 + wm * kRows;
-        const int64_t col_base = n0 + wn * 128;
+        const int64_t col_base = n0 + wn * (BN / 2);
         // All of the tile's scales and bias in one batch, from in-range
         // addresses without branches (rows / columns past the end read the
         // last valid ones and are never stored): vector-memory operations
@@ -440,11 +455,11 @@ __global__ __launch_bounds__(kThreads, kWaves / 4) void int8_gemm_kernel(
         // wait a full round trip.
         const float *bp = bias ? bias : ws;
         float arow[kFragsM];
-        f32x4 wsv[8], bv[8];
+        f32x4 wsv[kFragsN], bv[kFragsN];
 #pragma unroll
         for (int j = 0; j < kFragsM; ++j) arow[j] = as[min(row_base + j * 16 + frow, m - 1)];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        for (int i = 0; i < kFragsN; ++i) {
             const int64_t col = min(col_base + i * 16 + 4 * g, n - 4);
             wsv[i] = *reinterpret_cast<const f32x4 *>(ws + col);
             bv[i] = *reinterpret_cast<const f32x4 *>(bp + col);
@@ -461,7 +476,7 @@ __global__ __launch_bounds__(kThreads, kWaves / 4) void int8_gemm_kernel(
 #pragma unroll
         for (int j = 0; j < kFragsM; ++j) finite_max = max(finite_max, __float_as_uint(arow[j]) & 0x7fffffffu);
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
+        for (int i = 0; i < kFragsN; ++i)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 finite_max = max(finite_max, __float_as_uint(bv[i][r]) & 0x7fffffffu);
@@ -471,13 +486,13 @@ __global__ __launch_bounds__(kThreads, kWaves / 4) void int8_gemm_kernel(
         const bool hw_round = !kResidual &&
             __builtin_amdgcn_ballot_w64(finite_max >= 0x7f800000u || ws_max >= 0x7f7fffffu) == 0;
         __syncthreads();
-        int8_t *tile = &lds[0][0] + wave * kRows * 256;
+        int8_t *tile = lds_mem + wave * kRows * 256;
         auto stage_tile = [&](auto hw) {
 #pragma unroll
             for (int j = 0; j < kFragsM; ++j) {
                 const int lrow = j * 16 + frow;
 #pragma unroll
-                for (int i = 0; i < 8; ++i) {
+                for (int i = 0; i < kFragsN; ++i) {
                     float v[4];
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
@@ -515,7 +530,8 @@ __global__ __launch_bounds__(kThreads, kWaves / 4) void int8_gemm_kernel(
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        // 4 rows of 16 chunks per pass
+        // 4 rows of 16 chunks per pass (a wave's BN / 2 columns are the
+        // first BN / 16 chunks of a row)
         const int rsub = lane >> 4, c = lane & 15;
         // residual (and gate) chunks of every pass, loaded before any store
         u32x4 res[kResidual ? kRows / 4 : 1], gv[kResidual ? kRows / 4 : 1];
@@ -546,7 +562,7 @@ __global__ __launch_bounds__(kThreads, kWaves / 4) void int8_gemm_kernel(
                     val[e] = pack_bf16x2(lo, hi);
                 }
             }
-            if (row < m && col < n)  // n % 8 == 0: a chunk is all in or all out
+            if (row < m && col < n && c < BN / 16)  // n % 8 == 0: a chunk is all in or all out
                 __builtin_nontemporal_store(val, reinterpret_cast<u32x4 *>(static_cast<uint16_t *>(out) + row * n + col));
         }
     }
@@ -589,7 +605,7 @@ int32_t check_gemm_args(const int8_t *a, const int8_t *w, const void *out, int64
     TU_REQUIRE(k % 16 == 0 && n % 8 == 0, "INT8 GEMM requires K%%16==0 and N%%8==0 (K=%lld N=%lld)",
                static_cast<long long>(k), static_cast<long long>(n));
     TU_REQUIRE(k < 131072, "INT8 GEMM K=%lld would overflow the int32 accumulator", static_cast<long long>(k));
-    TU_REQUIRE((m + 127) / 128 * ((n + kBN - 1) / kBN) < 0x7fffffff, "INT8 GEMM grid too large");
+    TU_REQUIRE((m + 127) / 128 * ((n + 191) / 192) < 0x7fffffff, "INT8 GEMM grid too large");
     TU_REQUIRE(a && w && out, "INT8 GEMM pointers must be non-null");
     TU_REQUIRE((reinterpret_cast<uintptr_t>(a) & 15) == 0 && (reinterpret_cast<uintptr_t>(w) & 15) == 0,
                "INT8 GEMM operands must be 16-byte aligned");
@@ -618,15 +634,23 @@ int32_t device_cus(int &cus) {
 // K 5120 (a tile's fixed part, the epilogue's stores and the first loads, does
 // not halve with its rows).
 constexpr double kHalfTileCost = TU_GEMM_HALF_TILE_COST;
+// The same for a round of 256 x 192 tiles: 0.83-0.88 measured at K 1536 and
+// K 5120 (0.75 of the MFMAs plus the fixed part).
+constexpr double kTile192Cost = 0.85;
 
 // Tile policy from the grid: one workgroup per CU, so tiles run in rounds of
-// `cus`; 128-row tiles are chosen when their rounds cost less than the
-// 256-row tiles' (a grid of a few, partly empty rounds).
+// `cus`; 128 x 256 or 256 x 192 tiles are chosen when their rounds cost less
+// than the 256 x 256 tiles' (a grid of a few, partly empty rounds).
 int pick_tile_policy(int64_t m, int64_t n, int cus) {
-    const int64_t tn = (n + kBN - 1) / kBN;
-    const int64_t r256 = ((m + 255) / 256 * tn + cus - 1) / cus;
-    const int64_t r128 = ((m + 127) / 128 * tn + cus - 1) / cus;
-    return static_cast<double>(r128) * kHalfTileCost < static_cast<double>(r256) ? TU_GEMM_TILE_128 : TU_GEMM_TILE_256;
+    const int64_t t256 = (m + 255) / 256 * ((n + 255) / 256);
+    const int64_t t128 = (m + 127) / 128 * ((n + 255) / 256);
+    const int64_t t192 = (m + 255) / 256 * ((n + 191) / 192);
+    const double c256 = static_cast<double>((t256 + cus - 1) / cus);
+    const double c128 = static_cast<double>((t128 + cus - 1) / cus) * kHalfTileCost;
+    const double c192 = static_cast<double>((t192 + cus - 1) / cus) * kTile192Cost;
+    if (c128 < c256 && c128 <= c192) return TU_GEMM_TILE_128;
+    if (c192 < c256) return TU_GEMM_TILE_192;
+    return TU_GEMM_TILE_256;
 }
 
 template <int kOut, bool kResidual = false>
@@ -639,15 +663,18 @@ int32_t launch_gemm(const int8_t *a, const int8_t *w, const float *as, const flo
         if (device_cus(cus)) return -1;
         policy = pick_tile_policy(m, n, cus);
     }
-    const int tiles_n = static_cast<int>((n + kBN - 1) / kBN);
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (policy == TU_GEMM_TILE_128) {
-        const int tiles_m = static_cast<int>((m + 127) / 128);
-        int8_gemm_kernel<128, kOut, kResidual><<<dim3(tiles_m * tiles_n), kThreads, 0, st>>>(
+        const int tiles_m = static_cast<int>((m + 127) / 128), tiles_n = static_cast<int>((n + 255) / 256);
+        int8_gemm_kernel<128, 256, kOut, kResidual><<<dim3(tiles_m * tiles_n), kThreads, 0, st>>>(
+            a, w, as, ws, bias, out, m, n, k, tiles_m, tiles_n, residual, gate, gate_rows);
+    } else if (policy == TU_GEMM_TILE_192) {
+        const int tiles_m = static_cast<int>((m + 255) / 256), tiles_n = static_cast<int>((n + 191) / 192);
+        int8_gemm_kernel<256, 192, kOut, kResidual><<<dim3(tiles_m * tiles_n), kThreads, 0, st>>>(
             a, w, as, ws, bias, out, m, n, k, tiles_m, tiles_n, residual, gate, gate_rows);
     } else {
-        const int tiles_m = static_cast<int>((m + 255) / 256);
-        int8_gemm_kernel<256, kOut, kResidual><<<dim3(tiles_m * tiles_n), kThreads, 0, st>>>(
+        const int tiles_m = static_cast<int>((m + 255) / 256), tiles_n = static_cast<int>((n + 255) / 256);
+        int8_gemm_kernel<256, 256, kOut, kResidual><<<dim3(tiles_m * tiles_n), kThreads, 0, st>>>(
             a, w, as, ws, bias, out, m, n, k, tiles_m, tiles_n, residual, gate, gate_rows);
     }
     return check_launch(kOut == kOutI32   ? "tu_int8_gemm_i32"
@@ -744,8 +771,10 @@ extern "C" int32_t tu_int8_gemm_ex(const int8_t *a, const int8_t *w, const float
                                    const float *bias, void *out, int32_t out_type, int64_t m, int64_t n, int64_t k,
                                    int32_t tile_policy, void *stream) {
     using namespace tu;
-    TU_REQUIRE(tile_policy == TU_GEMM_TILE_AUTO || tile_policy == TU_GEMM_TILE_256 || tile_policy == TU_GEMM_TILE_128,
-               "INT8 GEMM tile_policy must be 0 (auto), 1 (256 x 256) or 2 (128 x 256), got %d", tile_policy);
+    TU_REQUIRE(tile_policy == TU_GEMM_TILE_AUTO || tile_policy == TU_GEMM_TILE_256 || tile_policy == TU_GEMM_TILE_128 ||
+                   tile_policy == TU_GEMM_TILE_192,
+               "INT8 GEMM tile_policy must be 0 (auto), 1 (256 x 256), 2 (128 x 256) or 3 (256 x 192), got %d",
+               tile_policy);
     if (check_gemm_args(a, w, out, m, n, k)) return -1;
     switch (out_type) {
     case TU_OUT_I32:

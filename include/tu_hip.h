@@ -118,6 +118,7 @@ int32_t tu_int8_gemm_f32(const int8_t *a, const int8_t *w, const float *a_scale,
 #define TU_GEMM_TILE_AUTO 0 /* chosen from the grid: tu_int8_gemm_tile_policy */
 #define TU_GEMM_TILE_256 1  /* 256 x 256 output tiles */
 #define TU_GEMM_TILE_128 2  /* 128 (rows of a) x 256 output tiles */
+#define TU_GEMM_TILE_192 3  /* 256 (rows of a) x 192 output tiles */
 
 /* The GEMM above with its output type and tile policy as arguments: out_type
  * TU_OUT_BF16 / _F16 / _F32 as tu_int8_gemm_bf16 / _f16 / _f32, TU_OUT_I32 as
@@ -130,9 +131,10 @@ int32_t tu_int8_gemm_ex(const int8_t *a, const int8_t *w, const float *a_scale, 
                         int32_t tile_policy, void *stream);
 
 /* The tile policy TU_GEMM_TILE_AUTO picks for an m x n output on a device
- * with `cus` compute units: TU_GEMM_TILE_128 when the 128-row tiles' rounds
- * of `cus` workgroups cost less than the 256-row tiles' (host only, no HIP
- * call).  Counterpart of the heuristic of w4a8.cu:837-851. */
+ * with `cus` compute units: TU_GEMM_TILE_128 or TU_GEMM_TILE_192 when that
+ * tile's rounds of `cus` workgroups cost less than the 256 x 256 tiles'
+ * (host only, no HIP call).  Counterpart of the heuristic of
+ * w4a8.cu:837-851. */
 int32_t tu_int8_gemm_tile_policy(int64_t m, int64_t n, int32_t cus);
 
 /* The same GEMM with a gated residual add fused into the epilogue, for a DiT

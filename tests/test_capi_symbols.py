@@ -94,27 +94,30 @@ def test_attention_key_split_plan(lib):
 
 def test_gemm_tile_policy_plan(lib):
     """The GEMM's tile policy is host arithmetic over rounds of one workgroup
-    per CU: the four config-4 shapes (10-30 full rounds of 256-row tiles)
-    keep 256-row tiles; grids of a few partly empty rounds take 128-row tiles
-    when their rounds (each 0.635 of a 256-row round, measured) cost less,
-    which config 1 (3 rounds against 5) does not;
-    bad arguments fall back to 256-row tiles.  tu_int8_gemm_ex refuses an
-    unknown policy or output type before any HIP call."""
+    per CU: the four config-4 shapes (10-30 full rounds of 256 x 256 tiles)
+    keep them; grids of a few partly empty rounds take 128 x 256 tiles (each
+    round 0.635 of a 256 x 256 round, measured) or 256 x 192 tiles (0.85)
+    when their rounds cost less: config 1 takes 256 x 192 (3 rounds of them
+    against 3 of 256 x 256), the cross-attention's 512-row kv projection
+    128-row tiles; bad arguments fall back to 256 x 256.  tu_int8_gemm_ex
+    refuses an unknown policy or output type before any HIP call."""
     pol = lambda m, n, cus=256: lib.tu_int8_gemm_tile_policy(m, n, cus)  # noqa: E731
     for n in (15360, 5120, 13824):
         assert pol(32760, n) == 1
-    assert pol(4096, 8960) == 1                  # config 1: 3 rounds against 5 x 0.635
-    assert pol(2048, 8960) == 2                  # 2 rounds against 3 x 0.635
+    assert pol(4096, 8960) == 3                  # config 1: 3 rounds x 0.85 against 3
+    assert pol(2048, 8960) == 3                  # 2 x 0.85 against 2 (and 3 x 0.635)
+    assert pol(512, 10240) == 2                  # 1 x 0.635 against 1 x 0.85 and 1
     assert pol(256 * 16, 256 * 16) == 1          # exactly one full round
-    assert pol(300, 264) == 2                    # 4 tiles or 6 half tiles: one round either way
     assert pol(0, 8960) == 1 and pol(4096, 8960, 0) == 1
-    for m, n in ((4096, 8960), (8192, 8960), (2048, 3072), (32760, 15360)):
-        # the rule: 128-row tiles when their rounds x the half-tile cost are fewer
-        t256 = -(-m // 256) * -(-n // 256)
-        t128 = -(-m // 128) * -(-n // 256)
-        r256, r128 = -(-t256 // 256), -(-t128 // 256)
-        assert pol(m, n) == (2 if r128 * 0.635 < r256 else 1)
-    assert lib.tu_int8_gemm_ex(None, None, None, None, None, None, 0, 16, 16, 16, 3, None) != 0
+    ceil = lambda a, b: -(-a // b)  # noqa: E731
+    for m, n in ((4096, 8960), (8192, 8960), (2048, 3072), (32760, 15360), (300, 264), (4096, 5120), (512, 10240)):
+        # the rule: the cheapest of the three by rounds x the tile's round cost
+        c256 = ceil(ceil(m, 256) * ceil(n, 256), 256)
+        c128 = ceil(ceil(m, 128) * ceil(n, 256), 256) * 0.635
+        c192 = ceil(ceil(m, 256) * ceil(n, 192), 256) * 0.85
+        want = 2 if (c128 < c256 and c128 <= c192) else 3 if c192 < c256 else 1
+        assert pol(m, n) == want, (m, n)
+    assert lib.tu_int8_gemm_ex(None, None, None, None, None, None, 0, 16, 16, 16, 4, None) != 0
     assert b"tile_policy" in lib.tu_last_error()
     assert lib.tu_int8_gemm_ex(None, None, None, None, None, None, 7, 16, 16, 16, 0, None) != 0
 

@@ -155,6 +155,35 @@ def test_int8_linear_residual_exact(gpu_device, m, n, k, with_bias, gate_rows):
     np.testing.assert_array_equal(inputs.bits(res_dev), inputs.bits(residual))
 
 
+def test_residual_and_bf16_on_192_wide_tiles(gpu_device):
+    """A grid that the tile policy runs on 256 x 192 tiles (2048 x 8968: two
+    rounds of them on 256 CUs, a ragged last 192-wide tile): the bf16 output
+    and the gated residual epilogue, 96 sampled rows bit-exact against the
+    oracle."""
+    from comfyui_turing_utils_kernel import _lib
+
+    m, n, k, gate_rows = 2048, 8968, 256, 16
+    print(f"[gemm 256x192] m={m} n={n} k={k} policy={_lib.load().tu_int8_gemm_tile_policy(m, n, 256)}", flush=True)
+    assert _lib.load().tu_int8_gemm_tile_policy(m, n, 256) == 3
+    a = _rand_i8((m, k), 5)
+    w, ws, bias = inputs.weights(n, k, 6, True)
+    g = torch.Generator().manual_seed(9)
+    as_ = torch.empty(m).uniform_(1e-3, 1e-1, generator=g)
+    residual = (torch.randn(m, n, generator=g) * 4).to(torch.bfloat16)
+    gate = torch.empty(m // gate_rows, n).uniform_(-2, 2, generator=g).to(torch.bfloat16)
+    dev = gpu_device
+    ad, wd, asd, wsd, bd = a.to(dev), w.to(dev), as_.to(dev), ws.to(dev), bias.to(dev)
+    y_dev = torch.ops.turing_utils.int8_linear(ad, wd, asd, wsd, bd)
+    out = torch.ops.turing_utils.int8_linear_residual(ad, wd, asd, wsd, bd, residual.to(dev), gate.to(dev), gate_rows)
+    torch.cuda.synchronize(dev)
+    rows = np.sort(np.random.default_rng(4).choice(m, 96, replace=False))
+    acc = oracle.int8_gemm_i32(a.numpy()[rows], w.numpy())
+    y = oracle.epilogue_bf16(acc, as_.numpy()[rows], ws.numpy(), bias.numpy())
+    np.testing.assert_array_equal(inputs.bits(y_dev)[rows], y)
+    ref = oracle.residual_gate_bf16(y, inputs.bits(residual)[rows], inputs.bits(gate)[rows // gate_rows], 1)
+    np.testing.assert_array_equal(inputs.bits(out)[rows], ref)
+
+
 @pytest.mark.parametrize("gate_rows", [None, 37])
 @pytest.mark.parametrize("m,n,k", [(300, 264, 192), (257, 520, 1040), (513, 776, 1536)])
 def test_residual_in_place_through_the_c_abi(gpu_device, m, n, k, gate_rows):
@@ -306,14 +335,16 @@ def test_int8_linear_out_config1_rows(gpu_device, out_dtype):
 OUT_TYPES = {"bf16": (0, torch.bfloat16), "f16": (1, torch.float16), "f32": (2, torch.float32), "i32": (3, torch.int32)}
 
 
-@pytest.mark.parametrize("policy", [1, 2])
+@pytest.mark.parametrize("policy", [1, 2, 3])
 @pytest.mark.parametrize("out", sorted(OUT_TYPES))
 @pytest.mark.parametrize("m,n,k", [(1, 8, 16), (129, 8, 256), (300, 264, 192), (513, 520, 1040), (257, 264, 384),
                                    (200, 1024, 5120)])
 def test_gemm_tile_policies_exact(gpu_device, m, n, k, out, policy):
     """tu_int8_gemm_ex with each tile policy forced (1: 256 x 256 tiles, 2:
-    128 x 256) and each output type: bit-exact against the oracle on ragged M
-    and N tiles, partial last K steps and one-tile grids."""
+    128 x 256, 3: 256 x 192) and each output type: bit-exact against the
+    oracle on ragged M and N tiles (N 264 and 1024 leave a 192-wide tile
+    partly or one wave's half of it wholly empty), partial last K steps and
+    one-tile grids."""
     from comfyui_turing_utils_kernel import _lib
 
     print(f"[gemm ex] m={m} n={n} k={k} out={out} policy={policy}", flush=True)
@@ -338,7 +369,7 @@ def test_gemm_tile_policies_exact(gpu_device, m, n, k, out, policy):
         _linear_out_check(res, acc, as_, ws, bias, dtype)
 
 
-@pytest.mark.parametrize("policy", [1, 2])
+@pytest.mark.parametrize("policy", [1, 2, 3])
 def test_gemm_tile_policies_config1(gpu_device, policy):
     """Config 1 (4096 x 1536 -> 8960, bias) with each tile policy: identical
     bf16 output, 128 sampled rows bit-exact against the oracle."""

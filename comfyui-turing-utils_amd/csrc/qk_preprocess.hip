@@ -126,18 +126,6 @@ __device__ __forceinline__ float pack_sum(float v) {
     return butterfly_add<1>(v);
 }
 
-// Maximum over the wave of non-negative floats that are not NaN, compared as
-// integers (their bit patterns order as the values do): DPP within rows of
-// 16, then the permlane swaps across rows.
-__device__ __forceinline__ float wave_max_nonneg(float v) {
-    int b = __float_as_int(v);
-    b = max(b, __builtin_amdgcn_mov_dpp(b, 0x128, 0xf, 0xf, false));   // row_ror:8
-    b = max(b, __builtin_amdgcn_mov_dpp(b, 0x124, 0xf, 0xf, false));   // row_ror:4
-    b = max(b, __builtin_amdgcn_mov_dpp(b, 0x4E, 0xf, 0xf, false));
-    b = max(b, __builtin_amdgcn_mov_dpp(b, 0xB1, 0xf, 0xf, false));
-    return __int_as_float(xmax_i32(b));
-}
-
 // max(m, |a|, |b|) in one instruction.  A quiet NaN operand is passed over
 // (IEEE maxNum), as fmaxf passes it over; a and b are never signalling NaNs
 // here (they come out of hardware conversions).

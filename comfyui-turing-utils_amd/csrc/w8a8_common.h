@@ -1,10 +1,11 @@
 // Device pieces of the W8A8 Q/K transform shared by the standalone W8A8
 // quantizer (w8a8_quant.hip) and the fused RMSNorm + RoPE producer
 // (qk_preprocess.hip): the sign-diagonal Walsh-Hadamard rotation of one
-// 8-channel pack across a token's lanes, and the K-anchor decision.
+// 8-channel pack across a token's lanes, the K-anchor decision, and the
+// cross-lane helpers they use (DPP lane exchanges, wave maxima).
 #pragma once
 
-#include "tu_common.h"
+#include "attn_common.h"
 
 namespace tu {
 
@@ -13,6 +14,52 @@ namespace tu {
 __device__ __forceinline__ bool w8a8_sign_negative(int c) {
     constexpr uint32_t kSigns[4] = {0x1035997bu, 0x8087f5eeu, 0xee2e4e1au, 0x71132418u};
     return ((kSigns[c >> 5] >> (c & 31)) & 1u) == 0u;
+}
+
+// Maximum over the wave of non-negative floats that are not NaN, compared as
+// integers (their bit patterns order as the values do): DPP within rows of
+// 16, then the permlane swaps across rows.
+__device__ __forceinline__ float wave_max_nonneg(float v) {
+    int b = __float_as_int(v);
+    b = max(b, __builtin_amdgcn_mov_dpp(b, 0x128, 0xf, 0xf, false));   // row_ror:8
+    b = max(b, __builtin_amdgcn_mov_dpp(b, 0x124, 0xf, 0xf, false));   // row_ror:4
+    b = max(b, __builtin_amdgcn_mov_dpp(b, 0x4E, 0xf, 0xf, false));
+    b = max(b, __builtin_amdgcn_mov_dpp(b, 0xB1, 0xf, 0xf, false));
+    return __int_as_float(xmax_i32(b));
+}
+
+// v of lane i ^ kBit (kBit < 16) with no index arithmetic: DPP quad
+// permutations for 1 and 2; for 4 the mirror of each 8-lane half (lane
+// 7 - i) and then the reversal of each quad, which together give i ^ 4; for
+// 8 the rotation of each 16-lane row by 8 ((i + 8) mod 16 = i ^ 8).
+template <int kBit>
+__device__ __forceinline__ float w8a8_lane_xor(float v) {
+    int x = __float_as_int(v);
+    if constexpr (kBit == 1) {
+        x = __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xf, 0xf, true);
+    } else if constexpr (kBit == 2) {
+        x = __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xf, 0xf, true);
+    } else if constexpr (kBit == 4) {
+        x = __builtin_amdgcn_update_dpp(0, x, 0x141, 0xf, 0xf, true);   // row_half_mirror
+        x = __builtin_amdgcn_update_dpp(0, x, 0x1B, 0xf, 0xf, true);    // quad (3, 2, 1, 0)
+    } else {
+        static_assert(kBit == 8, "lane xor of 1, 2, 4 or 8");
+        x = __builtin_amdgcn_update_dpp(0, x, 0x128, 0xf, 0xf, true);   // row_ror:8
+    }
+    return __int_as_float(x);
+}
+
+// One cross-pack butterfly stage: v = other - v on lanes with bit `kBit` of
+// the pack index set, v + other elsewhere, as other + (+-1 * v): IEEE
+// subtraction is addition of the negation, and addition commutes, so the
+// bits are those of the two-sided form.
+template <int kBit>
+__device__ __forceinline__ void w8a8_cross_stage(float (&v)[8], int p) {
+    float sgn = (p & kBit) ? -1.0f : 1.0f;
+    // opaque to the compiler, which would otherwise form both sums and select
+    asm("" : "+v"(sgn));
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = w8a8_lane_xor<kBit>(v[j]) + sgn * v[j];
 }
 
 // The transform of one pack (8 channels of pack index p) across the lanes of
@@ -35,13 +82,11 @@ __device__ __forceinline__ void w8a8_hadamard_pack(float (&v)[8], int p) {
                 v[base + o] = l + r;
                 v[base + o + span] = l - r;
             }
-#pragma unroll
-    for (int bit = 1; bit < D / 8; bit <<= 1)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const float other = __shfl_xor(v[j], bit);
-            v[j] = (p & bit) ? other - v[j] : v[j] + other;
-        }
+    static_assert(D == 64 || D == 128, "head_dim 64 or 128");
+    w8a8_cross_stage<1>(v, p);
+    w8a8_cross_stage<2>(v, p);
+    w8a8_cross_stage<4>(v, p);
+    if constexpr (D == 128) w8a8_cross_stage<8>(v, p);
     constexpr float kNorm = D == 64 ? 0.125f : 0.08838834764831845f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) v[j] *= kNorm;

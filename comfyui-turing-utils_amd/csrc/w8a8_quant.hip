@@ -40,6 +40,21 @@ __device__ __forceinline__ int32_t sat_rne_s8(float v) {
     return static_cast<int32_t>(fminf(127.0f, fmaxf(-128.0f, r)));
 }
 
+// sat_rne_s8 of four values packed little-endian, without conversions: the
+// clamp comes first (the bounds are integers, so clamping and rounding
+// commute; NaN clamps to -128 as above), then adding 1.5 * 2^23 rounds half
+// to even to an integer whose two's complement sits in the low byte.
+__device__ __forceinline__ uint32_t sat_rne_s8x4(float a, float b, float c, float d) {
+    const float vs[4] = {a, b, c, d};
+    uint32_t w = 0u;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const float x = fminf(127.0f, fmaxf(-128.0f, vs[k]));
+        w |= (__float_as_uint(x + 12582912.0f) & 0xffu) << (8 * k);
+    }
+    return w;
+}
+
 __device__ __forceinline__ uint32_t pack_s8x4(int32_t a, int32_t b, int32_t c, int32_t d) {
     return (static_cast<uint32_t>(a) & 0xffu) | ((static_cast<uint32_t>(b) & 0xffu) << 8) |
            ((static_cast<uint32_t>(c) & 0xffu) << 16) | (static_cast<uint32_t>(d) << 24);
@@ -149,9 +164,7 @@ __global__ __launch_bounds__(kQkThreads) void rot_quant_kernel(RotArgs args) {
         float a = 0.0000001f;
 #pragma unroll
         for (int j = 0; j < 8; ++j) a = fmaxf(a, fabsf(v[it][j]));
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) a = fmaxf(a, __shfl_xor(a, off));
-        amax[it] = a;
+        amax[it] = wave_max_nonneg(a);   // a >= 1e-7 and never NaN (fmaxf passes NaN over)
     }
     if ((tid & 63) == 0) {
 #pragma unroll
@@ -205,12 +218,10 @@ __global__ __launch_bounds__(kQkThreads) void rot_quant_kernel(RotArgs args) {
     for (int it = 0; it < kIters; ++it) {
         const int64_t t = t0 + it * kTokPerPass + tid / kPacks;
         if (t >= len) continue;
-        int32_t q[8];
+        float y[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) q[j] = sat_rne_s8(v[it][j] * mult[it]);
-        u32x2 packed;
-        packed.x = pack_s8x4(q[0], q[1], q[2], q[3]);
-        packed.y = pack_s8x4(q[4], q[5], q[6], q[7]);
+        for (int j = 0; j < 8; ++j) y[j] = v[it][j] * mult[it];
+        const u32x2 packed{sat_rne_s8x4(y[0], y[1], y[2], y[3]), sat_rne_s8x4(y[4], y[5], y[6], y[7])};
         *reinterpret_cast<u32x2 *>(obase + t * args.o_sl[which] + pack * 8) = packed;
     }
 }
@@ -338,25 +349,45 @@ __global__ __launch_bounds__(kVThreads) void v_quant_kernel(const uint16_t *__re
 }
 
 // Exclusive prefix over tiles of the per-channel tile sums:
-// prefix[t] = sum of tiles < t, t = 0 .. ntiles.
+// prefix[t] = sum of tiles < t, t = 0 .. ntiles.  One workgroup per (batch,
+// head): kPrefixSegs segments of consecutive tiles per channel, each summed
+// by its own thread, the segment totals scanned through LDS, then each
+// segment's running prefix written.  Integer sums, so the split changes no
+// result.
+constexpr int kPrefixSegs = 8;
+
 template <int D>
-__global__ __launch_bounds__(D) void v_prefix_kernel(const int32_t *__restrict__ tile_sum, int64_t ntiles,
-                                                     int32_t *__restrict__ prefix) {
-    constexpr int kBatch = 16;  // independent loads in flight per thread
-    const int c = threadIdx.x;
+__global__ __launch_bounds__(D * kPrefixSegs) void v_prefix_kernel(const int32_t *__restrict__ tile_sum, int64_t ntiles,
+                                                                  int32_t *__restrict__ prefix) {
+    constexpr int kBatch = 8;  // independent loads in flight per thread
+    __shared__ int32_t seg_total[kPrefixSegs][D];
+    const int c = threadIdx.x % D, seg = threadIdx.x / D;
     const int64_t bh = blockIdx.x;
+    const int64_t per = (ntiles + kPrefixSegs - 1) / kPrefixSegs;
+    const int64_t t_begin = min(ntiles, seg * per), t_end = min(ntiles, t_begin + per);
     const int32_t *src = tile_sum + bh * ntiles * D + c;
     int32_t *dst = prefix + bh * (ntiles + 1) * D + c;
-    int32_t acc = 0;
-    dst[0] = 0;
-    for (int64_t t0 = 0; t0 < ntiles; t0 += kBatch) {
+    int32_t total = 0;
+    for (int64_t t0 = t_begin; t0 < t_end; t0 += kBatch) {
         int32_t v[kBatch];
 #pragma unroll
-        for (int j = 0; j < kBatch; ++j) v[j] = t0 + j < ntiles ? src[(t0 + j) * D] : 0;
+        for (int j = 0; j < kBatch; ++j) v[j] = t0 + j < t_end ? src[(t0 + j) * D] : 0;
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) total += v[j];
+    }
+    seg_total[seg][c] = total;
+    __syncthreads();
+    int32_t acc = 0;
+    for (int s2 = 0; s2 < seg; ++s2) acc += seg_total[s2][c];
+    if (seg == 0) dst[0] = 0;
+    for (int64_t t0 = t_begin; t0 < t_end; t0 += kBatch) {
+        int32_t v[kBatch];
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) v[j] = t0 + j < t_end ? src[(t0 + j) * D] : 0;
 #pragma unroll
         for (int j = 0; j < kBatch; ++j) {
             acc += v[j];
-            if (t0 + j < ntiles) dst[(t0 + j + 1) * D] = acc;
+            if (t0 + j < t_end) dst[(t0 + j + 1) * D] = acc;
         }
     }
 }
@@ -466,7 +497,7 @@ extern "C" int32_t tu_w8a8_quant_v(const void *v, int32_t dtype, int64_t batch, 
         v_amax_kernel<F16, DD><<<g1, kVThreads, 0, s>>>(vp, len, s_b, s_h, s_l, partial);                     \
         v_scale_kernel<DD><<<bh, DD, 0, s>>>(partial, chunks, scale);                                         \
         v_quant_kernel<F16, DD><<<g3, kVThreads, 0, s>>>(vp, len, lpad, s_b, s_h, s_l, scale, vq, tile_sum);  \
-        v_prefix_kernel<DD><<<bh, DD, 0, s>>>(tile_sum, ntiles, prefix);                                      \
+        v_prefix_kernel<DD><<<bh, DD * kPrefixSegs, 0, s>>>(tile_sum, ntiles, prefix);                                      \
     } while (0)
     if (dtype) {
         if (dim == 128) TU_V_LAUNCH(true, 128);

@@ -19,6 +19,9 @@ from .ops import (
     turing_int8_linear,
     turing_int8_linear_out,
     turing_layer_norm_adaln,
+    turing_layer_norm_adaln_int8_convrot_quantize,
+    turing_layer_norm_affine,
+    turing_layer_norm_affine_int8_convrot_quantize,
     turing_swiglu_int8_convrot_quantize,
 )
 from . import turing_sage
@@ -37,6 +40,9 @@ __all__ = [
     "turing_int8_linear",
     "turing_int8_linear_out",
     "turing_layer_norm_adaln",
+    "turing_layer_norm_adaln_int8_convrot_quantize",
+    "turing_layer_norm_affine",
+    "turing_layer_norm_affine_int8_convrot_quantize",
     "turing_sage",
     "turing_swiglu_int8_convrot_quantize",
 ]

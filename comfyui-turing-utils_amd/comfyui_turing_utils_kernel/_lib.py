@@ -129,9 +129,17 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _i32,
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i32, _i64, _i64, _f32, _c_void_p],
     ),
+    "tu_layer_norm_adaln_convrot_quant_i8": (
+        _i32,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _f32, _c_void_p],
+    ),
+    "tu_layer_norm_affine_convrot_quant_i8": (
+        _i32,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _f32, _c_void_p],
+    ),
 }
 
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

@@ -468,3 +468,109 @@ def turing_layer_norm_affine(
 @turing_layer_norm_affine.register_fake
 def _turing_layer_norm_affine_fake(x, weight, bias, epsilon=1.0e-5):
     return torch.empty_like(x)
+
+
+# ---------------------------------------------------------------------------
+# LayerNorm fused with the ConvRot INT8 quantizer (no reference op: the
+# reference runs the norm, ops.py:399-418, and the linear's activation
+# quantizer, quantization/dispatch.py:538-615, as two ops)
+# ---------------------------------------------------------------------------
+LN_CONVROT_MAX_HIDDEN = 5120  # rows and rotated values stay in registers
+
+
+def _ln_convrot_fused(x: torch.Tensor, hidden: int, group_size: int) -> bool:
+    """The one-kernel path: bf16, G = 128, hidden a multiple of 256 up to 5120."""
+    return (x.dtype == torch.bfloat16 and group_size == 128 and hidden % 256 == 0
+            and 256 <= hidden <= LN_CONVROT_MAX_HIDDEN)
+
+
+def _aligned16(*tensors: torch.Tensor) -> bool:
+    return all(t.data_ptr() % 16 == 0 for t in tensors)
+
+
+@torch.library.custom_op("turing_utils::layer_norm_adaln_int8_convrot_quantize", mutates_args=())
+def turing_layer_norm_adaln_int8_convrot_quantize(
+    x: torch.Tensor,
+    scale: torch.Tensor,
+    shift: torch.Tensor,
+    epsilon: float = 1.0e-5,
+    group_size: int = 128,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """ConvRot INT8 codes [B*L, H] and row scales [B*L, 1] of
+    layer_norm_adaln(x, scale, shift, epsilon), bit for bit those of
+    bf16_int8_convrot_quantize(layer_norm_adaln(...).reshape(-1, H), group_size).
+    bf16 x with group 128 and H a multiple of 256 up to 5120 runs as one
+    kernel (the normalized rows never reach memory); anything else runs the
+    two ops."""
+    _require_device(x, "LayerNorm+AdaLN ConvRot")
+    if x.dtype not in _LN_DTYPES or x.ndim != 3:
+        raise TypeError("LayerNorm+AdaLN input must be 3D float16, bfloat16, or float32")
+    batch, length, hidden = x.shape
+    if not _ln_convrot_fused(x, hidden, group_size):
+        normed = turing_layer_norm_adaln(x, scale, shift, epsilon)
+        return _convrot_quantize(normed.reshape(batch * length, hidden), group_size, ACT_NONE,
+                                 "BF16 row-buffer ConvRot")
+    scale = scale.to(device=x.device, dtype=x.dtype).contiguous()
+    shift = shift.to(device=x.device, dtype=x.dtype).contiguous()
+    if scale.ndim != 3 or scale.shape != shift.shape or scale.size(0) != batch or scale.size(2) != hidden:
+        raise ValueError("LayerNorm+AdaLN scale / shift must be [B, steps, H] and match")
+    x = x.contiguous()
+    if not _aligned16(x, scale, shift):  # the kernel reads 16-byte vectors
+        x, scale, shift = x.clone(), scale.clone(), shift.clone()
+    q = torch.empty((batch * length, hidden), dtype=torch.int8, device=x.device)
+    scales = torch.empty((batch * length, 1), dtype=torch.float32, device=x.device)
+    with torch.cuda.device(x.device):
+        _lib.call("tu_layer_norm_adaln_convrot_quant_i8", x.data_ptr(), scale.data_ptr(), shift.data_ptr(),
+                  q.data_ptr(), scales.data_ptr(), batch, length, hidden, scale.size(1), float(epsilon),
+                  _lib.stream_of(x.device))
+    return q, scales
+
+
+@turing_layer_norm_adaln_int8_convrot_quantize.register_fake
+def _turing_layer_norm_adaln_int8_convrot_quantize_fake(x, scale, shift, epsilon=1.0e-5, group_size=128):
+    rows = x.size(0) * x.size(1)
+    return (torch.empty((rows, x.size(2)), dtype=torch.int8, device=x.device),
+            torch.empty((rows, 1), dtype=torch.float32, device=x.device))
+
+
+@torch.library.custom_op("turing_utils::layer_norm_affine_int8_convrot_quantize", mutates_args=())
+def turing_layer_norm_affine_int8_convrot_quantize(
+    x: torch.Tensor,
+    weight: torch.Tensor,
+    bias: torch.Tensor,
+    epsilon: float = 1.0e-5,
+    group_size: int = 128,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """ConvRot INT8 codes [rows, H] and row scales [rows, 1] of
+    layer_norm_affine(x, weight, bias, epsilon) over x [..., H], bit for bit
+    those of bf16_int8_convrot_quantize on that output; one kernel under the
+    conditions of layer_norm_adaln_int8_convrot_quantize, else the two ops."""
+    _require_device(x, "LayerNorm ConvRot")
+    if x.dtype not in _LN_DTYPES or x.ndim < 1:
+        raise TypeError("LayerNorm input must be float16, bfloat16, or float32")
+    hidden = x.shape[-1]
+    rows = x.numel() // hidden if hidden else 0
+    if not _ln_convrot_fused(x, hidden, group_size) or rows == 0:
+        normed = turing_layer_norm_affine(x, weight, bias, epsilon)
+        return _convrot_quantize(normed.reshape(rows, hidden), group_size, ACT_NONE, "BF16 row-buffer ConvRot")
+    weight = weight.to(device=x.device, dtype=x.dtype).reshape(-1).contiguous()
+    bias = bias.to(device=x.device, dtype=x.dtype).reshape(-1).contiguous()
+    if weight.numel() != hidden or bias.numel() != hidden:
+        raise ValueError(f"LayerNorm weight and bias must hold {hidden} values")
+    x = x.contiguous()
+    if not _aligned16(x, weight, bias):
+        x, weight, bias = x.clone(), weight.clone(), bias.clone()
+    q = torch.empty((rows, hidden), dtype=torch.int8, device=x.device)
+    scales = torch.empty((rows, 1), dtype=torch.float32, device=x.device)
+    with torch.cuda.device(x.device):
+        _lib.call("tu_layer_norm_affine_convrot_quant_i8", x.data_ptr(), weight.data_ptr(), bias.data_ptr(),
+                  q.data_ptr(), scales.data_ptr(), rows, hidden, float(epsilon), _lib.stream_of(x.device))
+    return q, scales
+
+
+@turing_layer_norm_affine_int8_convrot_quantize.register_fake
+def _turing_layer_norm_affine_int8_convrot_quantize_fake(x, weight, bias, epsilon=1.0e-5, group_size=128):
+    hidden = x.shape[-1]
+    rows = x.numel() // hidden if hidden else 0
+    return (torch.empty((rows, hidden), dtype=torch.int8, device=x.device),
+            torch.empty((rows, 1), dtype=torch.float32, device=x.device))

@@ -17,7 +17,12 @@ ops into the whole block so that it can be run and timed without ComfyUI:
 
 * norm1 / norm2: ``turing_utils::layer_norm_adaln``.  norm3, LayerNorm with
   an elementwise weight and bias (ComfyUI's own LayerNorm in the reference's
-  setting): ``turing_utils::layer_norm_affine``, any weight values.
+  setting): ``turing_utils::layer_norm_affine``, any weight values.  In the
+  forward each norm's output has one consumer, the next projection's ConvRot
+  quantizer, so norm and quantizer run as one kernel
+  (``turing_utils::layer_norm_adaln_int8_convrot_quantize`` /
+  ``layer_norm_affine_int8_convrot_quantize``) and the normalized rows are
+  never written; the codes are those of the two ops, bit for bit.
 * SelfAttn: q, k and v come from one W8A8 GEMM (N = 3C).  q and k go through
   one fused RMSNorm + RoPE + INT8 kernel.  Then Sage INT8 attention, and the
   o projection.
@@ -48,6 +53,29 @@ from . import ops  # noqa: F401  (registers torch.ops.turing_utils.*)
 from .turing_sage import core as sage_core
 
 GROUP = 128
+
+
+@dataclass
+class QuantizedActivation:
+    """ConvRot INT8 codes [B*L, C] and row scales [B*L, 1] (group ``group``)
+    of a bf16 activation [B, L, C], as a fused norm + quantizer makes them."""
+    codes: torch.Tensor
+    scale: torch.Tensor
+    batch: int
+    length: int
+    group: int
+
+    @property
+    def shape(self) -> tuple[int, int, int]:
+        return (self.batch, self.length, self.codes.shape[1])
+
+
+def _token_rows(h):
+    """[B*L, C] rows of a bf16 activation [B, L, C], or its codes as they are."""
+    if isinstance(h, QuantizedActivation):
+        return h
+    b, l, c = h.shape
+    return h.reshape(b * l, c)
 
 
 class W8A8Linear:
@@ -81,15 +109,22 @@ class W8A8Linear:
             weight.to(torch.bfloat16).contiguous(), group)
         return cls(codes, scale, bias, group)
 
-    def __call__(self, x: torch.Tensor, gelu: bool = False, residual: Optional[torch.Tensor] = None,
+    def __call__(self, x, gelu: bool = False, residual: Optional[torch.Tensor] = None,
                  gate: Optional[torch.Tensor] = None, gate_rows: int = 1) -> torch.Tensor:
         """y = x W^T + b, or residual + y * gate[row // gate_rows] (gate 1 when
-        None) fused into the GEMM epilogue when ``residual`` [M, N] is given."""
-        if x.dim() != 2 or x.shape[1] != self.in_features:
-            raise ValueError(f"W8A8 linear expects [M, {self.in_features}], got {tuple(x.shape)}")
-        quantize = (torch.ops.turing_utils.bf16_gelu_int8_convrot_quantize if gelu
-                    else torch.ops.turing_utils.bf16_int8_convrot_quantize)
-        codes, scale = quantize(x.contiguous(), self.group)
+        None) fused into the GEMM epilogue when ``residual`` [M, N] is given.
+        x: bf16 [M, K], or a QuantizedActivation of this linear's group."""
+        if isinstance(x, QuantizedActivation):
+            if gelu or x.group != self.group or x.codes.shape[1] != self.in_features:
+                raise ValueError(f"W8A8 linear expects codes of [M, {self.in_features}] at group {self.group} "
+                                 f"without an activation, got {tuple(x.codes.shape)} at group {x.group}")
+            codes, scale = x.codes, x.scale
+        else:
+            if x.dim() != 2 or x.shape[1] != self.in_features:
+                raise ValueError(f"W8A8 linear expects [M, {self.in_features}], got {tuple(x.shape)}")
+            quantize = (torch.ops.turing_utils.bf16_gelu_int8_convrot_quantize if gelu
+                        else torch.ops.turing_utils.bf16_int8_convrot_quantize)
+            codes, scale = quantize(x.contiguous(), self.group)
         if residual is None:
             return torch.ops.turing_utils.int8_linear(codes, self.weight, scale, self.weight_scale, self.bias)
         return torch.ops.turing_utils.int8_linear_residual(codes, self.weight, scale, self.weight_scale, self.bias,
@@ -191,13 +226,15 @@ class WanBlockW8A8:
 
     # -- sublayers (each takes and returns bf16 [B, L, C]) ---------------------
 
-    def self_attention(self, h: torch.Tensor, freqs: torch.Tensor, residual: Optional[torch.Tensor] = None,
+    # (h: bf16 [B, L, C] or its QuantizedActivation for the first projection)
+
+    def self_attention(self, h, freqs: torch.Tensor, residual: Optional[torch.Tensor] = None,
                        gate: Optional[torch.Tensor] = None) -> torch.Tensor:
         """The attention output projected by o; with ``residual`` [B, L, C],
         residual + that * gate (gate [B, 1, C] or None) from one epilogue."""
         cfg = self.cfg
         b, l, c = h.shape
-        qkv = self.self_qkv(h.reshape(b * l, c)).view(b, l, 3, cfg.heads, cfg.head_dim)
+        qkv = self.self_qkv(_token_rows(h)).view(b, l, 3, cfg.heads, cfg.head_dim)
         q, k, v = qkv[:, :, 0], qkv[:, :, 1], qkv[:, :, 2]
         qk = sage_core.prequantize_rms_rope_qk(
             q, k, self.self_norm_q, self.self_norm_k, freqs, epsilon=cfg.eps, rot_dim=cfg.head_dim,
@@ -214,12 +251,12 @@ class WanBlockW8A8:
         g = None if gate is None else gate.reshape(b, c)
         return lin(x2d, gelu=gelu, residual=residual.reshape(b * l, c), gate=g, gate_rows=l)
 
-    def cross_attention(self, h: torch.Tensor, context: torch.Tensor,
+    def cross_attention(self, h, context: torch.Tensor,
                         residual: Optional[torch.Tensor] = None) -> torch.Tensor:
         cfg = self.cfg
         b, l, c = h.shape
         lc = context.shape[1]
-        q = self.cross_q(h.reshape(b * l, c)).view(b, l, cfg.heads, cfg.head_dim)
+        q = self.cross_q(_token_rows(h)).view(b, l, cfg.heads, cfg.head_dim)
         kv = self.cross_kv(context.reshape(b * lc, c)).view(b, lc, 2, cfg.heads, cfg.head_dim)
         k, v = kv[:, :, 0], kv[:, :, 1]
         qk = sage_core.prequantize_rms_rope_qk(
@@ -230,10 +267,10 @@ class WanBlockW8A8:
         out = sage_core.sageattn_from_prequantized(state)
         return self._project(self.cross_o, out.reshape(b * l, c), residual, None).view(b, l, c)
 
-    def ffn(self, h: torch.Tensor, residual: Optional[torch.Tensor] = None,
+    def ffn(self, h, residual: Optional[torch.Tensor] = None,
             gate: Optional[torch.Tensor] = None) -> torch.Tensor:
         b, l, c = h.shape
-        up = self.ffn_up(h.reshape(b * l, c))
+        up = self.ffn_up(_token_rows(h))
         return self._project(self.ffn_down, up, residual, gate, gelu=True).view(b, l, c)
 
     def modulation_chunks(self, e: torch.Tensor) -> list[torch.Tensor]:
@@ -249,14 +286,21 @@ class WanBlockW8A8:
             raise TypeError(f"Wan block input must be bf16 [B, L, {cfg.dim}]")
         if context.dtype != torch.bfloat16 or context.dim() != 3 or context.shape[2] != cfg.dim:
             raise TypeError(f"Wan block context must be bf16 [B, Lc, {cfg.dim}]")
-        lnadaln = torch.ops.turing_utils.layer_norm_adaln
         e0, e1, e2, e3, e4, e5 = self.modulation_chunks(e)
         x = x.contiguous()
-        # each residual add runs in the epilogue of the projection before it
-        x = self.self_attention(lnadaln(x, e1, e0, cfg.eps), freqs, residual=x, gate=e2)
-        x = self.cross_attention(torch.ops.turing_utils.layer_norm_affine(x, self.norm3_weight, self.norm3_bias,
-                                                                          cfg.eps), context, residual=x)
-        return self.ffn(lnadaln(x, e4, e3, cfg.eps), residual=x, gate=e5)
+        b, l, _ = x.shape
+
+        def adaln_codes(x, scale, shift, group):
+            codes, rs = torch.ops.turing_utils.layer_norm_adaln_int8_convrot_quantize(x, scale, shift, cfg.eps, group)
+            return QuantizedActivation(codes, rs, b, l, group)
+
+        # each norm runs with the next projection's quantizer, each residual
+        # add in the epilogue of the projection before it
+        x = self.self_attention(adaln_codes(x, e1, e0, self.self_qkv.group), freqs, residual=x, gate=e2)
+        codes, rs = torch.ops.turing_utils.layer_norm_affine_int8_convrot_quantize(
+            x, self.norm3_weight, self.norm3_bias, cfg.eps, self.cross_q.group)
+        x = self.cross_attention(QuantizedActivation(codes, rs, b, l, self.cross_q.group), context, residual=x)
+        return self.ffn(adaln_codes(x, e4, e3, self.ffn_up.group), residual=x, gate=e5)
 
     __call__ = forward
 

@@ -45,6 +45,7 @@
 // produce, that the INT8 code is the IEEE division's.
 #include <type_traits>
 
+#include "ln_common.h"
 #include "tu_common.h"
 
 namespace tu {
@@ -57,6 +58,10 @@ constexpr int kMaxPasses = 4;     // so a row holds at most 65536 columns
 constexpr int kMaxCols = kChunk * kMaxWaves * kMaxPasses;
 constexpr int kScratchBytes = 8 * 144 * 4;  // per wave: the larger of the two padded layouts
 constexpr float kInvSqrt2 = 0.70710678118654752440f;
+// Per-group slots of a wave's scratch: the fp32 transpose (dwords, padded so
+// the groups of a wave fall on different banks) and the code transpose (bytes).
+template <int G> constexpr int group_dwords() { return G == 128 ? 144 : 272; }
+template <int G> constexpr int code_group_bytes() { return G + 16; }
 
 __device__ __forceinline__ void lds_wave_sync() {
     // LDS operations of one wave complete in order; this stops the compiler
@@ -317,6 +322,96 @@ __device__ __forceinline__ uint32_t gelu_pair_select(uint32_t w, uint32_t rel2, 
     return (tiny & is_tiny) | (r & ~is_tiny);
 }
 
+// Rotation of one pass.  Lane (gi, L) holds v = the 16 consecutive columns
+// 16 L .. 16 L + 15 of group gi (element index 16 L + p, p = d0 + 4 d1); on
+// return z holds its rotated values after the transpose through `grp` (the
+// group's slot of the wave's scratch): for G = 256, p = L and t = d2 + 4 d3 =
+// 0..15 in z[t]; for G = 128, p = 2L and 2L + 1 in z[t] and z[8 + t] with
+// t = d2 + 4 d3 = 0..7.
+template <int G>
+__device__ __forceinline__ void rotate_pass(float (&v)[16], float *grp, int L, float (&z)[16]) {
+    // Digits d0 (stride 1) and d1 (stride 4) in registers (convrot_quant.cu:384-391).
+#pragma unroll
+    for (int d1 = 0; d1 < 4; ++d1) r4(v[4 * d1], v[4 * d1 + 1], v[4 * d1 + 2], v[4 * d1 + 3]);
+#pragma unroll
+    for (int d0 = 0; d0 < 4; ++d0) r4(v[d0], v[d0 + 4], v[d0 + 8], v[d0 + 12]);
+
+    // Wave-local transpose through LDS.
+    lds_wave_sync();  // earlier reads of the scratch are done
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+        *reinterpret_cast<f32x4 *>(grp + 16 * L + 4 * ((c + (L >> 2)) & 3)) =
+            f32x4{v[4 * c], v[4 * c + 1], v[4 * c + 2], v[4 * c + 3]};
+    lds_wave_sync();
+    if constexpr (G == 256) {
+#pragma unroll
+        for (int t = 0; t < 16; ++t) z[t] = grp[16 * t + 4 * (((L >> 2) + (t >> 2)) & 3) + (L & 3)];
+    } else {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const f32x2 pair = *reinterpret_cast<const f32x2 *>(
+                grp + 16 * t + 4 * (((L >> 1) + (t >> 2)) & 3) + ((2 * L) & 3));
+            z[t] = pair.x;
+            z[8 + t] = pair.y;
+        }
+    }
+
+    // Digits d2 (stride 16) and d3 (stride 64) in registers (convrot_quant.cu:311-330).
+    if constexpr (G == 256) {
+#pragma unroll
+        for (int d3 = 0; d3 < 4; ++d3) r4(z[4 * d3], z[4 * d3 + 1], z[4 * d3 + 2], z[4 * d3 + 3]);
+#pragma unroll
+        for (int d2 = 0; d2 < 4; ++d2) r4(z[d2], z[d2 + 4], z[d2 + 8], z[d2 + 12]);
+    } else {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int d3 = 0; d3 < 2; ++d3)
+                r4(z[8 * h + 4 * d3], z[8 * h + 4 * d3 + 1], z[8 * h + 4 * d3 + 2], z[8 * h + 4 * d3 + 3]);
+            // Radix-2 digit on stride 64: (1/sqrt2) [[1, 1], [1, -1]].
+#pragma unroll
+            for (int d2 = 0; d2 < 4; ++d2) {
+                const float a0 = z[8 * h + d2], a1 = z[8 * h + d2 + 4];
+                z[8 * h + d2] = kInvSqrt2 * (a0 + a1);
+                z[8 * h + d2 + 4] = kInvSqrt2 * (a0 - a1);
+            }
+        }
+    }
+}
+
+// Codes of one pass back in column order: element 16 t + p of the lane's
+// group is byte 16 t + p of `gb` (the group's slot of the wave's scratch,
+// G + 16 bytes); returns the 16 codes of the lane's own columns.  `packed`
+// holds the rotated values as element-type pairs in z order (G = 256:
+// t = 2j, 2j + 1 of p = L; G = 128: p = 2L (low) and 2L + 1 (high) of t = j).
+template <int G, bool kF16>
+__device__ __forceinline__ u32x4 pass_codes(const uint32_t (&packed)[8], float rs, float ry, unsigned char *gb,
+                                            int L) {
+    lds_wave_sync();  // the scratch is free (transposed reads consumed)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const uint32_t w = packed[j];
+        uint32_t c0, c1;
+        if constexpr (kF16) {
+            c0 = static_cast<uint32_t>(quant_code_f16(f16_bits_to_f32(w & 0xffffu), rs)) & 0xffu;
+            c1 = static_cast<uint32_t>(quant_code_f16(f16_bits_to_f32(w >> 16), rs)) & 0xffu;
+        } else {
+            int32_t i0, i1;
+            quant_code2(bf16_bits_to_f32(w & 0xffffu), __uint_as_float(w & 0xffff0000u), ry, i0, i1);
+            c0 = static_cast<uint32_t>(i0) & 0xffu;
+            c1 = static_cast<uint32_t>(i1) & 0xffu;
+        }
+        if constexpr (G == 256) {
+            gb[32 * j + L] = static_cast<unsigned char>(c0);
+            gb[32 * j + 16 + L] = static_cast<unsigned char>(c1);
+        } else {
+            *reinterpret_cast<uint16_t *>(gb + 16 * j + 2 * L) = static_cast<uint16_t>(c0 | (c1 << 8));
+        }
+    }
+    lds_wave_sync();
+    return *reinterpret_cast<const u32x4 *>(gb + 16 * L);
+}
+
 // Raw bf16 input of one lane for one pass: 16 columns (and 16 "up" columns
 // for SwiGLU).
 template <int kAct>
@@ -369,8 +464,8 @@ __global__ __launch_bounds__(kGeluTable ? kTableThreads : 1024) void convrot_qua
     // the groups of a wave fall on different banks); element p of source lane
     // L sits at 16 L + 4 ((p / 4 + L / 4) % 4) + p % 4 (16-byte chunks rotated
     // by L / 4, so the 16-byte writes of lanes L and L + 4 hit different banks).
-    constexpr int kGroupDwords = G == 128 ? 144 : 272;
-    constexpr int kCodeGroupBytes = G + 16;  // code scratch, padded likewise
+    constexpr int kGroupDwords = group_dwords<G>();
+    constexpr int kCodeGroupBytes = code_group_bytes<G>();  // code scratch, padded likewise
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -461,54 +556,8 @@ __global__ __launch_bounds__(kGeluTable ? kTableThreads : 1024) void convrot_qua
                                                   std::integral_constant<int, kAct>{});
                 }
             }
-            // Digits d0 (stride 1) and d1 (stride 4) in registers (convrot_quant.cu:384-391).
-#pragma unroll
-            for (int d1 = 0; d1 < 4; ++d1) r4(v[4 * d1], v[4 * d1 + 1], v[4 * d1 + 2], v[4 * d1 + 3]);
-#pragma unroll
-            for (int d0 = 0; d0 < 4; ++d0) r4(v[d0], v[d0 + 4], v[d0 + 8], v[d0 + 12]);
-
-            // Wave-local transpose through LDS.
-            lds_wave_sync();  // earlier reads of the scratch are done
-#pragma unroll
-            for (int c = 0; c < 4; ++c)
-                *reinterpret_cast<f32x4 *>(grp + 16 * L + 4 * ((c + (L >> 2)) & 3)) =
-                    f32x4{v[4 * c], v[4 * c + 1], v[4 * c + 2], v[4 * c + 3]};
-            lds_wave_sync();
             float z[16];
-            if constexpr (G == 256) {
-#pragma unroll
-                for (int t = 0; t < 16; ++t) z[t] = grp[16 * t + 4 * (((L >> 2) + (t >> 2)) & 3) + (L & 3)];
-            } else {
-#pragma unroll
-                for (int t = 0; t < 8; ++t) {
-                    const f32x2 pair = *reinterpret_cast<const f32x2 *>(
-                        grp + 16 * t + 4 * (((L >> 1) + (t >> 2)) & 3) + ((2 * L) & 3));
-                    z[t] = pair.x;
-                    z[8 + t] = pair.y;
-                }
-            }
-
-            // Digits d2 (stride 16) and d3 (stride 64) in registers (convrot_quant.cu:311-330).
-            if constexpr (G == 256) {
-#pragma unroll
-                for (int d3 = 0; d3 < 4; ++d3) r4(z[4 * d3], z[4 * d3 + 1], z[4 * d3 + 2], z[4 * d3 + 3]);
-#pragma unroll
-                for (int d2 = 0; d2 < 4; ++d2) r4(z[d2], z[d2 + 4], z[d2 + 8], z[d2 + 12]);
-            } else {
-#pragma unroll
-                for (int h = 0; h < 2; ++h) {
-#pragma unroll
-                    for (int d3 = 0; d3 < 2; ++d3)
-                        r4(z[8 * h + 4 * d3], z[8 * h + 4 * d3 + 1], z[8 * h + 4 * d3 + 2], z[8 * h + 4 * d3 + 3]);
-                    // Radix-2 digit on stride 64: (1/sqrt2) [[1, 1], [1, -1]].
-#pragma unroll
-                    for (int d2 = 0; d2 < 4; ++d2) {
-                        const float a0 = z[8 * h + d2], a1 = z[8 * h + d2 + 4];
-                        z[8 * h + d2] = kInvSqrt2 * (a0 + a1);
-                        z[8 * h + d2 + 4] = kInvSqrt2 * (a0 - a1);
-                    }
-                }
-            }
+            rotate_pass<G>(v, grp, L, z);
             if (active) {
 #pragma unroll
                 for (int t = 0; t < 16; ++t) absmax = fmaxf(absmax, fabsf(z[t]));
@@ -540,37 +589,212 @@ __global__ __launch_bounds__(kGeluTable ? kTableThreads : 1024) void convrot_qua
             const int chunk = wave + pass * waves;
             if (chunk >= nchunks) break;
             const int col = chunk * kChunk + 16 * lane;
-            // Codes back to column order: element 16 t + p of group gi is byte
-            // gi * kCodeGroupBytes + 16 t + p of the wave's scratch.
-            lds_wave_sync();  // the scratch is free (transposed reads consumed)
-            unsigned char *gb = scr8 + gi * kCodeGroupBytes;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const uint32_t w = packed[pass][j];
-                uint32_t c0, c1;
-                if constexpr (kF16) {
-                    c0 = static_cast<uint32_t>(quant_code_f16(f16_bits_to_f32(w & 0xffffu), rs)) & 0xffu;
-                    c1 = static_cast<uint32_t>(quant_code_f16(f16_bits_to_f32(w >> 16), rs)) & 0xffu;
-                } else {
-                    int32_t i0, i1;
-                    quant_code2(bf16_bits_to_f32(w & 0xffffu), __uint_as_float(w & 0xffff0000u), ry, i0, i1);
-                    c0 = static_cast<uint32_t>(i0) & 0xffu;
-                    c1 = static_cast<uint32_t>(i1) & 0xffu;
-                }
-                if constexpr (G == 256) {
-                    gb[32 * j + L] = static_cast<unsigned char>(c0);
-                    gb[32 * j + 16 + L] = static_cast<unsigned char>(c1);
-                } else {
-                    *reinterpret_cast<uint16_t *>(gb + 16 * j + 2 * L) = static_cast<uint16_t>(c0 | (c1 << 8));
-                }
-            }
-            lds_wave_sync();
-            const u32x4 codes = *reinterpret_cast<const u32x4 *>(gb + 16 * L);
+            const u32x4 codes = pass_codes<G, kF16>(packed[pass], rs, ry, scr8 + gi * kCodeGroupBytes, L);
             if (col < k) *reinterpret_cast<u32x4 *>(qrow + col) = codes;
         }
         // the next row rewrites wave_amax: every wave has read this row's first
         if (row + 1 < row_end) __syncthreads();
     }
+}
+
+
+// ---------------------------------------------------------------------------
+// LayerNorm fused with the G = 128 quantizer, bf16 rows of hidden = 256 per
+// columns (per <= kPer).  The codes and scales are those of the bf16
+// LayerNorm (AdaLN modulation, or the affine weight and bias) followed by the
+// row-buffer quantizer above on its bf16 output; the normalized row never
+// leaves the chip.
+//
+// Workgroup = 256 threads = 8 rows, one per 32-lane half-wave, as the 16-bit
+// LayerNorm kernel: ln16_row_stats, then ln16_emit8 per column block (lane p
+// holds columns 256 i + 8 p .. + 7 of block i).  A pass takes two blocks
+// (512 columns): their outputs go through the wave's scratch so that lane p
+// holds columns 512 P + 16 p .. + 15, the quantizer's layout (group
+// 4 P + p / 8, lane L = p % 8 of it), and rotate_pass / pass_codes run as in
+// the quantizer with the wave's 8 groups taken from its two rows.  The
+// rotated values stay in registers as bf16 pairs until the row's absmax
+// (a half-wave reduction) is known.
+// LDS (6 B per column + kScratchBytes per wave: three workgroups per CU at
+// hidden 5120): the modulation row of the workgroup's first row, m as fp32
+// and the shift as bf16, then the waves' scratch.
+// ---------------------------------------------------------------------------
+// f(integral_constant<int, I>) for I = I0 .. N - 1, in order.
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F &&f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for<I + 1, N>(f);
+    }
+}
+
+template <int kPer, bool kAffine>
+__global__ __launch_bounds__(kLnThreads) void ln_convrot_quant_kernel(
+    const uint16_t *__restrict__ x, const uint16_t *__restrict__ scale, const uint16_t *__restrict__ shift,
+    int8_t *__restrict__ q, float *__restrict__ scales, int64_t rows, int64_t len, int hidden, int per, int64_t steps,
+    float eps, Recips rc) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    constexpr int kPasses = kPer / 2;
+    float *mod = reinterpret_cast<float *>(smem);
+    uint16_t *mod_h16 = reinterpret_cast<uint16_t *>(smem + 4 * static_cast<size_t>(hidden));
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int p = tid & 31;  // lane of the half-wave
+    const int wave = tid >> 6;
+    const int gi = lane >> 3, L = lane & 7;
+    unsigned char *scr8 = smem + 6 * static_cast<size_t>(hidden) + wave * kScratchBytes;
+    float *grp = reinterpret_cast<float *>(scr8) + gi * group_dwords<128>();
+    unsigned char *relay = scr8 + 32 * (lane & 32);  // 1 KiB per half-wave
+
+    const int64_t row0 = static_cast<int64_t>(blockIdx.x) * (kLnThreads / 32);
+    const int64_t row_raw = row0 + (tid >> 5);
+    // a half-wave past the last row computes the last row again and stores nothing
+    const int64_t row = min(row_raw, rows - 1);
+    const bool live = row_raw < rows;
+    const int64_t mrow = modulation_row(row, len, steps);
+    const int64_t mrow0 = modulation_row(row0, len, steps);
+    const bool staged = mrow == mrow0;
+    const uint16_t *xr = x + row * hidden + 8 * p;
+    const uint16_t *sc = scale + mrow * hidden + 8 * p;
+    const uint16_t *sh = shift + mrow * hidden + 8 * p;
+
+    u32x4 xs[kPer];
+#pragma unroll
+    for (int i = 0; i < kPer; ++i)
+        if (i < per) xs[i] = *reinterpret_cast<const u32x4 *>(xr + 256 * i);
+
+    // the workgroup's first row's modulation row: m = T(1 + scale) (or the
+    // weight) as fp32, the shift (or bias) as its bf16 bits
+    for (int c = 8 * tid; c < hidden; c += 8 * kLnThreads) {
+        const u32x4 sv = *reinterpret_cast<const u32x4 *>(scale + mrow0 * hidden + c);
+        f32x4 m0, m1;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float sf = unpack16<0>(sv, e);
+            const float m = kAffine ? sf : t_round<0>(1.0f + sf);
+            if (e < 4) m0[e] = m; else m1[e - 4] = m;
+        }
+        *reinterpret_cast<f32x4 *>(mod + c) = m0;
+        *reinterpret_cast<f32x4 *>(mod + c + 4) = m1;
+        *reinterpret_cast<u32x4 *>(mod_h16 + c) = *reinterpret_cast<const u32x4 *>(shift + mrow0 * hidden + c);
+    }
+    __syncthreads();
+
+    float mu, inv;
+    ln16_row_stats<0, kPer>(xs, per, hidden, eps, rc, (tid & 32) << 2, mu, inv);
+
+    // The rotated values of pass P replace its two input blocks in xs (as bf16
+    // pairs in z order: packed word j = (z[j], z[8 + j]) in xs[2P + j / 4]),
+    // which keeps the row's registers at one copy.  kPer is even, so
+    // xs[2P + 1] exists whenever 2P < per.
+    static_assert(kPer % 2 == 0, "passes take two column blocks");
+    float absmax = 0.0f;
+    // passes as a compile-time sequence, so that xs[] is never indexed at run
+    // time (a loop this long is not unrolled); per is uniform
+    static_for<0, kPasses>([&](auto pass_c) {
+        constexpr int pass = decltype(pass_c)::value;
+        if (2 * pass >= per) return;
+        u32x4 o[2];
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            const int i = 2 * pass + b;
+            o[b] = u32x4{0u, 0u, 0u, 0u};
+            if (i < per) {
+                float mv[8], hv[8];
+                if (staged) {
+                    const float *mod_m = mod + 256 * i + 8 * p;
+                    const f32x4 m0 = *reinterpret_cast<const f32x4 *>(mod_m);
+                    const f32x4 m1 = *reinterpret_cast<const f32x4 *>(mod_m + 4);
+                    const u32x4 hw = *reinterpret_cast<const u32x4 *>(mod_h16 + 256 * i + 8 * p);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        mv[e] = m0[e]; mv[e + 4] = m1[e];
+                    }
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) hv[e] = unpack16<0>(hw, e);
+                } else {
+                    const u32x4 sv = *reinterpret_cast<const u32x4 *>(sc + 256 * i);
+                    const u32x4 shv = *reinterpret_cast<const u32x4 *>(sh + 256 * i);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const float sf = unpack16<0>(sv, e);
+                        mv[e] = kAffine ? sf : t_round<0>(1.0f + sf);
+                        hv[e] = unpack16<0>(shv, e);
+                    }
+                }
+                // the block's words made opaque, so that the statistics'
+                // unpacked fp32 copies of them need not stay live until here
+                uint32_t w0 = xs[i][0], w1 = xs[i][1], w2 = xs[i][2], w3 = xs[i][3];
+                asm("" : "+v"(w0), "+v"(w1), "+v"(w2), "+v"(w3));
+                o[b] = ln16_emit8<0, kAffine>(u32x4{w0, w1, w2, w3}, mv, hv, mu, inv);
+            }
+        }
+        // blocks 2 pass and 2 pass + 1 in column order, read back 16 columns a lane
+        lds_wave_sync();  // earlier reads of the scratch are done
+        *reinterpret_cast<u32x4 *>(relay + 16 * p) = o[0];
+        *reinterpret_cast<u32x4 *>(relay + 512 + 16 * p) = o[1];
+        lds_wave_sync();
+        const u32x4 y0 = *reinterpret_cast<const u32x4 *>(relay + 32 * p);
+        const u32x4 y1 = *reinterpret_cast<const u32x4 *>(relay + 32 * p + 16);
+        float v[16];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            v[2 * j] = bf16_bits_to_f32(y0[j] & 0xffffu);
+            v[2 * j + 1] = __uint_as_float(y0[j] & 0xffff0000u);
+            v[8 + 2 * j] = bf16_bits_to_f32(y1[j] & 0xffffu);
+            v[8 + 2 * j + 1] = __uint_as_float(y1[j] & 0xffff0000u);
+        }
+        float z[16];
+        rotate_pass<128>(v, grp, L, z);
+        if (512 * pass + 16 * p < hidden) {
+#pragma unroll
+            for (int t = 0; t < 16; ++t) absmax = fmaxf(absmax, fabsf(z[t]));
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) xs[2 * pass + j / 4][j % 4] = hw_bf16x2_bits(z[j], z[8 + j]);
+    });
+
+    // the row's absmax over its half-wave
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1) absmax = fmaxf(absmax, __shfl_xor(absmax, off, 64));
+    const float clipped = fminf(absmax, 3.38953139e38f);
+    const float row_scale = fmaxf(clipped / 127.0f, 1.0e-30f);
+    if (p == 0 && live) scales[row] = row_scale;
+    const float rs = bf16_round(row_scale);
+    const float ry = 1.0f / rs;
+
+    int8_t *qrow = q + row * static_cast<int64_t>(hidden);
+    static_for<0, kPasses>([&](auto pass_c) {
+        constexpr int pass = decltype(pass_c)::value;
+        if (2 * pass >= per) return;
+        const uint32_t packed[8] = {xs[2 * pass][0], xs[2 * pass][1], xs[2 * pass][2], xs[2 * pass][3],
+                                    xs[2 * pass + 1][0], xs[2 * pass + 1][1], xs[2 * pass + 1][2], xs[2 * pass + 1][3]};
+        const u32x4 codes = pass_codes<128, false>(packed, rs, ry, scr8 + gi * code_group_bytes<128>(), L);
+        const int col = 512 * pass + 16 * p;
+        if (live && col < hidden) *reinterpret_cast<u32x4 *>(qrow + col) = codes;
+    });
+}
+
+// hidden = 256 per, per <= 20 (register-resident rows and rotated values).
+constexpr int kLnQuantMaxPer = 20;
+
+template <bool kAffine>
+void launch_ln_quant(const void *x, const void *sc, const void *sh, int8_t *q, float *scales, int64_t rows,
+                     int64_t len, int hidden, int64_t steps, float eps, hipStream_t s) {
+    const int per = hidden / kLnThreads;
+    const Recips rc = uniform_recips(per);
+    const dim3 grid(static_cast<unsigned>((rows + kLnThreads / 32 - 1) / (kLnThreads / 32)));
+    const size_t lds = 6 * static_cast<size_t>(hidden) + (kLnThreads / 64) * kScratchBytes;
+    const auto *x16 = static_cast<const uint16_t *>(x), *sc16 = static_cast<const uint16_t *>(sc),
+               *sh16 = static_cast<const uint16_t *>(sh);
+#define TU_LNQ(P) \
+    ln_convrot_quant_kernel<P, kAffine><<<grid, kLnThreads, lds, s>>>(x16, sc16, sh16, q, scales, rows, len, hidden, \
+                                                                      per, steps, eps, rc)
+    if (per <= 4) TU_LNQ(4);
+    else if (per <= 8) TU_LNQ(8);
+    else if (per <= 12) TU_LNQ(12);
+    else if (per <= 16) TU_LNQ(16);
+    else TU_LNQ(20);
+#undef TU_LNQ
 }
 
 }  // namespace
@@ -636,4 +860,47 @@ extern "C" int32_t tu_convrot_quant_i8(const void *x_bf16, int8_t *q, float *sca
 #undef TU_CONVROT_LAUNCH
 #undef TU_CONVROT_LAUNCH_T
     return check_launch("tu_convrot_quant_i8");
+}
+
+namespace {
+int32_t check_ln_quant(const void *x, const void *sc, const void *sh, const int8_t *q, const float *scales,
+                       int64_t rows, int64_t hidden, float eps, const char *what) {
+    TU_REQUIRE(rows >= 0 && rows <= 0x7fffffff, "%s rows must be in [0, 2^31)", what);
+    TU_REQUIRE(hidden > 0 && hidden % tu::kLnThreads == 0 && hidden <= tu::kLnThreads * tu::kLnQuantMaxPer,
+               "%s hidden must be a multiple of %d in [%d, %d], got %lld", what, tu::kLnThreads, tu::kLnThreads,
+               tu::kLnThreads * tu::kLnQuantMaxPer, static_cast<long long>(hidden));
+    TU_REQUIRE(eps > 0.0f && eps <= 3.4e38f, "%s epsilon must be finite and positive", what);
+    TU_REQUIRE(x && sc && sh && q && scales, "%s pointers must be non-null", what);
+    TU_REQUIRE(((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(sc) | reinterpret_cast<uintptr_t>(sh) |
+                 reinterpret_cast<uintptr_t>(q)) & 15) == 0,
+               "%s input, modulation and codes must be 16-byte aligned", what);
+    return 0;
+}
+}  // namespace
+
+extern "C" int32_t tu_layer_norm_adaln_convrot_quant_i8(const void *x, const void *scale, const void *shift,
+                                                        int8_t *q, float *row_scale, int64_t batch, int64_t len,
+                                                        int64_t hidden, int64_t steps, float eps, void *stream) {
+    using namespace tu;
+    TU_REQUIRE(batch > 0 && len > 0 && steps > 0 && steps <= 0x7fffffff,
+               "LayerNorm+AdaLN ConvRot dimensions must be positive");
+    TU_REQUIRE(batch <= 0x7fffffff / len, "LayerNorm+AdaLN ConvRot rows exceed the kernel range");
+    if (check_ln_quant(x, scale, shift, q, row_scale, batch * len, hidden, eps, "LayerNorm+AdaLN ConvRot")) return -1;
+    if (require_gfx950()) return -1;
+    launch_ln_quant<false>(x, scale, shift, q, row_scale, batch * len, len, static_cast<int>(hidden), steps, eps,
+                           static_cast<hipStream_t>(stream));
+    return check_launch("tu_layer_norm_adaln_convrot_quant_i8");
+}
+
+extern "C" int32_t tu_layer_norm_affine_convrot_quant_i8(const void *x, const void *weight, const void *bias,
+                                                         int8_t *q, float *row_scale, int64_t rows, int64_t hidden,
+                                                         float eps, void *stream) {
+    using namespace tu;
+    if (check_ln_quant(x, weight, bias, q, row_scale, rows, hidden, eps, "LayerNorm ConvRot")) return -1;
+    if (require_gfx950()) return -1;
+    if (rows == 0) return 0;
+    // one batch of `rows` tokens and a single "modulation" row: weight / bias
+    launch_ln_quant<true>(x, weight, bias, q, row_scale, rows, rows, static_cast<int>(hidden), 1, eps,
+                          static_cast<hipStream_t>(stream));
+    return check_launch("tu_layer_norm_affine_convrot_quant_i8");
 }

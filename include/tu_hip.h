@@ -406,6 +406,23 @@ int32_t tu_layer_norm_adaln(const void *x, const void *scale, const void *shift,
 int32_t tu_layer_norm_affine(const void *x, const void *weight, const void *bias, void *out,
                              int32_t dtype, int64_t rows, int64_t hidden, float eps, void *stream);
 
+/* LayerNorm fused with the ConvRot INT8 quantizer (G = 128, bf16 only): the
+ * codes q [rows, hidden] and row scales row_scale [rows] that
+ * tu_convrot_quant_i8(out, q, row_scale, rows, hidden, 128, 0) writes for the
+ * bf16 out of tu_layer_norm_adaln (dtype 0, same arguments) resp.
+ * tu_layer_norm_affine, bit for bit; the normalized rows are not written.
+ * hidden a multiple of 256 in [256, 5120]; x, scale / weight, shift / bias
+ * and q 16-byte aligned.  No counterpart in the reference, which runs the
+ * norm (ops.py:399-418) and the linear's activation quantizer
+ * (quantization/dispatch.py:538-615) as two ops; for the Wan block's norm1 /
+ * norm2 -> qkv / FFN-up and norm3 -> cross-attention q projections. */
+int32_t tu_layer_norm_adaln_convrot_quant_i8(const void *x, const void *scale, const void *shift, int8_t *q,
+                                             float *row_scale, int64_t batch, int64_t len, int64_t hidden,
+                                             int64_t steps, float eps, void *stream);
+int32_t tu_layer_norm_affine_convrot_quant_i8(const void *x, const void *weight, const void *bias, int8_t *q,
+                                              float *row_scale, int64_t rows, int64_t hidden, float eps,
+                                              void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -405,6 +405,15 @@ def extra_kernels(torch, dev, ops, lin, q, k, v, copy_gbs) -> dict:
     nbytes = 4.0 * xn.numel()
     out["layer_norm_adaln"] = {"ms_avg": ms, "gbs": nbytes / ms / 1e6, "frac_copy": nbytes / ms / 1e6 / copy_gbs,
                                "frac_hbm_peak": nbytes / ms / 1e6 / PEAK_HBM_GBS, "shape": [b, l, h * d]}
+    # the same norm fused with the next projection's ConvRot quantizer (G 128):
+    # 2 B read + 1 B code written per element, a 4-byte scale per row; and
+    # the two kernels it replaces
+    ms = timed(lambda: ops.layer_norm_adaln_int8_convrot_quantize(xn, mod, mod, 1e-6, GROUP))
+    ms_two = timed(lambda: ops.bf16_int8_convrot_quantize(
+        ops.layer_norm_adaln(xn, mod, mod, 1e-6).view(b * l, h * d), GROUP))
+    nbytes = 3.0 * xn.numel() + 4.0 * b * l
+    out["layer_norm_adaln_convrot_quant"] = {"ms_avg": ms, "gbs": nbytes / ms / 1e6, "ms_two_kernels": ms_two,
+                                             "shape": [b, l, h * d]}
     del xn, mod
     # C5: the whole Wan-14B block forward (norms, seven W8A8 projections, fused
     # Q/K producers, self- and cross-attention, gated residuals)

@@ -598,6 +598,15 @@ __global__ __launch_bounds__(kGeluTable ? kTableThreads : 1024) void convrot_qua
 }
 
 
+// f(integral_constant<int, J>{}) for J = I, I + 1, .., N - 1, in order.
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F &&f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for<I + 1, N>(f);
+    }
+}
+
 // ---------------------------------------------------------------------------
 // LayerNorm fused with the G = 128 quantizer, bf16 rows of hidden = 256 per
 // columns (per <= kPer).  The codes and scales are those of the bf16
@@ -618,15 +627,6 @@ __global__ __launch_bounds__(kGeluTable ? kTableThreads : 1024) void convrot_qua
 // hidden 5120): the modulation row of the workgroup's first row, m as fp32
 // and the shift as bf16, then the waves' scratch.
 // ---------------------------------------------------------------------------
-// f(integral_constant<int, I>) for I = I0 .. N - 1, in order.
-template <int I, int N, typename F>
-__device__ __forceinline__ void static_for(F &&f) {
-    if constexpr (I < N) {
-        f(std::integral_constant<int, I>{});
-        static_for<I + 1, N>(f);
-    }
-}
-
 template <int kPer, bool kAffine>
 __global__ __launch_bounds__(kLnThreads) void ln_convrot_quant_kernel(
     const uint16_t *__restrict__ x, const uint16_t *__restrict__ scale, const uint16_t *__restrict__ shift,

@@ -456,7 +456,7 @@ CSRC_DIR = os.path.join(ROOT, "comfyui-turing-utils_amd", "csrc")
 # The sources each bench kernel is built from (the headers every kernel
 # includes are added by kernel_sources_digest).
 KERNEL_SOURCES = (
-    ("convrot_quant", ("convrot_quant.hip",)),
+    ("convrot_quant", ("convrot_quant.hip", "ln_common.h")),
     ("int8_gemm", ("int8_gemm.hip",)),
     ("sage_kmean", ("sage_quant.hip",)),
     ("sage_quant", ("sage_quant.hip",)),

@@ -613,22 +613,6 @@ int32_t check_gemm_args(const int8_t *a, const int8_t *w, const void *out, int64
     return require_gfx950();
 }
 
-// Compute units of the current device (cached per device id).
-int32_t device_cus(int &cus) {
-    static int cache[64];
-    int dev = 0;
-    hipError_t err = hipGetDevice(&dev);
-    if (err != hipSuccess) return fail("hipGetDevice failed: %s", hipGetErrorString(err));
-    if (dev >= 0 && dev < 64 && cache[dev] > 0) {
-        cus = cache[dev];
-        return 0;
-    }
-    err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-    if (err != hipSuccess || cus <= 0) return fail("hipDeviceGetAttribute(CU count) failed: %s", hipGetErrorString(err));
-    if (dev >= 0 && dev < 64) cache[dev] = cus;
-    return 0;
-}
-
 // Time of a round of 128-row tiles relative to a round of 256-row tiles of the
 // same N and K, measured on MI355X: 0.635 at N 8960 / K 1536 and at N 5120 /
 // K 5120 (a tile's fixed part, the epilogue's stores and the first loads, does

@@ -695,23 +695,6 @@ __global__ __launch_bounds__(kRowQThreads) __attribute__((amdgpu_waves_per_eu(3)
 // the head-group kernel's arithmetic.  Two barriers a tile.  Buffer offsets
 // are 32-bit: the host requires a batch's rows to span less than 2 GiB, and
 // rows past the sequence read as zeros (their offsets are past the range).
-// Compute units of the current device (cached per device id): the streamed
-// kernel's grid.
-int32_t device_cus(int &cus) {
-    static int cache[64];
-    int dev = 0;
-    hipError_t err = hipGetDevice(&dev);
-    if (err != hipSuccess) return fail("hipGetDevice failed: %s", hipGetErrorString(err));
-    if (dev >= 0 && dev < 64 && cache[dev] > 0) {
-        cus = cache[dev];
-        return 0;
-    }
-    err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-    if (err != hipSuccess || cus <= 0) return fail("hipDeviceGetAttribute(CU count) failed: %s", hipGetErrorString(err));
-    if (dev >= 0 && dev < 64) cache[dev] = cus;
-    return 0;
-}
-
 constexpr int kRowSWaves = 16;
 constexpr int kRowSThreads = kRowSWaves * 64;
 constexpr int kRowSMaxHeads = 3 * kRowSWaves;

@@ -20,6 +20,8 @@ int32_t fail(const char *fmt, ...) __attribute__((format(printf, 1, 2)));
 int32_t check_launch(const char *what);
 // Returns 0 if the current device is gfx950, otherwise sets an error.
 int32_t require_gfx950();
+// Compute units of the current device (cached per device id); 0 or an error.
+int32_t device_cus(int &cus);
 
 #define TU_REQUIRE(cond, ...)          \
     do {                               \

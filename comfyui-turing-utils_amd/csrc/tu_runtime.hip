@@ -38,6 +38,21 @@ int32_t require_gfx950() {
     return 0;
 }
 
+int32_t device_cus(int &cus) {
+    static int cache[64];
+    int dev = 0;
+    hipError_t err = hipGetDevice(&dev);
+    if (err != hipSuccess) return fail("hipGetDevice failed: %s", hipGetErrorString(err));
+    if (dev >= 0 && dev < 64 && cache[dev] > 0) {
+        cus = cache[dev];
+        return 0;
+    }
+    err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (err != hipSuccess || cus <= 0) return fail("hipDeviceGetAttribute(CU count) failed: %s", hipGetErrorString(err));
+    if (dev >= 0 && dev < 64) cache[dev] = cus;
+    return 0;
+}
+
 }  // namespace tu
 
 extern "C" {

@@ -267,3 +267,28 @@ def test_layer_norm_adaln_fake_contract_and_refusals():
     with pytest.raises(RuntimeError, match="CUDA|HIP"):
         kernel.turing_layer_norm_adaln(cpu, cpu[:, :1], cpu[:, :1])
     assert "turing_layer_norm_adaln" in kernel.__all__
+
+
+def test_layer_norm_convrot_fake_contract_and_refusals():
+    """The LayerNorm-fused ConvRot quantizers (no reference op): codes
+    [rows, H] int8 and row scales [rows, 1] fp32, as bf16_int8_convrot_quantize
+    returns them; CPU tensors refused before any launch."""
+    x = torch.empty((2, 9, 5120), dtype=torch.bfloat16, device=META)
+    mod = torch.empty((2, 4, 5120), dtype=torch.bfloat16, device=META)
+    q, s = torch.ops.turing_utils.layer_norm_adaln_int8_convrot_quantize(x, mod, mod, 1e-6, 128)
+    assert q.shape == (18, 5120) and q.dtype == torch.int8 and q.device.type == META
+    assert s.shape == (18, 1) and s.dtype == torch.float32
+    w = torch.empty((5120,), dtype=torch.bfloat16, device=META)
+    q, s = torch.ops.turing_utils.layer_norm_affine_int8_convrot_quantize(x, w, w, 1e-6, 128)
+    assert q.shape == (18, 5120) and s.shape == (18, 1)
+    compiled = torch.compile(
+        lambda a, m: kernel.turing_layer_norm_adaln_int8_convrot_quantize(a, m, m, 1e-6, 128), backend="eager",
+        fullgraph=True)
+    assert compiled(x, mod)[0].shape == (18, 5120)
+    cpu = torch.zeros((1, 4, 256), dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="CUDA|HIP"):
+        kernel.turing_layer_norm_adaln_int8_convrot_quantize(cpu, cpu[:, :1], cpu[:, :1])
+    with pytest.raises(RuntimeError, match="CUDA|HIP"):
+        kernel.turing_layer_norm_affine_int8_convrot_quantize(cpu[0], cpu[0, 0], cpu[0, 0])
+    for name in ("turing_layer_norm_adaln_int8_convrot_quantize", "turing_layer_norm_affine_int8_convrot_quantize"):
+        assert name in kernel.__all__

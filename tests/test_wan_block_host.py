@@ -59,3 +59,19 @@ def test_rope_table():
     w3 = t[0, 3, 0]  # f 0, h 0, w 3: only the last 21 pairs rotate
     assert torch.allclose(w3[:43], torch.eye(2, dtype=torch.float64).expand(43, 2, 2))
     assert abs(w3[43, 1, 0] - torch.sin(torch.tensor(3.0, dtype=torch.float64))) < 1e-6
+
+
+def test_quantized_activation_must_match_the_linear():
+    """A projection fed the codes of a fused norm + quantizer refuses codes of
+    another width or ConvRot group, and a GELU request (the codes are already
+    made), before any launch."""
+    from comfyui_turing_utils_kernel.wan_block import QuantizedActivation
+
+    lin = W8A8Linear(torch.zeros(512, 256, dtype=torch.int8), torch.ones(512), None)
+    codes, scale = torch.zeros(8, 256, dtype=torch.int8), torch.ones(8, 1)
+    assert QuantizedActivation(codes, scale, 1, 8, 128).shape == (1, 8, 256)
+    for bad, kw in ((QuantizedActivation(codes, scale, 1, 8, 256), {}),
+                    (QuantizedActivation(codes[:, :128], scale, 1, 8, 128), {}),
+                    (QuantizedActivation(codes, scale, 1, 8, 128), {"gelu": True})):
+        with pytest.raises(ValueError, match="expects codes"):
+            lin(bad, **kw)

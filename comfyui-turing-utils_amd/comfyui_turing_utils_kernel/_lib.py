@@ -111,12 +111,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "tu_w8a8_quant_v": (
         _i32,
         [_c_void_p, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _c_void_p, _i64,
-         _c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p],
+         _c_void_p, _c_void_p, _i64, _c_void_p],
     ),
     "tu_w8a8_attn_fwd": (
         _i32,
         [_c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p,
-         _c_void_p, _i64, _c_void_p, _i32,
+         _i64, _c_void_p, _i32,
          _i64, _i64, _i64, _i64, _i64, _i64,
          _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
          _f32, _i32, _c_void_p],
@@ -139,7 +139,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
 }
 
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

@@ -457,9 +457,7 @@ class PrequantizedW8A8Attention:
     V^T, ready for ``w8a8attn_from_prequantized``: the dense (force_dense,
     use_w8a8) subset of the reference's PrequantizedSolAttention
     (core.py:50-72).  All tensors are HND with the kernel's 128 channels;
-    ``value_int8`` is [B, Hkv, 128, Lpad] with keys in natural order and
-    ``value_prefix`` the per-channel prefix sums of its codes over 64-key
-    tiles [B, Hkv, Lpad / 64 + 1, 128]."""
+    ``value_int8`` is [B, Hkv, 128, Lpad] with keys in natural order."""
 
     query_int8: torch.Tensor
     query_scale: torch.Tensor
@@ -467,7 +465,6 @@ class PrequantizedW8A8Attention:
     key_scale: torch.Tensor
     value_int8: torch.Tensor
     value_scale: torch.Tensor
-    value_prefix: torch.Tensor
     output_dtype: torch.dtype
     sm_scale: float
     original_head_dim: int
@@ -536,18 +533,17 @@ def prequantize_w8a8attn_from_qk(
         raise ValueError("preprocessed Q/K and V shapes are incompatible")
     tile = _key_tile_tokens(key_tile_tokens, qk.key_int8.size(2))
     with torch.cuda.device(value.device):
-        value_int8, value_scale, value_prefix = quantize_v_int8(value)
+        value_int8, value_scale = quantize_v_int8(value)
         if value_int8.size(2) != KERNEL_HEAD_DIM:
             pad = KERNEL_HEAD_DIM - value_int8.size(2)
             value_int8 = torch.nn.functional.pad(value_int8, (0, 0, 0, pad))
             value_scale = torch.nn.functional.pad(value_scale, (0, pad), value=1.0e-12)
-            value_prefix = _pad_channels(value_prefix, KERNEL_HEAD_DIM)
         q_int8 = _pad_channels(qk.query_int8, KERNEL_HEAD_DIM)
         k_int8 = _pad_channels(qk.key_int8, KERNEL_HEAD_DIM)
     scale = float(sm_scale) if sm_scale is not None else qk.original_head_dim ** -0.5
     return PrequantizedW8A8Attention(
         query_int8=q_int8, query_scale=qk.query_scale, key_int8=k_int8, key_scale=qk.key_scale,
-        value_int8=value_int8, value_scale=value_scale, value_prefix=value_prefix, output_dtype=value.dtype,
+        value_int8=value_int8, value_scale=value_scale, output_dtype=value.dtype,
         sm_scale=scale, original_head_dim=qk.original_head_dim, key_tile_tokens=tile,
         is_causal=bool(is_causal), route_original_basis=bool(qk.route_original_basis),
     )
@@ -614,8 +610,7 @@ def w8a8attn_from_prequantized(quantized: PrequantizedW8A8Attention) -> torch.Te
         _lib.call(
             "tu_w8a8_attn_fwd", q8.data_ptr(), quantized.query_scale.data_ptr(), quantized.query_scale.size(-1),
             k8.data_ptr(), quantized.key_scale.data_ptr(), quantized.key_scale.size(-1),
-            quantized.value_int8.data_ptr(), quantized.value_scale.data_ptr(), quantized.value_prefix.data_ptr(),
-            quantized.value_int8.size(-1), out.data_ptr(), int(quantized.output_dtype == torch.float16),
+            quantized.value_int8.data_ptr(), quantized.value_scale.data_ptr(), quantized.value_int8.size(-1), out.data_ptr(), int(quantized.output_dtype == torch.float16),
             batch, hq, hkv, lq, lk, dim, q8.stride(0), q8.stride(1), q8.stride(2),
             k8.stride(0), k8.stride(1), k8.stride(2), out.stride(0), out.stride(1), out.stride(2),
             float(quantized.sm_scale), int(quantized.is_causal), _lib.stream_of(device),

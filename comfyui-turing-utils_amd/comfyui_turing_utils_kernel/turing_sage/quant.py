@@ -230,11 +230,10 @@ def per_warp_int8_hadamard(
     return q_int8, q_scale, k_int8, k_scale
 
 
-def quantize_v_int8(value: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+def quantize_v_int8(value: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     """Channel-wise signed INT8 of HND V, the reference's quantize_v_int8_sm75
     (turing_sage/core.py:772-784): (codes [B, H, D, ceil(L/64)*64] with keys
-    in natural order and zero padding, fp32 scales [B, H, D], int32 prefix
-    sums of the codes over 64-key tiles [B, H, ceil(L/64) + 1, D])."""
+    in natural order and zero padding, fp32 scales [B, H, D])."""
     if value.ndim != 4 or value.stride(-1) != 1:
         raise ValueError("W8A8 V must be four-dimensional with contiguous channels")
     if value.dtype not in (torch.float16, torch.bfloat16):
@@ -247,13 +246,11 @@ def quantize_v_int8(value: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, to
     lpad = (length + 63) // 64 * 64
     codes = torch.empty((batch, heads, dim, lpad), dtype=torch.int8, device=value.device)
     scale = torch.empty((batch, heads, dim), dtype=torch.float32, device=value.device)
-    prefix = torch.empty((batch, heads, lpad // 64 + 1, dim), dtype=torch.int32, device=value.device)
     lib = _lib.load()
     ws_bytes = int(lib.tu_w8a8_quant_v_workspace(batch, heads, length, dim))
     workspace = torch.empty((ws_bytes,), dtype=torch.uint8, device=value.device)
     with torch.cuda.device(value.device):
         _lib.call("tu_w8a8_quant_v", value.data_ptr(), 1 if value.dtype == torch.float16 else 0, batch, heads,
                   length, dim, value.stride(0), value.stride(1), value.stride(2), codes.data_ptr(), lpad,
-                  scale.data_ptr(), prefix.data_ptr(), workspace.data_ptr(), ws_bytes,
-                  _lib.stream_of(value.device))
-    return codes, scale, prefix
+                  scale.data_ptr(), workspace.data_ptr(), ws_bytes, _lib.stream_of(value.device))
+    return codes, scale

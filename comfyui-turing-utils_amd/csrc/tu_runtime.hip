@@ -59,7 +59,7 @@ extern "C" {
 
 const char *tu_last_error(void) { return tu::g_last_error.c_str(); }
 
-int32_t tu_abi_version(void) { return 12; }
+int32_t tu_abi_version(void) { return 13; }
 
 int32_t tu_device_supported(int32_t device) {
     // The answer cannot change for a device during the process: cache it.

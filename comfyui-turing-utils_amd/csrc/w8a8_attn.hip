@@ -22,14 +22,16 @@
 //     PV MFMA.
 //   * O^T = V^T P on v_mfma_i32_16x16x64_i8 (one MFMA covers the whole
 //     64-key tile).  CDNA4 multiplies signed x signed only, so P goes in as
-//     P - 128 and the 128 * sum_k v8 it drops is added back from per-tile
-//     prefix sums of the V codes.  v_cvt_pk_u8_f32 rounds p to an integer
-//     half-to-even into its byte of the packed operand, and an XOR with
-//     0x80 per byte turns P into P - 128.
+//     127 - P (a signed byte for every P in [0, 255]), and one more MFMA per
+//     fragment against a constant -127 operand adds -127 * sum_k v8.  The
+//     accumulator then holds -(P . v8) exactly, with no V code sums to load.
+//     v_cvt_pk_u8_f32 rounds p to an integer half-to-even into its byte of
+//     the packed operand, and an XOR with 0x7f per byte turns P into 127 - P.
 //   * The PV products stay in int32 accumulators across tiles and are
 //     converted to fp32 only when the row maximum moves (the reference
 //     rescales O every tile; a rescale by 2^0 is exact) or every 512 tiles
-//     (int32 headroom).
+//     (int32 headroom: each key adds at most 255 * 127 in magnitude per
+//     product, and 2 * 127 * 127 with the constant MFMA's term).
 //   * V^T arrives channel-major as INT8 codes [d][key] (keys padded to a
 //     multiple of 64 with zeros) from tu_w8a8_quant_v: the V^T stage is
 //     8 KiB, half of the Sage kernel's bf16 stage.
@@ -156,22 +158,18 @@ __device__ __forceinline__ void mask_tile8(i32x4 (&s)[4][kQT], int key_lim, int 
     }
 }
 
-// Adds the int32 segment [st.seg, tile) to acc_o: acc_i + 128 * (sum of the
-// segment's V codes per channel), scaled by beta, then clears acc_i.
-__device__ __forceinline__ void flush_segment(W8State &st, int tile, const int32_t *__restrict__ vpre, int g) {
+// Adds the int32 segment [st.seg, tile) to acc_o: acc_i holds -(P . v8)
+// exactly, so acc_o += float(acc_i) * -beta; then clears acc_i.
+__device__ __forceinline__ void flush_segment(W8State &st, int tile) {
     if (tile > st.seg) {
-        const int32_t *hi = vpre + static_cast<int64_t>(tile) * kD + 4 * g;
-        const int32_t *lo = vpre + static_cast<int64_t>(st.seg) * kD + 4 * g;
 #pragma unroll
         for (int ds = 0; ds < 8; ++ds) {
-            const i32x4 corr = (*reinterpret_cast<const i32x4 *>(hi + 16 * ds) -
-                                *reinterpret_cast<const i32x4 *>(lo + 16 * ds)) * 128;
 #pragma unroll
             for (int qt = 0; qt < kQT; ++qt) {
-                const i32x4 tot = st.acc_i[ds][qt] + corr;
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
-                    st.acc_o[ds][qt][r] = __builtin_fmaf(static_cast<float>(tot[r]), st.beta[qt], st.acc_o[ds][qt][r]);
+                    st.acc_o[ds][qt][r] =
+                        __builtin_fmaf(static_cast<float>(st.acc_i[ds][qt][r]), -st.beta[qt], st.acc_o[ds][qt][r]);
                 st.acc_i[ds][qt] = i32x4{0, 0, 0, 0};
             }
         }
@@ -179,11 +177,17 @@ __device__ __forceinline__ void flush_segment(W8State &st, int tile, const int32
     st.seg = tile;
 }
 
+// The constant PV operand: -127 in every byte.
+__device__ __forceinline__ i32x4 neg127_operand() {
+    constexpr int32_t kNeg127x4 = static_cast<int32_t>(0x81818181u);
+    return i32x4{kNeg127x4, kNeg127x4, kNeg127x4, kNeg127x4};
+}
+
 // Softmax of tile `tile`: new row maxima (with the u8 offset), flush and
-// rescale when one moved, then P - 128 packed as the PV B operands p8[qt]
+// rescale when one moved, then 127 - P packed as the PV B operands p8[qt]
 // (dword kt = keys 16 g + 4 kt .. + 3 of query 16 qt + lc) and l += p.
 __device__ __forceinline__ void softmax_tile8(const i32x4 (&s)[4][kQT], const float (&f)[kQT], W8State &st,
-                                              i32x4 (&p8)[kQT], int tile, const int32_t *__restrict__ vpre, int g) {
+                                              i32x4 (&p8)[kQT], int tile) {
     float mlane[kQT];
     bool need = false;
 #pragma unroll
@@ -200,7 +204,7 @@ __device__ __forceinline__ void softmax_tile8(const i32x4 (&s)[4][kQT], const fl
         need = need || (mlane[qt] > st.m_used[qt]);
     }
     if (__any(need) || tile - st.seg >= kFlushTiles) {
-        flush_segment(st, tile, vpre, g);
+        flush_segment(st, tile);
         bool rebase = false;
 #pragma unroll
         for (int qt = 0; qt < kQT; ++qt) {
@@ -251,8 +255,8 @@ __device__ __forceinline__ void softmax_tile8(const i32x4 (&s)[4][kQT], const fl
                     // <= 255 since the base sits log2(255) above the maximum
                     packed = __builtin_amdgcn_cvt_pk_u8_f32(p, r, packed);
                 }
-                // P - 128 as signed bytes for the signed-only MFMA
-                p8[qt][kt] = static_cast<int32_t>(packed ^ 0x80808080u);
+                // 127 - P as signed bytes for the signed-only MFMA
+                p8[qt][kt] = static_cast<int32_t>(packed ^ 0x7f7f7f7fu);
             }
             st.l[qt] = __builtin_fmaf(lsum, st.beta[qt], st.l[qt]);
         }
@@ -267,8 +271,10 @@ __device__ __forceinline__ void pv_tile8(const int8_t *stage, const LaneGeom8 &g
     for (int ds = 0; ds < 8; ++ds) {
         const i32x4 vf = *reinterpret_cast<const i32x4 *>(stage + gm.v_rd + ds * 16 * 64);
 #pragma unroll
-        for (int qt = 0; qt < kQT; ++qt)
+        for (int qt = 0; qt < kQT; ++qt) {
             st.acc_i[ds][qt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(vf, p8[qt], st.acc_i[ds][qt], 0, 0, 0);
+            st.acc_i[ds][qt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(vf, neg127_operand(), st.acc_i[ds][qt], 0, 0, 0);
+        }
     }
 }
 
@@ -285,8 +291,11 @@ __device__ __forceinline__ void mfma_cluster8(const int8_t *kst, const int8_t *v
 #pragma unroll
     for (int ds = 0; ds < 8; ++ds)
 #pragma unroll
-        for (int qt = 0; qt < kQT; ++qt)
+        for (int qt = 0; qt < kQT; ++qt) {
             st.acc_i[ds][qt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(vf[ds], p8[qt], st.acc_i[ds][qt], 0, 0, 0);
+            st.acc_i[ds][qt] =
+                __builtin_amdgcn_mfma_i32_16x16x64_i8(vf[ds], neg127_operand(), st.acc_i[ds][qt], 0, 0, 0);
+        }
     i32x4 kf[4][2];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
@@ -322,7 +331,7 @@ template <bool kCausal, bool kFp16Out>
 __global__ __launch_bounds__(kThreads, 1) void w8a8_attn_kernel(
     const int8_t *__restrict__ q8, const float *__restrict__ q_scale, const int8_t *__restrict__ k8,
     const float *__restrict__ k_scale, const int8_t *__restrict__ vt, const float *__restrict__ v_scale,
-    const int32_t *__restrict__ v_prefix, uint16_t *__restrict__ o, int hq, int groups, int64_t lq, int64_t lk,
+    uint16_t *__restrict__ o, int hq, int groups, int64_t lq, int64_t lk,
     int64_t lpad, int64_t nqs, int64_t nks, int64_t q_sb, int64_t q_sh, int64_t q_sl, int64_t k_sb, int64_t k_sh,
     int64_t k_sl, int64_t o_sb, int64_t o_sh, int64_t o_sl, float sm_log2) {
     __shared__ __align__(1024) int8_t lds[kStages][kStageBytes];
@@ -344,7 +353,6 @@ __global__ __launch_bounds__(kThreads, 1) void w8a8_attn_kernel(
     const int8_t *qp = q8 + b * q_sb + h * q_sh;
     const int8_t *kp = k8 + b * k_sb + hk * k_sh;
     const int8_t *vtp = vt + (b * hkv + hk) * kD * lpad;
-    const int32_t *vpre = v_prefix + (b * hkv + hk) * (lpad / kBKey + 1) * kD;
     const float *ks_row = k_scale + (b * hkv + hk) * nks;
 
     int64_t key_end = lk;
@@ -406,16 +414,14 @@ __global__ __launch_bounds__(kThreads, 1) void w8a8_attn_kernel(
                 static_cast<int>(max(min(q0 - key0, static_cast<int64_t>(kBKey)), static_cast<int64_t>(-kBQ)));
             mask_tile8<kCausal>(s, key_lim, q_rel, g, lc);
         }
-        softmax_tile8(s, f, st, p8, it, vpre, g);
+        softmax_tile8(s, f, st, p8, it);
     };
 
     // The schedule of the Sage kernel (sage_attn.hip): one barrier per key
     // tile; both groups run M_it = {QK(it + 1), PV(it)} then softmax(it + 1),
     // group 0's barrier after the softmax, group 1's before it, so the two
     // groups' MFMA clusters overlap on each SIMD.  Unlike there, group 0
-    // issues the next tile's loads after its softmax: a softmax that flushes
-    // waits on its own prefix-sum loads, and vector memory retires in order,
-    // so loads issued just before would be waited for too.
+    // issues the next tile's loads after its softmax.
     if (grp == 0) __builtin_amdgcn_s_waitcnt(vmcnt_imm((kAhead - 1) * kLoadsPerTile));
     wg_barrier();
     qk_tile8(lds[0], gm, qf, s);
@@ -453,7 +459,7 @@ __global__ __launch_bounds__(kThreads, 1) void w8a8_attn_kernel(
 
     // Final segment, then out = O / l * v_scale.  acc_o[ds][qt][r] holds
     // O^T[16 ds + 4 g + r][q0 + 16 qt + lc].
-    flush_segment(st, my_tiles, vpre, g);
+    flush_segment(st, my_tiles);
     const float *vs = v_scale + (b * hkv + hk) * kD + 4 * g;
     uint16_t *op = o + b * o_sb + h * o_sh;
 #pragma unroll
@@ -487,7 +493,7 @@ __global__ __launch_bounds__(kThreads, 1) void w8a8_attn_kernel(
 
 extern "C" int32_t tu_w8a8_attn_fwd(const int8_t *q8, const float *q_scale, int64_t nqs, const int8_t *k8,
                                     const float *k_scale, int64_t nks, const int8_t *vt, const float *v_scale,
-                                    const int32_t *v_prefix, int64_t lpad, void *out, int32_t out_fp16,
+                                    int64_t lpad, void *out, int32_t out_fp16,
                                     int64_t batch, int64_t hq, int64_t hkv, int64_t lq, int64_t lk, int64_t dim,
                                     int64_t q_sb, int64_t q_sh, int64_t q_sl, int64_t k_sb, int64_t k_sh,
                                     int64_t k_sl, int64_t o_sb, int64_t o_sh, int64_t o_sl, float sm_scale,
@@ -498,18 +504,17 @@ extern "C" int32_t tu_w8a8_attn_fwd(const int8_t *q8, const float *q_scale, int6
     TU_REQUIRE(lq > 0 && lk > 0, "W8A8 attention requires non-empty sequences");
     TU_REQUIRE(lpad == (lk + kBKey - 1) / kBKey * kBKey, "W8A8 attention: V^T padded length must be ceil(lk/64)*64");
     TU_REQUIRE(nqs >= (lq + 15) / 16 && nks >= (lk + kBKey - 1) / kBKey, "W8A8 attention scale rows too short");
-    TU_REQUIRE(lk <= (int64_t{1} << 24), "W8A8 attention: lk above 2^24 overflows the V code prefix sums");
     TU_REQUIRE((lq + kBQ - 1) / kBQ <= 0x7fffffff && batch * hq <= 65535, "W8A8 attention grid too large");
     TU_REQUIRE(lk * k_sl < (int64_t{1} << 32) && kD * lpad < (int64_t{1} << 32),
                "W8A8 attention: one head's K or V^T exceeds 4 GiB of addressable bytes");
-    TU_REQUIRE(q8 && q_scale && k8 && k_scale && vt && v_scale && v_prefix && out,
+    TU_REQUIRE(q8 && q_scale && k8 && k_scale && vt && v_scale && out,
                "W8A8 attention pointers must be non-null");
     TU_REQUIRE(sm_scale > 0.0f, "W8A8 attention sm_scale must be positive");
     TU_REQUIRE(q_sl % 16 == 0 && q_sh % 16 == 0 && q_sb % 16 == 0 && (reinterpret_cast<uintptr_t>(q8) & 15) == 0 &&
                    k_sl % 16 == 0 && k_sh % 16 == 0 && k_sb % 16 == 0 && (reinterpret_cast<uintptr_t>(k8) & 15) == 0,
                "W8A8 attention Q/K rows must be 16-byte aligned");
     TU_REQUIRE((reinterpret_cast<uintptr_t>(vt) & 15) == 0 && (reinterpret_cast<uintptr_t>(v_scale) & 15) == 0 &&
-                   (reinterpret_cast<uintptr_t>(v_prefix) & 15) == 0 && o_sl % 4 == 0 && o_sh % 4 == 0 &&
+                   o_sl % 4 == 0 && o_sh % 4 == 0 &&
                    o_sb % 4 == 0 && (reinterpret_cast<uintptr_t>(out) & 7) == 0,
                "W8A8 attention V^T/scales/O must be aligned");
     if (require_gfx950()) return -1;
@@ -518,7 +523,7 @@ extern "C" int32_t tu_w8a8_attn_fwd(const int8_t *q8, const float *q_scale, int6
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int groups = static_cast<int>(hq / hkv);
 #define TU_W8_ARGS                                                                                            \
-    q8, q_scale, k8, k_scale, vt, v_scale, v_prefix, static_cast<uint16_t *>(out), static_cast<int>(hq), groups, \
+    q8, q_scale, k8, k_scale, vt, v_scale, static_cast<uint16_t *>(out), static_cast<int>(hq), groups,           \
         lq, lk, lpad, nqs, nks, q_sb, q_sh, q_sl, k_sb, k_sh, k_sl, o_sb, o_sh, o_sl, sm_log2
     if (causal) {
         if (out_fp16) w8a8_attn_kernel<true, true><<<grid, kThreads, 0, s>>>(TU_W8_ARGS);

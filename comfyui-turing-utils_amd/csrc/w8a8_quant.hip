@@ -20,9 +20,7 @@
 //
 // MI355X layout of V: channel-major codes [B][H][D][Lpad] with keys in
 // natural order (the INT8 PV MFMA reads 16 consecutive keys of one channel
-// per lane), plus per-64-key-tile code sums and their exclusive prefix over
-// tiles [B][H][Lpad/64 + 1][D]: the attention feeds P - 128 (signed) to the
-// MFMA and adds back 128 * sum(V) from the prefix.
+// per lane).
 #include "w8a8_common.h"
 
 namespace tu {
@@ -227,7 +225,7 @@ __global__ __launch_bounds__(kQkThreads) void rot_quant_kernel(RotArgs args) {
 }
 
 // ---------------------------------------------------------------------------
-// V: per-channel amax over token chunks, scales, codes + tile sums, prefix.
+// V: per-channel amax over token chunks, scales, codes.
 // ---------------------------------------------------------------------------
 constexpr int kVThreads = 256;
 constexpr int kVChunk = 1024;  // tokens per amax workgroup
@@ -285,13 +283,11 @@ __global__ __launch_bounds__(D) void v_scale_kernel(const float *__restrict__ pa
 }
 
 // One workgroup per 64-key tile: codes through an LDS byte tile (rows of D
-// + 16 bytes), written channel-major as 16-byte key runs, with the tile's
-// per-channel code sums.
+// + 16 bytes), written channel-major as 16-byte key runs.
 template <bool kFp16, int D>
 __global__ __launch_bounds__(kVThreads) void v_quant_kernel(const uint16_t *__restrict__ v, int64_t len, int64_t lpad,
                                                            int64_t s_b, int64_t s_h, int64_t s_l,
-                                                           const float *__restrict__ scale, int8_t *__restrict__ vq,
-                                                           int32_t *__restrict__ tile_sum) {
+                                                           const float *__restrict__ scale, int8_t *__restrict__ vq) {
     constexpr int kPacks = D / 8;
     constexpr int kRows = kVThreads / kPacks;
     constexpr int kRowBytes = D + 16;
@@ -299,7 +295,7 @@ __global__ __launch_bounds__(kVThreads) void v_quant_kernel(const uint16_t *__re
     const int tid = threadIdx.x;
     const int pack = tid % kPacks;
     const int64_t tix = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-    const int64_t heads = gridDim.y, ntiles = gridDim.x;
+    const int64_t heads = gridDim.y;
     const int64_t bh = b * heads + h;
     const uint16_t *base = v + b * s_b + h * s_h;
     float inv[8];
@@ -323,72 +319,22 @@ __global__ __launch_bounds__(kVThreads) void v_quant_kernel(const uint16_t *__re
         *reinterpret_cast<u32x2 *>(tile + r * kRowBytes + pack * 8) = packed;
     }
     __syncthreads();
-    // item = (channel, 16-key run); the four runs of a channel are
-    // consecutive lanes, so the channel sum is two lane xors.
+    // item = (channel, 16-key run)
 #pragma unroll
     for (int item = tid; item < D * 4; item += kVThreads) {
         const int c = item >> 2, run = item & 3;
         u32x4 out;
-        int32_t s = 0;
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
             uint32_t word = 0;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int8_t code = tile[(run * 16 + 4 * w + e) * kRowBytes + c];
-                s += code;
                 word |= (static_cast<uint32_t>(code) & 0xffu) << (8 * e);
             }
             out[w] = word;
         }
         *reinterpret_cast<u32x4 *>(vq + (bh * D + c) * lpad + tix * 64 + run * 16) = out;
-        s += __shfl_xor(s, 1);
-        s += __shfl_xor(s, 2);
-        if (run == 0) tile_sum[(bh * ntiles + tix) * D + c] = s;
-    }
-}
-
-// Exclusive prefix over tiles of the per-channel tile sums:
-// prefix[t] = sum of tiles < t, t = 0 .. ntiles.  One workgroup per (batch,
-// head): kPrefixSegs segments of consecutive tiles per channel, each summed
-// by its own thread, the segment totals scanned through LDS, then each
-// segment's running prefix written.  Integer sums, so the split changes no
-// result.
-constexpr int kPrefixSegs = 8;
-
-template <int D>
-__global__ __launch_bounds__(D * kPrefixSegs) void v_prefix_kernel(const int32_t *__restrict__ tile_sum, int64_t ntiles,
-                                                                  int32_t *__restrict__ prefix) {
-    constexpr int kBatch = 8;  // independent loads in flight per thread
-    __shared__ int32_t seg_total[kPrefixSegs][D];
-    const int c = threadIdx.x % D, seg = threadIdx.x / D;
-    const int64_t bh = blockIdx.x;
-    const int64_t per = (ntiles + kPrefixSegs - 1) / kPrefixSegs;
-    const int64_t t_begin = min(ntiles, seg * per), t_end = min(ntiles, t_begin + per);
-    const int32_t *src = tile_sum + bh * ntiles * D + c;
-    int32_t *dst = prefix + bh * (ntiles + 1) * D + c;
-    int32_t total = 0;
-    for (int64_t t0 = t_begin; t0 < t_end; t0 += kBatch) {
-        int32_t v[kBatch];
-#pragma unroll
-        for (int j = 0; j < kBatch; ++j) v[j] = t0 + j < t_end ? src[(t0 + j) * D] : 0;
-#pragma unroll
-        for (int j = 0; j < kBatch; ++j) total += v[j];
-    }
-    seg_total[seg][c] = total;
-    __syncthreads();
-    int32_t acc = 0;
-    for (int s2 = 0; s2 < seg; ++s2) acc += seg_total[s2][c];
-    if (seg == 0) dst[0] = 0;
-    for (int64_t t0 = t_begin; t0 < t_end; t0 += kBatch) {
-        int32_t v[kBatch];
-#pragma unroll
-        for (int j = 0; j < kBatch; ++j) v[j] = t0 + j < t_end ? src[(t0 + j) * D] : 0;
-#pragma unroll
-        for (int j = 0; j < kBatch; ++j) {
-            acc += v[j];
-            if (t0 + j < t_end) dst[(t0 + j + 1) * D] = acc;
-        }
     }
 }
 
@@ -460,14 +406,13 @@ extern "C" int32_t tu_w8a8_quant_qk(const void *q, const void *k, int32_t dtype,
 extern "C" int64_t tu_w8a8_quant_v_workspace(int64_t batch, int64_t heads, int64_t len, int64_t dim) {
     if (batch <= 0 || heads <= 0 || len <= 0 || dim <= 0) return -1;
     const int64_t chunks = (len + tu::kVChunk - 1) / tu::kVChunk;
-    const int64_t ntiles = (len + 63) / 64;
-    // partial maxima (fp32) + tile sums (int32)
-    return batch * heads * dim * (chunks + ntiles) * 4;
+    // partial maxima (fp32)
+    return batch * heads * dim * chunks * 4;
 }
 
 extern "C" int32_t tu_w8a8_quant_v(const void *v, int32_t dtype, int64_t batch, int64_t heads, int64_t len,
                                    int64_t dim, int64_t s_b, int64_t s_h, int64_t s_l, int8_t *vq, int64_t lpad,
-                                   float *scale, int32_t *prefix, void *workspace, int64_t workspace_bytes,
+                                   float *scale, void *workspace, int64_t workspace_bytes,
                                    void *stream) {
     using namespace tu;
     TU_REQUIRE(dtype == 0 || dtype == 1, "W8A8 V dtype must be 0 (bf16) or 1 (fp16)");
@@ -476,7 +421,7 @@ extern "C" int32_t tu_w8a8_quant_v(const void *v, int32_t dtype, int64_t batch, 
     TU_REQUIRE(batch > 0 && heads > 0 && len > 0 && batch <= 65535 && heads <= 65535,
                "W8A8 V quantizer dimensions out of range");
     TU_REQUIRE(lpad == (len + 63) / 64 * 64, "W8A8 V padded length must be ceil(len / 64) * 64");
-    TU_REQUIRE(v && vq && scale && prefix && workspace, "W8A8 V quantizer pointers must be non-null");
+    TU_REQUIRE(v && vq && scale && workspace, "W8A8 V quantizer pointers must be non-null");
     TU_REQUIRE(workspace_bytes >= tu_w8a8_quant_v_workspace(batch, heads, len, dim),
                "W8A8 V quantizer workspace too small");
     TU_REQUIRE(s_b % 8 == 0 && s_h % 8 == 0 && s_l % 8 == 0 && (reinterpret_cast<uintptr_t>(v) & 15) == 0 &&
@@ -487,7 +432,6 @@ extern "C" int32_t tu_w8a8_quant_v(const void *v, int32_t dtype, int64_t batch, 
     const int64_t chunks = (len + kVChunk - 1) / kVChunk;
     const int64_t ntiles = lpad / 64;
     float *partial = static_cast<float *>(workspace);
-    int32_t *tile_sum = reinterpret_cast<int32_t *>(partial + batch * heads * dim * chunks);
     const uint16_t *vp = static_cast<const uint16_t *>(v);
     const dim3 g1(static_cast<unsigned>(chunks), static_cast<unsigned>(heads), static_cast<unsigned>(batch));
     const dim3 g3(static_cast<unsigned>(ntiles), static_cast<unsigned>(heads), static_cast<unsigned>(batch));
@@ -496,8 +440,7 @@ extern "C" int32_t tu_w8a8_quant_v(const void *v, int32_t dtype, int64_t batch, 
     do {                                                                                                      \
         v_amax_kernel<F16, DD><<<g1, kVThreads, 0, s>>>(vp, len, s_b, s_h, s_l, partial);                     \
         v_scale_kernel<DD><<<bh, DD, 0, s>>>(partial, chunks, scale);                                         \
-        v_quant_kernel<F16, DD><<<g3, kVThreads, 0, s>>>(vp, len, lpad, s_b, s_h, s_l, scale, vq, tile_sum);  \
-        v_prefix_kernel<DD><<<bh, DD * kPrefixSegs, 0, s>>>(tile_sum, ntiles, prefix);                                      \
+        v_quant_kernel<F16, DD><<<g3, kVThreads, 0, s>>>(vp, len, lpad, s_b, s_h, s_l, scale, vq);            \
     } while (0)
     if (dtype) {
         if (dim == 128) TU_V_LAUNCH(true, 128);

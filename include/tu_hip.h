@@ -337,20 +337,17 @@ int64_t tu_w8a8_quant_v_workspace(int64_t batch, int64_t heads, int64_t len, int
 
 /* Channel-wise signed INT8 V:
  *   scale[c] = max(amax_c / 127, 1e-12) over all len tokens;
- *   vq[c][t] = cvt.rni.sat.s8(v[t][c] * (1 / scale[c])), 0 for t >= len;
- *   prefix[t][c] = sum of vq[c][0 .. 64 t) (t = 0 .. lpad/64).
+ *   vq[c][t] = cvt.rni.sat.s8(v[t][c] * (1 / scale[c])), 0 for t >= len.
  * v: bf16/fp16 by element strides, 16-byte aligned rows; dim in {64, 128}.
  * vq: int8 [batch, heads, dim, lpad] with lpad = ceil(len/64)*64 (keys in
- * natural order); scale: fp32 [batch, heads, dim]; prefix: int32
- * [batch, heads, lpad/64 + 1, dim]; workspace: tu_w8a8_quant_v_workspace
- * bytes.  Replaces quantize_v_int8_sm75 (turing_sage/core.py:772-784 ->
+ * natural order); scale: fp32 [batch, heads, dim]; workspace:
+ * tu_w8a8_quant_v_workspace bytes.  Replaces quantize_v_int8_sm75 (turing_sage/core.py:772-784 ->
  * kernel/csrc/turing/sage/quant_v_int8_cuda_sm75.cu:58-164, :177-246); the
  * reference's 16-token key permutation (its Turing MMA fragment order) is
  * not used, the codes are the same. */
 int32_t tu_w8a8_quant_v(const void *v, int32_t dtype, int64_t batch, int64_t heads, int64_t len,
                         int64_t dim, int64_t s_b, int64_t s_h, int64_t s_l, int8_t *vq, int64_t lpad,
-                        float *scale, int32_t *prefix, void *workspace, int64_t workspace_bytes,
-                        void *stream);
+                        float *scale, void *workspace, int64_t workspace_bytes, void *stream);
 
 /* Dense W8A8 attention forward on INT8 Q/K/V:
  *   s = float(q8 . k8); masked keys (>= lk; causal: key > query, top-left)
@@ -362,8 +359,8 @@ int32_t tu_w8a8_quant_v(const void *v, int32_t dtype, int64_t batch, int64_t hea
  *   out = O / l * v_scale[channel], bf16 (out_fp16 0) or fp16 (1)
  * q8, k8: int8 by element strides (16-byte aligned rows), dim == 128, GQA
  * hq % hkv == 0; q_scale: fp32 [batch, hq, nqs >= ceil(lq/16)]; k_scale:
- * fp32 [batch, hkv, nks >= ceil(lk/64)]; vq, v_scale, prefix from
- * tu_w8a8_quant_v (lpad = ceil(lk/64)*64); out by strides.
+ * fp32 [batch, hkv, nks >= ceil(lk/64)]; vq, v_scale from tu_w8a8_quant_v
+ * (lpad = ceil(lk/64)*64); out by strides.
  * Replaces sol_sparse_online_w8a8_prequantized_attn with force_dense
  * (turing_sage/core.py:916-982 -> kernel/csrc/turing/sage/
  * sol_sparse_cuda_sm75.cu:2767-2932 -> sparse_attention_kernel
@@ -371,7 +368,7 @@ int32_t tu_w8a8_quant_v(const void *v, int32_t dtype, int64_t batch, int64_t hea
  * turing_utils::w8a8_attention (turing_sage/custom_ops.py:171-210). */
 int32_t tu_w8a8_attn_fwd(const int8_t *q8, const float *q_scale, int64_t nqs, const int8_t *k8,
                          const float *k_scale, int64_t nks, const int8_t *vt, const float *v_scale,
-                         const int32_t *v_prefix, int64_t lpad, void *out, int32_t out_fp16,
+                         int64_t lpad, void *out, int32_t out_fp16,
                          int64_t batch, int64_t hq, int64_t hkv, int64_t lq, int64_t lk, int64_t dim,
                          int64_t q_sb, int64_t q_sh, int64_t q_sl, int64_t k_sb, int64_t k_sh,
                          int64_t k_sl, int64_t o_sb, int64_t o_sh, int64_t o_sl, float sm_scale,

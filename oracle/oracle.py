@@ -114,7 +114,7 @@ def lib():
             L.or_w8a8_quant_tiles.argtypes = [_p, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                                               _i32, _p, _p, _p]
             L.or_w8a8_quant_v.restype = _i32
-            L.or_w8a8_quant_v.argtypes = [_p, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p]
+            L.or_w8a8_quant_v.argtypes = [_p, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p]
             L.or_w8a8_attn_rows.restype = _i32
             L.or_w8a8_attn_rows.argtypes = [_p, _i64, _i64, _i64, _p, _i64, _p, _i64, _i64, _i64, _p, _i64,
                                             _p, _i64, _p, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _i32,
@@ -481,18 +481,17 @@ def w8a8_quant_qk(q_bits: np.ndarray, k_bits: np.ndarray, dtype: int = DTYPE_BF1
     return q8, qs, k8, ks, anchors
 
 
-def w8a8_quant_v(v_bits: np.ndarray, dtype: int = DTYPE_BF16) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
-    """(int8 [B, H, D, Lpad], fp32 scales [B, H, D], int32 tile sums
-    [B, H, Lpad/64, D]) of the channel-wise V quantizer; v_bits HND."""
+def w8a8_quant_v(v_bits: np.ndarray, dtype: int = DTYPE_BF16) -> tuple[np.ndarray, np.ndarray]:
+    """(int8 [B, H, D, Lpad], fp32 scales [B, H, D]) of the channel-wise V
+    quantizer; v_bits HND."""
     v_bits = np.ascontiguousarray(v_bits, dtype=np.uint16)
     b, h, l, d, sb, sh, sl = _hnd(v_bits)
     lpad = (l + 63) // 64 * 64
     q = np.empty((b, h, d, lpad), dtype=np.int8)
     s = np.empty((b, h, d), dtype=np.float32)
-    ts = np.empty((b, h, lpad // 64, d), dtype=np.int32)
-    _check(lib().or_w8a8_quant_v(_ptr(v_bits), dtype, b, h, l, d, sb, sh, sl, lpad, _ptr(q), _ptr(s), _ptr(ts)),
+    _check(lib().or_w8a8_quant_v(_ptr(v_bits), dtype, b, h, l, d, sb, sh, sl, lpad, _ptr(q), _ptr(s)),
            "w8a8_quant_v")
-    return q, s, ts
+    return q, s
 
 
 def w8a8_attn_rows(q8: np.ndarray, qs: np.ndarray, k8: np.ndarray, ks: np.ndarray, v8: np.ndarray,

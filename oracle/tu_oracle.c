@@ -1017,15 +1017,11 @@ OR_API int or_w8a8_quant_tiles(const uint16_t *x, int dtype, int64_t batch, int6
 /*   scale[c] = max(amax_c / 127, 1e-12)  (amax over all L tokens)           */
 /*   q[c][t]  = cvt.rni.sat.s8(float(v[t][c]) * (1 / scale[c]))              */
 /* Output layout (this build's, channel-major with keys in natural order):   */
-/* q [B][H][D][lpad] with zeros for t >= L, and tile_sum [B][H][lpad/64][D]  */
-/* = the sum of each 64-key tile's codes per channel (used by the offset     */
-/* form of the u8 x s8 product).  The reference permutes keys within groups  */
-/* of 16 for its Turing MMA fragment; the codes are the same.                */
+/* q [B][H][D][lpad] with zeros for t >= L.  The reference permutes keys     */
+/* within groups of 16 for its Turing MMA fragment; the codes are the same.  */
 OR_API int or_w8a8_quant_v(const uint16_t *v, int dtype, int64_t batch, int64_t heads, int64_t len, int64_t dim,
-                           int64_t s_b, int64_t s_h, int64_t s_l, int64_t lpad, int8_t *q, float *scale,
-                           int32_t *tile_sum) {
+                           int64_t s_b, int64_t s_h, int64_t s_l, int64_t lpad, int8_t *q, float *scale) {
     if (lpad < len || lpad % 64) return -1;
-    const int64_t ntiles = lpad / 64;
     for (int64_t b = 0; b < batch; ++b)
         for (int64_t h = 0; h < heads; ++h) {
             const uint16_t *vb = v + b * s_b + h * s_h;
@@ -1038,11 +1034,6 @@ OR_API int or_w8a8_quant_v(const uint16_t *v, int dtype, int64_t batch, int64_t 
                 int8_t *qc = q + ((b * heads + h) * dim + c) * lpad;
                 for (int64_t t = 0; t < lpad; ++t)
                     qc[t] = t < len ? sat_rne_s8(t_to_f32(vb[t * s_l + c], dtype) * inv) : 0;
-                for (int64_t ti = 0; ti < ntiles; ++ti) {
-                    int32_t s = 0;
-                    for (int64_t t = 64 * ti; t < 64 * ti + 64; ++t) s += qc[t];
-                    tile_sum[((b * heads + h) * ntiles + ti) * dim + c] = s;
-                }
             }
         }
     return 0;

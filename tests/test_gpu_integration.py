@@ -259,7 +259,7 @@ def test_w8a8_override_nhd(gpu_device, stabilize):
     assert out.shape == (b, l, h * d) and out.dtype == torch.bfloat16
     rows = _sample(b, h, l, 96, 71)
     q8, qs, k8, ks, _ = oracle.w8a8_quant_qk(inputs.bits(q), inputs.bits(k), oracle.DTYPE_BF16, True, stabilize)
-    v8, vs, _ = oracle.w8a8_quant_v(inputs.bits(v), oracle.DTYPE_BF16)
+    v8, vs = oracle.w8a8_quant_v(inputs.bits(v), oracle.DTYPE_BF16)
     ref = oracle.w8a8_attn_rows(q8, qs, k8, ks, v8, vs, l, d ** -0.5, rows, False)
     got = out.view(b, l, h, d)[torch.from_numpy(rows[:, 0]), torch.from_numpy(rows[:, 2]), torch.from_numpy(rows[:, 1])]
     _check(got, ref)

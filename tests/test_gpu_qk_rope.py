@@ -293,7 +293,7 @@ def test_w8a8_variant_feeds_both_attentions(gpu_device):
     q8, qs = oracle.qk_rms_rope_int8_ex(_bits(q), 0, _bits(qw), "row", 1e-6, f32, 128, False, 16, 20, True)
     k8, ks = oracle.qk_rms_rope_int8_ex(_bits(k), 0, _bits(kw), "row", 1e-6, f32, 128, False, 64, 5, True,
                                         anchors, values)
-    v8, vs, _ = oracle.w8a8_quant_v(_bits(v))
+    v8, vs = oracle.w8a8_quant_v(_bits(v))
     rows = np.array([[0, h, i] for h in range(4) for i in range(300)])
     ref = oracle.w8a8_attn_rows(q8, qs, k8, ks, v8, vs, 300, 128 ** -0.5, rows).reshape(1, 4, 300, 128)
     require_attention_correctness(attention_error_metrics(out, torch.from_numpy(ref)), max_abs=2e-2, cosine=0.999)

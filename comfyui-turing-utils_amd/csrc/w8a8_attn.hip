@@ -420,8 +420,8 @@ __global__ __launch_bounds__(kThreads, 1) void w8a8_attn_kernel(
     // The schedule of the Sage kernel (sage_attn.hip): one barrier per key
     // tile; both groups run M_it = {QK(it + 1), PV(it)} then softmax(it + 1),
     // group 0's barrier after the softmax, group 1's before it, so the two
-    // groups' MFMA clusters overlap on each SIMD.  Unlike there, group 0
-    // issues the next tile's loads after its softmax.
+    // groups' MFMA clusters overlap on each SIMD.  Group 0 issues the next
+    // tile's loads between its MFMA and softmax clusters, as there.
     if (grp == 0) __builtin_amdgcn_s_waitcnt(vmcnt_imm((kAhead - 1) * kLoadsPerTile));
     wg_barrier();
     qk_tile8(lds[0], gm, qf, s);
@@ -435,10 +435,10 @@ __global__ __launch_bounds__(kThreads, 1) void w8a8_attn_kernel(
 #pragma clang loop unroll(disable)
     for (int it = 0; it < main_steps; ++it) {
         mfma_cluster8(lds[(it + 1) % kStages], lds[it % kStages], gm, qf, s, p8, st);
+        if (grp == 0) issue_tile8(lds[(it + kAhead) % kStages], krs, vrs, gm, k_sl32, tile_key0(it + kAhead), w4);
         if (grp == 1) wg_barrier();
         softmax(it + 1, std::false_type{});
         if (grp == 0) {
-            issue_tile8(lds[(it + kAhead) % kStages], krs, vrs, gm, k_sl32, tile_key0(it + kAhead), w4);
             __builtin_amdgcn_s_waitcnt(vmcnt_imm((kAhead - 2) * kLoadsPerTile));
             wg_barrier();
         }
@@ -447,10 +447,10 @@ __global__ __launch_bounds__(kThreads, 1) void w8a8_attn_kernel(
     for (int it = main_steps; it < tiles; ++it) {
         if (it + 1 < my_tiles) qk_tile8(lds[(it + 1) % kStages], gm, qf, s);
         if (it < my_tiles) pv_tile8(lds[it % kStages], gm, p8, st);
+        if (grp == 0) issue_tile8(lds[(it + kAhead) % kStages], krs, vrs, gm, k_sl32, tile_key0(it + kAhead), w4);
         if (grp == 1) wg_barrier();
         if (it + 1 < my_tiles) softmax(it + 1, std::true_type{});
         if (grp == 0) {
-            issue_tile8(lds[(it + kAhead) % kStages], krs, vrs, gm, k_sl32, tile_key0(it + kAhead), w4);
             __builtin_amdgcn_s_waitcnt(vmcnt_imm((kAhead - 2) * kLoadsPerTile));
             wg_barrier();
         }

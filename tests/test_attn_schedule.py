@@ -3,8 +3,8 @@
 ``sage_attn_kernel`` (csrc/sage_attn.hip) and ``w8a8_attn_kernel``
 (csrc/w8a8_attn.hip, 4 loads per tile instead of 6) run 8 waves in two groups that
 share one workgroup barrier per key tile.  Group 0 issues a tile's loads
-between its MFMA and softmax clusters in the Sage kernel, and after the
-softmax in the W8A8 kernel (whose flushes wait on loads of their own).  Every wave executes, per tile t,
+between its MFMA and softmax clusters.  The model also covers issuing them
+after the softmax, an order the W8A8 kernel once used.  Every wave executes, per tile t,
 an MFMA cluster M_t = {QK(t + 1), PV(t)} and a softmax cluster V_t; group 0
 orders an interval as [M_t, V_{t+1}], group 1 as [V_t, M_t], so the two
 groups' MFMA clusters overlap on each SIMD.  Group 0 alone streams the K and
@@ -34,7 +34,7 @@ K_AHEAD = K_STAGES - 1
 # per kernel: 1 KiB blocks a group-0 wave loads per tile (Sage head_dim 128:
 # 2 K + 4 V^T, Sage head_dim 64: 1 K + 2 V^T, W8A8 2 K + 2 V^T), and whether
 # it issues them after the softmax
-KERNELS = {"sage": (6, False), "sage64": (3, False), "w8a8": (4, True)}
+KERNELS = {"sage": (6, False), "sage64": (3, False), "w8a8": (4, False), "w8a8_after": (4, True)}
 KBKEY = 64
 KBQ = 256
 KWAVEQ = 32
@@ -334,7 +334,7 @@ def test_k_loads_stay_in_bounds(kernel, lk, layout, kv_splits):
     alloc_end = lk * k_sl  # bytes of the K tensor
     rng = lk * k_sl  # buffer range from the head's base
     splits = [(None, 0)]
-    if kv_splits > 1 and kernel != "w8a8" and (lk + KBKEY - 1) // KBKEY >= kv_splits:
+    if kv_splits > 1 and not kernel.startswith("w8a8") and (lk + KBKEY - 1) // KBKEY >= kv_splits:
         st, n = split_plan(lk, kv_splits)
         splits = [(z, st) for z in range(n)]
     offs = k_load_offsets(kernel, k_sl)

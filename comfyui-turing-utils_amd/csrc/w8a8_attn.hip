@@ -28,7 +28,8 @@
 //     v_cvt_pk_u8_f32 rounds p to an integer half-to-even into its byte of
 //     the packed operand, and an XOR with 0x7f per byte turns P into 127 - P.
 //   * The PV products stay in int32 accumulators across tiles and are
-//     converted to fp32 only when the row maximum moves (the reference
+//     converted to fp32, per 16-row query fragment, only when the maximum
+//     of one of its rows moves (the reference
 //     rescales O every tile; a rescale by 2^0 is exact) or every 512 tiles
 //     (int32 headroom: each key adds at most 255 * 127 in magnitude per
 //     product, and 2 * 127 * 127 with the constant MFMA's term).
@@ -73,22 +74,26 @@ struct LaneGeom8 {
     uint32_t v_rd;      // LDS byte offset of the PV A operand (channel lc, keys 16 g ..)
 };
 
-// K rows are 128 B with 16-byte chunks XOR-swizzled by row bits 1..3; V^T
-// rows are 64 B with chunks XOR-swizzled by row bits 2..3.  Both are
-// conflict-free for the 16 lanes that read one chunk column.
+// K rows are 128 B with 16-byte chunks XOR-swizzled by row bits 1..3.  A
+// V^T block (16 channels x 64 keys) holds chunk (channel c, keys 16 g ..) at
+// 16-byte position 16 g + 8 (c & 1) + (g ^ (c >> 1)), so a lane's PV read
+// lands on the same position modulo 256 bytes as its K read of chunk column
+// g: both reads are spread over the LDS banks alike.  (Plain 64-byte rows
+// with a 2-bit XOR swizzle cost 4 bank-conflict cycles per V^T read.)
 __device__ __forceinline__ LaneGeom8 lane_geom8(int wave, int lane, int64_t k_sl, int64_t lpad) {
     LaneGeom8 gm;
     const int g = lane >> 4, lc = lane & 15, sw = (lc >> 1) & 7;
+    // the chunk that DMA lane `lane` writes to position `lane` of its block
+    const int vc = 2 * ((lane & 7) ^ g) + ((lane >> 3) & 1);
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         const int row = (2 * wave + i) * 8 + (lane >> 3);
         gm.k_src[i] = static_cast<uint32_t>(kperm8(row) * k_sl + ((lane & 7) ^ ((row >> 1) & 7)) * 16);
         gm.k_rd[i] = static_cast<uint32_t>(lc * 128 + (((4 * i + g) ^ sw) << 4));
-        const int d = 16 * (2 * wave + i) + (lane >> 2);
-        const int c = (lane & 3) ^ ((lane >> 4) & 3);
-        gm.v_src[i] = static_cast<uint32_t>(d * lpad + 16 * c);
+        const int d = 16 * (2 * wave + i) + vc;
+        gm.v_src[i] = static_cast<uint32_t>(d * lpad + 16 * g);
     }
-    gm.v_rd = static_cast<uint32_t>(kKTileBytes + lc * 64 + ((g ^ ((lc >> 2) & 3)) << 4));
+    gm.v_rd = static_cast<uint32_t>(kKTileBytes + ((16 * g + 8 * (lc & 1) + (g ^ sw)) << 4));
     return gm;
 }
 
@@ -122,8 +127,8 @@ __device__ __forceinline__ void qk_tile8(const int8_t *stage, const LaneGeom8 &g
     }
 }
 
-// Wave softmax state.  acc_i holds the PV products of tiles [seg, current)
-// in int32 (with P - 128 operands).  acc_o and l are kept at a fixed
+// Wave softmax state.  acc_i[.][qt] holds -(P . v8) of tiles [seg[qt],
+// current) in int32; each 16-row query fragment qt has its own segment.  acc_o and l are kept at a fixed
 // exponent base per query, the first one: a segment computed at base m_used
 // enters them scaled by beta = 2^(m_used - that base), so a move of the
 // running maximum rescales nothing (O / l does not depend on the base).  The
@@ -135,7 +140,7 @@ struct W8State {
     float l[kQT];
     f32x4 acc_o[8][kQT];
     i32x4 acc_i[8][kQT];
-    int seg;
+    int seg[kQT];
 };
 constexpr float kRebase = 0x1p64f;
 
@@ -158,23 +163,50 @@ __device__ __forceinline__ void mask_tile8(i32x4 (&s)[4][kQT], int key_lim, int 
     }
 }
 
-// Adds the int32 segment [st.seg, tile) to acc_o: acc_i holds -(P . v8)
-// exactly, so acc_o += float(acc_i) * -beta; then clears acc_i.
-__device__ __forceinline__ void flush_segment(W8State &st, int tile) {
-    if (tile > st.seg) {
+// Adds fragment qt's int32 segment [st.seg[qt], tile) to acc_o: acc_i holds
+// -(P . v8) exactly, so acc_o += float(acc_i) * -beta; then clears acc_i.
+template <int qt>
+__device__ __forceinline__ void flush_fragment(W8State &st, int tile) {
+    if (tile > st.seg[qt]) {
 #pragma unroll
         for (int ds = 0; ds < 8; ++ds) {
 #pragma unroll
-            for (int qt = 0; qt < kQT; ++qt) {
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    st.acc_o[ds][qt][r] =
-                        __builtin_fmaf(static_cast<float>(st.acc_i[ds][qt][r]), -st.beta[qt], st.acc_o[ds][qt][r]);
-                st.acc_i[ds][qt] = i32x4{0, 0, 0, 0};
-            }
+            for (int r = 0; r < 4; ++r)
+                st.acc_o[ds][qt][r] =
+                    __builtin_fmaf(static_cast<float>(st.acc_i[ds][qt][r]), -st.beta[qt], st.acc_o[ds][qt][r]);
+            st.acc_i[ds][qt] = i32x4{0, 0, 0, 0};
         }
     }
-    st.seg = tile;
+    st.seg[qt] = tile;
+}
+
+// Flushes both fragments (at the end of the key range).
+__device__ __forceinline__ void flush_segment(W8State &st, int tile) {
+    flush_fragment<0>(st, tile);
+    flush_fragment<1>(st, tile);
+}
+
+// The reference's exact running maximum of fragment qt: when some row's
+// maximum moves (or the int32 headroom runs out), only this fragment's
+// segment is flushed.
+template <int qt>
+__device__ __forceinline__ void move_max(W8State &st, const float (&mlane)[kQT], int tile) {
+    if (__any(mlane[qt] > st.m_used[qt]) || tile - st.seg[qt] >= kFlushTiles) {
+        flush_fragment<qt>(st, tile);
+        const float mx = xmax_f32(mlane[qt]);
+        const float m_new = mx > st.m_used[qt] ? mx : st.m_used[qt];
+        // the first tile fixes the base (acc_o and l are still 0)
+        st.beta[qt] = st.m_used[qt] == -INFINITY ? 1.0f
+                                                 : st.beta[qt] * __builtin_amdgcn_exp2f(m_new - st.m_used[qt]);
+        st.m_used[qt] = m_new;
+        if (__any(st.beta[qt] > kRebase)) {
+            const float alpha = 1.0f / st.beta[qt];
+            st.beta[qt] = 1.0f;
+            st.l[qt] *= alpha;
+#pragma unroll
+            for (int ds = 0; ds < 8; ++ds) st.acc_o[ds][qt] *= alpha;
+        }
+    }
 }
 
 // The constant PV operand: -127 in every byte.
@@ -189,7 +221,6 @@ __device__ __forceinline__ i32x4 neg127_operand() {
 __device__ __forceinline__ void softmax_tile8(const i32x4 (&s)[4][kQT], const float (&f)[kQT], W8State &st,
                                               i32x4 (&p8)[kQT], int tile) {
     float mlane[kQT];
-    bool need = false;
 #pragma unroll
     for (int qt = 0; qt < kQT; ++qt) {
         int mi = imax3(s[0][qt][0], s[0][qt][1], s[0][qt][2]);
@@ -201,33 +232,9 @@ __device__ __forceinline__ void softmax_tile8(const i32x4 (&s)[4][kQT], const fl
         mi = imax3(mi, s[3][qt][1], s[3][qt][2]);
         mi = max(mi, s[3][qt][3]);
         mlane[qt] = __builtin_fmaf(__int_as_float(mi) - kBiasF, f[qt], -kU8Offset);
-        need = need || (mlane[qt] > st.m_used[qt]);
     }
-    if (__any(need) || tile - st.seg >= kFlushTiles) {
-        flush_segment(st, tile);
-        bool rebase = false;
-#pragma unroll
-        for (int qt = 0; qt < kQT; ++qt) {
-            // the reference's exact running maximum
-            const float mx = xmax_f32(mlane[qt]);
-            const float m_new = mx > st.m_used[qt] ? mx : st.m_used[qt];
-            // the first tile fixes the base (acc_o and l are still 0)
-            st.beta[qt] = st.m_used[qt] == -INFINITY ? 1.0f
-                                                     : st.beta[qt] * __builtin_amdgcn_exp2f(m_new - st.m_used[qt]);
-            st.m_used[qt] = m_new;
-            rebase = rebase || st.beta[qt] > kRebase;
-        }
-        if (__any(rebase)) {
-#pragma unroll
-            for (int qt = 0; qt < kQT; ++qt) {
-                const float alpha = 1.0f / st.beta[qt];
-                st.beta[qt] = 1.0f;
-                st.l[qt] *= alpha;
-#pragma unroll
-                for (int ds = 0; ds < 8; ++ds) st.acc_o[ds][qt] *= alpha;
-            }
-        }
-    }
+    move_max<0>(st, mlane, tile);
+    move_max<1>(st, mlane, tile);
     float c[kQT];
     bool exact = false;
 #pragma unroll
@@ -249,7 +256,7 @@ __device__ __forceinline__ void softmax_tile8(const i32x4 (&s)[4][kQT], const fl
                     const float x = decltype(exact_tag)::value ? __builtin_fmaf(v - kBiasF, f[qt], nm)
                                                                : __builtin_fmaf(v, f[qt], c[qt]);
                     const float p = __builtin_amdgcn_exp2f(x);
-                    lsum += p;
+                    lsum = kt == 0 && r == 0 ? p : lsum + p;
                     // byte r = rint(p): v_cvt_pk_u8_f32 rounds half to even
                     // (checked against rint on every float in [0, 256]); p
                     // <= 255 since the base sits log2(255) above the maximum
@@ -386,7 +393,7 @@ __global__ __launch_bounds__(kThreads, 1) void w8a8_attn_kernel(
         for (int j = 0; j < kAhead; ++j) issue_tile8(lds[j], krs, vrs, gm, k_sl32, tile_key0(j), w4);
     }
     W8State st;
-    st.seg = 0;
+    st.seg[0] = st.seg[1] = 0;
 #pragma unroll
     for (int qt = 0; qt < kQT; ++qt) {
         st.m_used[qt] = -INFINITY;

@@ -380,3 +380,48 @@ def test_model_catches_a_missing_wait(kernel):
             check_schedule(1000, 1000, False, 0, kernel)
     finally:
         K_AHEAD = saved
+
+
+# LDS layout of the W8A8 kernel's V^T blocks (lane_geom8 in csrc/w8a8_attn.hip):
+# a loader lane writes its 16 bytes to position `lane` of a 1 KiB block (16
+# channels x 64 keys), fetching channel 2 ((lane & 7) ^ g) + ((lane >> 3) & 1)
+# and keys 16 g .. 16 g + 15 with g = lane >> 4; the PV reader (g, lc) wants
+# channel lc, keys 16 g .., and reads position 16 g + 8 (lc & 1) + (g ^ (lc >> 1)).
+def w8a8_v_dma_chunk(lane: int):
+    g = lane >> 4
+    return 2 * ((lane & 7) ^ g) + ((lane >> 3) & 1), g
+
+
+def w8a8_v_read_pos(lane: int) -> int:
+    g, lc = lane >> 4, lane & 15
+    return 16 * g + 8 * (lc & 1) + (g ^ ((lc >> 1) & 7))
+
+
+def sage_k_read_pos(lane: int, i: int) -> int:
+    """16-byte position of the K read of chunk column 4 i + g (128-byte rows)."""
+    g, lc = lane >> 4, lane & 15
+    return 8 * lc + ((4 * i + g) ^ ((lc >> 1) & 7))
+
+
+def test_w8a8_v_layout_is_consistent():
+    """Every reader finds at its position the chunk a loader lane wrote
+    there, and the 64 positions are a permutation of the block."""
+    reads = [w8a8_v_read_pos(lane) for lane in range(64)]
+    assert sorted(reads) == list(range(64))
+    for lane in range(64):
+        g, lc = lane >> 4, lane & 15
+        assert w8a8_v_dma_chunk(reads[lane]) == (lc, g)
+
+
+def test_w8a8_v_reads_spread_like_k_reads():
+    """Each lane's V^T read falls on the same 16-byte slot modulo 256 bytes
+    (the same banks) as its K read, a pattern the bank-conflict counter
+    reads as zero; the plain 64-byte-row layout does not."""
+    for lane in range(64):
+        assert w8a8_v_read_pos(lane) % 16 == sage_k_read_pos(lane, 0) % 16
+
+    def plain(lane):
+        g, lc = lane >> 4, lane & 15
+        return 4 * lc + (g ^ ((lc >> 2) & 3))
+
+    assert any(plain(lane) % 16 != sage_k_read_pos(lane, 0) % 16 for lane in range(64))

@@ -7,8 +7,9 @@
   * attention (tu_w8a8_attn_fwd vs or_w8a8_attn_rows on the same codes): the
     north-star attention bar, cosine >= 0.999 and max-abs <= 2e-2, plus a
     tighter relative bound measured for this kernel; causal, GQA, ragged Lq /
-    Lk, head_dim 64 through the padded path, fp16 output, and the reference's
-    finite-mask behaviour on an all-zero K tile;
+    Lk, head_dim 64 through the padded path, fp16 output, the reference's
+    finite-mask behaviour on an all-zero K tile, and one fragment flushing on
+    every tile while the other reaches the 512-tile int32 headroom;
   * the reference's own W8A8 self-test (turing_sage/__init__.py:573-609:
     allclose rtol 0.12 / atol 0.09 to fp32 SDPA) through preflight_w8a8 and
     the registered op, eager and under torch.compile;
@@ -288,3 +289,33 @@ def test_wan_shape_b1_h40_l32760(gpu_device):
     got = out[:, heads][:, :, sel].cpu().float().reshape(-1, 128)
     _compare(got, ref)
 
+
+
+def test_attention_fragment_flushes_and_headroom(gpu_device):
+    """Queries 0-15 (the first 16-row fragment of a wave) see scores that rise
+    with the key index, so their running maximum moves on every key tile and
+    that fragment flushes every tile.  Queries 16-31 (the second fragment) see
+    nearly equal scores whose maximum never moves after the first tile: P is
+    254-255 on every key and every V code is +-127, so that fragment's int32
+    segment grows by about 2.1e6 a tile and must be flushed at the 512-tile
+    headroom: over the 1100 tiles here it would pass 2^31 otherwise.  All V
+    rows are equal, so every output row is that row times sum(P) / sum(p)."""
+    from comfyui_turing_utils_kernel.turing_sage import w8a8attn
+
+    print("[w8a8-attn] fragment flushes + int32 headroom", flush=True)
+    lq, lk, d = 32, 1100 * 64, 128
+    g = torch.Generator().manual_seed(5)
+    u = torch.randn(d, generator=g)
+    ramp = torch.linspace(0.05, 4.0, lk)
+    k = (ramp[:, None] * u[None, :]).reshape(1, 1, lk, d)
+    q = torch.cat([u.expand(16, d), -1e-4 * u.expand(16, d)]).reshape(1, 1, lq, d)
+    v = torch.randn(d, generator=g).expand(lk, d).reshape(1, 1, lk, d)
+    q, k, v = (t.contiguous().to(torch.bfloat16) for t in (q, k, v))
+    out = w8a8attn(q.to(gpu_device), k.to(gpu_device), v.to(gpu_device))
+    torch.cuda.synchronize(gpu_device)
+    rows = np.array([(0, 0, i) for i in range(lq)])
+    ref = _oracle_attention(q, k, v, False, d ** -0.5, rows).reshape(1, 1, lq, d)
+    got = out.cpu().float()
+    _compare(got, ref)
+    # sum(P) / sum(p) is within a few tenths of a percent of 1 here
+    torch.testing.assert_close(got[0, 0], v[0, 0, :1].float().expand(lq, d), rtol=1e-2, atol=1e-2)
